@@ -1,0 +1,125 @@
+/*
+ * pbgdn.h - C ABI of the MI355X (gfx950) Gated DeltaNet operator.
+ *
+ * Two entry points carry the compute, each the device-side replacement of one
+ * kernel of the reference module pseudobrain/gated_deltanet.py:
+ *
+ *   pbgdn_chunk_fwd      chunkwise prefill; replaces the fla custom op
+ *                        `pseudobrain::gated_delta_chunk` (_fla_chunk_op,
+ *                        gated_deltanet.py:200-216) behind delta_rule_fla
+ *                        (gated_deltanet.py:280-285), and computes the same
+ *                        recurrence as delta_rule_chunked (gated_deltanet.py:110-165).
+ *   pbgdn_recurrent_fwd  per-token recurrence (decode steps, T <= SEQUENTIAL_MAX);
+ *                        replaces delta_rule_sequential (gated_deltanet.py:93-107).
+ *
+ * Conventions (all entry points):
+ *   - every pointer is device memory owned by the caller; nothing is allocated;
+ *   - tensors are dense row-major in the reference layouts:
+ *       q, k  [B, T, Hk, K]     v, o  [B, T, Hv, V]     g, beta  [B, T, Hv]
+ *       states [N, Hv, K, V] float32, S stored [d_k, d_v] per head;
+ *   - GQA: value head h reads query/key head h / (Hv / Hk)
+ *     (repeat_interleave, gated_deltanet.py:422-424); Hk == Hv is the
+ *     reference's already-repeated layout;
+ *   - g is the log decay (<= 0), float32; beta float32 or the q/k/v dtype;
+ *   - arithmetic: the state and every accumulation are float32;
+ *   - launches are asynchronous on `stream` (a hipStream_t; NULL = the null
+ *     stream); no host synchronisation; the kernels keep no global state and
+ *     are safe to call from several threads;
+ *   - return 0 (PBGDN_OK) or a PBGDN_ERR_* code; no exception crosses the ABI.
+ */
+#ifndef PBGDN_H_
+#define PBGDN_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PBGDN_ABI_VERSION 1
+
+/* element types */
+#define PBGDN_F32 0
+#define PBGDN_BF16 1
+#define PBGDN_F16 2
+
+/* status codes */
+#define PBGDN_OK 0
+#define PBGDN_ERR_INVALID_ARGUMENT 1 /* a null pointer, a bad size or dtype code */
+#define PBGDN_ERR_UNSUPPORTED 2      /* valid, but a head width / chunk this build has no kernel for */
+#define PBGDN_ERR_LAUNCH 3           /* the HIP launch failed (hipGetLastError) */
+
+/* Version of this ABI (PBGDN_ABI_VERSION). */
+int pbgdn_abi_version(void);
+
+/* Static text for a status code. */
+const char *pbgdn_status_string(int status);
+
+/*
+ * Chunkwise prefill (chunk = 64 tokens).
+ *
+ * Reference: _fla_chunk_op (pseudobrain/gated_deltanet.py:200-216) and
+ * delta_rule_chunked (gated_deltanet.py:110-165); the semantics are those of
+ * gated_delta_rule(q, k, v, g, beta, scale, h0) (gated_deltanet.py:300-308)
+ * with cu_seqlens varlen packing added.
+ *
+ *   q, k        [B, T, Hk, K]   dtype in_dtype (F32, BF16 or F16)
+ *   v           [B, T, Hv, V]   dtype in_dtype
+ *   g           [B, T, Hv]      float32 log decay
+ *   beta        [B, T, Hv]      dtype beta_dtype (F32 or in_dtype)
+ *   h0          [N, Hv, K, V]   float32 initial states, or NULL for zeros
+ *   cu_seqlens  [N + 1] int32 sequence boundaries into the T axis (B must be
+ *               1, cu_seqlens[0] == 0, cu_seqlens[N] == T, nondecreasing), or
+ *               NULL: then N = B sequences of T tokens each
+ *   o           [B, T, Hv, V]   dtype out_dtype, written
+ *   ht          [N, Hv, K, V]   float32 final states, written (may be NULL;
+ *               may equal h0 for an in-place state update)
+ *   num_seqs    N (must equal B when cu_seqlens is NULL)
+ *   scale       query scale (the reference passes K ** -0.5)
+ *   chunk       must be 64 (CHUNK, gated_deltanet.py:49)
+ *
+ * Supported: K in {64, 128}; V a multiple of 16; Hv a multiple of Hk.
+ */
+int pbgdn_chunk_fwd(const void *q, const void *k, const void *v, int in_dtype,
+                    const float *g, const void *beta, int beta_dtype,
+                    const float *h0, float *ht, const int32_t *cu_seqlens,
+                    int num_seqs, void *o, int out_dtype, int B, int T, int Hk,
+                    int Hv, int K, int V, float scale, int chunk,
+                    void *stream);
+
+/*
+ * Fused recurrent steps: for each token, in one pass over the state,
+ *   S <- exp(g) S;  u = beta (v - S^T k);  S <- S + k u^T;  o = S^T (q scale).
+ *
+ * Reference: delta_rule_sequential (pseudobrain/gated_deltanet.py:93-107),
+ * the kernel gated_delta_rule selects for T <= SEQUENTIAL_MAX (:291-297) and
+ * for one-token decode.
+ *
+ *   q, k        [B, T, Hk, K]   dtype in_dtype
+ *   v           [B, T, Hv, V]   dtype in_dtype
+ *   g, beta     [B, T, Hv]      g float32, beta beta_dtype
+ *   state_in    [S, Hv, K, V]   float32 states read (S = num_states)
+ *   state_out   [S, Hv, K, V]   float32 states written; may equal state_in
+ *               (in-place update: each state is read whole before it is written;
+ *               the slots of one call must be distinct)
+ *   state_idx   [B] int32 state slot of each sequence, or NULL for slot b;
+ *               a slot outside [0, num_states) (e.g. -1 padding) is skipped:
+ *               no state is touched and that sequence's o is written as zeros
+ *   num_states  S (must be >= B when state_idx is NULL)
+ *   o           [B, T, Hv, V]   dtype out_dtype
+ *
+ * Supported: K in {32, 64, 128, 256}, V in {32, 64, 128, 256}.
+ */
+int pbgdn_recurrent_fwd(const void *q, const void *k, const void *v,
+                        int in_dtype, const float *g, const void *beta,
+                        int beta_dtype, const float *state_in,
+                        float *state_out, const int32_t *state_idx,
+                        int num_states, void *o, int out_dtype, int B, int T,
+                        int Hk, int Hv, int K, int V, float scale,
+                        void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PBGDN_H_ */

@@ -1,0 +1,85 @@
+"""ctypes binding of libpbgdn.so (the C ABI declared in include/pbgdn.h).
+
+torch is imported first so that its HIP runtime is the one in the process:
+the library links libamdhip64 by soname and binds to whatever is loaded.
+A missing or stale library raises; there is no fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (loads torch's HIP runtime before the library)
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpbgdn.so")
+ABI_VERSION = 1
+
+F32, BF16, F16 = 0, 1, 2
+OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3
+
+DTYPE_CODES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
+
+# Every function the header declares, with its ctypes signature.
+_vp, _i, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+SIGNATURES = {
+    "pbgdn_abi_version": ([], _i),
+    "pbgdn_status_string": ([_i], ctypes.c_char_p),
+    "pbgdn_chunk_fwd": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _i,
+                         _i, _i, _i, _i, _i, _i, _f, _i, _vp], _i),
+    "pbgdn_recurrent_fwd": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _i,
+                             _i, _i, _i, _i, _i, _i, _f, _vp], _i),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+class PbgdnError(RuntimeError):
+    """A nonzero status returned by the C ABI."""
+
+    def __init__(self, status: int, where: str):
+        self.status = status
+        super().__init__(f"{where}: pbgdn status {status}: {status_string(status)}")
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises RuntimeError when it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"pbgdn HIP library not found at {LIB_PATH}; build it with "
+                    "`python -m pseudobrain_amd.build` (there is no CPU fallback)")
+            handle = ctypes.CDLL(LIB_PATH)
+            for name, (args, res) in SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.argtypes = args
+                fn.restype = res
+            version = handle.pbgdn_abi_version()
+            if version != ABI_VERSION:
+                raise RuntimeError(f"libpbgdn.so ABI version {version}, expected {ABI_VERSION}; rebuild it")
+            _lib = handle
+    return _lib
+
+
+def status_string(status: int) -> str:
+    return lib().pbgdn_status_string(int(status)).decode()
+
+
+def check(status: int, where: str) -> None:
+    if status != OK:
+        raise PbgdnError(status, where)
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    """Device address of a tensor (None for an absent optional tensor)."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device: torch.device) -> int:
+    """hipStream_t of torch's current stream on `device`."""
+    return torch.cuda.current_stream(device).cuda_stream

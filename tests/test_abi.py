@@ -1,0 +1,97 @@
+"""The C-ABI library: it loads, exports every symbol include/pbgdn.h declares,
+and rejects bad arguments with status codes before any launch (no GPU needed)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from pseudobrain_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "pbgdn.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pbgdn_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    assert declared_functions() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    for name in declared_functions():
+        assert isinstance(getattr(lib, name), ctypes._CFuncPtr), name
+
+
+def test_abi_version_and_status_strings():
+    assert _lib.lib().pbgdn_abi_version() == _lib.ABI_VERSION == 1
+    assert _lib.status_string(0) == "ok"
+    for code in (1, 2, 3, 99):
+        assert _lib.status_string(code)
+    with pytest.raises(_lib.PbgdnError, match="status 2"):
+        _lib.check(2, "x")
+
+
+FAKE = 0x1000  # never dereferenced: every call below fails validation first
+
+
+def chunk_call(**over):
+    args = dict(q=FAKE, k=FAKE, v=FAKE, in_dtype=1, g=FAKE, beta=FAKE, beta_dtype=0, h0=None,
+                ht=None, cu=None, nseq=1, o=FAKE, out_dtype=1, B=1, T=64, Hk=16, Hv=32, K=128,
+                V=128, scale=0.1, chunk=64, stream=None)
+    args.update(over)
+    return _lib.lib().pbgdn_chunk_fwd(*args.values())
+
+
+def recurrent_call(**over):
+    args = dict(q=FAKE, k=FAKE, v=FAKE, in_dtype=1, g=FAKE, beta=FAKE, beta_dtype=0, sin=FAKE,
+                sout=FAKE, idx=None, nstates=1, o=FAKE, out_dtype=1, B=1, T=1, Hk=16, Hv=32, K=128,
+                V=128, scale=0.1, stream=None)
+    args.update(over)
+    return _lib.lib().pbgdn_recurrent_fwd(*args.values())
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(in_dtype=5), _lib.ERR_INVALID_ARGUMENT),
+    (dict(out_dtype=-1), _lib.ERR_INVALID_ARGUMENT),
+    (dict(beta_dtype=2), _lib.ERR_INVALID_ARGUMENT),   # beta must be f32 or the input dtype
+    (dict(Hv=24), _lib.ERR_INVALID_ARGUMENT),          # not a multiple of Hk
+    (dict(T=-1), _lib.ERR_INVALID_ARGUMENT),
+    (dict(nseq=2), _lib.ERR_INVALID_ARGUMENT),         # N must equal B without cu_seqlens
+    (dict(cu=FAKE, B=2, nseq=2), _lib.ERR_INVALID_ARGUMENT),  # cu_seqlens needs B == 1
+    (dict(q=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(chunk=32), _lib.ERR_UNSUPPORTED),
+    (dict(K=96), _lib.ERR_UNSUPPORTED),
+    (dict(K=256), _lib.ERR_UNSUPPORTED),
+    (dict(V=120), _lib.ERR_UNSUPPORTED),
+])
+def test_chunk_fwd_rejects(over, code):
+    assert chunk_call(**over) == code
+
+
+def test_chunk_fwd_empty_is_ok():
+    assert chunk_call(B=0, nseq=0) == _lib.OK
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(in_dtype=3), _lib.ERR_INVALID_ARGUMENT),
+    (dict(Hk=0), _lib.ERR_INVALID_ARGUMENT),
+    (dict(Hv=20), _lib.ERR_INVALID_ARGUMENT),
+    (dict(sin=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(o=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(nstates=-1), _lib.ERR_INVALID_ARGUMENT),
+    (dict(B=4, nstates=3), _lib.ERR_INVALID_ARGUMENT),  # without state_idx, slot b must exist
+    (dict(K=48), _lib.ERR_UNSUPPORTED),
+    (dict(V=512), _lib.ERR_UNSUPPORTED),
+    (dict(B=70000, nstates=70000), _lib.ERR_UNSUPPORTED),
+])
+def test_recurrent_fwd_rejects(over, code):
+    assert recurrent_call(**over) == code
+
+
+def test_recurrent_fwd_empty_is_ok():
+    assert recurrent_call(B=0) == _lib.OK

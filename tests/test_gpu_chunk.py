@@ -1,0 +1,173 @@
+"""Parity of the chunkwise prefill kernel with the fp32 oracle
+(delta_rule_chunked, gated_deltanet.py:110-165), through the C ABI.
+
+Tolerances (infinity-norm relative error vs the fp32 reference on the same
+inputs): outputs 2e-2, final states 1e-3. At the full sizes of the varlen and
+million-token workloads the oracle is too slow for a test; there the checks are
+size-independent properties (packing == separate calls, streaming == one pass)
+plus oracle checks of windows taken from the GPU's own carried state."""
+import numpy as np
+import pytest
+import torch
+
+from pseudobrain_amd import gated_deltanet as gd
+from pseudobrain_amd.workloads import (STREAM_SEGMENT, generate, varlen_workload, workload)
+from tests.gpu_util import assert_parity, oracle, rel_err
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+SCALE = 128 ** -0.5
+
+
+def to_dev(*xs):
+    return [x.to(DEV) for x in xs]
+
+
+def run(q, k, v, g, beta, scale, h0, cu=None):
+    o, s = gd.chunk_fwd(*to_dev(q, k, v, g, beta), scale, None if h0 is None else h0.to(DEV),
+                        None if cu is None else cu.to(DEV))
+    torch.cuda.synchronize()
+    return o, s
+
+
+def test_prefill_small_fp32_inputs():
+    """B=1, T=2048, H=4, K=V=64, fp32 inputs, zero initial state."""
+    q, k, v, g, beta, h0 = workload("prefill_small", seed=0)
+    o_ref, s_ref = oracle(q, k, v, g, beta, 64 ** -0.5, h0)
+    o, s = gd.gated_delta_rule(*to_dev(q, k, v, g, beta), 64 ** -0.5, h0.to(DEV), kernel="chunked")
+    torch.cuda.synchronize()
+    assert o.dtype == torch.float32 and s.dtype == torch.float32
+    assert_parity("prefill_small", o, o_ref, s, s_ref)
+
+
+@pytest.mark.parametrize("length", [4096])
+def test_prefill_qwen3next_shape(length):
+    """Hk=16 -> Hv=32, K=V=128, bf16 in, fp32 state, seeded h0."""
+    q, k, v, g, beta, h0 = workload("prefill_qwen3next", seed=1, length=length)
+    o_ref, s_ref = oracle(q, k, v, g, beta, SCALE, h0)
+    o, s = run(q, k, v, g, beta, SCALE, h0)
+    assert o.dtype == torch.bfloat16
+    assert_parity(f"qwen3next T={length}", o, o_ref, s, s_ref)
+
+
+def test_prefill_qwen3next_full_length():
+    """The full T=32768 prefill against the oracle."""
+    q, k, v, g, beta, h0 = workload("prefill_qwen3next", seed=2)
+    o, s = run(q, k, v, g, beta, SCALE, h0)
+    o_ref, s_ref = oracle(q, k, v, g, beta, SCALE, h0)
+    assert_parity("qwen3next T=32768", o, o_ref, s, s_ref)
+
+
+@pytest.mark.parametrize("length", [1, 2, 17, 63, 64, 65, 130, 200])
+def test_padding_and_short_sequences(length):
+    """T not a multiple of 64 (padded steps are the identity) and T < 64."""
+    q, k, v, g, beta, h0 = generate(2, length, 2, 4, 128, 32, torch.bfloat16, 0.05, seed=length)
+    o_ref, s_ref = oracle(q, k, v, g, beta, SCALE, h0)
+    o, s = run(q, k, v, g, beta, SCALE, h0)
+    assert_parity(f"T={length}", o, o_ref, s, s_ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_input_dtypes_and_zero_state(dtype):
+    q, k, v, g, beta, _ = generate(1, 500, 4, 4, 64, 64, dtype, 0.0, seed=3)
+    o_ref, s_ref = oracle(q, k, v, g, beta, 0.125, torch.zeros(1, 4, 64, 64))
+    o, s = run(q, k, v, g, beta, 0.125, None)
+    assert_parity(f"dtype {dtype}, h0=None", o, o_ref, s, s_ref)
+
+
+def test_slow_decay_long_range():
+    """g scaled by 0.01: the state is carried over hundreds of chunks."""
+    q, k, v, g, beta, h0 = generate(1, 8192, 16, 32, 128, 128, torch.bfloat16, 0.02, seed=6,
+                                    g_scale=0.01)
+    o_ref, s_ref = oracle(q, k, v, g, beta, SCALE, h0)
+    o, s = run(q, k, v, g, beta, SCALE, h0)
+    assert_parity("slow decay", o, o_ref, s, s_ref)
+
+
+def test_beta_in_input_dtype_and_fp32_output():
+    q, k, v, g, beta, h0 = generate(1, 300, 2, 4, 128, 64, torch.bfloat16, 0.02, seed=8)
+    beta = beta.to(torch.bfloat16)
+    o_ref, s_ref = oracle(q, k, v, g, beta, SCALE, h0)
+    o, s = gd.chunk_fwd(*to_dev(q, k, v, g, beta), SCALE, h0.to(DEV), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert o.dtype == torch.float32
+    assert_parity("bf16 beta, fp32 o", o, o_ref, s, s_ref)
+
+
+def test_varlen_small():
+    """8 packed sequences (ragged, one empty, lengths not multiples of 64)."""
+    lengths = [700, 64, 0, 1, 1500, 333, 129, 2000]
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lengths)]), dtype=torch.int32)
+    q, k, v, g, beta, h0 = generate(1, int(cu[-1]), 16, 32, 128, 128, torch.bfloat16, 0.02, seed=12,
+                                    nstates=len(lengths))
+    o_ref, s_ref = oracle(q, k, v, g, beta, SCALE, h0, cu_seqlens=cu)
+    o, s = run(q, k, v, g, beta, SCALE, h0, cu)
+    assert_parity("varlen small", o, o_ref, s, s_ref)
+    assert torch.equal(s[2].cpu(), h0[2])  # the empty sequence returns its initial state
+
+
+def test_varlen_full_size_packing_equals_separate_calls():
+    """262,144 packed tokens in 8 sequences: the packed call equals one call per
+    sequence bit for bit, and the shortest sequence matches the oracle."""
+    q, k, v, g, beta, h0, cu = varlen_workload(seed=0)
+    o, s = run(q, k, v, g, beta, SCALE, h0, cu)
+    bounds = cu.tolist()
+    dq, dk, dv, dg, db, dh = to_dev(q, k, v, g, beta, h0)
+    for n in range(len(bounds) - 1):
+        lo, hi = bounds[n], bounds[n + 1]
+        o_n, s_n = gd.chunk_fwd(dq[:, lo:hi], dk[:, lo:hi], dv[:, lo:hi], dg[:, lo:hi], db[:, lo:hi],
+                                SCALE, dh[n:n + 1])
+        assert torch.equal(o[:, lo:hi], o_n), f"sequence {n}"
+        assert torch.equal(s[n:n + 1], s_n), f"sequence {n}"
+    n = int(np.argmin(np.diff(bounds)))
+    lo, hi = bounds[n], bounds[n + 1]
+    o_ref, s_ref = oracle(q[:, lo:hi], k[:, lo:hi], v[:, lo:hi], g[:, lo:hi], beta[:, lo:hi], SCALE,
+                          h0[n:n + 1])
+    assert_parity(f"varlen sequence {n} (T={hi - lo})", o[:, lo:hi], o_ref, s[n:n + 1], s_ref)
+
+
+def test_streamed_segments_small():
+    """16 segments of 1024 tokens, the final state of each fed to the next; the
+    output and state after every segment match the oracle's streamed run."""
+    seg = 1024
+    q, k, v, g, beta, h0 = workload("stream_1m", seed=21, length=16 * seg)
+    dq, dk, dv, dg, db = to_dev(q, k, v, g, beta)
+    state = h0.to(DEV)
+    from oracle import gdn
+    from pseudobrain_amd.workloads import to_numpy
+    ref = gdn.streamed(*(to_numpy(x).astype(np.float32) for x in (q, k, v, g, beta)), SCALE,
+                       to_numpy(h0), seg)
+    for i, (o_ref, s_ref) in enumerate(ref):
+        sl = slice(i * seg, (i + 1) * seg)
+        o, state = gd.chunk_fwd(dq[:, sl], dk[:, sl], dv[:, sl], dg[:, sl], db[:, sl], SCALE, state)
+        torch.cuda.synchronize()
+        assert_parity(f"segment {i}", o, o_ref, state, s_ref)
+
+
+def test_streamed_million_tokens_equals_one_pass():
+    """1,048,576 tokens as 16 x 65,536 segments with state carry equal one pass
+    over all tokens bit for bit; the last 4096 tokens of every segment, started
+    from the GPU's own carried state, match the oracle. Inputs are drawn on the
+    device (16 GiB of them)."""
+    nseg, seg, win = 16, STREAM_SEGMENT, 4096
+    segments = [workload("stream_1m", seed=1000 + i, length=seg, device=DEV) for i in range(nseg)]
+    h0 = segments[0][5]
+    state = h0
+    last_rows = []
+    for i, (q, k, v, g, beta, _) in enumerate(segments):
+        head, tail = slice(0, seg - win), slice(seg - win, seg)
+        _, mid = gd.chunk_fwd(q[:, head], k[:, head], v[:, head], g[:, head], beta[:, head], SCALE, state)
+        o_b, state = gd.chunk_fwd(q[:, tail], k[:, tail], v[:, tail], g[:, tail], beta[:, tail], SCALE, mid)
+        torch.cuda.synchronize()
+        o_ref, s_ref = oracle(q[:, tail], k[:, tail], v[:, tail], g[:, tail], beta[:, tail], SCALE, mid)
+        assert_parity(f"segment {i} last {win} tokens", o_b, o_ref, state, s_ref)
+        last_rows.append(o_b[:, -8:].clone())
+    # One pass over the concatenation (B=1, T=2^20) reproduces the carried run.
+    cat = [torch.cat([s[j] for s in segments], 1) for j in range(5)]
+    del segments
+    o_all, s_all = gd.chunk_fwd(*cat, SCALE, h0)
+    torch.cuda.synchronize()
+    assert torch.equal(s_all, state)
+    for i in range(nseg):
+        end = (i + 1) * seg
+        assert torch.equal(o_all[:, end - 8:end], last_rows[i])

@@ -1,0 +1,295 @@
+"""Pins of the CPU oracle (oracle/gdn.py) against what the mathematics fixes.
+
+The reference ships no tests, fixtures or golden vectors for this path, so the
+oracle is pinned by closed forms, special cases and invariants written
+independently of its code, plus mutation checks showing that plausible
+mistakes planted in the oracle fail those pins.
+"""
+import inspect
+
+import numpy as np
+import pytest
+
+from oracle import gdn
+
+RNG = np.random.default_rng(1234)
+
+
+def rand_inputs(batch, length, heads, dk, dv, *, hk=None, rng=RNG, unit=True, h0_std=0.3,
+                dtype=np.float64, g_scale=1.0):
+    hk = heads if hk is None else hk
+    q = rng.standard_normal((batch, length, hk, dk))
+    k = rng.standard_normal((batch, length, hk, dk))
+    if unit:
+        q /= np.linalg.norm(q, axis=-1, keepdims=True)
+        k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    v = rng.standard_normal((batch, length, heads, dv))
+    beta = 1 / (1 + np.exp(-rng.standard_normal((batch, length, heads))))
+    g = -np.log1p(np.exp(rng.standard_normal((batch, length, heads)))) * g_scale
+    h0 = rng.standard_normal((batch, heads, dk, dv)) * h0_std
+    return tuple(x.astype(dtype) for x in (q, k, v, g, beta, h0))
+
+
+def close(a, b, tol):
+    return gdn.rel_inf_error(a, b) < tol
+
+
+# ---------------------------------------------------------------------------
+# Sequential recurrence (gated_deltanet.py:93-107)
+# ---------------------------------------------------------------------------
+def householder_step(q, k, v, g, beta, scale, s0):
+    """One step in the Householder form of the module docstring
+    (gated_deltanet.py:12): S1 = a (I - b k k^T) S0 + b k v^T, o = S1^T q scale.
+    Shapes for one head: q, k [K], v [V], s0 [K,V]."""
+    a = np.exp(g)
+    eye = np.eye(k.shape[0])
+    s1 = a * (eye - beta * np.outer(k, k)) @ s0 + beta * np.outer(k, v)
+    return s1.T @ q * scale, s1
+
+
+@pytest.mark.parametrize("unit", [True, False])
+def test_sequential_one_step_closed_form(unit):
+    q, k, v, g, beta, h0 = rand_inputs(2, 1, 3, 8, 5, unit=unit)
+    o, s = gdn.delta_rule_sequential(q, k, v, g, beta, 0.7, h0)
+    for b in range(2):
+        for h in range(3):
+            o_ref, s_ref = householder_step(q[b, 0, h], k[b, 0, h], v[b, 0, h], g[b, 0, h],
+                                            beta[b, 0, h], 0.7, h0[b, h])
+            np.testing.assert_allclose(o[b, 0, h], o_ref, rtol=1e-12, atol=1e-12)
+            np.testing.assert_allclose(s[b, h], s_ref, rtol=1e-12, atol=1e-12)
+
+
+def test_sequential_many_steps_householder_product():
+    """T steps = the product of T Householder steps (one head, K=6, V=4)."""
+    q, k, v, g, beta, h0 = rand_inputs(1, 9, 1, 6, 4)
+    o, s = gdn.delta_rule_sequential(q, k, v, g, beta, 0.5, h0)
+    state = h0[0, 0]
+    for t in range(9):
+        o_t, state = householder_step(q[0, t, 0], k[0, t, 0], v[0, t, 0], g[0, t, 0],
+                                      beta[0, t, 0], 0.5, state)
+        np.testing.assert_allclose(o[0, t, 0], o_t, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(s[0, 0], state, rtol=1e-12, atol=1e-12)
+
+
+def test_scalar_recurrence_closed_form():
+    """K = V = 1: S_t = m_t S_{t-1} + b_t k_t v_t with m_t = a_t (1 - b_t k_t^2), so
+    S_t = (prod_{s<=t} m_s) S_0 + sum_{j<=t} (prod_{j<s<=t} m_s) b_j k_j v_j."""
+    rng = np.random.default_rng(7)
+    length = 12
+    q, k, v, g, beta, h0 = rand_inputs(1, length, 1, 1, 1, unit=False, rng=rng)
+    o, s = gdn.delta_rule_sequential(q, k, v, g, beta, 1.3, h0)
+    a = np.exp(g[0, :, 0])
+    kk, vv, bb, qq = k[0, :, 0, 0], v[0, :, 0, 0], beta[0, :, 0], q[0, :, 0, 0]
+    m = a * (1 - bb * kk * kk)
+    for t in range(length):
+        state = np.prod(m[: t + 1]) * h0[0, 0, 0, 0]
+        for j in range(t + 1):
+            state += np.prod(m[j + 1: t + 1]) * bb[j] * kk[j] * vv[j]
+        assert abs(o[0, t, 0, 0] - state * qq[t] * 1.3) < 1e-12
+    assert abs(s[0, 0, 0, 0] - state) < 1e-12
+
+
+@pytest.mark.parametrize("kernel", ["sequential", "chunked"])
+def test_beta_zero_is_pure_decay(kernel):
+    """beta = 0: S_t = exp(c_t) S_0 and o_t = exp(c_t) S_0^T q_t scale, c = cumsum g."""
+    q, k, v, g, beta, h0 = rand_inputs(1, 70, 2, 8, 8)
+    beta[:] = 0
+    o, s = gdn.gated_delta_rule(q, k, v, g, beta, 0.9, h0, kernel)
+    c = np.cumsum(g, axis=1)
+    o_ref = np.exp(c)[..., None] * np.einsum("bhkv,bthk->bthv", h0, q) * 0.9
+    np.testing.assert_allclose(o, o_ref, rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(s, np.exp(c[:, -1])[..., None, None] * h0, rtol=1e-10, atol=1e-14)
+
+
+@pytest.mark.parametrize("kernel", ["sequential", "chunked"])
+def test_orthonormal_keys_retrieve_exactly(kernel):
+    """g = 0, beta = 1, S_0 = 0, orthonormal keys: S_T^T k_j = v_j (the delta rule
+    writes exactly), and a query equal to an earlier key reads its value."""
+    rng = np.random.default_rng(3)
+    dk, dv, length = 16, 5, 10
+    basis, _ = np.linalg.qr(rng.standard_normal((dk, dk)))
+    k = basis[:length][None, :, None, :]
+    q = k.copy()
+    v = rng.standard_normal((1, length, 1, dv))
+    g = np.zeros((1, length, 1))
+    beta = np.ones((1, length, 1))
+    h0 = np.zeros((1, 1, dk, dv))
+    o, s = gdn.gated_delta_rule(q, k, v, g, beta, 1.0, h0, kernel)
+    np.testing.assert_allclose(s[0, 0].T @ k[0, :, 0].T, v[0, :, 0].T, atol=1e-12)
+    np.testing.assert_allclose(o[0, :, 0], v[0, :, 0], atol=1e-12)
+
+
+def test_rewriting_a_key_replaces_its_value():
+    """beta = 1, unit key written twice: the second value replaces the first."""
+    dk = 4
+    key = np.zeros(dk)
+    key[1] = 1.0
+    k = np.stack([key, key])[None, :, None, :]
+    v = np.array([[1.0, 2.0], [5.0, -3.0]])[None, :, None, :]
+    g = np.zeros((1, 2, 1))
+    beta = np.ones((1, 2, 1))
+    o, s = gdn.delta_rule_sequential(k, k, v, g, beta, 1.0, np.zeros((1, 1, dk, 2)))
+    np.testing.assert_allclose(s[0, 0].T @ key, [5.0, -3.0], atol=1e-14)
+
+
+# ---------------------------------------------------------------------------
+# Chunked algorithm (gated_deltanet.py:110-165)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("chunk", [1, 16, 32, 64, 128])
+@pytest.mark.parametrize("length", [1, 5, 63, 64, 65, 200])
+def test_chunked_equals_sequential(chunk, length):
+    q, k, v, g, beta, h0 = rand_inputs(2, length, 2, 16, 8)
+    o1, s1 = gdn.delta_rule_chunked(q, k, v, g, beta, 0.25, h0, chunk=chunk)
+    o2, s2 = gdn.delta_rule_sequential(q, k, v, g, beta, 0.25, h0)
+    assert close(o1, o2, 1e-10) and close(s1, s2, 1e-10)
+
+
+def test_chunked_low_decay_long_range():
+    """Slow decay (g scaled by 0.01): the initial state stays visible for hundreds
+    of steps; chunked still equals sequential."""
+    q, k, v, g, beta, h0 = rand_inputs(1, 300, 2, 16, 16, g_scale=0.01)
+    o1, s1 = gdn.delta_rule_chunked(q, k, v, g, beta, 0.25, h0)
+    o2, s2 = gdn.delta_rule_sequential(q, k, v, g, beta, 0.25, h0)
+    assert close(o1, o2, 1e-10) and close(s1, s2, 1e-10)
+    assert np.abs(np.exp(np.cumsum(g, 1))[0, -1]).min() > 1e-2  # the carry is not negligible
+
+
+def test_segment_invariance():
+    """Any split of T with the state carried equals one pass (gated_deltanet.py:26)."""
+    q, k, v, g, beta, h0 = rand_inputs(1, 250, 2, 16, 8)
+    o_full, s_full = gdn.delta_rule_chunked(q, k, v, g, beta, 0.3, h0)
+    outs, state = [], h0
+    for lo, hi in ((0, 37), (37, 101), (101, 250)):
+        o, state = gdn.delta_rule_chunked(q[:, lo:hi], k[:, lo:hi], v[:, lo:hi], g[:, lo:hi],
+                                          beta[:, lo:hi], 0.3, state)
+        outs.append(o)
+    assert close(np.concatenate(outs, 1), o_full, 1e-11) and close(state, s_full, 1e-11)
+    streamed = list(gdn.streamed(q, k, v, g, beta, 0.3, h0, 64))
+    assert close(np.concatenate([o for o, _ in streamed], 1), o_full, 1e-11)
+    assert close(streamed[-1][1], s_full, 1e-11)
+
+
+def test_linearity_in_values_and_state():
+    """For fixed q, k, g, beta the map (V, S_0) -> (O, S_T) is linear."""
+    q, k, v1, g, beta, h1 = rand_inputs(1, 90, 2, 8, 8)
+    v2 = RNG.standard_normal(v1.shape)
+    h2 = RNG.standard_normal(h1.shape)
+    oa, sa = gdn.delta_rule_chunked(q, k, v1, g, beta, 0.5, h1)
+    ob, sb = gdn.delta_rule_chunked(q, k, v2, g, beta, 0.5, h2)
+    oc, sc = gdn.delta_rule_chunked(q, k, 2 * v1 - 3 * v2, g, beta, 0.5, 2 * h1 - 3 * h2)
+    assert close(oc, 2 * oa - 3 * ob, 1e-11) and close(sc, 2 * sa - 3 * sb, 1e-11)
+
+
+def test_gqa_equals_repeat_interleave():
+    q, k, v, g, beta, h0 = rand_inputs(1, 40, 4, 8, 8, hk=2)
+    o1, s1 = gdn.delta_rule_chunked(q, k, v, g, beta, 0.5, h0)
+    rq, rk = np.repeat(q, 2, axis=2), np.repeat(k, 2, axis=2)
+    o2, s2 = gdn.delta_rule_sequential(rq, rk, v, g, beta, 0.5, h0)
+    assert close(o1, o2, 1e-11) and close(s1, s2, 1e-11)
+    # head 1 reads key head 0, head 2 reads key head 1 (not head 1 -> 1)
+    o3, _ = gdn.delta_rule_sequential(rq[:, :, 1:2], rk[:, :, 1:2], v[:, :, 1:2], g[:, :, 1:2],
+                                      beta[:, :, 1:2], 0.5, h0[:, 1:2])
+    o4, _ = gdn.delta_rule_sequential(q[:, :, 0:1], k[:, :, 0:1], v[:, :, 1:2], g[:, :, 1:2],
+                                      beta[:, :, 1:2], 0.5, h0[:, 1:2])
+    assert close(o3, o4, 1e-13)
+
+
+def test_varlen_is_a_loop_of_calls():
+    q, k, v, g, beta, _ = rand_inputs(1, 150, 2, 8, 8)
+    h0 = RNG.standard_normal((4, 2, 8, 8))
+    cu = np.array([0, 40, 40, 107, 150])  # includes an empty sequence
+    o, finals = gdn.varlen(q, k, v, g, beta, 0.5, h0, cu)
+    for n in range(4):
+        lo, hi = cu[n], cu[n + 1]
+        o_n, s_n = gdn.delta_rule_sequential(q[:, lo:hi], k[:, lo:hi], v[:, lo:hi], g[:, lo:hi],
+                                             beta[:, lo:hi], 0.5, h0[n:n + 1])
+        assert close(o[:, lo:hi], o_n, 1e-11) if hi > lo else True
+        assert close(finals[n], s_n[0], 1e-11)
+    np.testing.assert_array_equal(finals[1], h0[1])  # the empty sequence keeps its state
+
+
+def test_fp32_oracle_tracks_fp64():
+    q, k, v, g, beta, h0 = rand_inputs(1, 300, 2, 64, 64)
+    o64, s64 = gdn.delta_rule_chunked(q, k, v, g, beta, 0.125, h0)
+    o32, s32 = gdn.delta_rule_chunked(*(x.astype(np.float32) for x in (q, k, v, g, beta)), 0.125,
+                                      h0.astype(np.float32))
+    assert o32.dtype == np.float32
+    assert close(o32, o64, 1e-5) and close(s32, s64, 1e-5)
+
+
+def test_unknown_kernel_raises():
+    q, k, v, g, beta, h0 = rand_inputs(1, 4, 1, 4, 4)
+    with pytest.raises(ValueError):
+        gdn.gated_delta_rule(q, k, v, g, beta, 1.0, h0, "fla")
+
+
+# ---------------------------------------------------------------------------
+# l2 normalisation (gated_deltanet.py:59-70): the reference docstring's
+# known answers, [1e-4, 0] -> [1, 0] ('max') vs [0.0995, 0] ('hf').
+# ---------------------------------------------------------------------------
+def test_l2_normalize_known_answers():
+    x = np.array([[1e-4, 0.0]], dtype=np.float32)
+    np.testing.assert_allclose(gdn.l2_normalize(x, "max"), [[1.0, 0.0]], rtol=1e-6)
+    np.testing.assert_allclose(gdn.l2_normalize(x, "hf"), [[0.0995, 0.0]], rtol=1e-3)
+    y = RNG.standard_normal((5, 7)).astype(np.float32)
+    np.testing.assert_allclose(np.linalg.norm(gdn.l2_normalize(y), axis=-1), 1.0, rtol=1e-6)
+    with pytest.raises(ValueError):
+        gdn.l2_normalize(y, "l1")
+
+
+def test_round_bf16_and_fp16():
+    x = np.array([1.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -2.5, 1e-30], dtype=np.float32)
+    # ties to even at bf16's 2^-7 spacing
+    np.testing.assert_array_equal(gdn.round_bf16(x)[:3], [1.0, 1.0, 1.0 + 2 ** -6])
+    assert gdn.round_bf16(x)[3] == -2.5
+    np.testing.assert_array_equal(gdn.round_fp16(np.array([1 + 2 ** -12], np.float32)), [1.0])
+
+
+# ---------------------------------------------------------------------------
+# Mutation checks: a plausible mistake planted in the oracle fails a pin above.
+# ---------------------------------------------------------------------------
+def _mutant(fn, old, new):
+    src = inspect.getsource(fn)
+    assert old in src, old
+    namespace = dict(vars(gdn))
+    exec(compile(src.replace(old, new), gdn.__file__, "exec"), namespace)  # noqa: S102
+    return namespace[fn.__name__]
+
+
+SEQUENTIAL_MUTANTS = [
+    ("state = state * decay[:, t, :, None, None]", "state = state"),                      # dropped decay
+    ("(v[:, t] - np.einsum", "(v[:, t] + np.einsum"),                                      # wrong sign
+    ('np.einsum("bhkv,bhk->bhv", state, kt)', 'np.einsum("bhvk,bhk->bhv", state, kt)'),  # transposed S
+    ("state = state + kt[..., None] * u[..., None, :]", "state = state + kt[..., None] * u[..., None, :] * 0.999"),
+]
+
+
+@pytest.mark.parametrize("old,new", SEQUENTIAL_MUTANTS)
+def test_sequential_pins_catch_mutants(old, new, monkeypatch):
+    bad = _mutant(gdn.delta_rule_sequential, old, new)
+    q, k, v, g, beta, h0 = rand_inputs(1, 1, 1, 6, 6)
+    o, s = bad(q, k, v, g, beta, 0.7, h0)
+    o_ref, s_ref = householder_step(q[0, 0, 0], k[0, 0, 0], v[0, 0, 0], g[0, 0, 0], beta[0, 0, 0],
+                                    0.7, h0[0, 0])
+    assert not (close(o[0, 0, 0], o_ref, 1e-9) and close(s[0, 0], s_ref, 1e-9))
+
+
+CHUNKED_MUTANTS = [
+    ("inclusive = np.tril(np.ones((size, size), dtype=bool))",
+     "inclusive = np.tril(np.ones((size, size), dtype=bool), -1)"),          # exclusive decay mask
+    ("c[:, :, None] - c[:, None, :]", "c[:, None, :] - c[:, :, None]"),     # decay exponent sign
+    ("w = solve @ (k * (beta * gamma)[..., None])", "w = solve @ (k * beta[..., None])"),  # dropped gamma
+    ("state = state * last[n] + tail[n].T @ u", "state = state + tail[n].T @ u"),          # no carry decay
+    ("tail = np.exp(c[:, -1:] - c)[..., None] * k", "tail = k"),                            # no tail decay
+    ("u = u0[n] - w[n] @ state", "u = u0[n] - w[n] @ state.T"),                             # transposed S
+]
+
+
+@pytest.mark.parametrize("old,new", CHUNKED_MUTANTS)
+def test_chunked_pins_catch_mutants(old, new, monkeypatch):
+    bad_head = _mutant(gdn._chunked_head, old, new)
+    monkeypatch.setattr(gdn, "_chunked_head", bad_head)
+    q, k, v, g, beta, h0 = rand_inputs(1, 100, 1, 8, 8)
+    o1, s1 = gdn.delta_rule_chunked(q, k, v, g, beta, 0.5, h0)
+    o2, s2 = gdn.delta_rule_sequential(q, k, v, g, beta, 0.5, h0)
+    assert not (close(o1, o2, 1e-6) and close(s1, s2, 1e-6))
