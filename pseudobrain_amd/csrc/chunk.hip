@@ -13,60 +13,67 @@
 //
 // Decomposition. The recurrence is separable along the value columns, so a
 // workgroup owns one (sequence, value head, 16-column tile of V): grid =
-// V/16 x Hv x N, 512 threads (8 waves), one workgroup per CU (~150 KB LDS).
+// V/16 x Hv x N, 1024 threads (16 waves, 4 per SIMD), one workgroup per CU
+// (~156 KB LDS).
 // The fp32 state tile S [K, 16] lives in MFMA accumulators for the whole
-// sequence (wave w owns key rows 16w..16w+15) and is written out once.
+// sequence (wave 8 + j owns key rows 16j..16j+15) and is written out once.
 //
 // Pipeline. Each loop iteration ("tick" n) has three barrier-separated phases
 // and overlaps three chunks:
 //   phase 1: chain   K S, X = V - gamma K S              (chunk n, waves 0-3)
 //            output  Q S                                 (chunk n, waves 4-7)
-//            inverse off-diagonal 16x16 blocks of T, Tb  (chunk n, waves 6-7)
+//            inverse off-diagonal 16x16 blocks of T, Tb  (chunk n, waves 8-10)
 //            inputs  chunk n+1 registers -> LDS, cumsum of g;
 //                    buffer loads of chunk n+2 issued into registers
 //   phase 2: chain   U = Tb X                            (chunk n, waves 0-3)
-//            prep    K K^T -> A, Q K^T -> QKD            (chunk n+1, all waves)
-//   phase 3: chain   S <- gamma_C S + K^T (dec U)        (chunk n, waves owning S)
+//            prep    K K^T -> A, Q K^T -> QKD            (chunk n+1, waves 4-13)
+//   phase 3: chain   S <- gamma_C S + K^T (dec U)        (chunk n, waves 8-15)
 //            output  O = gamma scale Q S + QKD U, store  (chunk n, waves 4-7)
 //            inverse diagonal 16x16 blocks of T          (chunk n+1, waves 0-3)
 // so the S-dependent chain of one chunk runs beside the S-independent work of
 // the next. Barriers wait for LDS traffic only, so the prefetch of chunk n+2
 // stays in flight for a whole tick.
 //
-// Costs that shape the code (measured on MI355X): a wave64 VALU instruction
-// occupies its SIMD for 4 cycles and a 16x16x32 MFMA for ~14-16, and the LDS
-// delivers ~200 B/clk per CU for conflict-free 16-byte reads. Hence:
+// Costs that shape the code (measured on MI355X, CU cycles per wave64
+// instruction): VALU 4 per SIMD; 16x16x32 MFMA ~14 per SIMD; LDS 16-byte
+// fragment reads 4 and transposing reads 4 (conflict-free layouts), 8-byte
+// tile writes 6.7, but 4-byte reads ~17. Hence:
 //   * global traffic uses buffer instructions: per-lane byte offsets are fixed
 //     for the whole sequence and each chunk only moves a scalar base, whose
-//     range check also zero-fills tokens past the end (no address arithmetic
-//     or masking in the vector unit);
-//   * every LDS row pitch is its length + 32 bytes, the conflict-free stride
-//     for 16-byte fragment reads;
-//   * the A and QKD tiles are computed transposed so each lane stores 4
-//     consecutive elements of a row with one write;
-//   * K^T fragments for the state update come from ds_read_b64_tr_b16, which
-//     transposes 16-bit elements across each group of 16 lanes;
+//     range check also zero-fills tokens past the end;
+//   * LDS rows are an odd multiple of 32 bytes long and the 16-byte chunk
+//     index within a row is XORed with bit 2 of the row index: conflict-free
+//     for 16-byte fragment reads and 8-byte accumulator-tile writes alike, and
+//     the swizzle folds into each lane's base address (no per-access VALU);
+//   * no 4-byte LDS accesses in the loop: per-row scalars (cumulative decay,
+//     beta) are also kept in a [16][4] layout read as one float4 per lane, V
+//     is staged row-major and read column-wise with ds_read_b64_tr_b16, and
+//     so are the K^T and D_s operands;
+//   * A, QKD and the off-diagonal Tb blocks are computed transposed so that
+//     each lane writes 4 consecutive elements of a row at once;
 //   * role parameters (tile indices, buffers) are wave-uniform runtime values,
 //     so the loop body stays small for the instruction cache.
 //
 // Arithmetic (fp32 accumulation throughout):
 //   * q/k products use the input's own 16-bit type on v_mfma_f32_16x16x32:
 //     bf16 inputs are fed to the bf16 MFMA unconverted; fp16 inputs as fp16;
-//     fp32 inputs are rounded to fp16 once when staged.
+//     fp32 inputs are rounded to fp16 once when staged (V likewise).
 //   * S enters K S as a high + low pair of that type (two MFMAs), so X sees
 //     the fp32 state to ~16 bits; Q S, which only reaches the output, uses the
 //     high part. The state update K^T (dec U) uses dec U as a pair.
-//   * Tb, X, U and QKD are fp16 (11-bit significand) on the fp16 MFMA.
+//   * Tb, X, U, QKD and the off-diagonal A blocks are fp16 (11-bit
+//     significand) on the fp16 MFMA.
 //   * The diagonal 16x16 blocks of T come from the nilpotent product
 //     (I + M)(I + M^2)(I + M^4)(I + M^8) on fp16 high/low MFMAs (~22-bit
-//     products); the off-diagonal blocks from 16x16x16 fp16 MFMAs.
+//     products) from fp32 A; the off-diagonal blocks from 16x16x16 fp16 MFMAs.
 //
 // Fragment layouts (lane l, g = l >> 4, c = l & 15). 16x16x32: A holds
 // A[m = c][k = 8g + j], B holds B[k = 8g + j][n = c], j = 0..7; 16x16x16:
 // k = 4g + j, j = 0..3; the accumulator holds D[4g + i][c], i = 0..3. Any
 // consistent assignment of contraction slots works, as long as A and B agree.
-// B operands are kept in LDS transposed ([n][k]) so both fragments are one
-// 16-byte read, and an accumulator tile is written there as one 8-byte store.
+// Written tile(X) for the accumulator layout of a 16x16 X: tile(X) is the B
+// operand of X and the A operand of X^T, so MFMA(tile(P^T), tile(Q)) = tile(PQ)
+// and MFMA(tile(Q), tile(P^T)) = tile((PQ)^T).
 #include "common.hpp"
 
 namespace pbgdn {
@@ -78,9 +85,10 @@ typedef short i16x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int CH = 64;        // chunk length (CHUNK, gated_deltanet.py:49)
 constexpr int VT = 16;        // value columns per workgroup
-constexpr int NT = 512;       // threads per workgroup
+constexpr int NT = 1024;      // threads per workgroup
 constexpr int NW = NT / 64;   // waves per workgroup
-constexpr int SCAN_WAVE = 5;  // wave that loads g, beta and scans them
+constexpr int SCAN_WAVE = 11; // wave that loads g, beta and scans them
+constexpr int S_WAVE0 = 8;    // waves S_WAVE0 + j own key tile j of the state
 constexpr int RSRC_WORD3 = 0x00020000;  // raw buffer resource, gfx9 family
 
 struct ChunkParams {
@@ -103,6 +111,7 @@ struct OpOf {
   using T8 = half8_t;
   __device__ static T4 from(float4_t x) { return to_half4(x); }
   __device__ static float4_t to(T4 x) { return to_float4(x); }
+  __device__ static float4_t bits_to_float(i16x4_t x) { return to_float4(__builtin_bit_cast(half4_t, x)); }
 };
 template <>
 struct OpOf<u16> {
@@ -116,6 +125,7 @@ struct OpOf<u16> {
     return float4_t{static_cast<float>(x[0]), static_cast<float>(x[1]), static_cast<float>(x[2]),
                     static_cast<float>(x[3])};
   }
+  __device__ static float4_t bits_to_float(i16x4_t x) { return to(__builtin_bit_cast(bf16x4_t, x)); }
 };
 
 __device__ __forceinline__ float4_t mma(half8_t a, half8_t b, float4_t c) {
@@ -123,23 +133,6 @@ __device__ __forceinline__ float4_t mma(half8_t a, half8_t b, float4_t c) {
 }
 __device__ __forceinline__ float4_t mma(bf16x8_t a, bf16x8_t b, float4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-template <typename V8>
-__device__ __forceinline__ V8 ld8(const void *p) { return *reinterpret_cast<const V8 *>(p); }
-template <typename V4>
-__device__ __forceinline__ void st4(void *p, V4 x) { *reinterpret_cast<V4 *>(p) = x; }
-__device__ __forceinline__ half8_t lds8(const half_t *p) { return *reinterpret_cast<const half8_t *>(p); }
-__device__ __forceinline__ float4_t ldf4(const float *p) { return *reinterpret_cast<const float4_t *>(p); }
-
-// Transposing LDS read of four 16-bit elements (ds_read_b64_tr_b16). Within
-// each group of 16 lanes, lane o receives element (o & 3) of the 8 bytes read
-// by lanes 4k + (o >> 2), k = 0..3: if lanes 4k..4k+3 of a group point at row
-// r_k, columns 0-3, 4-7, 8-11, 12-15 of a 16-column block, lane o gets column
-// o of rows r_0..r_3.
-__device__ __forceinline__ i16x4_t ld_tr(const u16 *p) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) i16x4_t *)(reinterpret_cast<uintptr_t>(p)));
 }
 
 // Workgroup barrier for LDS traffic: waits for this wave's LDS operations, not
@@ -171,26 +164,38 @@ __device__ __forceinline__ void put_out<float>(__amdgpu_buffer_rsrc_t r, uint32_
   __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, x), r, off, 0, 0);
 }
 
+// LDS layout (byte offsets). Rows of [.][K] 16-bit are KPB bytes, rows of
+// [.][64] 16-bit SPB bytes and rows of [.][64] fp32 FPB bytes; arrays marked
+// (swz) store the 16-byte chunk j of row r at chunk j ^ ((r >> 2) & 1).
 template <int K>
-struct ChunkSmem {
-  static constexpr int KP = K + 16;   // pitch (16-bit elements) of [t][key] and [col][key] rows
-  static constexpr int SP = CH + 16;  // pitch (16-bit elements) of [.][t] rows
-  static constexpr int FP = CH + 8;   // pitch (floats) of fp32 rows of 64
-  alignas(16) u16 kq[2][2][CH][KP];   // [buffer][K, Q][t][key], operand type
-  alignas(16) float vt[2][VT][FP];    // V column tile, transposed [col][t]
-  alignas(16) float cum[2][CH];       // inclusive cumsum of g
-  alignas(16) float gam[2][CH];       // exp(cum)
-  alignas(16) float dec[2][CH];       // exp(cum[C-1] - cum)
-  alignas(16) float bet[2][CH];       // beta
-  alignas(16) float at[CH][FP];       // A, then T's diagonal blocks in place (fp32)
-  alignas(16) half_t tb[CH][SP];      // Tb = T diag(beta), [t][s]
-  alignas(16) half_t qkd[2][CH][SP];  // scale (Q K^T o D), inclusive lower, [t][s]
-  alignas(16) half_t xt[VT][SP];      // X^T [col][t]
-  alignas(16) half_t ut[VT][SP];      // U^T [col][t]
-  alignas(16) u16 uh[VT][SP];         // (dec U)^T high part, operand type
-  alignas(16) u16 ul[VT][SP];         // (dec U)^T low part
-  alignas(16) u16 sh[VT][KP];         // S^T [col][key] high part, operand type
-  alignas(16) u16 sl[VT][KP];         // S^T low part
+struct Layout {
+  static constexpr int KPB = 2 * K + 32;
+  static constexpr int SPB = 2 * CH + 32;
+  static constexpr int FPB = 4 * CH + 32;
+  static constexpr int KQ_MAT = CH * KPB;
+  static constexpr int KQ = 0;                        // [2 buf][K, Q][64 t][K] operand type (swz)
+  static constexpr int V16 = KQ + 4 * KQ_MAT;         // [2 buf][64 t][16] 16-bit, 32-byte rows
+  static constexpr int V16_BUF = CH * 32;
+  static constexpr int SC = V16 + 2 * V16_BUF;        // [2 buf][11][64] fp32 per-token scalars (below)
+  static constexpr int SC_BUF = 11 * CH * 4;
+  static constexpr int AT = SC + 2 * SC_BUF;          // [64 t][64 s] fp32 A (diagonal tiles used)
+  static constexpr int TB = AT + CH * FPB;            // [64 t][64 s] fp16 Tb (swz)
+  static constexpr int QKD = TB + CH * SPB;           // [2 buf][64 t][64 s] fp16 (swz)
+  static constexpr int A16 = QKD + 2 * CH * SPB;      // [64 t][64 s] fp16: off-diagonal A, diagonal D (swz)
+  static constexpr int XT = A16 + CH * SPB;           // [16 col][64 t] fp16 X^T (swz)
+  static constexpr int UT = XT + VT * SPB;            // U^T fp16 (swz)
+  static constexpr int UH = UT + VT * SPB;            // (dec U)^T high, operand type (swz)
+  static constexpr int UL = UH + VT * SPB;            // (dec U)^T low (swz)
+  static constexpr int SH = UL + VT * SPB;            // [16 col][K] S^T high, operand type (swz)
+  static constexpr int SL = SH + VT * KPB;            // S^T low (swz)
+  static constexpr int BYTES = SL + VT * KPB;
+  // scalar arrays within a buffer's SC block
+  // Per-token scalars of a chunk (fp32 [64] each): c (inclusive cumsum of g),
+  // gamma = exp(c), dec = exp(c_63 - c), beta; [16][4] tables (entry (i, r) is
+  // token 16 r + i): c, beta, beta u, scale u with u_t = exp(c_t - c_16(t/16));
+  // and W_R[s] = exp(c_16R - c_s) for s < 16 R (R = 1, 2, 3), else 0.
+  static constexpr int CUM = 0, GAM = 256, DEC = 512, BET = 768, CUM4 = 1024, BET4 = 1280, BU4 = 1536,
+                       SU4 = 1792, W1 = 2048;
 };
 
 // One chunk of raw inputs held in registers between its buffer load (issued a
@@ -201,27 +206,37 @@ struct ChunkSmem {
 // gated_deltanet.py:127).
 template <int K, typename TIn>
 struct ChunkInputs {
-  static constexpr int EPU = 16 / sizeof(TIn);              // elements per 16-byte unit
+  using L = Layout<K>;
+  static constexpr int EPU = 16 / sizeof(TIn);       // elements per 16-byte unit
   static constexpr int ROW_UNITS = K / EPU;
-  static constexpr int MAT_UNITS = CH * ROW_UNITS;          // units of one of K, Q
-  static constexpr int PER_MAT = MAT_UNITS / NT;            // units per thread per matrix
+  static constexpr int MAT_UNITS = CH * ROW_UNITS;   // units of one of K, Q
+  static constexpr int UPT = 2 * MAT_UNITS / NT;     // K then Q units per thread
   static constexpr int V_UNITS = CH * VT / EPU;
-  static_assert(MAT_UNITS % NT == 0, "K/Q units must tile the workgroup");
+  static_assert(UPT >= 1 && (2 * MAT_UNITS) % NT == 0 && MAT_UNITS % 64 == 0, "K/Q units must tile the workgroup");
   static_assert(V_UNITS <= NT, "V units exceed the workgroup");
 
-  uint32_t qk_off[PER_MAT];  // byte offset of this thread's units within a chunk
-  uint32_t v_off, g_off, b_off;
-  uint4 kx[PER_MAT], qx[PER_MAT], vx;
+  uint32_t qk_off[UPT];  // global byte offset of this thread's units within a chunk
+  uint32_t qk_lds[UPT];  // LDS byte offset of the same units within a K or Q matrix
+  uint32_t v_off, v_lds, g_off, b_off;
+  uint4 x[UPT], vx;
   float g, b;
+
+  // Unit i of this thread belongs to Q (1) or K (0); uniform across a wave.
+  __device__ static int mat_of(int tid, int i) { return (tid + NT * i) / MAT_UNITS; }
 
   __device__ void init(const ChunkParams &p, int tid, int lane) {
 #pragma unroll
-    for (int i = 0; i < PER_MAT; ++i) {
-      const int u = tid + NT * i;
-      qk_off[i] = ((u / ROW_UNITS) * p.Hk * K + (u % ROW_UNITS) * EPU) * sizeof(TIn);
+    for (int i = 0; i < UPT; ++i) {
+      const int u = (tid + NT * i) % MAT_UNITS;
+      const int t = u / ROW_UNITS;
+      const int byte = (u % ROW_UNITS) * EPU * 2;  // staged as 16-bit elements
+      qk_off[i] = (t * p.Hk * K + (u % ROW_UNITS) * EPU) * sizeof(TIn);
+      qk_lds[i] = t * L::KPB + (byte ^ (((t >> 2) & 1) << 4));
     }
     const int tv = tid / (VT / EPU);
-    v_off = (tv * p.Hv * p.V + (tid % (VT / EPU)) * EPU) * sizeof(TIn);
+    const int c0 = (tid % (VT / EPU)) * EPU;
+    v_off = (tv * p.Hv * p.V + c0) * sizeof(TIn);
+    v_lds = tv * 32 + c0 * 2;
     g_off = lane * p.Hv * 4;
     b_off = lane * p.Hv * (p.beta_dtype == PBGDN_F32 ? 4 : 2);
   }
@@ -235,9 +250,8 @@ struct ChunkInputs {
     const __amdgpu_buffer_rsrc_t rk = rsrc(static_cast<const TIn *>(p.k) + qk_base, qk_bytes);
     const __amdgpu_buffer_rsrc_t rq = rsrc(static_cast<const TIn *>(p.q) + qk_base, qk_bytes);
 #pragma unroll
-    for (int i = 0; i < PER_MAT; ++i) {
-      kx[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, qk_off[i], 0, 0));
-      qx[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, qk_off[i], 0, 0));
+    for (int i = 0; i < UPT; ++i) {
+      x[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(mat_of(tid, i) ? rq : rk, qk_off[i], 0, 0));
     }
     if (tid < V_UNITS) {
       const long v_bytes = rows > 0 ? ((rows - 1) * p.Hv * p.V + VT) * static_cast<long>(sizeof(TIn)) : 0;
@@ -261,43 +275,23 @@ struct ChunkInputs {
     }
   }
 
-  __device__ static float elem(const uint4 &raw, int i) {
-    const uint32_t w = (EPU == 4) ? ((i == 0) ? raw.x : (i == 1) ? raw.y : (i == 2) ? raw.z : raw.w)
-                                  : ((i < 2) ? raw.x : (i < 4) ? raw.y : (i < 6) ? raw.z : raw.w);
-    if constexpr (EPU == 4) {
-      return __uint_as_float(w);
-    } else if constexpr (__is_same(TIn, u16)) {  // bf16
-      return (i & 1) ? __uint_as_float(w & 0xffff0000u) : __uint_as_float(w << 16);
-    } else {
-      const u16 bits = (i & 1) ? static_cast<u16>(w >> 16) : static_cast<u16>(w & 0xffffu);
-      return static_cast<float>(__builtin_bit_cast(half_t, bits));
-    }
-  }
-
-  __device__ static void put_unit(u16 *dst, const uint4 &x) {
+  // A 16-byte unit as staged: 16-bit elements unchanged, fp32 rounded to fp16.
+  __device__ static void put_unit(unsigned char *dst, const uint4 &x) {
     if constexpr (EPU == 8) {
       *reinterpret_cast<uint4 *>(dst) = x;
     } else {
-      st4(dst, to_half4(float4_t{__uint_as_float(x.x), __uint_as_float(x.y), __uint_as_float(x.z),
-                                 __uint_as_float(x.w)}));
+      *reinterpret_cast<half4_t *>(dst) = to_half4(float4_t{__uint_as_float(x.x), __uint_as_float(x.y),
+                                                            __uint_as_float(x.z), __uint_as_float(x.w)});
     }
   }
 
-  // Registers -> LDS buffer `buf`: K and Q in the operand type [t][key], V^T in
-  // fp32, and (scan wave) the cumulative decays and beta of the chunk.
-  __device__ void store(ChunkSmem<K> &sm, int buf, int tid, int lane, bool scan) const {
+  // Registers -> LDS buffer `buf`: K and Q [t][key], V [t][col], and (scan
+  // wave) the cumulative decays and beta of the chunk, also as [16][4] tables
+  // (entry (c, r) = value of row 16 r + c).
+  __device__ void store(unsigned char *lds, int buf, int tid, int lane, bool scan, float scale) const {
 #pragma unroll
-    for (int i = 0; i < PER_MAT; ++i) {
-      const int u = tid + NT * i;
-      put_unit(&sm.kq[buf][0][u / ROW_UNITS][(u % ROW_UNITS) * EPU], kx[i]);
-      put_unit(&sm.kq[buf][1][u / ROW_UNITS][(u % ROW_UNITS) * EPU], qx[i]);
-    }
-    if (tid < V_UNITS) {
-      const int t = tid / (VT / EPU);
-      const int c0 = (tid % (VT / EPU)) * EPU;
-#pragma unroll
-      for (int j = 0; j < EPU; ++j) sm.vt[buf][c0 + j][t] = elem(vx, j);
-    }
+    for (int i = 0; i < UPT; ++i) put_unit(lds + L::KQ + (2 * buf + mat_of(tid, i)) * L::KQ_MAT + qk_lds[i], x[i]);
+    if (tid < V_UNITS) put_unit(lds + L::V16 + buf * L::V16_BUF + v_lds, vx);
     if (scan) {
       float x = g;
 #pragma unroll
@@ -306,10 +300,22 @@ struct ChunkInputs {
         if (lane >= off) x += y;
       }
       const float last = __shfl(x, 63, 64);
-      sm.cum[buf][lane] = x;
-      sm.gam[buf][lane] = __expf(x);
-      sm.dec[buf][lane] = __expf(last - x);
-      sm.bet[buf][lane] = b;
+      float *sc = reinterpret_cast<float *>(lds + L::SC + buf * L::SC_BUF);
+      const int t4 = (lane & 15) * 4 + (lane >> 4);
+      const float u = __expf(x - __shfl(x, lane & ~15, 64));
+      sc[L::CUM / 4 + lane] = x;
+      sc[L::GAM / 4 + lane] = __expf(x);
+      sc[L::DEC / 4 + lane] = __expf(last - x);
+      sc[L::BET / 4 + lane] = b;
+      sc[L::CUM4 / 4 + t4] = x;
+      sc[L::BET4 / 4 + t4] = b;
+      sc[L::BU4 / 4 + t4] = b * u;
+      sc[L::SU4 / 4 + t4] = scale * u;
+#pragma unroll
+      for (int r = 1; r < 4; ++r) {
+        const float cr = __shfl(x, 16 * r, 64);
+        sc[L::W1 / 4 + (r - 1) * CH + lane] = (lane < 16 * r) ? __expf(cr - x) : 0.f;
+      }
     }
   }
 };
@@ -338,9 +344,13 @@ __device__ __forceinline__ void decode_block(int L, int total, int nv, int group
   vtile = in % nv;
 }
 
+__device__ __forceinline__ float pick(float4_t v, int i) {
+  return (i == 0) ? v[0] : (i == 1) ? v[1] : (i == 2) ? v[2] : v[3];
+}
+
 template <int K, typename TIn, typename TOut>
 struct ChunkBlock {
-  using Smem = ChunkSmem<K>;
+  using L = Layout<K>;
   using Op = OpOf<TIn>;
   using O4 = typename Op::T4;
   using O8 = typename Op::T8;
@@ -349,15 +359,17 @@ struct ChunkBlock {
   static_assert(K == 64 || K == 128, "K must be 64 or 128");
   static_assert(NKT <= NW, "one S key tile per wave");
 
-  Smem &sm;
+  unsigned char *lds;
   const ChunkParams &p;
   int tid, lane, c16, g4, wave, seq, h, hk, v0;
   long bos, eos, nchunks;
   uint32_t o_off;  // byte offset of this lane's first output element in a chunk
   float4_t sacc, qs;
   ChunkInputs<K, TIn> in;
+  // Per-lane LDS byte offsets (see tick()).
+  uint32_t kp_frag, sp_frag, kp_tile, sp_tile, at_lane, tr_v, tr_a, tr_k0, tr_k1;
 
-  __device__ ChunkBlock(Smem &s, const ChunkParams &prm) : sm(s), p(prm) {
+  __device__ ChunkBlock(unsigned char *l, const ChunkParams &prm) : lds(l), p(prm) {
     tid = threadIdx.x;
     lane = tid & 63;
     wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -380,7 +392,34 @@ struct ChunkBlock {
     qs = sacc;
     in.init(p, tid, lane);
     o_off = ((16 * (wave & 3) + 4 * g4) * p.Hv * p.V + c16) * sizeof(TOut);
+    lane_offsets();
   }
+
+  // Per-lane parts of LDS addresses; everything else is a wave-uniform or
+  // immediate offset. s4 is the swizzle of rows 16 m + c (bit 2 of the row).
+  __device__ void lane_offsets() {
+    const uint32_t s4 = ((c16 >> 2) & 1) << 4;
+    kp_frag = c16 * L::KPB + ((16 * g4) ^ s4);                         // row c, 16 bytes at 16 g
+    sp_frag = c16 * L::SPB + ((16 * g4) ^ s4);
+    kp_tile = c16 * L::KPB + ((16 * (g4 >> 1)) ^ s4) + 8 * (g4 & 1);  // row c, 8 bytes at 8 g
+    sp_tile = c16 * L::SPB + ((16 * (g4 >> 1)) ^ s4) + 8 * (g4 & 1);
+    at_lane = c16 * L::FPB + 16 * g4;
+    // transposing reads: lanes 4k..4k+3 of group g point at row 4g + k (V, A16)
+    // or 8g + k (K), 8 bytes at 8 (c & 3)
+    tr_v = (4 * g4 + (c16 >> 2)) * 32 + 8 * (c16 & 3);
+    tr_a = (4 * g4 + (c16 >> 2)) * L::SPB + ((8 * (c16 & 3)) ^ ((g4 & 1) << 4));
+    tr_k0 = (8 * g4 + (c16 >> 2)) * L::KPB + 8 * (c16 & 3);
+    tr_k1 = (8 * g4 + 4 + (c16 >> 2)) * L::KPB + ((8 * (c16 & 3)) ^ 16);
+  }
+
+  template <typename T>
+  __device__ T ld(uint32_t off) const { return *reinterpret_cast<const T *>(lds + off); }
+  template <typename T>
+  __device__ void st(uint32_t off, T x) const { *reinterpret_cast<T *>(lds + off) = x; }
+  __device__ i16x4_t ld_tr(uint32_t off) const {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t *)(lds + off));
+  }
+  __device__ uint32_t sc(int buf, int arr) const { return L::SC + buf * L::SC_BUF + arr; }
 
   __device__ void load_chunk(long n) {
     const long t0 = bos + n * CH;
@@ -389,82 +428,85 @@ struct ChunkBlock {
 
   // ---------------------------------------------------------------- phase 1
   // Waves 0-3: chain X = V - gamma K S for token rows 16w.. (S as a high/low
-  // pair); waves 4-7: Q S (high part) for token rows 16(w-4)..; waves 6, 7
-  // also the off-diagonal blocks of T.
+  // pair); waves 4-7: Q S (high part) for token rows 16(w-4)..; waves 8-10:
+  // the off-diagonal blocks of T.
   __device__ void phase1(long n, int b) {
+    if (wave >= 8) {
+      in.store(lds, b ^ 1, tid, lane, wave == SCAN_WAVE, p.scale);
+      load_chunk(n + 2);
+      if (wave <= 10) offdiag(b, wave - 8);
+      return;
+    }
     const int r = wave & 3;
     const bool chain = wave < 4;
+    const uint32_t mat = L::KQ + (2 * b + (chain ? 0 : 1)) * L::KQ_MAT + 16 * r * L::KPB + kp_frag;
     O8 a[KS], shi[KS], slo[KS];
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
-      a[kk] = ld8<O8>(&sm.kq[b][chain ? 0 : 1][16 * r + c16][32 * kk + 8 * g4]);
-      shi[kk] = ld8<O8>(&sm.sh[c16][32 * kk + 8 * g4]);
+      a[kk] = ld<O8>(mat + 64 * kk);
+      shi[kk] = ld<O8>(L::SH + kp_frag + 64 * kk);
     }
-    const int tr = 16 * r + 4 * g4;
     float4_t vv, gg;
     if (chain) {
 #pragma unroll
-      for (int kk = 0; kk < KS; ++kk) slo[kk] = ld8<O8>(&sm.sl[c16][32 * kk + 8 * g4]);
-      vv = ldf4(&sm.vt[b][c16][tr]);
-      gg = ldf4(&sm.gam[b][tr]);
+      for (int kk = 0; kk < KS; ++kk) slo[kk] = ld<O8>(L::SL + kp_frag + 64 * kk);
+      vv = Op::bits_to_float(ld_tr(L::V16 + b * L::V16_BUF + 16 * r * 32 + tr_v));
+      gg = ld<float4_t>(sc(b, L::GAM) + (16 * r + 4 * g4) * 4);
     }
-    in.store(sm, b ^ 1, tid, lane, wave == SCAN_WAVE);
+    in.store(lds, b ^ 1, tid, lane, wave == SCAN_WAVE, p.scale);
+    load_chunk(n + 2);
     float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) acc = mma(a[kk], shi[kk], acc);
     if (chain) {
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk) acc = mma(a[kk], slo[kk], acc);
-      st4(&sm.xt[c16][tr], to_half4(vv - gg * acc));
+      st(L::XT + sp_tile + 32 * r, to_half4(vv - gg * acc));
     } else {
       qs = acc;
-      if (wave >= 6) offdiag(b, wave == 6);
     }
-    load_chunk(n + 2);
   }
 
   // Off-diagonal blocks of T for the chunk in buffer b:
-  //   T_rs = -D_r sum_{s<=j<r} A_rj T_js,  D_r = T_rr (fp32 in `at`),
-  // written as Tb blocks T_rs diag(beta). First: T10, T20, T30; else T21, T31, T32.
-  __device__ void offdiag(int b, bool first) {
+  //   T_rs = -D_r Y_rs,  Y_rs = sum_{s<=j<r} A_rj T_js,  T_ss = D_s,
+  // with A_rj and D_r from A16 (fp16). Blocks needed by later products are
+  // formed as tiles (tile(D_r Y) = MFMA(A op D_r, tile(Y))); every block is
+  // also formed transposed (MFMA(tile(Y), A op D_r) = tile((D_r Y)^T)) and
+  // written as Tb rows T_rs diag(beta). The three independent dependency
+  // chains run on three waves: T10 -> T20 -> T30; T21 -> T31; T32.
+  __device__ void offdiag(int b, int chain) {
     const float4_t z = {0.f, 0.f, 0.f, 0.f};
-    auto aop = [&](int R, int C) {  // A[m = c][k = 4g + j] = at[R + m][C + k]
-      return to_half4(ldf4(&sm.at[R + c16][C + 4 * g4]));
+    auto aop = [&](int r, int s) { return ld<half4_t>(L::A16 + 16 * r * L::SPB + 32 * s + sp_tile); };
+    auto dop = [&](int s) {  // tile(D_s) via a transposing read
+      return __builtin_bit_cast(half4_t, ld_tr(L::A16 + 16 * s * L::SPB + 32 * s + tr_a));
     };
-    auto dop = [&](int S) {  // B[k = 4g + j][n = c] = D_S[k][n]
-      half4_t x;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) x[j] = static_cast<half_t>(sm.at[16 * S + 4 * g4 + j][16 * S + c16]);
-      return x;
+    auto put = [&](int r, int s, float4_t mt) {  // mt = tile((D_r Y_rs)^T) = -tile(T_rs^T)
+      const float4_t bs = ld<float4_t>(sc(b, L::BET) + (16 * s + 4 * g4) * 4);
+      st(L::TB + 16 * r * L::SPB + 32 * s + sp_tile, to_half4(-mt * bs));
     };
-    auto put = [&](int r, int s, float4_t mv, float bs) {  // mv = -T_rs
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sm.tb[16 * r + 4 * g4 + i][16 * s + c16] = static_cast<half_t>(-mv[i] * bs);
-    };
-    if (first) {
-      const half4_t a10 = aop(16, 0), a20 = aop(32, 0), a21 = aop(32, 16);
-      const half4_t a30 = aop(48, 0), a31 = aop(48, 16), a32 = aop(48, 32);
-      const half4_t d1 = aop(16, 16), d2 = aop(32, 32), d3 = aop(48, 48), d0 = dop(0);
-      const float bs = sm.bet[b][c16];
-      const float4_t m10 = mfma16(d1, to_half4(mfma16(a10, d0, z)), z);
-      const half4_t t10 = to_half4(-m10);
-      const float4_t m20 = mfma16(d2, to_half4(mfma16(a21, t10, mfma16(a20, d0, z))), z);
-      const half4_t t20 = to_half4(-m20);
-      const float4_t m30 = mfma16(d3, to_half4(mfma16(a32, t20, mfma16(a31, t10, mfma16(a30, d0, z)))), z);
-      put(1, 0, m10, bs);
-      put(2, 0, m20, bs);
-      put(3, 0, m30, bs);
+    if (chain == 0) {
+      const half4_t a10 = aop(1, 0), a20 = aop(2, 0), a21 = aop(2, 1);
+      const half4_t a30 = aop(3, 0), a31 = aop(3, 1), a32 = aop(3, 2);
+      const half4_t d1 = aop(1, 1), d2 = aop(2, 2), d3 = aop(3, 3), d0 = dop(0);
+      const half4_t y10 = to_half4(mfma16(a10, d0, z));
+      const half4_t t10 = to_half4(-mfma16(d1, y10, z));
+      put(1, 0, mfma16(y10, d1, z));
+      const half4_t y20 = to_half4(mfma16(a21, t10, mfma16(a20, d0, z)));
+      const half4_t t20 = to_half4(-mfma16(d2, y20, z));
+      put(2, 0, mfma16(y20, d2, z));
+      const half4_t y30 = to_half4(mfma16(a32, t20, mfma16(a31, t10, mfma16(a30, d0, z))));
+      put(3, 0, mfma16(y30, d3, z));
+    } else if (chain == 1) {
+      const half4_t a21 = aop(2, 1), a31 = aop(3, 1), a32 = aop(3, 2);
+      const half4_t d2 = aop(2, 2), d3 = aop(3, 3), d1 = dop(1);
+      const half4_t y21 = to_half4(mfma16(a21, d1, z));
+      const half4_t t21 = to_half4(-mfma16(d2, y21, z));
+      put(2, 1, mfma16(y21, d2, z));
+      const half4_t y31 = to_half4(mfma16(a32, t21, mfma16(a31, d1, z)));
+      put(3, 1, mfma16(y31, d3, z));
     } else {
-      const half4_t a21 = aop(32, 16), a31 = aop(48, 16), a32 = aop(48, 32);
-      const half4_t d2 = aop(32, 32), d3 = aop(48, 48), d1b = dop(1), d2b = dop(2);
-      const float bs1 = sm.bet[b][16 + c16], bs2 = sm.bet[b][32 + c16];
-      const float4_t m21 = mfma16(d2, to_half4(mfma16(a21, d1b, z)), z);
-      const half4_t t21 = to_half4(-m21);
-      const float4_t m31 = mfma16(d3, to_half4(mfma16(a32, t21, mfma16(a31, d1b, z))), z);
-      const float4_t m32 = mfma16(d3, to_half4(mfma16(a32, d2b, z)), z);
-      put(2, 1, m21, bs1);
-      put(3, 1, m31, bs1);
-      put(3, 2, m32, bs2);
+      const half4_t a32 = aop(3, 2), d3 = aop(3, 3), d2 = dop(2);
+      put(3, 2, mfma16(to_half4(mfma16(a32, d2, z)), d3, z));
     }
   }
 
@@ -478,36 +520,31 @@ struct ChunkBlock {
       half8_t ta[2], xb[2];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        ta[ks] = lds8(&sm.tb[16 * wave + c16][32 * ks + 8 * g4]);
-        xb[ks] = lds8(&sm.xt[c16][32 * ks + 8 * g4]);
+        ta[ks] = ld<half8_t>(L::TB + 16 * wave * L::SPB + sp_frag + 64 * ks);
+        xb[ks] = ld<half8_t>(L::XT + sp_frag + 64 * ks);
       }
-      const int tr = 16 * wave + 4 * g4;
-      const float4_t dd = ldf4(&sm.dec[b][tr]);
+      const float4_t dd = ld<float4_t>(sc(b, L::DEC) + (16 * wave + 4 * g4) * 4);
       float4_t u = mfma32(ta[0], xb[0], float4_t{0.f, 0.f, 0.f, 0.f});
       u = mfma32(ta[1], xb[1], u);
-      st4(&sm.ut[c16][tr], to_half4(u));
+      const uint32_t o = sp_tile + 32 * wave;
+      st(L::UT + o, to_half4(u));
       const float4_t du = u * dd;
       const O4 hi = Op::from(du);
-      st4(&sm.uh[c16][tr], hi);
-      st4(&sm.ul[c16][tr], Op::from(du - Op::to(hi)));
+      st(L::UH + o, hi);
+      st(L::UL + o, Op::from(du - Op::to(hi)));
     }
     products(nb);
   }
 
-  // The 10 lower 16x16 tile pairs (R, S) of A and QKD: (3,0), (3,1), (2,0),
-  // (2,1) on waves 0-3 (which also run U = Tb X), two pairs on waves 4 and 5,
-  // one on waves 6 and 7.
+  // The 10 lower 16x16 tile pairs (R, S) of A and QKD for the chunk in buffer
+  // nb, one per wave 4..13: (3,0) (3,1) (3,2) (3,3) (2,0) (2,1) (2,2) (1,0)
+  // (1,1) (0,0).
   __device__ void products(int nb) {
-    if (wave < 4) {
-      tile_pair(nb, 3 - (wave >> 1), wave & 1);
-    } else if (wave == 4) {
-      tile_pair(nb, 3, 2);
-      tile_pair(nb, 3, 3);
-    } else if (wave == 5) {
-      tile_pair(nb, 2, 2);
-      tile_pair(nb, 1, 1);
-    } else {
-      tile_pair(nb, wave == 6 ? 1 : 0, 0);
+    const int i = wave - 4;
+    if (i >= 0 && i < 10) {
+      const int R = (i < 4) ? 3 : (i < 7) ? 2 : (i < 9) ? 1 : 0;
+      const int S = i - ((i < 4) ? 0 : (i < 7) ? 4 : (i < 9) ? 7 : 9);
+      tile_pair(nb, R, S);
     }
   }
 
@@ -515,35 +552,59 @@ struct ChunkBlock {
   // QKD = scale (Q K^T o D) (inclusive) for the chunk in buffer nb. The
   // products are formed transposed (rows s from K_S, columns t from K_R and
   // Q_R), so lane (g, c) holds row t = 16R + c, columns s = 16S + 4g..4g+3 and
-  // stores them with one write each; the decays exp(c_t - c_s) are shared.
+  // writes them at once. Off the diagonal, s < 16R <= t and the decay factors
+  // as exp(c_t - c_s) = u_t W_R[s] with u_t = exp(c_t - c_16R) and
+  // W_R[s] = exp(c_16R - c_s), both <= 1 (no overflow; an underflow only
+  // drops a product that is itself below the fp32 range), taken from the
+  // chunk's tables: two multiplies per element. Diagonal tiles use
+  // exp(c_t - c_s) directly with the triangular masks and go to AT (fp32, for
+  // the inverse); off-diagonal A tiles go to A16.
   __device__ void tile_pair(int nb, int R, int S) {
-    O8 ks[KS], kr[KS], qr[KS];
+    const uint32_t kmat = L::KQ + 2 * nb * L::KQ_MAT + kp_frag;
+    const uint32_t qmat = kmat + L::KQ_MAT;
+    const bool diag_tile = R == S;
+    O8 kr[KS], qr[KS], ks[KS];
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
-      ks[kk] = ld8<O8>(&sm.kq[nb][0][16 * S + c16][32 * kk + 8 * g4]);
-      kr[kk] = ld8<O8>(&sm.kq[nb][0][16 * R + c16][32 * kk + 8 * g4]);
-      qr[kk] = ld8<O8>(&sm.kq[nb][1][16 * R + c16][32 * kk + 8 * g4]);
+      kr[kk] = ld<O8>(kmat + 16 * R * L::KPB + 64 * kk);
+      qr[kk] = ld<O8>(qmat + 16 * R * L::KPB + 64 * kk);
     }
-    const int t = 16 * R + c16;
+    if (diag_tile) {
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) ks[kk] = kr[kk];
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) ks[kk] = ld<O8>(kmat + 16 * S * L::KPB + 64 * kk);
+    }
     const int s0 = 16 * S + 4 * g4;
-    const float ct = sm.cum[nb][t];
-    const float bt = sm.bet[nb][t];
-    const float4_t cs = ldf4(&sm.cum[nb][s0]);
     float4_t acck = {0.f, 0.f, 0.f, 0.f}, accq = acck;
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
       acck = mma(ks[kk], kr[kk], acck);
       accq = mma(ks[kk], qr[kk], accq);
     }
-    float4_t av, qv;
+    const uint32_t qkd_out = L::QKD + nb * CH * L::SPB + 16 * R * L::SPB + 32 * S + sp_tile;
+    if (diag_tile) {
+      const int t = 16 * R + c16;
+      const float ct = pick(ld<float4_t>(sc(nb, L::CUM4) + c16 * 16), R);
+      const float bt = pick(ld<float4_t>(sc(nb, L::BET4) + c16 * 16), R);
+      const float4_t cs = ld<float4_t>(sc(nb, L::CUM) + s0 * 4);
+      float4_t av, qv;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float d = __expf(ct - cs[i]);
-      av[i] = (s0 + i < t) ? bt * acck[i] * d : 0.f;
-      qv[i] = (s0 + i <= t) ? p.scale * accq[i] * d : 0.f;
+      for (int i = 0; i < 4; ++i) {
+        const float d = __expf(ct - cs[i]);
+        av[i] = (s0 + i < t) ? bt * acck[i] * d : 0.f;
+        qv[i] = (s0 + i <= t) ? p.scale * accq[i] * d : 0.f;
+      }
+      st(L::AT + 16 * R * (L::FPB + 4) + at_lane, av);
+      st(qkd_out, to_half4(qv));
+    } else {
+      const float bu = pick(ld<float4_t>(sc(nb, L::BU4) + c16 * 16), R);
+      const float su = pick(ld<float4_t>(sc(nb, L::SU4) + c16 * 16), R);
+      const float4_t w = ld<float4_t>(sc(nb, L::W1) + ((R - 1) * CH + s0) * 4);
+      st(L::A16 + 16 * R * L::SPB + 32 * S + sp_tile, to_half4(acck * bu * w));
+      st(qkd_out, to_half4(accq * su * w));
     }
-    *reinterpret_cast<float4_t *>(&sm.at[t][s0]) = av;
-    st4(&sm.qkd[nb][t][s0], to_half4(qv));
   }
 
   // ---------------------------------------------------------------- phase 3
@@ -551,40 +612,39 @@ struct ChunkBlock {
   // Q S + QKD U for token rows 16(w-4).., stored; waves 0-3: diagonal blocks
   // of T for chunk n+1.
   __device__ void phase3(long n, int b) {
-    if (wave < NKT) {
+    if (wave >= S_WAVE0 && wave < S_WAVE0 + NKT) {
+      const int kt = wave - S_WAVE0;
       // K^T fragment of key tile w, token step ts: contraction slot j of lane
       // group g is token 32 ts + 8 g + j, the slot order of uh / ul.
+      const uint32_t kmat = L::KQ + 2 * b * L::KQ_MAT + 32 * kt;
       O8 ka[2], hb[2], lb[2];
-      const int trow = 8 * g4 + (c16 >> 2);
-      const int tcol = 16 * wave + 4 * (c16 & 3);
 #pragma unroll
       for (int ts = 0; ts < 2; ++ts) {
-        const i16x4_t lo4 = ld_tr(&sm.kq[b][0][32 * ts + trow][tcol]);
-        const i16x4_t hi4 = ld_tr(&sm.kq[b][0][32 * ts + trow + 4][tcol]);
+        const i16x4_t lo4 = ld_tr(kmat + 32 * ts * L::KPB + tr_k0);
+        const i16x4_t hi4 = ld_tr(kmat + 32 * ts * L::KPB + tr_k1);
         ka[ts] = __builtin_bit_cast(O8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
-        hb[ts] = ld8<O8>(&sm.uh[c16][32 * ts + 8 * g4]);
-        lb[ts] = ld8<O8>(&sm.ul[c16][32 * ts + 8 * g4]);
+        hb[ts] = ld<O8>(L::UH + sp_frag + 64 * ts);
+        lb[ts] = ld<O8>(L::UL + sp_frag + 64 * ts);
       }
-      sacc *= sm.gam[b][CH - 1];
+      sacc *= ld<float4_t>(sc(b, L::GAM) + (CH - 4) * 4)[3];
 #pragma unroll
       for (int ts = 0; ts < 2; ++ts) {
         sacc = mma(ka[ts], hb[ts], sacc);
         sacc = mma(ka[ts], lb[ts], sacc);
       }
       const O4 hi = Op::from(sacc);
-      st4(&sm.sh[c16][16 * wave + 4 * g4], hi);
-      st4(&sm.sl[c16][16 * wave + 4 * g4], Op::from(sacc - Op::to(hi)));
+      st(L::SH + kp_tile + 32 * kt, hi);
+      st(L::SL + kp_tile + 32 * kt, Op::from(sacc - Op::to(hi)));
     }
-    if (wave >= 4) {
+    if (wave >= 4 && wave < 8) {
       const int r = wave - 4;
       half8_t qa[2], ub[2];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        qa[ks] = lds8(&sm.qkd[b][16 * r + c16][32 * ks + 8 * g4]);
-        ub[ks] = lds8(&sm.ut[c16][32 * ks + 8 * g4]);
+        qa[ks] = ld<half8_t>(L::QKD + b * CH * L::SPB + 16 * r * L::SPB + sp_frag + 64 * ks);
+        ub[ks] = ld<half8_t>(L::UT + sp_frag + 64 * ks);
       }
-      const int tr = 16 * r + 4 * g4;
-      float4_t o = qs * ldf4(&sm.gam[b][tr]) * p.scale;
+      float4_t o = qs * ld<float4_t>(sc(b, L::GAM) + (16 * r + 4 * g4) * 4) * p.scale;
       o = mfma32(qa[0], ub[0], o);
       o = mfma32(qa[1], ub[1], o);
       const long t0 = bos + n * CH;
@@ -596,7 +656,7 @@ struct ChunkBlock {
       const uint32_t row = p.Hv * p.V * sizeof(TOut);
 #pragma unroll
       for (int i = 0; i < 4; ++i) put_out<TOut>(ro, o_off + i * row, o[i]);
-    } else {
+    } else if (wave < 4) {
       diag(b ^ 1);
     }
   }
@@ -621,39 +681,43 @@ struct ChunkBlock {
   // Diagonal block D_w = (I + A_ww)^-1 (w = this wave) of the chunk in buffer
   // nb. A_ww is strictly lower triangular (nilpotent), so with M = -A_ww
   //   D = (I + M)(I + M^2)(I + M^4)(I + M^8).
-  // A 16x16 matrix X held as an accumulator tile (lane (g, c): X[4g + i][c]) is
-  // the B operand of a 16x16x16 MFMA as is, and the A operand of X^T; keeping
-  // P_k = M^k and its transpose as tiles gives every operand without LDS, and
-  // Y = D is built transposed: Y^T <- Y^T + P_k^T Y^T. D replaces A_ww in `at`
-  // (fp32), and D diag(beta) is the diagonal block of Tb.
+  // Keeping P_k = M^k both as tile(P_k) and tile(P_k^T) gives every operand
+  // in registers; tile(M) comes from tile(M^T) as MFMA(tile(M^T), tile(I)).
+  // Y = D is built transposed: Y^T <- Y^T + P_k^T Y^T. D goes to A16 (fp16)
+  // for the off-diagonal blocks, D diag(beta) to the diagonal block of Tb.
   __device__ void diag(int nb) {
-    const int base = 16 * wave;
+    const int w = wave;
     const float4_t z = {0.f, 0.f, 0.f, 0.f};
-    float4_t p1;  // M as a tile
+    const float4_t p1t = -ld<float4_t>(L::AT + 16 * w * (L::FPB + 4) + at_lane);  // tile(M^T)
+    const float4_t bw = ld<float4_t>(sc(nb, L::BET) + (16 * w + 4 * g4) * 4);
+    half4_t eye;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) p1[i] = -sm.at[base + 4 * g4 + i][base + c16];
-    const float4_t p1t = -ldf4(&sm.at[base + c16][base + 4 * g4]);  // M^T as a tile
-    const float4_t bw = ldf4(&sm.bet[nb][base + 4 * g4]);
-    float4_t yt = p1t;  // (I + M)^T
+    for (int j = 0; j < 4; ++j) eye[j] = static_cast<half_t>((4 * g4 + j == c16) ? 1.f : 0.f);
+    float4_t yt = p1t;  // tile((I + M)^T)
 #pragma unroll
     for (int i = 0; i < 4; ++i) yt[i] += (4 * g4 + i == c16) ? 1.f : 0.f;
-    const Pair16 s1 = split16(p1), s1t = split16(p1t);
+    const Pair16 s1t = split16(p1t);
+    Pair16 s1;  // tile(M), exactly, from the pair of tile(M^T)
+    s1.h = to_half4(mfma16(s1t.h, eye, z));
+    s1.l = to_half4(mfma16(s1t.l, eye, z));
     const Pair16 s2 = split16(mul3(s1t, s1, z)), s2t = split16(mul3(s1, s1t, z));  // M^2, (M^2)^T
     yt = mul3(s2, split16(yt), yt);
     const Pair16 s4 = split16(mul3(s2t, s2, z)), s4t = split16(mul3(s2, s2t, z));  // M^4, (M^4)^T
     yt = mul3(s4, split16(yt), yt);
     const Pair16 s8 = split16(mul3(s4t, s4, z));                                    // M^8
     yt = mul3(s8, split16(yt), yt);
-    // yt holds D^T: lane (g, c) has D[c][4g + i].
-    *reinterpret_cast<float4_t *>(&sm.at[base + c16][base + 4 * g4]) = yt;
-    st4(&sm.tb[base + c16][base + 4 * g4], to_half4(yt * bw));
+    // yt = tile(D^T): lane (g, c) holds D[c][4g + i], row c of D at columns 4g..
+    const uint32_t o = 16 * w * L::SPB + 32 * w + sp_tile;
+    st(L::A16 + o, to_half4(yt));
+    st(L::TB + o, to_half4(yt * bw));
   }
 
   __device__ void tick(long n) {
-    // Re-define the lane indices opaquely each tick: the per-lane LDS addresses
-    // derived from them are then formed where they are used instead of being
-    // hoisted out of the loop, where they would hold ~100 registers.
-    asm volatile("" : "+v"(c16), "+v"(g4), "+v"(lane), "+v"(tid));
+    // Re-define the lane offsets opaquely each tick: addresses derived from
+    // them are then formed where they are used instead of being hoisted out
+    // of the loop, where they would hold ~100 registers.
+    asm volatile("" : "+v"(kp_frag), "+v"(sp_frag), "+v"(kp_tile), "+v"(sp_tile), "+v"(at_lane));
+    asm volatile("" : "+v"(tr_v), "+v"(tr_a), "+v"(tr_k0), "+v"(tr_k1), "+v"(c16), "+v"(g4));
     const int b = static_cast<int>(n & 1);
     phase1(n, b);
     block_sync();
@@ -665,26 +729,28 @@ struct ChunkBlock {
 
   __device__ void run() {
     // Blocks of Tb and QKD above the diagonal are read as zeros and never written.
-    for (int i = tid; i < CH * Smem::SP; i += NT) {
-      (&sm.tb[0][0])[i] = static_cast<half_t>(0.f);
-      (&sm.qkd[0][0][0])[i] = static_cast<half_t>(0.f);
-      (&sm.qkd[1][0][0])[i] = static_cast<half_t>(0.f);
+    for (int i = tid; i < CH * L::SPB / 4; i += NT) {
+      reinterpret_cast<uint32_t *>(lds + L::TB)[i] = 0u;
+      reinterpret_cast<uint32_t *>(lds + L::QKD)[i] = 0u;
+      reinterpret_cast<uint32_t *>(lds + L::QKD + CH * L::SPB)[i] = 0u;
     }
-    // Initial state: wave w owns key rows 16w..16w+15.
+    // Initial state: wave S_WAVE0 + j owns key rows 16j..16j+15.
     const long state_base = (static_cast<long>(seq) * p.Hv + h) * K * p.V + v0 + c16;
-    if (wave < NKT) {
+    const int kt = wave - S_WAVE0;
+    const bool owner = kt >= 0 && kt < NKT;
+    if (owner) {
       if (p.h0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sacc[i] = p.h0[state_base + static_cast<long>(16 * wave + 4 * g4 + i) * p.V];
+        for (int i = 0; i < 4; ++i) sacc[i] = p.h0[state_base + static_cast<long>(16 * kt + 4 * g4 + i) * p.V];
       }
       const O4 hi = Op::from(sacc);
-      st4(&sm.sh[c16][16 * wave + 4 * g4], hi);
-      st4(&sm.sl[c16][16 * wave + 4 * g4], Op::from(sacc - Op::to(hi)));
+      st(L::SH + kp_tile + 32 * kt, hi);
+      st(L::SL + kp_tile + 32 * kt, Op::from(sacc - Op::to(hi)));
     }
     load_chunk(0);
     block_sync();
     // Prologue: chunk 0 into buffer 0 and through the S-independent prep.
-    in.store(sm, 0, tid, lane, wave == SCAN_WAVE);
+    in.store(lds, 0, tid, lane, wave == SCAN_WAVE, p.scale);
     load_chunk(1);
     block_sync();
     products(0);
@@ -692,9 +758,9 @@ struct ChunkBlock {
     if (wave < 4) diag(0);
     block_sync();
     for (long n = 0; n < nchunks; ++n) tick(n);
-    if (p.ht && wave < NKT) {
+    if (p.ht && owner) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) p.ht[state_base + static_cast<long>(16 * wave + 4 * g4 + i) * p.V] = sacc[i];
+      for (int i = 0; i < 4; ++i) p.ht[state_base + static_cast<long>(16 * kt + 4 * g4 + i) * p.V] = sacc[i];
     }
   }
 };
@@ -702,14 +768,14 @@ struct ChunkBlock {
 template <int K, typename TIn, typename TOut>
 __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  ChunkBlock<K, TIn, TOut> blk(*reinterpret_cast<ChunkSmem<K> *>(smem_raw), p);
+  ChunkBlock<K, TIn, TOut> blk(smem_raw, p);
   blk.run();
 }
 
 template <int K, typename TIn, typename TOut>
 static int launch_chunk(const ChunkParams &p, hipStream_t stream) {
   static bool configured = false;  // benign race: the attribute call is idempotent
-  const size_t smem = sizeof(ChunkSmem<K>);
+  const size_t smem = Layout<K>::BYTES;
   auto kernel = chunk_kernel<K, TIn, TOut>;
   if (!configured) {
     if (hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
