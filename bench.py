@@ -1,6 +1,7 @@
 """Benchmark of the Gated DeltaNet operator on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
+                    [--no-b256] [--copy-probe]
 
 Prints ONE JSON line. The headline workload is the Qwen3-Next-shaped prefill
 (B=1, T=32768, Hk=16 -> Hv=32, K=V=128, bf16 q/k/v, fp32 state, chunk 64):
@@ -13,6 +14,12 @@ the 256 MB Infinity Cache), the roofline of the prefill kernel measured with
 HIP events on the stream it runs on, and the CPU baseline: the numpy oracle
 (oracle/gdn.py) on a bounded sample of the same prefill, run first, before the
 GPU is touched, as one single-threaded process per core over the heads.
+
+`roofline.traffic` (HBM bytes per launch) comes from the rocprofv3 counter
+summary committed under profiles/ (FETCH_SIZE and WRITE_SIZE per dispatch,
+each scaled by what the counter reads for a plain device copy of known size,
+which `--copy-probe` runs in the same process); it is null when that file is
+absent.
 """
 from __future__ import annotations
 
@@ -23,6 +30,7 @@ os.environ.setdefault("OPENBLAS_NUM_THREADS", "1")  # the CPU baseline pins one 
 import argparse
 import json
 import multiprocessing
+import re
 import sys
 import time
 
@@ -34,6 +42,21 @@ import numpy as np
 #   bytes = q, k (Hk heads) and v, o (Hv heads) once, g and beta fp32, h0 and final fp32.
 MFMA_PEAK_TFLOPS = 2500.0   # MI355X dense bf16/fp16 MFMA
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+COPY_PROBE_BYTES = 256 << 20  # the copy probe reads this many bytes and writes as many
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "traffic_chunk_and_recurrent_kernels.md")
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` ("chunk" or "recurrent_b64") from the
+    committed counter summary: lines of the form `traffic_bytes[<kernel>]: <int>`."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            text = f.read()
+    except OSError:
+        return None
+    m = re.search(r"traffic_bytes\[" + re.escape(kernel) + r"\]:\s*(\d+)", text)
+    return int(m.group(1)) if m else None
 
 
 def prefill_flops(tokens, hv, dk, dv, chunk=64):
@@ -102,30 +125,29 @@ def cpu_baseline(sample_tokens: int, seed: int = 0):
 # GPU measurements
 # ---------------------------------------------------------------------------
 def timed_steps(fn, steps, warmup):
+    """Run `warmup` untimed steps, then time `steps` back-to-back steps. Returns
+    (host seconds per step between two synchronizations, device seconds per
+    launch from two HIP events recorded around the same launches on the stream
+    they run on, torch's current stream)."""
     import torch
     for _ in range(warmup):
         fn()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    start.record(stream)
     for _ in range(steps):
         fn()
+    end.record(stream)
     torch.cuda.synchronize()
-    return (time.perf_counter() - t0) / steps
+    wall = (time.perf_counter() - t0) / steps
+    return wall, start.elapsed_time(end) / 1e3 / steps
 
 
 def kernel_time(fn, reps):
-    """Mean duration of fn's launches from HIP events recorded on the stream the
-    kernels run on (torch's current stream), in seconds."""
-    import torch
-    stream = torch.cuda.current_stream()
-    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(reps)]
-    for start, end in events:
-        start.record(stream)
-        fn()
-        end.record(stream)
-    torch.cuda.synchronize()
-    return sum(s.elapsed_time(e) for s, e in events) / reps / 1e3
+    """Mean device duration of fn's launches, timed as in timed_steps (seconds)."""
+    return timed_steps(fn, reps, 1)[1]
 
 
 def bench_prefill(steps, warmup):
@@ -140,8 +162,7 @@ def bench_prefill(steps, warmup):
     def step():
         gd.chunk_fwd(q, k, v, g, beta, scale, h0, out=out)
 
-    sec = timed_steps(step, steps, warmup)
-    ksec = kernel_time(step, max(steps, 10))
+    sec, ksec = timed_steps(step, steps, warmup)
     flops = prefill_flops(s.length, s.hv, s.dk, s.dv)
     nbytes = prefill_bytes(s.length, s.hk, s.hv, s.dk, s.dv)
     return s, sec, ksec, flops, nbytes
@@ -158,14 +179,30 @@ def bench_decode(batch, steps, warmup=10):
     def step():
         torch.ops.pbgdn.recurrent_step_(q, k, v, g, beta, state, None, scale)
 
-    sec = timed_steps(step, steps, warmup)
-    ksec = kernel_time(step, 100)
+    sec, ksec = timed_steps(step, steps, warmup)
     nbytes = decode_bytes(batch, s.hk, s.hv, s.dk, s.dv)
     return {
         "batch": batch, "steps": steps, "us_per_step": sec * 1e6, "kernel_us": ksec * 1e6,
         "bytes_per_step": nbytes, "achieved_GBs": nbytes / ksec / 1e9,
         "hbm_frac": nbytes / ksec / 1e9 / HBM_PEAK_GBS,
     }
+
+
+def copy_probe(reps=5):
+    """A plain device copy of COPY_PROBE_BYTES (torch's copy kernel): the
+    reference point that scales the FETCH_SIZE/WRITE_SIZE counters, and a
+    practical read+write bandwidth ceiling on this GPU."""
+    import torch
+    src = torch.ones(COPY_PROBE_BYTES // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+
+    def step():
+        dst.copy_(src)
+
+    step()
+    ksec = kernel_time(step, reps)
+    return {"bytes_read": COPY_PROBE_BYTES, "bytes_written": COPY_PROBE_BYTES, "kernel_us": ksec * 1e6,
+            "GBs": 2 * COPY_PROBE_BYTES / ksec / 1e9}
 
 
 def main(argv=None):
@@ -177,6 +214,8 @@ def main(argv=None):
     ap.add_argument("--cpu-tokens", type=int, default=16384)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-b256", action="store_true", help="skip the ungraded 256-sequence decode")
+    ap.add_argument("--copy-probe", action="store_true", help="also time a plain 256 MiB device copy")
     args = ap.parse_args(argv)
     world = int(os.environ.get("WORLD_SIZE", args.gpus))
     if args.gpus != 1 or world != 1:
@@ -210,7 +249,7 @@ def main(argv=None):
                    "Hk": shape.hk, "Hv": shape.hv, "K": shape.dk, "V": shape.dv, "chunk": 64,
                    "out_dtype": "bf16", "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / MFMA_PEAK_TFLOPS, "traffic": None,
+                     "frac": achieved / MFMA_PEAK_TFLOPS, "traffic": measured_traffic("chunk"),
                      "kernel_ms": ksec * 1e3, "algorithmic_flops": flops, "algorithmic_bytes": nbytes,
                      "hbm_GBs_algorithmic": nbytes / ksec / 1e9,
                      "io_bound_TFLOPs": min(MFMA_PEAK_TFLOPS, flops / nbytes * HBM_PEAK_GBS / 1e3)},
@@ -222,8 +261,12 @@ def main(argv=None):
         dec = bench_decode(64, args.decode_steps)
         result["decode"] = dict(dec, roofline={"bound": "hbm", "achieved": dec["achieved_GBs"],
                                                "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                               "frac": dec["hbm_frac"], "traffic": None})
-        result["decode_b256_ungraded"] = bench_decode(256, 200)
+                                               "frac": dec["hbm_frac"],
+                                               "traffic": measured_traffic("recurrent_b64")})
+        if not args.no_b256:
+            result["decode_b256_ungraded"] = bench_decode(256, 200)
+    if args.copy_probe:
+        result["copy_probe"] = copy_probe()
     print(json.dumps(result), flush=True)
     return 0
 

@@ -71,7 +71,8 @@ const char *pbgdn_status_string(int status);
  *   cu_seqlens  [N + 1] int32 sequence boundaries into the T axis (B must be
  *               1, cu_seqlens[0] == 0, cu_seqlens[N] == T, nondecreasing), or
  *               NULL: then N = B sequences of T tokens each
- *   o           [B, T, Hv, V]   dtype out_dtype, written
+ *   o           [B, T, Hv, V]   dtype out_dtype (F32 or in_dtype; another
+ *               type is PBGDN_ERR_UNSUPPORTED), written
  *   ht          [N, Hv, K, V]   float32 final states, written (may be NULL;
  *               may equal h0 for an in-place state update)
  *   num_seqs    N (must equal B when cu_seqlens is NULL)

@@ -87,6 +87,8 @@ def chunk_fwd(q, k, v, g, beta, scale: float, h0=None, cu_seqlens=None, *,
     """Launch pbgdn_chunk_fwd. Returns (o [B,T,Hv,V] in out_dtype (default q's dtype),
     final [N,Hv,K,V] fp32 or None). `out` may supply the output buffer."""
     batch, length, hk, hv, dk, dv = _shapes(q, k, v, g, beta)
+    if out_dtype is not None and out_dtype not in (torch.float32, q.dtype):
+        raise ValueError(f"chunk kernel writes o as float32 or q's dtype ({q.dtype}), not {out_dtype}")
     dev = _require_device(q, k, v, g, beta, h0, cu_seqlens)
     if dk not in CHUNK_HEAD_DIMS or dv % 16:
         raise ValueError(f"chunk kernel supports K in {CHUNK_HEAD_DIMS} and V a multiple of 16")

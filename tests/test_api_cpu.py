@@ -50,6 +50,8 @@ def test_shape_errors():
         gd.chunk_fwd(q, k[:, :4], v, g, beta, 0.1)
     with pytest.raises(ValueError, match="initial state"):
         gd.delta_rule_sequential(q, k, v, g, beta, 0.1, h0[:, :2])
+    with pytest.raises(ValueError, match="float32 or q's dtype"):
+        gd.chunk_fwd(q, k, v, g, beta, 0.1, out_dtype=torch.float16 if q.dtype != torch.float16 else torch.bfloat16)
 
 
 def test_custom_ops_are_registered_with_shape_inference():
