@@ -13,7 +13,8 @@
  *                        replaces delta_rule_sequential (gated_deltanet.py:93-107).
  *
  * Conventions (all entry points):
- *   - every pointer is device memory owned by the caller; nothing is allocated;
+ *   - every pointer is device memory owned by the caller; nothing is allocated
+ *     (scratch memory comes in as a caller-provided workspace);
  *   - tensors are dense row-major in the reference layouts:
  *       q, k  [B, T, Hk, K]     v, o  [B, T, Hv, V]     g, beta  [B, T, Hv]
  *       states [N, Hv, K, V] float32, S stored [d_k, d_v] per head;
@@ -30,13 +31,14 @@
 #ifndef PBGDN_H_
 #define PBGDN_H_
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
 #endif
 
-#define PBGDN_ABI_VERSION 1
+#define PBGDN_ABI_VERSION 2
 
 /* element types */
 #define PBGDN_F32 0
@@ -78,6 +80,11 @@ const char *pbgdn_status_string(int status);
  *   num_seqs    N (must equal B when cu_seqlens is NULL)
  *   scale       query scale (the reference passes K ** -0.5)
  *   chunk       must be 64 (CHUNK, gated_deltanet.py:49)
+ *   workspace   device scratch of at least pbgdn_chunk_workspace_size(B, T,
+ *               Hv, num_seqs) bytes, 16-byte aligned: per-chunk intermediates
+ *               (Tb, Q K^T o D, decays) passed from the first kernel of the
+ *               call to the second; its contents need no initialisation and
+ *               are dead when the call's work on `stream` completes
  *
  * Supported: K in {64, 128}; V a multiple of 16; Hv a multiple of Hk.
  */
@@ -86,7 +93,16 @@ int pbgdn_chunk_fwd(const void *q, const void *k, const void *v, int in_dtype,
                     const float *h0, float *ht, const int32_t *cu_seqlens,
                     int num_seqs, void *o, int out_dtype, int B, int T, int Hk,
                     int Hv, int K, int V, float scale, int chunk,
-                    void *stream);
+                    void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Bytes of workspace pbgdn_chunk_fwd needs for a call with these sizes
+ * (B * T tokens in num_seqs sequences, Hv value heads): about 13 KiB per
+ * 64-token chunk and value head. 0 for invalid sizes. No reference
+ * counterpart: the reference materialises the same per-chunk tensors
+ * (gated_deltanet.py:143-157) with torch allocations.
+ */
+size_t pbgdn_chunk_workspace_size(int B, int T, int Hv, int num_seqs);
 
 /*
  * Fused recurrent steps: for each token, in one pass over the state,

@@ -1,0 +1,395 @@
+// Prep kernel of the chunkwise prefill: the state-independent part of every
+// (chunk, value head), computed in parallel over all chunks of all sequences.
+//
+// Reference: delta_rule_chunked, pseudobrain/gated_deltanet.py:139-157 (cumsum
+// of g, decay D, A = strict_lower(beta K K^T o D), the unit-lower-triangular
+// solve, Q K^T o D). For chunk record r and value head h it writes the
+// workspace record (chunk.hpp):
+//   Tb  = (I + A)^-1 diag(beta)                  as 16x16x32 fp16 A fragments
+//   QKD = scale (Q K^T o D), D inclusive        as 16x16x32 fp16 A fragments
+//   exp(c_t), scale exp(c_t), exp(c_63 - c_t)  fp32
+//
+// A persistent grid of 4-wave workgroups walks the (record, head) items; the
+// inputs of a workgroup's next item are loaded into registers while it works
+// on the current one. Item numbering keeps the value heads that share a key
+// head on one XCD, so a q/k chunk comes from HBM once per pair.
+//
+// Per item (barrier-separated stages):
+//   stage   K, Q -> LDS (bf16/fp16 kept, fp32 rounded to fp16); wave 3 scans g
+//           into the decay tables
+//   tiles   the 10 lower 16x16 tile pairs of A and QKD (bf16/fp16 16x16x32
+//           MFMA, fp32 accumulate), computed transposed so each lane writes 4
+//           consecutive elements of a row; off-diagonal tiles take the decay
+//           as u_t W_R[s] (two multiplies, no masks), diagonal tiles exp(c_t -
+//           c_s) with the triangular masks, in fp32 for the inverse
+//   diag    the 4 diagonal blocks of T as (I+M)(I+M^2)(I+M^4)(I+M^8), M = -A_ww
+//           strictly lower (nilpotent), on fp16 high/low MFMAs (~22-bit products)
+//   offdiag the off-diagonal blocks of T by block forward substitution
+//           T_rs = -D_r sum_{s<=j<r} A_rj T_js in three independent chains
+//   out     Tb and QKD fragments and the decay vectors -> the record
+#include "chunk.hpp"
+
+namespace pbgdn {
+namespace {
+
+constexpr int PNT = 256;          // threads per prep workgroup
+constexpr int PREP_SCAN_WAVE = 3; // wave that loads g, beta and scans them
+constexpr int PREP_WG_PER_CU = 2;
+constexpr int NUM_CU = 256;
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// LDS layout (byte offsets); (swz) as in chunk.hpp.
+template <int K>
+struct PrepLayout {
+  static constexpr int KPB = 2 * K + 32;
+  static constexpr int SPB = 2 * CH + 32;
+  static constexpr int ATP = 4 * 16 + 16;               // fp32 16-column rows + pad
+  static constexpr int KQ_MAT = CH * KPB;
+  static constexpr int KQ = 0;                          // [K, Q][64 t][K] operand type (swz)
+  static constexpr int SC = KQ + 2 * KQ_MAT;            // [11][64] fp32 decay tables
+  static constexpr int CUM = 0, GAM = 256, DEC = 512, BET = 768, CUM4 = 1024, BET4 = 1280, BU4 = 1536,
+                       SU4 = 1792, W1 = 2048;
+  static constexpr int AT = SC + 11 * CH * 4;           // [4 tiles][16][16] fp32 diagonal tiles of A
+  static constexpr int TB = AT + 4 * 16 * ATP;          // [64 t][64 s] fp16 Tb (swz)
+  static constexpr int QKD = TB + CH * SPB;             // [64 t][64 s] fp16 (swz)
+  static constexpr int A16 = QKD + CH * SPB;            // [64 t][64 s] fp16: off-diagonal A, diagonal D (swz)
+  static constexpr int BYTES = A16 + CH * SPB;
+};
+
+template <int K, typename TIn>
+struct PrepBlock {
+  using L = PrepLayout<K>;
+  using Op = OpOf<TIn>;
+  using O8 = typename Op::T8;
+  using Inputs = ChunkInputs<K, TIn, PNT, L, false, true>;
+  static constexpr int KS = K / 32;  // contraction steps over keys
+  static_assert(K == 64 || K == 128, "K must be 64 or 128");
+  static_assert(L::BYTES * PREP_WG_PER_CU <= 160 * 1024, "prep LDS");
+
+  unsigned char *lds;
+  const ChunkParams &p;
+  int tid, lane, c16, g4, wave, group_heads;
+  Inputs in;
+  uint32_t kp_frag, sp_frag, sp_tile, at_lane, tr_a;
+
+  __device__ PrepBlock(unsigned char *l, const ChunkParams &prm) : lds(l), p(prm) {
+    tid = threadIdx.x;
+    lane = tid & 63;
+    wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    c16 = lane & 15;
+    g4 = lane >> 4;
+    group_heads = p.Hv / p.Hk;
+    in.init(p, tid, lane);
+    const uint32_t s4 = ((c16 >> 2) & 1) << 4;
+    kp_frag = c16 * L::KPB + ((16 * g4) ^ s4);                         // row c, 16 bytes at 16 g
+    sp_frag = c16 * L::SPB + ((16 * g4) ^ s4);
+    sp_tile = c16 * L::SPB + ((16 * (g4 >> 1)) ^ s4) + 8 * (g4 & 1);  // row c, 8 bytes at 8 g
+    at_lane = c16 * L::ATP + 16 * g4;
+    // transposing read of a [16][16] fp16 tile: lanes 4k..4k+3 of group g point
+    // at row 4g + k, 8 bytes at 8 (c & 3)
+    tr_a = (4 * g4 + (c16 >> 2)) * L::SPB + ((8 * (c16 & 3)) ^ ((g4 & 1) << 4));
+  }
+
+  template <typename T>
+  __device__ T ld(uint32_t off) const { return *reinterpret_cast<const T *>(lds + off); }
+  template <typename T>
+  __device__ void st(uint32_t off, T x) const { *reinterpret_cast<T *>(lds + off) = x; }
+  __device__ i16x4_t ld_tr(uint32_t off) const {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t *)(lds + off));
+  }
+
+  // Item = (chunk record, value head) -> sequence, first token, tokens left.
+  // Returns false for a record that no sequence's chunk maps to. Everything
+  // here is wave-uniform and kept in scalar registers (readfirstlane), so the
+  // lookups are scalar loads that do not wait for outstanding vector memory
+  // operations.
+  __device__ bool locate(int item, int &h, long &rec, long &t0, long &len) const {
+    const int r32 = __builtin_amdgcn_readfirstlane(item / p.Hv);
+    rec = r32;
+    h = __builtin_amdgcn_readfirstlane(item - r32 * p.Hv);
+    int lo = 0, hi = p.num_seqs - 1;  // largest s with rec_base(s) <= rec
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      long b, e;
+      seq_bounds(p, mid, b, e);
+      if (rec_base(b, mid) <= rec) lo = mid; else hi = mid - 1;
+    }
+    long bos, eos;
+    seq_bounds(p, lo, bos, eos);
+    const long j = rec - rec_base(bos, lo);
+    t0 = bos + j * CH;
+    len = eos - t0;
+    return j >= 0 && len > 0;
+  }
+
+  // First valid item at or after `item` on this workgroup's stride.
+  __device__ int next_valid(int item, int stride, int items, int &h, long &rec, long &t0, long &len) const {
+    for (; item < items; item += stride) {
+      if (locate(item, h, rec, t0, len)) return item;
+    }
+    return items;
+  }
+
+  // Tile (R, S), S <= R, of A = strict_lower(b_t K K^T o D) and of
+  // QKD = scale (Q K^T o D) (inclusive). The products are formed transposed
+  // (rows s from K_S, columns t from K_R and Q_R), so lane (g, c) holds row
+  // t = 16R + c, columns s = 16S + 4g..4g+3 and writes them at once. Off the
+  // diagonal, s < 16R <= t and exp(c_t - c_s) = u_t W_R[s], both factors <= 1
+  // (an underflow only drops a product that is itself below the fp32 range).
+  __device__ void tile_pair(int R, int S) {
+    const uint32_t kmat = L::KQ + kp_frag;
+    const uint32_t qmat = kmat + L::KQ_MAT;
+    const bool diag_tile = R == S;
+    O8 kr[KS], qr[KS], ks[KS];
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      kr[kk] = ld<O8>(kmat + 16 * R * L::KPB + 64 * kk);
+      qr[kk] = ld<O8>(qmat + 16 * R * L::KPB + 64 * kk);
+    }
+    if (diag_tile) {
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) ks[kk] = kr[kk];
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) ks[kk] = ld<O8>(kmat + 16 * S * L::KPB + 64 * kk);
+    }
+    const int s0 = 16 * S + 4 * g4;
+    float4_t acck = {0.f, 0.f, 0.f, 0.f}, accq = acck;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      acck = mma(ks[kk], kr[kk], acck);
+      accq = mma(ks[kk], qr[kk], accq);
+    }
+    const uint32_t qkd_out = L::QKD + 16 * R * L::SPB + 32 * S + sp_tile;
+    if (diag_tile) {
+      const int t = 16 * R + c16;
+      const float ct = pick(ld<float4_t>(L::SC + L::CUM4 + c16 * 16), R);
+      const float bt = pick(ld<float4_t>(L::SC + L::BET4 + c16 * 16), R);
+      const float4_t cs = ld<float4_t>(L::SC + L::CUM + s0 * 4);
+      float4_t av, qv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float d = __expf(ct - cs[i]);
+        av[i] = (s0 + i < t) ? bt * acck[i] * d : 0.f;
+        qv[i] = (s0 + i <= t) ? p.scale * accq[i] * d : 0.f;
+      }
+      st(L::AT + 16 * R * L::ATP + at_lane, av);
+      st(qkd_out, to_half4(qv));
+    } else {
+      const float bu = pick(ld<float4_t>(L::SC + L::BU4 + c16 * 16), R);
+      const float su = pick(ld<float4_t>(L::SC + L::SU4 + c16 * 16), R);
+      const float4_t w = ld<float4_t>(L::SC + L::W1 + ((R - 1) * CH + s0) * 4);
+      st(L::A16 + 16 * R * L::SPB + 32 * S + sp_tile, to_half4(acck * bu * w));
+      st(qkd_out, to_half4(accq * su * w));
+    }
+  }
+
+  // Tile pairs i = wave, wave + 4, wave + 8 of the list (3,0) (3,1) (3,2)
+  // (3,3) (2,0) (2,1) (2,2) (1,0) (1,1) (0,0): 3, 3, 2, 2 per wave.
+  __device__ void tiles() {
+    for (int i = wave; i < 10; i += 4) {
+      const int R = (i < 4) ? 3 : (i < 7) ? 2 : (i < 9) ? 1 : 0;
+      const int S = i - ((i < 4) ? 0 : (i < 7) ? 4 : (i < 9) ? 7 : 9);
+      tile_pair(R, S);
+    }
+  }
+
+  // fp16 high/low pair of an fp32 tile, and c + a b from pairs (3 MFMAs, the
+  // low*low term dropped): a product accurate to ~22 bits.
+  struct Pair16 {
+    half4_t h, l;
+  };
+  __device__ static Pair16 split16(float4_t x) {
+    Pair16 r;
+    r.h = to_half4(x);
+    r.l = to_half4(x - to_float4(r.h));
+    return r;
+  }
+  __device__ static float4_t mul3(const Pair16 &a, const Pair16 &b, float4_t c) {
+    c = mfma16(a.h, b.h, c);
+    c = mfma16(a.h, b.l, c);
+    return mfma16(a.l, b.h, c);
+  }
+
+  // Diagonal block D_w = (I + A_ww)^-1 (w = this wave). A_ww is strictly lower
+  // triangular (nilpotent), so with M = -A_ww
+  //   D = (I + M)(I + M^2)(I + M^4)(I + M^8).
+  // Keeping P_k = M^k both as tile(P_k) and tile(P_k^T) gives every operand
+  // in registers; tile(M) comes from tile(M^T) as MFMA(tile(M^T), tile(I)).
+  // Y = D is built transposed: Y^T <- Y^T + P_k^T Y^T. D goes to A16 (fp16)
+  // for the off-diagonal blocks, D diag(beta) to the diagonal block of Tb.
+  __device__ void diag() {
+    const int w = wave;
+    const float4_t z = {0.f, 0.f, 0.f, 0.f};
+    const float4_t p1t = -ld<float4_t>(L::AT + 16 * w * L::ATP + at_lane);  // tile(M^T)
+    const float4_t bw = ld<float4_t>(L::SC + L::BET + (16 * w + 4 * g4) * 4);
+    half4_t eye;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) eye[j] = static_cast<half_t>((4 * g4 + j == c16) ? 1.f : 0.f);
+    float4_t yt = p1t;  // tile((I + M)^T)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) yt[i] += (4 * g4 + i == c16) ? 1.f : 0.f;
+    const Pair16 s1t = split16(p1t);
+    Pair16 s1;  // tile(M), exactly, from the pair of tile(M^T)
+    s1.h = to_half4(mfma16(s1t.h, eye, z));
+    s1.l = to_half4(mfma16(s1t.l, eye, z));
+    const Pair16 s2 = split16(mul3(s1t, s1, z)), s2t = split16(mul3(s1, s1t, z));  // M^2, (M^2)^T
+    yt = mul3(s2, split16(yt), yt);
+    const Pair16 s4 = split16(mul3(s2t, s2, z)), s4t = split16(mul3(s2, s2t, z));  // M^4, (M^4)^T
+    yt = mul3(s4, split16(yt), yt);
+    const Pair16 s8 = split16(mul3(s4t, s4, z));                                    // M^8
+    yt = mul3(s8, split16(yt), yt);
+    // yt = tile(D^T): lane (g, c) holds D[c][4g + i], row c of D at columns 4g..
+    const uint32_t o = 16 * w * L::SPB + 32 * w + sp_tile;
+    st(L::A16 + o, to_half4(yt));
+    st(L::TB + o, to_half4(yt * bw));
+  }
+
+  // Off-diagonal blocks of T:
+  //   T_rs = -D_r Y_rs,  Y_rs = sum_{s<=j<r} A_rj T_js,  T_ss = D_s,
+  // with A_rj and D_r from A16 (fp16). Blocks needed by later products are
+  // formed as tiles (tile(D_r Y) = MFMA(A op D_r, tile(Y))); every block is
+  // also formed transposed (MFMA(tile(Y), A op D_r) = tile((D_r Y)^T)) and
+  // written as Tb rows T_rs diag(beta). Chains: T10 -> T20 -> T30; T21 -> T31;
+  // T32.
+  __device__ void offdiag(int chain) {
+    const float4_t z = {0.f, 0.f, 0.f, 0.f};
+    auto aop = [&](int r, int s) { return ld<half4_t>(L::A16 + 16 * r * L::SPB + 32 * s + sp_tile); };
+    auto dop = [&](int s) {  // tile(D_s) via a transposing read
+      return __builtin_bit_cast(half4_t, ld_tr(L::A16 + 16 * s * L::SPB + 32 * s + tr_a));
+    };
+    auto put = [&](int r, int s, float4_t mt) {  // mt = tile((D_r Y_rs)^T) = -tile(T_rs^T)
+      const float4_t bs = ld<float4_t>(L::SC + L::BET + (16 * s + 4 * g4) * 4);
+      st(L::TB + 16 * r * L::SPB + 32 * s + sp_tile, to_half4(-mt * bs));
+    };
+    if (chain == 0) {
+      const half4_t a10 = aop(1, 0), a20 = aop(2, 0), a21 = aop(2, 1);
+      const half4_t a30 = aop(3, 0), a31 = aop(3, 1), a32 = aop(3, 2);
+      const half4_t d1 = aop(1, 1), d2 = aop(2, 2), d3 = aop(3, 3), d0 = dop(0);
+      const half4_t y10 = to_half4(mfma16(a10, d0, z));
+      const half4_t t10 = to_half4(-mfma16(d1, y10, z));
+      put(1, 0, mfma16(y10, d1, z));
+      const half4_t y20 = to_half4(mfma16(a21, t10, mfma16(a20, d0, z)));
+      const half4_t t20 = to_half4(-mfma16(d2, y20, z));
+      put(2, 0, mfma16(y20, d2, z));
+      const half4_t y30 = to_half4(mfma16(a32, t20, mfma16(a31, t10, mfma16(a30, d0, z))));
+      put(3, 0, mfma16(y30, d3, z));
+    } else if (chain == 1) {
+      const half4_t a21 = aop(2, 1), a31 = aop(3, 1), a32 = aop(3, 2);
+      const half4_t d2 = aop(2, 2), d3 = aop(3, 3), d1 = dop(1);
+      const half4_t y21 = to_half4(mfma16(a21, d1, z));
+      const half4_t t21 = to_half4(-mfma16(d2, y21, z));
+      put(2, 1, mfma16(y21, d2, z));
+      const half4_t y31 = to_half4(mfma16(a32, t21, mfma16(a31, d1, z)));
+      put(3, 1, mfma16(y31, d3, z));
+    } else {
+      const half4_t a32 = aop(3, 2), d3 = aop(3, 3), d2 = dop(2);
+      put(3, 2, mfma16(to_half4(mfma16(a32, d2, z)), d3, z));
+    }
+  }
+
+  // Fragments f = wave, wave + 4, wave + 8 of Tb (f < 6) and QKD (f >= 6) and
+  // one decay vector per wave (wave 3: c itself, unused by the scan) -> the
+  // workspace record. rec < 0 issues the same stores with a zero-size resource.
+  __device__ void out(long rec, int h) const {
+    const __amdgpu_buffer_rsrc_t rr =
+        rsrc(p.ws + (rec * p.Hv + h) * static_cast<long>(REC_BYTES), rec >= 0 ? REC_BYTES : 0);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int f = wave + 4 * j;
+      const int fi = f < NFRAG ? f : f - NFRAG;
+      const int r = fi < 2 ? fi : 2 + ((fi - 2) >> 1);
+      const int kk = fi < 2 ? 0 : ((fi - 2) & 1);
+      const uint32_t src = (f < NFRAG ? L::TB : L::QKD) + 16 * r * L::SPB + sp_frag + 64 * kk;
+      const uint32_t dst = (f < NFRAG ? REC_TB : REC_QKD) + fi * FRAG_BYTES + lane * 16;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, ld<half8_t>(src)), rr, dst, 0, 0);
+    }
+    const float gam = ld<float>(L::SC + L::GAM + lane * 4);
+    const float val = wave == 0 ? gam
+                      : wave == 1 ? p.scale * gam
+                      : ld<float>(L::SC + (wave == 2 ? L::DEC : L::CUM) + lane * 4);
+    const uint32_t dst = REC_SC + 256 * wave + lane * 4;  // SC_GAM, SC_GSC, SC_DEC, spare
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, val), rr, dst, 0, 0);
+  }
+
+  __device__ void run(int items) {
+    // Blocks of Tb and QKD above the diagonal stay zero (never written).
+    for (int i = tid; i < 2 * CH * L::SPB / 4; i += PNT) reinterpret_cast<uint32_t *>(lds + L::TB)[i] = 0u;
+    const int stride = gridDim.x;
+    const int nx = stride / 8;
+    // Workgroups are dispatched round-robin over the 8 XCDs: number the items
+    // so that consecutive ones (the value heads of one key head) share an XCD.
+    const int first = (stride % 8 == 0) ? static_cast<int>(blockIdx.x & 7) * nx + static_cast<int>(blockIdx.x >> 3)
+                                        : static_cast<int>(blockIdx.x);
+    int h;
+    long rec, t0, len;
+    int item = next_valid(first, stride, items, h, rec, t0, len);
+    if (item >= items) return;
+    // Every wave issues the same memory operations on every path (loads of an
+    // absent next item have zero length; the stores before the first item go
+    // nowhere), so waits for the item's inputs never cover newer stores.
+    in.load(p, t0, len, h / group_heads, h, 0);
+    out(-1, 0);
+    while (true) {
+      int h_n = 0;
+      long rec_n = 0, t0_n = 0, len_n = 0;
+      const int next = next_valid(item + stride, stride, items, h_n, rec_n, t0_n, len_n);
+      block_sync();  // the previous item's readers of K, Q, the tables and Tb/QKD are done
+      in.store(lds, 0, tid, lane, wave == PREP_SCAN_WAVE, p.scale);
+      in.load(p, t0_n, next < items ? len_n : 0, h_n / group_heads, h_n, 0);
+      block_sync();
+      tiles();
+      block_sync();
+      diag();
+      block_sync();
+      if (wave < 3) offdiag(wave);
+      block_sync();
+      out(rec, h);
+      if (next >= items) break;
+      item = next;
+      h = h_n;
+      rec = rec_n;
+      t0 = t0_n;
+      len = len_n;
+    }
+  }
+};
+
+template <int K, typename TIn>
+__global__ __launch_bounds__(PNT) void prep_kernel(ChunkParams p, int items) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  PrepBlock<K, TIn> blk(smem_raw, p);
+  blk.run(items);
+}
+
+}  // namespace
+
+template <int K, typename TIn>
+int launch_prep(const ChunkParams &p, long records, hipStream_t stream) {
+  static bool configured = false;  // benign race: the attribute call is idempotent
+  const size_t smem = PrepLayout<K>::BYTES;
+  auto kernel = prep_kernel<K, TIn>;
+  if (!configured) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(smem)) != hipSuccess) {
+      return PBGDN_ERR_LAUNCH;
+    }
+    configured = true;
+  }
+  const long items = records * p.Hv;
+  if (items > 0x3fffffffL) return PBGDN_ERR_UNSUPPORTED;  // item numbers are 32-bit
+  long grid = static_cast<long>(NUM_CU) * PREP_WG_PER_CU;
+  if (items < grid) grid = (items + 7) / 8 * 8;
+  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(PNT), smem, stream, p, static_cast<int>(items));
+  return hipGetLastError() == hipSuccess ? PBGDN_OK : PBGDN_ERR_LAUNCH;
+}
+
+template int launch_prep<64, u16>(const ChunkParams &, long, hipStream_t);
+template int launch_prep<64, half_t>(const ChunkParams &, long, hipStream_t);
+template int launch_prep<64, float>(const ChunkParams &, long, hipStream_t);
+template int launch_prep<128, u16>(const ChunkParams &, long, hipStream_t);
+template int launch_prep<128, half_t>(const ChunkParams &, long, hipStream_t);
+template int launch_prep<128, float>(const ChunkParams &, long, hipStream_t);
+
+}  // namespace pbgdn

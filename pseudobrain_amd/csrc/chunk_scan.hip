@@ -1,0 +1,522 @@
+// Scan kernel of the chunkwise prefill: the state-dependent part, chunk by
+// chunk (the serial loop of delta_rule_chunked, pseudobrain/gated_deltanet.py:158-165).
+//
+// The recurrence is separable along the value columns, so a workgroup owns
+// one (sequence, value head, 16-column tile of V): grid = V/16 x Hv x N. The
+// fp32 state tile S [K, 16] lives in MFMA accumulators for the whole sequence
+// (compute wave j owns key rows 16j..16j+15) and is read and written once.
+// Everything that does not involve S (Tb, QKD, the decay vectors) comes from
+// the prep kernel's workspace records.
+//
+// 12 waves (3 per SIMD): compute waves 0-7 and loader waves 8-11. Per chunk n
+// ("tick"), three barrier-separated phases:
+//   phase 1: X = V - diag(gamma) K S   (compute 0-3, token rows 16w..)
+//            Q S                        (compute 4-7)
+//            loaders: chunk n+1 registers -> LDS; loads of chunk n+3 issued
+//   phase 2: U = Tb X; U^T, (dec U)^T high/low -> LDS   (compute 0-3)
+//            loaders: O of chunk n-1, LDS -> HBM
+//   phase 3: S <- gamma_63 S + K^T (dec U)              (owner of each key tile)
+//            O = scale gamma Q S + QKD U -> LDS         (compute 4-7)
+// A chunk's inputs are its K, Q and V tile and its workspace record (Tb and
+// QKD fragments, decay vectors), all staged into one LDS buffer of a double
+// buffer, loaded two ticks ahead into one of two register sets of the loader
+// waves (the loop is unrolled by two so that the sets have fixed registers).
+// The compute waves issue no global memory operations in the loop, so the
+// state chain never stalls on the memory pipeline. Barriers wait for LDS
+// traffic only, so loads stay in flight across them. The two roles run
+// separate loops with the same barrier sequence (a workgroup barrier does not
+// need its waves at the same instruction), so the registers of one role are
+// not held by the other.
+//
+// Loader threads all issue the same memory operations each tick (units past
+// the end use out-of-range offsets or zero-size resources): the compiler
+// counts outstanding operations per wave statically, and with identical
+// counts on every path the wait before a use lets every newer operation stay
+// in flight.
+//
+// Arithmetic (fp32 accumulation throughout):
+//   * K, Q enter MFMA in the input's 16-bit type (bf16 unconverted; fp32
+//     inputs staged as fp16); V as staged.
+//   * S enters K S as a high + low pair of that type (two MFMAs), so X sees
+//     the fp32 state to ~16 bits; Q S, which only reaches the output, uses the
+//     high part. The state update K^T (dec U) uses dec U as a pair.
+//   * Tb, X, U and QKD are fp16 (11-bit significand) on the fp16 MFMA.
+//
+// LDS costs that shape the code (MI355X, CU cycles per wave64 instruction):
+// 16-byte fragment reads and transposing reads 4, 8-byte tile writes 6.7 in
+// the swizzled layouts; V is staged row-major and read column-wise with
+// ds_read_b64_tr_b16, and so is K^T.
+#include "chunk.hpp"
+
+namespace pbgdn {
+namespace {
+
+constexpr int NCW = 8;                  // compute waves
+constexpr int NLT = 256;                // loader threads (waves 8-11)
+constexpr int NT = NCW * 64 + NLT;      // threads per scan workgroup
+
+// LDS layout (byte offsets); (swz) as in chunk.hpp. Two chunk buffers, each
+// [K, Q][64 t][K] in the operand type (swz), V [64 t][16] 16-bit in 32-byte
+// rows, and the chunk's workspace record as stored; two O tiles [64 t][16].
+template <int K>
+struct ScanLayout {
+  static constexpr int KPB = 2 * K + 32;
+  static constexpr int SPB = 2 * CH + 32;
+  static constexpr int KQ_MAT = CH * KPB;
+  static constexpr int V16_OFF = 2 * KQ_MAT;
+  static constexpr int REC_OFF = V16_OFF + CH * 32;
+  static constexpr int BUF = REC_OFF + REC_BYTES;
+  static constexpr int XT = 2 * BUF;                  // [16 col][64 t] fp16 X^T (swz)
+  static constexpr int UT = XT + VT * SPB;            // U^T fp16 (swz)
+  static constexpr int UH = UT + VT * SPB;            // (dec U)^T high, operand type (swz)
+  static constexpr int UL = UH + VT * SPB;            // (dec U)^T low (swz)
+  static constexpr int SH = UL + VT * SPB;            // [16 col][K] S^T high, operand type (swz)
+  static constexpr int SL = SH + VT * KPB;            // S^T low (swz)
+  static constexpr int OT = SL + VT * KPB;            // [2][64 t][16] output type
+  static constexpr int OT_BUF = CH * VT * 4;
+  static constexpr int BYTES = OT + 2 * OT_BUF;
+  __device__ static constexpr int kq(int b) { return b * BUF; }
+  __device__ static constexpr int v16(int b) { return b * BUF + V16_OFF; }
+  __device__ static constexpr int rec(int b) { return b * BUF + REC_OFF; }
+  __device__ static constexpr int ot(int b) { return OT + b * OT_BUF; }
+};
+
+// Staging of one chunk by the loader threads: 16-byte units numbered K, Q
+// (rows of 64 tokens), V tile, record; loader thread l moves unit
+// l + NLT i in slot i. K and Q fill whole slots, so the class of every slot
+// but one is a compile-time constant; the slot where V ends and the record
+// begins splits at a whole wave. Slot classes are fixed in the code so that
+// the loads and stores compile without branches.
+template <int K, typename TIn>
+struct ScanStage {
+  using L = ScanLayout<K>;
+  static constexpr int EPU = 16 / sizeof(TIn);  // elements per unit
+  static constexpr int ROW_UNITS = K / EPU;
+  static constexpr int MAT_UNITS = CH * ROW_UNITS;
+  static constexpr int KQ_UNITS = 2 * MAT_UNITS;
+  static constexpr int V_UNITS = CH * VT / EPU;
+  static constexpr int R_UNITS = REC_BYTES / 16;
+  static constexpr int UNITS = KQ_UNITS + V_UNITS + R_UNITS;
+  static constexpr int UPT = (UNITS + NLT - 1) / NLT;
+  static constexpr int SLOT_K = MAT_UNITS / NLT;   // slots [0, SLOT_K): K; [SLOT_K, SLOT_V): Q
+  static constexpr int SLOT_V = KQ_UNITS / NLT;    // slot SLOT_V: V (first V_UNITS threads), then record
+  static_assert(MAT_UNITS % NLT == 0, "K and Q must fill whole slots");
+  static_assert(V_UNITS % 64 == 0 && V_UNITS <= NLT, "V must end at a wave boundary of its slot");
+
+  struct Regs {
+    uint4 u[UPT];
+  };
+
+  uint32_t src[UPT];  // byte offset of the unit in its source (OUT_OF_RANGE if none)
+  uint32_t dst[UPT];  // LDS byte offset of the unit within a chunk buffer
+  bool v_wave;        // this loader wave's slot SLOT_V unit is V (else record); wave-uniform
+
+  __device__ void init(const ChunkParams &p, int l) {
+    v_wave = __builtin_amdgcn_readfirstlane(l & ~63) < V_UNITS;
+#pragma unroll
+    for (int i = 0; i < UPT; ++i) {
+      const int u = l + NLT * i;
+      src[i] = OUT_OF_RANGE;
+      dst[i] = 0;
+      if (u < KQ_UNITS) {
+        const int w = u % MAT_UNITS;
+        const int t = w / ROW_UNITS;
+        const int byte = (w % ROW_UNITS) * EPU * 2;  // staged as 16-bit elements
+        src[i] = (t * p.Hk * K + (w % ROW_UNITS) * EPU) * sizeof(TIn);
+        dst[i] = (u / MAT_UNITS) * L::KQ_MAT + t * L::KPB + (byte ^ (((t >> 2) & 1) << 4));
+      } else if (u < KQ_UNITS + V_UNITS) {
+        const int w = u - KQ_UNITS;
+        const int tv = w / (VT / EPU);
+        const int c0 = (w % (VT / EPU)) * EPU;
+        src[i] = (tv * p.Hv * p.V + c0) * sizeof(TIn);
+        dst[i] = L::V16_OFF + tv * 32 + c0 * 2;
+      } else if (u < UNITS) {
+        const int w = u - KQ_UNITS - V_UNITS;
+        src[i] = 16 * w;
+        dst[i] = L::REC_OFF + 16 * w;
+      }
+    }
+  }
+
+  // Issue the loads of the chunk at tokens t0.. (`len` left, may be <= 0) of
+  // value head h, columns v0.., and of its record `rec` (null past the end).
+  __device__ void load(const ChunkParams &p, Regs &r, long t0, long len, int hk, int h, int v0,
+                       const unsigned char *rec) const {
+    const long rows = len < CH ? len : CH;
+    const long qk_bytes = rows > 0 ? ((rows - 1) * p.Hk * K + K) * static_cast<long>(sizeof(TIn)) : 0;
+    const long qk_base = (t0 * p.Hk + hk) * static_cast<long>(K);
+    const long v_bytes = rows > 0 ? ((rows - 1) * p.Hv * p.V + VT) * static_cast<long>(sizeof(TIn)) : 0;
+    const __amdgpu_buffer_rsrc_t rk = rsrc(static_cast<const TIn *>(p.k) + qk_base, qk_bytes);
+    const __amdgpu_buffer_rsrc_t rq = rsrc(static_cast<const TIn *>(p.q) + qk_base, qk_bytes);
+    const __amdgpu_buffer_rsrc_t rr = rsrc(rec, rec ? REC_BYTES : 0);
+    const __amdgpu_buffer_rsrc_t rvr =
+        v_wave ? rsrc(static_cast<const TIn *>(p.v) + (t0 * p.Hv + h) * static_cast<long>(p.V) + v0, v_bytes) : rr;
+#pragma unroll
+    for (int i = 0; i < UPT; ++i) {
+      r.u[i] = buf_load16(i < SLOT_K ? rk : i < SLOT_V ? rq : i == SLOT_V ? rvr : rr, src[i]);
+    }
+  }
+
+  // Registers -> LDS chunk buffer at byte `base`: K, Q, V as staged 16-bit
+  // elements (fp32 rounded to fp16), the record unchanged. Units without a
+  // destination (past the record) write a harmless zero-offset copy of
+  // nothing: their slot is skipped by range.
+  __device__ void store(unsigned char *lds, int base, const Regs &r, int l) const {
+#pragma unroll
+    for (int i = 0; i < UPT; ++i) {
+      unsigned char *d = lds + base + dst[i];
+      const bool convert = EPU == 4 && (i < SLOT_V || (i == SLOT_V && v_wave));
+      if (l + NLT * i >= UNITS) continue;
+      if (convert) {
+        const uint4 x = r.u[i];
+        *reinterpret_cast<half4_t *>(d) = to_half4(float4_t{__uint_as_float(x.x), __uint_as_float(x.y),
+                                                            __uint_as_float(x.z), __uint_as_float(x.w)});
+      } else {
+        *reinterpret_cast<uint4 *>(d) = r.u[i];
+      }
+    }
+  }
+};
+
+// Block index -> (sequence, value head, column tile). All column tiles of the
+// value heads that share one query/key head of one sequence form a group; a
+// group is kept on one XCD (workgroups are dispatched round-robin over the 8
+// XCDs) so that its q/k chunks and Tb/QKD records are fetched into that XCD's
+// L2 once.
+__device__ __forceinline__ void decode_block(int L, int total, int nv, int group_heads, int Hk, int &seq, int &h,
+                                             int &vtile, int &member) {
+  const int gsize = nv * group_heads;
+  const int ngroups = total / gsize;
+  int grp, in;
+  if (ngroups % 8 == 0) {
+    const int xcd = L & 7;
+    const int slot = L >> 3;
+    grp = (slot / gsize) * 8 + xcd;
+    in = slot % gsize;
+  } else {
+    grp = L / gsize;
+    in = L % gsize;
+  }
+  const int hk = grp % Hk;
+  seq = grp / Hk;
+  h = hk * group_heads + in / nv;
+  vtile = in % nv;
+  member = in;
+}
+
+template <typename T>
+__device__ __forceinline__ T out_elem(float x);
+template <>
+__device__ __forceinline__ u16 out_elem<u16>(float x) { return __builtin_bit_cast(u16, static_cast<bf16_t>(x)); }
+template <>
+__device__ __forceinline__ half_t out_elem<half_t>(float x) { return static_cast<half_t>(x); }
+template <>
+__device__ __forceinline__ float out_elem<float>(float x) { return x; }
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+template <int K, typename TIn, typename TOut>
+struct ScanBlock {
+  using L = ScanLayout<K>;
+  using Op = OpOf<TIn>;
+  using O4 = typename Op::T4;
+  using O8 = typename Op::T8;
+  using Stage = ScanStage<K, TIn>;
+  static constexpr int NKT = K / 16;  // key tiles of S, one per compute wave
+  static constexpr int KS = K / 32;   // contraction steps over keys
+  static constexpr int OUT_UNITS = CH * VT * sizeof(TOut) / 16;  // 16-byte units of an O tile
+  static_assert(K == 64 || K == 128, "K must be 64 or 128");
+  static_assert(NKT <= NCW, "one S key tile per compute wave");
+  static_assert(OUT_UNITS <= NLT, "one O unit per loader thread");
+
+  unsigned char *lds;
+  const ChunkParams &p;
+  int tid, lane, c16, g4, wave, seq, h, hk, v0, lt;  // lt: loader thread index (loader waves)
+  long bos, eos, nchunks, rbase;
+  float4_t sacc, qs;
+  Stage stage;
+  typename Stage::Regs regs[2];
+  uint32_t out_src, out_dst;  // loader thread's O unit: LDS offset in a tile, byte offset in a chunk
+  // Per-lane LDS byte offsets (see lane_offsets()).
+  uint32_t kp_frag, sp_frag, kp_tile, sp_tile, tr_v, tr_k0, tr_k1;
+
+  __device__ ScanBlock(unsigned char *l, const ChunkParams &prm) : lds(l), p(prm) {
+    tid = threadIdx.x;
+    lane = tid & 63;
+    wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    c16 = lane & 15;
+    g4 = lane >> 4;
+    lt = tid - NCW * 64;
+    const int group_heads = p.Hv / p.Hk;
+    int vtile, member;
+    decode_block(blockIdx.x, gridDim.x, p.V / VT, group_heads, p.Hk, seq, h, vtile, member);
+    hk = h / group_heads;
+    v0 = vtile * VT;
+    seq_bounds(p, seq, bos, eos);
+    nchunks = (eos - bos + CH - 1) / CH;
+    rbase = rec_base(bos, seq);
+    sacc = float4_t{0.f, 0.f, 0.f, 0.f};
+    qs = sacc;
+    if (wave >= NCW) {
+      stage.init(p, lt);
+      constexpr int upr = VT * sizeof(TOut) / 16;  // units per output row
+      out_src = lt < OUT_UNITS ? 16 * lt : 0;
+      out_dst = lt < OUT_UNITS ? ((lt / upr) * p.Hv * p.V + (lt % upr) * (16 / sizeof(TOut))) * sizeof(TOut)
+                               : OUT_OF_RANGE;
+    }
+    lane_offsets();
+  }
+
+  // Per-lane parts of LDS addresses; everything else is a wave-uniform or
+  // immediate offset. s4 is the swizzle of rows 16 m + c (bit 2 of the row).
+  __device__ void lane_offsets() {
+    const uint32_t s4 = ((c16 >> 2) & 1) << 4;
+    kp_frag = c16 * L::KPB + ((16 * g4) ^ s4);                         // row c, 16 bytes at 16 g
+    sp_frag = c16 * L::SPB + ((16 * g4) ^ s4);
+    kp_tile = c16 * L::KPB + ((16 * (g4 >> 1)) ^ s4) + 8 * (g4 & 1);  // row c, 8 bytes at 8 g
+    sp_tile = c16 * L::SPB + ((16 * (g4 >> 1)) ^ s4) + 8 * (g4 & 1);
+    // transposing reads: lanes 4k..4k+3 of group g point at row 4g + k (V)
+    // or 8g + k (K), 8 bytes at 8 (c & 3)
+    tr_v = (4 * g4 + (c16 >> 2)) * 32 + 8 * (c16 & 3);
+    tr_k0 = (8 * g4 + (c16 >> 2)) * L::KPB + 8 * (c16 & 3);
+    tr_k1 = (8 * g4 + 4 + (c16 >> 2)) * L::KPB + ((8 * (c16 & 3)) ^ 16);
+  }
+
+  template <typename T>
+  __device__ T ld(uint32_t off) const { return *reinterpret_cast<const T *>(lds + off); }
+  template <typename T>
+  __device__ void st(uint32_t off, T x) const { *reinterpret_cast<T *>(lds + off) = x; }
+  __device__ i16x4_t ld_tr(uint32_t off) const {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t *)(lds + off));
+  }
+
+  // ------------------------------------------------------------ loader waves
+  __device__ void load_chunk(typename Stage::Regs &r, long n) const {
+    const long t0 = bos + n * CH;
+    const unsigned char *rec = n < nchunks ? p.ws + ((rbase + n) * p.Hv + h) * static_cast<long>(REC_BYTES) : nullptr;
+    stage.load(p, r, t0, eos - t0, hk, h, v0, rec);
+  }
+
+  // O tile of chunk n (LDS buffer n & 1) -> HBM, one 16-byte unit per loader
+  // thread; n < 0 issues the same store with a zero-size resource.
+  __device__ void store_out(long n) const {
+    const long t0 = bos + n * CH;
+    const long len = eos - t0;
+    const long rows = len < CH ? len : CH;
+    const long bytes = n >= 0 ? ((rows - 1) * p.Hv * p.V + VT) * static_cast<long>(sizeof(TOut)) : 0;
+    const __amdgpu_buffer_rsrc_t ro =
+        rsrc(static_cast<TOut *>(p.o) + (t0 * p.Hv + h) * static_cast<long>(p.V) + v0, bytes);
+    const uint4 x = ld<uint4>(L::ot(static_cast<int>(n & 1)) + out_src);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, x), ro, out_dst, 0, 0);
+  }
+
+  // ------------------------------------------------------------ compute waves
+  // Row float4 of a record vector (SC_GAM, SC_GSC, SC_DEC) for this lane's
+  // accumulator rows 16 r + 4 g.. of the chunk in buffer b.
+  __device__ float4_t rec_rows(int b, int vec, int r) const {
+    return ld<float4_t>(L::rec(b) + REC_SC + vec + (16 * r + 4 * g4) * 4);
+  }
+  // Tb (REC_TB) or QKD (REC_QKD) fragment (r, kk) of the chunk in buffer b.
+  __device__ half8_t rec_frag(int b, int mat, int r, int kk) const {
+    return ld<half8_t>(L::rec(b) + mat + frag_index(r, kk) * FRAG_BYTES + lane * 16);
+  }
+
+  // Phase 1: waves 0-3 X = V - gamma K S for token rows 16w.. (S as a
+  // high/low pair); waves 4-7 Q S (high part) for rows 16(w-4)..
+  __device__ void phase1(int b) {
+    const int r = wave & 3;
+    const bool chain = wave < 4;
+    const uint32_t mat = L::kq(b) + (chain ? 0 : L::KQ_MAT) + 16 * r * L::KPB + kp_frag;
+    O8 a[KS], shi[KS], slo[KS];
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      a[kk] = ld<O8>(mat + 64 * kk);
+      shi[kk] = ld<O8>(L::SH + kp_frag + 64 * kk);
+    }
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+    if (chain) {
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) slo[kk] = ld<O8>(L::SL + kp_frag + 64 * kk);
+      const float4_t vv = Op::bits_to_float(ld_tr(L::v16(b) + 16 * r * 32 + tr_v));
+      const float4_t gg = rec_rows(b, SC_GAM, r);
+      float4_t acl = acc;
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        acc = mma(a[kk], shi[kk], acc);
+        acl = mma(a[kk], slo[kk], acl);
+      }
+      st(L::XT + sp_tile + 32 * r, to_half4(vv - gg * (acc + acl)));
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) acc = mma(a[kk], shi[kk], acc);
+      qs = acc;
+    }
+  }
+
+  // Phase 2: waves 0-3 U = Tb X for token rows 16w.. (Tb rows 16w.. vanish
+  // past column 16w + 15, so row tiles 0, 1 need one contraction step and
+  // 2, 3 two).
+  __device__ void phase2(int b) {
+    const half8_t x0 = ld<half8_t>(L::XT + sp_frag);
+    float4_t u = mfma32(rec_frag(b, REC_TB, wave, 0), x0, float4_t{0.f, 0.f, 0.f, 0.f});
+    if (wave >= 2) u = mfma32(rec_frag(b, REC_TB, wave, 1), ld<half8_t>(L::XT + sp_frag + 64), u);
+    const uint32_t o = sp_tile + 32 * wave;
+    st(L::UT + o, to_half4(u));
+    const float4_t du = u * rec_rows(b, SC_DEC, wave);
+    const O4 hi = Op::from(du);
+    st(L::UH + o, hi);
+    st(L::UL + o, Op::from(du - Op::to(hi)));
+  }
+
+  // Phase 3: S key tile owners S <- gamma_63 S + K^T (dec U); waves 4-7
+  // O = scale gamma Q S + QKD U -> the O tile in LDS.
+  __device__ void phase3(int b) {
+    if (wave < NKT) {
+      const int kt = wave;
+      // K^T fragment of key tile kt, token step ts: contraction slot j of lane
+      // group g is token 32 ts + 8 g + j, the slot order of the dec U pair.
+      const uint32_t kmat = L::kq(b) + 32 * kt;
+      O8 ka[2], hb[2], lb[2];
+#pragma unroll
+      for (int ts = 0; ts < 2; ++ts) {
+        const i16x4_t lo4 = ld_tr(kmat + 32 * ts * L::KPB + tr_k0);
+        const i16x4_t hi4 = ld_tr(kmat + 32 * ts * L::KPB + tr_k1);
+        ka[ts] = __builtin_bit_cast(O8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+        hb[ts] = ld<O8>(L::UH + sp_frag + 64 * ts);
+        lb[ts] = ld<O8>(L::UL + sp_frag + 64 * ts);
+      }
+      float4_t acl = mma(ka[0], lb[0], float4_t{0.f, 0.f, 0.f, 0.f});
+      acl = mma(ka[1], lb[1], acl);
+      sacc *= ld<float>(L::rec(b) + REC_SC + SC_GAM + (CH - 1) * 4);
+      sacc = mma(ka[0], hb[0], sacc);
+      sacc = mma(ka[1], hb[1], sacc);
+      sacc += acl;
+      const O4 hi = Op::from(sacc);
+      st(L::SH + kp_tile + 32 * kt, hi);
+      st(L::SL + kp_tile + 32 * kt, Op::from(sacc - Op::to(hi)));
+    }
+    if (wave >= 4) {
+      const int r = wave - 4;
+      float4_t o = qs * rec_rows(b, SC_GSC, r);
+      o = mfma32(rec_frag(b, REC_QKD, r, 0), ld<half8_t>(L::UT + sp_frag), o);
+      if (r >= 2) o = mfma32(rec_frag(b, REC_QKD, r, 1), ld<half8_t>(L::UT + sp_frag + 64), o);
+      // lane (g, c) holds O[16 r + 4 g + i][c]
+#pragma unroll
+      for (int i = 0; i < 4; ++i) st(L::ot(b) + ((16 * r + 4 * g4 + i) * VT + c16) * sizeof(TOut), out_elem<TOut>(o[i]));
+    }
+  }
+
+  // Tick n of a compute wave; chunk n is in LDS buffer n mod 2 = P.
+  template <int P>
+  __device__ void tick_compute() {
+    // Re-define the lane offsets opaquely each tick: addresses derived from
+    // them are then formed where they are used instead of being hoisted out
+    // of the loop, where they would hold many registers.
+    asm volatile("" : "+v"(kp_frag), "+v"(sp_frag), "+v"(kp_tile), "+v"(sp_tile));
+    asm volatile("" : "+v"(tr_v), "+v"(tr_k0), "+v"(tr_k1), "+v"(c16), "+v"(g4));
+    phase1(P);
+    block_sync();
+    if (wave < 4) phase2(P);
+    block_sync();
+    phase3(P);
+    block_sync();
+  }
+
+  // Tick n of a loader wave: register set P (= n mod 2) holds chunk n+1 on
+  // entry, goes to LDS buffer 1 - P, and receives chunk n+3; then O of chunk
+  // n-1 goes out.
+  template <int P>
+  __device__ void tick_loader(long n) {
+    stage.store(lds, L::kq(P ^ 1), regs[P], lt);
+    load_chunk(regs[P], n + 3);
+    block_sync();
+    store_out(n - 1);
+    block_sync();
+    block_sync();
+  }
+
+  __device__ void run() {
+    // Initial state: compute wave j owns key rows 16j..16j+15.
+    const long state_base = (static_cast<long>(seq) * p.Hv + h) * K * p.V + v0 + c16;
+    const int kt = wave;
+    const bool owner = kt < NKT;
+    if (owner) {
+      if (p.h0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sacc[i] = p.h0[state_base + static_cast<long>(16 * kt + 4 * g4 + i) * p.V];
+      }
+      const O4 hi = Op::from(sacc);
+      st(L::SH + kp_tile + 32 * kt, hi);
+      st(L::SL + kp_tile + 32 * kt, Op::from(sacc - Op::to(hi)));
+    }
+    if (wave >= NCW) {
+      // Chunk 0 into buffer 0; chunks 1 and 2 in flight into register sets 0
+      // and 1, each followed by a store that goes nowhere, as in a tick.
+      load_chunk(regs[1], 0);
+      stage.store(lds, L::kq(0), regs[1], lt);
+      load_chunk(regs[0], 1);
+      store_out(-1);
+      load_chunk(regs[1], 2);
+      store_out(-1);
+      block_sync();
+      long n = 0;
+      for (; n + 1 < nchunks; n += 2) {
+        tick_loader<0>(n);
+        tick_loader<1>(n + 1);
+      }
+      if (n < nchunks) tick_loader<0>(n);
+      if (nchunks > 0) store_out(nchunks - 1);
+      return;
+    }
+    block_sync();
+    long n = 0;
+    for (; n + 1 < nchunks; n += 2) {
+      tick_compute<0>();
+      tick_compute<1>();
+    }
+    if (n < nchunks) tick_compute<0>();
+    if (p.ht && owner) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p.ht[state_base + static_cast<long>(16 * kt + 4 * g4 + i) * p.V] = sacc[i];
+    }
+  }
+};
+
+template <int K, typename TIn, typename TOut>
+__global__ __launch_bounds__(NT) void scan_kernel(ChunkParams p) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  ScanBlock<K, TIn, TOut> blk(smem_raw, p);
+  blk.run();
+}
+
+}  // namespace
+
+template <int K, typename TIn, typename TOut>
+int launch_scan(const ChunkParams &p, hipStream_t stream) {
+  static bool configured = false;  // benign race: the attribute call is idempotent
+  const size_t smem = ScanLayout<K>::BYTES;
+  auto kernel = scan_kernel<K, TIn, TOut>;
+  if (!configured) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(smem)) != hipSuccess) {
+      return PBGDN_ERR_LAUNCH;
+    }
+    configured = true;
+  }
+  const int total = (p.V / VT) * p.Hv * p.num_seqs;
+  hipLaunchKernelGGL(kernel, dim3(total), dim3(NT), smem, stream, p);
+  return hipGetLastError() == hipSuccess ? PBGDN_OK : PBGDN_ERR_LAUNCH;
+}
+
+template int launch_scan<64, u16, u16>(const ChunkParams &, hipStream_t);
+template int launch_scan<64, u16, float>(const ChunkParams &, hipStream_t);
+template int launch_scan<64, half_t, half_t>(const ChunkParams &, hipStream_t);
+template int launch_scan<64, half_t, float>(const ChunkParams &, hipStream_t);
+template int launch_scan<64, float, float>(const ChunkParams &, hipStream_t);
+template int launch_scan<128, u16, u16>(const ChunkParams &, hipStream_t);
+template int launch_scan<128, u16, float>(const ChunkParams &, hipStream_t);
+template int launch_scan<128, half_t, half_t>(const ChunkParams &, hipStream_t);
+template int launch_scan<128, half_t, float>(const ChunkParams &, hipStream_t);
+template int launch_scan<128, float, float>(const ChunkParams &, hipStream_t);
+
+}  // namespace pbgdn

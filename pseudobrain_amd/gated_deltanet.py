@@ -112,12 +112,15 @@ def chunk_fwd(q, k, v, g, beta, scale: float, h0=None, cu_seqlens=None, *,
     elif out.shape != (batch, length, hv, dv) or out.dtype != out_dtype or not out.is_contiguous():
         raise ValueError("out must be a contiguous [B,T,Hv,V] tensor of out_dtype")
     final = torch.empty(nseq, hv, dk, dv, dtype=torch.float32, device=dev) if output_final_state else None
+    lib = _lib.lib()
+    ws_bytes = lib.pbgdn_chunk_workspace_size(batch, length, hv, nseq)
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     codes = _lib.DTYPE_CODES
-    status = _lib.lib().pbgdn_chunk_fwd(
+    status = lib.pbgdn_chunk_fwd(
         _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), codes[q.dtype], _lib.ptr(g), _lib.ptr(beta),
         codes[beta.dtype], _lib.ptr(h0), _lib.ptr(final), _lib.ptr(cu_seqlens), nseq,
         _lib.ptr(out), codes[out_dtype], batch, length, hk, hv, dk, dv, float(scale), CHUNK,
-        _lib.stream_handle(dev))
+        _lib.ptr(workspace), ws_bytes, _lib.stream_handle(dev))
     _lib.check(status, "pbgdn_chunk_fwd")
     return out, final
 

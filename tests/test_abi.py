@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version_and_status_strings():
-    assert _lib.lib().pbgdn_abi_version() == _lib.ABI_VERSION == 1
+    assert _lib.lib().pbgdn_abi_version() == _lib.ABI_VERSION == 2
     assert _lib.status_string(0) == "ok"
     for code in (1, 2, 3, 99):
         assert _lib.status_string(code)
@@ -42,7 +42,7 @@ FAKE = 0x1000  # never dereferenced: every call below fails validation first
 def chunk_call(**over):
     args = dict(q=FAKE, k=FAKE, v=FAKE, in_dtype=1, g=FAKE, beta=FAKE, beta_dtype=0, h0=None,
                 ht=None, cu=None, nseq=1, o=FAKE, out_dtype=1, B=1, T=64, Hk=16, Hv=32, K=128,
-                V=128, scale=0.1, chunk=64, stream=None)
+                V=128, scale=0.1, chunk=64, ws=FAKE, ws_bytes=1 << 40, stream=None)
     args.update(over)
     return _lib.lib().pbgdn_chunk_fwd(*args.values())
 
@@ -68,6 +68,9 @@ def recurrent_call(**over):
     (dict(K=96), _lib.ERR_UNSUPPORTED),
     (dict(K=256), _lib.ERR_UNSUPPORTED),
     (dict(V=120), _lib.ERR_UNSUPPORTED),
+    (dict(ws=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(ws=FAKE + 8), _lib.ERR_INVALID_ARGUMENT),     # workspace must be 16-byte aligned
+    (dict(ws_bytes=1000), _lib.ERR_INVALID_ARGUMENT),  # smaller than pbgdn_chunk_workspace_size
 ])
 def test_chunk_fwd_rejects(over, code):
     assert chunk_call(**over) == code
@@ -95,3 +98,15 @@ def test_recurrent_fwd_rejects(over, code):
 
 def test_recurrent_fwd_empty_is_ok():
     assert recurrent_call(B=0) == _lib.OK
+
+
+def test_chunk_workspace_size():
+    lib = _lib.lib()
+    rec = 13 * 1024  # bytes per (64-token chunk, value head) record
+    # B*T tokens in N sequences: floor(B*T / 64) + N + 1 chunk records per value head
+    assert lib.pbgdn_chunk_workspace_size(1, 32768, 32, 1) == (512 + 2) * 32 * rec
+    assert lib.pbgdn_chunk_workspace_size(1, 262144, 32, 8) == (4096 + 9) * 32 * rec
+    assert lib.pbgdn_chunk_workspace_size(4, 100, 2, 4) == (6 + 5) * 2 * rec
+    assert lib.pbgdn_chunk_workspace_size(1, 0, 4, 1) == 2 * 4 * rec
+    assert lib.pbgdn_chunk_workspace_size(-1, 10, 4, 1) == 0
+    assert lib.pbgdn_chunk_workspace_size(1, 10, 0, 1) == 0
