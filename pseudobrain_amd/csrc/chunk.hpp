@@ -48,23 +48,24 @@ constexpr int VT = 16;                  // value columns per scan workgroup
 constexpr int RSRC_WORD3 = 0x00020000;  // raw buffer resource, gfx9 family
 
 // Workspace record of one (chunk, value head), REC_BYTES bytes:
+//   REC_SC   fp32 [64] gamma_t, [64] scale gamma_t, [64] exp(c_63 - c_t),
+//            [64] c_t
 //   REC_TB   6 fragments of Tb as 16x16x32 fp16 A operands (64 lanes x 16 B):
 //            row tile r, contraction step kk <= r / 2 (the others are zero),
 //            at fragment frag_index(r, kk); lane (g, c) holds
 //            Tb[16 r + c][32 kk + 8 g .. + 7]
 //   REC_QKD  the same for QKD = scale (Q K^T o D)
-//   REC_SC   fp32 [64] gamma_t, [64] scale gamma_t, [64] exp(c_63 - c_t)
 // Records are indexed (chunk record, value head); the chunk record of chunk j
 // of sequence s is rec_base(s) + j with rec_base(s) = floor(bos_s / 64) + s,
 // which is increasing in s, leaves room for every sequence's chunks, and is
 // below floor(total_tokens / 64) + num_seqs + 1 (see chunk_records()).
 constexpr int FRAG_BYTES = 64 * 16;
 constexpr int NFRAG = 6;
-constexpr int REC_TB = 0;
-constexpr int REC_QKD = NFRAG * FRAG_BYTES;
-constexpr int REC_SC = 2 * NFRAG * FRAG_BYTES;
+constexpr int REC_SC = 0;
 constexpr int SC_GAM = 0, SC_GSC = 256, SC_DEC = 512;
-constexpr int REC_BYTES = REC_SC + 1024;
+constexpr int REC_TB = 1024;
+constexpr int REC_QKD = REC_TB + NFRAG * FRAG_BYTES;
+constexpr int REC_BYTES = REC_QKD + NFRAG * FRAG_BYTES;
 
 __host__ __device__ constexpr int frag_index(int r, int kk) { return r < 2 ? r : 2 * r - 2 + kk; }
 

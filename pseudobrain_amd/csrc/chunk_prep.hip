@@ -290,8 +290,7 @@ struct PrepBlock {
   }
 
   // Fragments f = wave, wave + 4, wave + 8 of Tb (f < 6) and QKD (f >= 6) and
-  // one decay vector per wave (wave 3: c itself, unused by the scan) -> the
-  // workspace record. rec < 0 issues the same stores with a zero-size resource.
+  // one decay vector per wave (wave 3: c itself) -> the workspace record. rec < 0 issues the same stores with a zero-size resource.
   __device__ void out(long rec, int h) const {
     const __amdgpu_buffer_rsrc_t rr =
         rsrc(p.ws + (rec * p.Hv + h) * static_cast<long>(REC_BYTES), rec >= 0 ? REC_BYTES : 0);
@@ -309,7 +308,7 @@ struct PrepBlock {
     const float val = wave == 0 ? gam
                       : wave == 1 ? p.scale * gam
                       : ld<float>(L::SC + (wave == 2 ? L::DEC : L::CUM) + lane * 4);
-    const uint32_t dst = REC_SC + 256 * wave + lane * 4;  // SC_GAM, SC_GSC, SC_DEC, spare
+    const uint32_t dst = REC_SC + 256 * wave + lane * 4;  // SC_GAM, SC_GSC, SC_DEC, c
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, val), rr, dst, 0, 0);
   }
 

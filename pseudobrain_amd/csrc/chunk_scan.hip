@@ -12,11 +12,12 @@
 // ("tick"), three barrier-separated phases:
 //   phase 1: X = V - diag(gamma) K S   (compute 0-3, token rows 16w..)
 //            Q S                        (compute 4-7)
-//            loaders: chunk n+1 registers -> LDS; loads of chunk n+3 issued
 //   phase 2: U = Tb X; U^T, (dec U)^T high/low -> LDS   (compute 0-3)
-//            loaders: O of chunk n-1, LDS -> HBM
+//            O = scale gamma Q S + QKD U of chunk n-1 -> LDS tile (compute 4-7)
 //   phase 3: S <- gamma_63 S + K^T (dec U)              (owner of each key tile)
-//            O = scale gamma Q S + QKD U -> LDS         (compute 4-7)
+//   loaders: chunk n+1 registers -> LDS and loads of chunk n+3 issued, over
+//            the three phases; O of chunk n-1, LDS -> HBM, in phase 3.
+// Compute waves read the LDS operands of a phase during the phase before it.
 // A chunk's inputs are its K, Q and V tile and its workspace record (Tb and
 // QKD fragments, decay vectors), all staged into one LDS buffer of a double
 // buffer, loaded two ticks ahead into one of two register sets of the loader
@@ -67,8 +68,8 @@ struct ScanLayout {
   static constexpr int REC_OFF = V16_OFF + CH * 32;
   static constexpr int BUF = REC_OFF + REC_BYTES;
   static constexpr int XT = 2 * BUF;                  // [16 col][64 t] fp16 X^T (swz)
-  static constexpr int UT = XT + VT * SPB;            // U^T fp16 (swz)
-  static constexpr int UH = UT + VT * SPB;            // (dec U)^T high, operand type (swz)
+  static constexpr int UT = XT + VT * SPB;            // [2] U^T fp16 (swz), by chunk parity
+  static constexpr int UH = UT + 2 * VT * SPB;        // (dec U)^T high, operand type (swz)
   static constexpr int UL = UH + VT * SPB;            // (dec U)^T low (swz)
   static constexpr int SH = UL + VT * SPB;            // [16 col][K] S^T high, operand type (swz)
   static constexpr int SL = SH + VT * KPB;            // S^T low (swz)
@@ -79,6 +80,7 @@ struct ScanLayout {
   __device__ static constexpr int v16(int b) { return b * BUF + V16_OFF; }
   __device__ static constexpr int rec(int b) { return b * BUF + REC_OFF; }
   __device__ static constexpr int ot(int b) { return OT + b * OT_BUF; }
+  __device__ static constexpr int ut(int b) { return UT + b * VT * SPB; }
 };
 
 // Staging of one chunk by the loader threads: 16-byte units numbered K, Q
@@ -100,6 +102,13 @@ struct ScanStage {
   static constexpr int UPT = (UNITS + NLT - 1) / NLT;
   static constexpr int SLOT_K = MAT_UNITS / NLT;   // slots [0, SLOT_K): K; [SLOT_K, SLOT_V): Q
   static constexpr int SLOT_V = KQ_UNITS / NLT;    // slot SLOT_V: V (first V_UNITS threads), then record
+  // Slots are staged in three groups, one per phase: [0, SLOT_P2) in phase 1,
+  // [SLOT_P2, SLOT_P3) in phase 2 (through the record's decay vectors, which
+  // phase 3 reads), [SLOT_P3, UPT) in phase 3 (Tb and QKD fragments, first
+  // read in the next tick).
+  static constexpr int SLOT_P3 = (KQ_UNITS + V_UNITS + (REC_TB - REC_SC) / 16 - 1) / NLT + 1;
+  static constexpr int SLOT_P2 = SLOT_P3 / 2 + 1;
+  static_assert(REC_SC == 0 && SLOT_P2 < SLOT_P3 && SLOT_P3 <= UPT, "record vectors lead the record");
   static_assert(MAT_UNITS % NLT == 0, "K and Q must fill whole slots");
   static_assert(V_UNITS % 64 == 0 && V_UNITS <= NLT, "V must end at a wave boundary of its slot");
 
@@ -111,7 +120,7 @@ struct ScanStage {
   uint32_t dst[UPT];  // LDS byte offset of the unit within a chunk buffer
   bool v_wave;        // this loader wave's slot SLOT_V unit is V (else record); wave-uniform
 
-  __device__ void init(const ChunkParams &p, int l) {
+  __device__ __forceinline__ void init(const ChunkParams &p, int l) {
     v_wave = __builtin_amdgcn_readfirstlane(l & ~63) < V_UNITS;
 #pragma unroll
     for (int i = 0; i < UPT; ++i) {
@@ -140,7 +149,7 @@ struct ScanStage {
 
   // Issue the loads of the chunk at tokens t0.. (`len` left, may be <= 0) of
   // value head h, columns v0.., and of its record `rec` (null past the end).
-  __device__ void load(const ChunkParams &p, Regs &r, long t0, long len, int hk, int h, int v0,
+  __device__ __forceinline__ void load(const ChunkParams &p, Regs &r, long t0, long len, int hk, int h, int v0,
                        const unsigned char *rec) const {
     const long rows = len < CH ? len : CH;
     const long qk_bytes = rows > 0 ? ((rows - 1) * p.Hk * K + K) * static_cast<long>(sizeof(TIn)) : 0;
@@ -157,24 +166,47 @@ struct ScanStage {
     }
   }
 
+  // Slot by slot: registers -> LDS chunk buffer at byte `base` (as store()),
+  // then the slot's register receives the same unit of the chunk at tokens
+  // t0.. (as load()), so a load issues as soon as its register is free.
+  template <int I0, int I1>
+  __device__ __forceinline__ void restage(const ChunkParams &p, unsigned char *lds, int base, Regs &r, int l, long t0, long len,
+                          int hk, int h, int v0, const unsigned char *rec) const {
+    const long rows = len < CH ? len : CH;
+    const long qk_bytes = rows > 0 ? ((rows - 1) * p.Hk * K + K) * static_cast<long>(sizeof(TIn)) : 0;
+    const long qk_base = (t0 * p.Hk + hk) * static_cast<long>(K);
+    const long v_bytes = rows > 0 ? ((rows - 1) * p.Hv * p.V + VT) * static_cast<long>(sizeof(TIn)) : 0;
+    const __amdgpu_buffer_rsrc_t rk = rsrc(static_cast<const TIn *>(p.k) + qk_base, qk_bytes);
+    const __amdgpu_buffer_rsrc_t rq = rsrc(static_cast<const TIn *>(p.q) + qk_base, qk_bytes);
+    const __amdgpu_buffer_rsrc_t rr = rsrc(rec, rec ? REC_BYTES : 0);
+    const __amdgpu_buffer_rsrc_t rvr =
+        v_wave ? rsrc(static_cast<const TIn *>(p.v) + (t0 * p.Hv + h) * static_cast<long>(p.V) + v0, v_bytes) : rr;
+#pragma unroll
+    for (int i = I0; i < I1; ++i) {
+      store_unit(lds + base, r, l, i);
+      r.u[i] = buf_load16(i < SLOT_K ? rk : i < SLOT_V ? rq : i == SLOT_V ? rvr : rr, src[i]);
+    }
+  }
+
+  __device__ __forceinline__ void store_unit(unsigned char *buf, const Regs &r, int l, int i) const {
+    if (l + NLT * i >= UNITS) return;
+    unsigned char *d = buf + dst[i];
+    if (EPU == 4 && (i < SLOT_V || (i == SLOT_V && v_wave))) {
+      const uint4 x = r.u[i];
+      *reinterpret_cast<half4_t *>(d) = to_half4(float4_t{__uint_as_float(x.x), __uint_as_float(x.y),
+                                                          __uint_as_float(x.z), __uint_as_float(x.w)});
+    } else {
+      *reinterpret_cast<uint4 *>(d) = r.u[i];
+    }
+  }
+
   // Registers -> LDS chunk buffer at byte `base`: K, Q, V as staged 16-bit
   // elements (fp32 rounded to fp16), the record unchanged. Units without a
   // destination (past the record) write a harmless zero-offset copy of
   // nothing: their slot is skipped by range.
-  __device__ void store(unsigned char *lds, int base, const Regs &r, int l) const {
+  __device__ __forceinline__ void store(unsigned char *lds, int base, const Regs &r, int l) const {
 #pragma unroll
-    for (int i = 0; i < UPT; ++i) {
-      unsigned char *d = lds + base + dst[i];
-      const bool convert = EPU == 4 && (i < SLOT_V || (i == SLOT_V && v_wave));
-      if (l + NLT * i >= UNITS) continue;
-      if (convert) {
-        const uint4 x = r.u[i];
-        *reinterpret_cast<half4_t *>(d) = to_half4(float4_t{__uint_as_float(x.x), __uint_as_float(x.y),
-                                                            __uint_as_float(x.z), __uint_as_float(x.w)});
-      } else {
-        *reinterpret_cast<uint4 *>(d) = r.u[i];
-      }
-    }
+    for (int i = 0; i < UPT; ++i) store_unit(lds + base, r, l, i);
   }
 };
 
@@ -233,7 +265,7 @@ struct ScanBlock {
   const ChunkParams &p;
   int tid, lane, c16, g4, wave, seq, h, hk, v0, lt;  // lt: loader thread index (loader waves)
   long bos, eos, nchunks, rbase;
-  float4_t sacc, qs;
+  float4_t sacc;
   Stage stage;
   typename Stage::Regs regs[2];
   uint32_t out_src, out_dst;  // loader thread's O unit: LDS offset in a tile, byte offset in a chunk
@@ -256,7 +288,6 @@ struct ScanBlock {
     nchunks = (eos - bos + CH - 1) / CH;
     rbase = rec_base(bos, seq);
     sacc = float4_t{0.f, 0.f, 0.f, 0.f};
-    qs = sacc;
     if (wave >= NCW) {
       stage.init(p, lt);
       constexpr int upr = VT * sizeof(TOut) / 16;  // units per output row
@@ -269,7 +300,7 @@ struct ScanBlock {
 
   // Per-lane parts of LDS addresses; everything else is a wave-uniform or
   // immediate offset. s4 is the swizzle of rows 16 m + c (bit 2 of the row).
-  __device__ void lane_offsets() {
+  __device__ __forceinline__ void lane_offsets() {
     const uint32_t s4 = ((c16 >> 2) & 1) << 4;
     kp_frag = c16 * L::KPB + ((16 * g4) ^ s4);                         // row c, 16 bytes at 16 g
     sp_frag = c16 * L::SPB + ((16 * g4) ^ s4);
@@ -283,15 +314,15 @@ struct ScanBlock {
   }
 
   template <typename T>
-  __device__ T ld(uint32_t off) const { return *reinterpret_cast<const T *>(lds + off); }
+  __device__ __forceinline__ T ld(uint32_t off) const { return *reinterpret_cast<const T *>(lds + off); }
   template <typename T>
-  __device__ void st(uint32_t off, T x) const { *reinterpret_cast<T *>(lds + off) = x; }
-  __device__ i16x4_t ld_tr(uint32_t off) const {
+  __device__ __forceinline__ void st(uint32_t off, T x) const { *reinterpret_cast<T *>(lds + off) = x; }
+  __device__ __forceinline__ i16x4_t ld_tr(uint32_t off) const {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t *)(lds + off));
   }
 
   // ------------------------------------------------------------ loader waves
-  __device__ void load_chunk(typename Stage::Regs &r, long n) const {
+  __device__ __forceinline__ void load_chunk(typename Stage::Regs &r, long n) const {
     const long t0 = bos + n * CH;
     const unsigned char *rec = n < nchunks ? p.ws + ((rbase + n) * p.Hv + h) * static_cast<long>(REC_BYTES) : nullptr;
     stage.load(p, r, t0, eos - t0, hk, h, v0, rec);
@@ -299,7 +330,7 @@ struct ScanBlock {
 
   // O tile of chunk n (LDS buffer n & 1) -> HBM, one 16-byte unit per loader
   // thread; n < 0 issues the same store with a zero-size resource.
-  __device__ void store_out(long n) const {
+  __device__ __forceinline__ void store_out(long n) const {
     const long t0 = bos + n * CH;
     const long len = eos - t0;
     const long rows = len < CH ? len : CH;
@@ -313,129 +344,205 @@ struct ScanBlock {
   // ------------------------------------------------------------ compute waves
   // Row float4 of a record vector (SC_GAM, SC_GSC, SC_DEC) for this lane's
   // accumulator rows 16 r + 4 g.. of the chunk in buffer b.
-  __device__ float4_t rec_rows(int b, int vec, int r) const {
+  __device__ __forceinline__ float4_t rec_rows(int b, int vec, int r) const {
     return ld<float4_t>(L::rec(b) + REC_SC + vec + (16 * r + 4 * g4) * 4);
   }
   // Tb (REC_TB) or QKD (REC_QKD) fragment (r, kk) of the chunk in buffer b.
-  __device__ half8_t rec_frag(int b, int mat, int r, int kk) const {
+  __device__ __forceinline__ half8_t rec_frag(int b, int mat, int r, int kk) const {
     return ld<half8_t>(L::rec(b) + mat + frag_index(r, kk) * FRAG_BYTES + lane * 16);
   }
 
-  // Phase 1: waves 0-3 X = V - gamma K S for token rows 16w.. (S as a
-  // high/low pair); waves 4-7 Q S (high part) for rows 16(w-4)..
-  __device__ void phase1(int b) {
-    const int r = wave & 3;
-    const bool chain = wave < 4;
-    const uint32_t mat = L::kq(b) + (chain ? 0 : L::KQ_MAT) + 16 * r * L::KPB + kp_frag;
-    O8 a[KS], shi[KS], slo[KS];
+  // Operands are read from LDS one phase before the phase that uses them, so
+  // that each phase waits only for what the previous phase produced. The two
+  // compute roles run separate loops (same barrier sequence) with their own
+  // registers: chain waves 0-3 (X, U for token rows 16r..) and output waves
+  // 4-7 (Q S, O for rows 16r..), r = wave & 3; every wave below NKT also
+  // updates its key tile of S.
+
+  // K^T fragments of key tile kt of the chunk in buffer b: contraction slot j
+  // of lane group g is token 32 ts + 8 g + j, the slot order of the dec U pair.
+  __device__ __forceinline__ void fetch_kt(int b, O8 (&kt)[2]) const {
+    const uint32_t kmat = L::kq(b) + 32 * wave;
 #pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
-      a[kk] = ld<O8>(mat + 64 * kk);
-      shi[kk] = ld<O8>(L::SH + kp_frag + 64 * kk);
-    }
-    float4_t acc = {0.f, 0.f, 0.f, 0.f};
-    if (chain) {
-#pragma unroll
-      for (int kk = 0; kk < KS; ++kk) slo[kk] = ld<O8>(L::SL + kp_frag + 64 * kk);
-      const float4_t vv = Op::bits_to_float(ld_tr(L::v16(b) + 16 * r * 32 + tr_v));
-      const float4_t gg = rec_rows(b, SC_GAM, r);
-      float4_t acl = acc;
-#pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        acc = mma(a[kk], shi[kk], acc);
-        acl = mma(a[kk], slo[kk], acl);
-      }
-      st(L::XT + sp_tile + 32 * r, to_half4(vv - gg * (acc + acl)));
-    } else {
-#pragma unroll
-      for (int kk = 0; kk < KS; ++kk) acc = mma(a[kk], shi[kk], acc);
-      qs = acc;
+    for (int ts = 0; ts < 2; ++ts) {
+      const i16x4_t lo4 = ld_tr(kmat + 32 * ts * L::KPB + tr_k0);
+      const i16x4_t hi4 = ld_tr(kmat + 32 * ts * L::KPB + tr_k1);
+      kt[ts] = __builtin_bit_cast(O8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
     }
   }
 
-  // Phase 2: waves 0-3 U = Tb X for token rows 16w.. (Tb rows 16w.. vanish
-  // past column 16w + 15, so row tiles 0, 1 need one contraction step and
-  // 2, 3 two).
-  __device__ void phase2(int b) {
-    const half8_t x0 = ld<half8_t>(L::XT + sp_frag);
-    float4_t u = mfma32(rec_frag(b, REC_TB, wave, 0), x0, float4_t{0.f, 0.f, 0.f, 0.f});
-    if (wave >= 2) u = mfma32(rec_frag(b, REC_TB, wave, 1), ld<half8_t>(L::XT + sp_frag + 64), u);
-    const uint32_t o = sp_tile + 32 * wave;
-    st(L::UT + o, to_half4(u));
-    const float4_t du = u * rec_rows(b, SC_DEC, wave);
-    const O4 hi = Op::from(du);
-    st(L::UH + o, hi);
-    st(L::UL + o, Op::from(du - Op::to(hi)));
+  // A fragments of rows 16r.. of K (mat 0) or Q (mat 1) of the chunk in buffer b.
+  __device__ __forceinline__ void fetch_rows(int b, int mat, O8 (&mf)[KS]) const {
+    const uint32_t base = L::kq(b) + mat * L::KQ_MAT + 16 * (wave & 3) * L::KPB + kp_frag;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) mf[kk] = ld<O8>(base + 64 * kk);
   }
 
-  // Phase 3: S key tile owners S <- gamma_63 S + K^T (dec U); waves 4-7
-  // O = scale gamma Q S + QKD U -> the O tile in LDS.
-  __device__ void phase3(int b) {
-    if (wave < NKT) {
-      const int kt = wave;
-      // K^T fragment of key tile kt, token step ts: contraction slot j of lane
-      // group g is token 32 ts + 8 g + j, the slot order of the dec U pair.
-      const uint32_t kmat = L::kq(b) + 32 * kt;
-      O8 ka[2], hb[2], lb[2];
+  // S <- gamma_63 S + K^T (dec U) for the wave's key tile (chunk in buffer b).
+  __device__ __forceinline__ void update_state(int b, const O8 (&kt)[2]) {
+    O8 hb[2], lb[2];
 #pragma unroll
-      for (int ts = 0; ts < 2; ++ts) {
-        const i16x4_t lo4 = ld_tr(kmat + 32 * ts * L::KPB + tr_k0);
-        const i16x4_t hi4 = ld_tr(kmat + 32 * ts * L::KPB + tr_k1);
-        ka[ts] = __builtin_bit_cast(O8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
-        hb[ts] = ld<O8>(L::UH + sp_frag + 64 * ts);
-        lb[ts] = ld<O8>(L::UL + sp_frag + 64 * ts);
-      }
-      float4_t acl = mma(ka[0], lb[0], float4_t{0.f, 0.f, 0.f, 0.f});
-      acl = mma(ka[1], lb[1], acl);
-      sacc *= ld<float>(L::rec(b) + REC_SC + SC_GAM + (CH - 1) * 4);
-      sacc = mma(ka[0], hb[0], sacc);
-      sacc = mma(ka[1], hb[1], sacc);
-      sacc += acl;
-      const O4 hi = Op::from(sacc);
-      st(L::SH + kp_tile + 32 * kt, hi);
-      st(L::SL + kp_tile + 32 * kt, Op::from(sacc - Op::to(hi)));
+    for (int ts = 0; ts < 2; ++ts) {
+      hb[ts] = ld<O8>(L::UH + sp_frag + 64 * ts);
+      lb[ts] = ld<O8>(L::UL + sp_frag + 64 * ts);
     }
-    if (wave >= 4) {
-      const int r = wave - 4;
-      float4_t o = qs * rec_rows(b, SC_GSC, r);
-      o = mfma32(rec_frag(b, REC_QKD, r, 0), ld<half8_t>(L::UT + sp_frag), o);
-      if (r >= 2) o = mfma32(rec_frag(b, REC_QKD, r, 1), ld<half8_t>(L::UT + sp_frag + 64), o);
-      // lane (g, c) holds O[16 r + 4 g + i][c]
-#pragma unroll
-      for (int i = 0; i < 4; ++i) st(L::ot(b) + ((16 * r + 4 * g4 + i) * VT + c16) * sizeof(TOut), out_elem<TOut>(o[i]));
-    }
+    float4_t acl = mma(kt[0], lb[0], float4_t{0.f, 0.f, 0.f, 0.f});
+    acl = mma(kt[1], lb[1], acl);
+    sacc *= ld<float>(L::rec(b) + REC_SC + SC_GAM + (CH - 1) * 4);
+    sacc = mma(kt[0], hb[0], sacc);
+    sacc = mma(kt[1], hb[1], sacc);
+    sacc += acl;
+    const O4 hi = Op::from(sacc);
+    st(L::SH + kp_tile + 32 * wave, hi);
+    st(L::SL + kp_tile + 32 * wave, Op::from(sacc - Op::to(hi)));
   }
 
-  // Tick n of a compute wave; chunk n is in LDS buffer n mod 2 = P.
-  template <int P>
-  __device__ void tick_compute() {
+  __device__ __forceinline__ void launder() {
     // Re-define the lane offsets opaquely each tick: addresses derived from
     // them are then formed where they are used instead of being hoisted out
     // of the loop, where they would hold many registers.
     asm volatile("" : "+v"(kp_frag), "+v"(sp_frag), "+v"(kp_tile), "+v"(sp_tile));
     asm volatile("" : "+v"(tr_v), "+v"(tr_k0), "+v"(tr_k1), "+v"(c16), "+v"(g4));
-    phase1(P);
+  }
+
+  // Chain waves. Phase 1: X = V - gamma K S (S as a high/low pair) -> X^T;
+  // Tb fragments and dec rows for phase 2. Phase 2: U = Tb X (Tb rows 16r..
+  // vanish past column 16r + 15: row tiles 0, 1 need one contraction step,
+  // 2, 3 two) -> U^T, (dec U)^T high/low; K^T for phase 3. Phase 3: the state
+  // update, then K rows, V rows and gamma rows of the next chunk.
+  template <int P>
+  __device__ __forceinline__ void tick_chain(O8 (&mf)[KS], float4_t &vv, float4_t &gg) {
+    launder();
+    const int b = P;
+    const int r = wave;
+    half8_t f0, f1;
+    float4_t dd;
+    O8 kt[2];
+    {
+      O8 shi[KS], slo[KS];
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        shi[kk] = ld<O8>(L::SH + kp_frag + 64 * kk);
+        slo[kk] = ld<O8>(L::SL + kp_frag + 64 * kk);
+      }
+      f0 = rec_frag(b, REC_TB, r, 0);
+      f1 = rec_frag(b, REC_TB, r, 1);  // row tiles 0, 1: unused
+      dd = rec_rows(b, SC_DEC, r);
+      float4_t acc = {0.f, 0.f, 0.f, 0.f}, acl = acc;
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        acc = mma(mf[kk], shi[kk], acc);
+        acl = mma(mf[kk], slo[kk], acl);
+      }
+      st(L::XT + sp_tile + 32 * r, to_half4(vv - gg * (acc + acl)));
+    }
     block_sync();
-    if (wave < 4) phase2(P);
+    {
+      const half8_t x0 = ld<half8_t>(L::XT + sp_frag);
+      const half8_t x1 = ld<half8_t>(L::XT + sp_frag + 64);
+      fetch_kt(b, kt);
+      float4_t u = mfma32(f0, x0, float4_t{0.f, 0.f, 0.f, 0.f});
+      if (r >= 2) u = mfma32(f1, x1, u);
+      const uint32_t o = sp_tile + 32 * r;
+      st(L::ut(b) + o, to_half4(u));
+      const float4_t du = u * dd;
+      const O4 hi = Op::from(du);
+      st(L::UH + o, hi);
+      st(L::UL + o, Op::from(du - Op::to(hi)));
+    }
     block_sync();
-    phase3(P);
+    {
+      O8 nmf[KS];
+      fetch_rows(b ^ 1, 0, nmf);
+      const float4_t nvv = Op::bits_to_float(ld_tr(L::v16(b ^ 1) + 16 * r * 32 + tr_v));
+      const float4_t ngg = rec_rows(b ^ 1, SC_GAM, r);
+      update_state(b, kt);
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) mf[kk] = nmf[kk];
+      vv = nvv;
+      gg = ngg;
+    }
+    block_sync();
+  }
+
+  // Output waves: O = scale gamma Q S + QKD U of the chunk of parity ob (its
+  // U^T is in U^T buffer ob) -> O tile ob; lane (g, c) holds
+  // O[16 r + 4 g + i][c].
+  __device__ __forceinline__ void out_tile(int ob, const float4_t &qs, const float4_t &gs, const half8_t &f0,
+                                           const half8_t &f1) {
+    const int r = wave & 3;
+    float4_t o = qs * gs;
+    o = mfma32(f0, ld<half8_t>(L::ut(ob) + sp_frag), o);
+    if (r >= 2) o = mfma32(f1, ld<half8_t>(L::ut(ob) + sp_frag + 64), o);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st(L::ot(ob) + ((16 * r + 4 * g4 + i) * VT + c16) * sizeof(TOut), out_elem<TOut>(o[i]));
+  }
+
+  // Output waves. Phase 1: Q S (high part) of chunk n. Phase 2: O of chunk
+  // n-1, then this chunk's QKD fragments and scale gamma rows (for its O in
+  // the next tick); K^T for phase 3. Phase 3: the state update (K = 128),
+  // then the Q rows of the next chunk.
+  template <int P>
+  __device__ __forceinline__ void tick_output(long n, O8 (&mf)[KS], float4_t &qs, float4_t &qs_prev,
+                                              float4_t &gs, half8_t &f0, half8_t &f1) {
+    launder();
+    const int b = P;
+    const int r = wave & 3;
+    O8 kt[2];
+    {
+      O8 shi[KS];
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) shi[kk] = ld<O8>(L::SH + kp_frag + 64 * kk);
+      float4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) acc = mma(mf[kk], shi[kk], acc);
+      qs_prev = qs;
+      qs = acc;
+    }
+    block_sync();
+    {
+      const half8_t n0 = rec_frag(b, REC_QKD, r, 0);
+      const half8_t n1 = rec_frag(b, REC_QKD, r, 1);  // row tiles 0, 1: unused
+      const float4_t ngs = rec_rows(b, SC_GSC, r);
+      if constexpr (NKT > 4) fetch_kt(b, kt);
+      if (n > 0) out_tile(b ^ 1, qs_prev, gs, f0, f1);
+      f0 = n0;
+      f1 = n1;
+      gs = ngs;
+    }
+    block_sync();
+    {
+      O8 nmf[KS];
+      fetch_rows(b ^ 1, 1, nmf);
+      if constexpr (NKT > 4) update_state(b, kt);
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) mf[kk] = nmf[kk];
+    }
     block_sync();
   }
 
   // Tick n of a loader wave: register set P (= n mod 2) holds chunk n+1 on
-  // entry, goes to LDS buffer 1 - P, and receives chunk n+3; then O of chunk
-  // n-1 goes out.
+  // entry; slot by slot it goes to LDS buffer 1 - P and receives chunk n+3:
+  // what phase 3 reads (K, Q, V, decay vectors) in phases 1 and 2, the Tb and
+  // QKD fragments in phase 3. In phase 3 the O tile of chunk n-1 (written in
+  // phase 2) also goes out.
   template <int P>
-  __device__ void tick_loader(long n) {
-    stage.store(lds, L::kq(P ^ 1), regs[P], lt);
-    load_chunk(regs[P], n + 3);
+  __device__ __forceinline__ void tick_loader(long n) {
+    const long m = n + 3;
+    const long t0 = bos + m * CH;
+    const unsigned char *rec = m < nchunks ? p.ws + ((rbase + m) * p.Hv + h) * static_cast<long>(REC_BYTES) : nullptr;
+    stage.template restage<0, Stage::SLOT_P2>(p, lds, L::kq(P ^ 1), regs[P], lt, t0, eos - t0, hk, h, v0, rec);
+    block_sync();
+    stage.template restage<Stage::SLOT_P2, Stage::SLOT_P3>(p, lds, L::kq(P ^ 1), regs[P], lt, t0, eos - t0, hk, h,
+                                                            v0, rec);
     block_sync();
     store_out(n - 1);
-    block_sync();
+    stage.template restage<Stage::SLOT_P3, Stage::UPT>(p, lds, L::kq(P ^ 1), regs[P], lt, t0, eos - t0, hk, h, v0,
+                                                        rec);
     block_sync();
   }
 
-  __device__ void run() {
+  __device__ __forceinline__ void run() {
     // Initial state: compute wave j owns key rows 16j..16j+15.
     const long state_base = (static_cast<long>(seq) * p.Hv + h) * K * p.V + v0 + c16;
     const int kt = wave;
@@ -465,16 +572,37 @@ struct ScanBlock {
         tick_loader<1>(n + 1);
       }
       if (n < nchunks) tick_loader<0>(n);
+      block_sync();  // the O tile of the last chunk is complete
       if (nchunks > 0) store_out(nchunks - 1);
       return;
     }
     block_sync();
-    long n = 0;
-    for (; n + 1 < nchunks; n += 2) {
-      tick_compute<0>();
-      tick_compute<1>();
+    if (wave < 4) {
+      O8 mf[KS];
+      fetch_rows(0, 0, mf);
+      float4_t vv = Op::bits_to_float(ld_tr(L::v16(0) + 16 * wave * 32 + tr_v));
+      float4_t gg = rec_rows(0, SC_GAM, wave);
+      long n = 0;
+      for (; n + 1 < nchunks; n += 2) {
+        tick_chain<0>(mf, vv, gg);
+        tick_chain<1>(mf, vv, gg);
+      }
+      if (n < nchunks) tick_chain<0>(mf, vv, gg);
+      block_sync();
+    } else {
+      O8 mf[KS];
+      fetch_rows(0, 1, mf);
+      float4_t qs = {0.f, 0.f, 0.f, 0.f}, qs_prev = qs, gs = qs;
+      half8_t f0 = {}, f1 = {};
+      long n = 0;
+      for (; n + 1 < nchunks; n += 2) {
+        tick_output<0>(n, mf, qs, qs_prev, gs, f0, f1);
+        tick_output<1>(n + 1, mf, qs, qs_prev, gs, f0, f1);
+      }
+      if (n < nchunks) tick_output<0>(n, mf, qs, qs_prev, gs, f0, f1);
+      if (nchunks > 0) out_tile(static_cast<int>((nchunks - 1) & 1), qs, gs, f0, f1);
+      block_sync();
     }
-    if (n < nchunks) tick_compute<0>();
     if (p.ht && owner) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) p.ht[state_base + static_cast<long>(16 * kt + 4 * g4 + i) * p.V] = sacc[i];
