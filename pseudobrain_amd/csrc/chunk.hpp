@@ -170,6 +170,31 @@ __device__ __forceinline__ void put_out<float>(__amdgpu_buffer_rsrc_t r, uint32_
   __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, x), r, off, 0, 0);
 }
 
+// DPP move of a float: lanes of disabled rows (row_mask) and, with
+// bound_ctrl, lanes whose source is outside the row, get 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp0(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, ROW_MASK, 0xf, true));
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave: row_shr 1, 2, 4, 8 scan
+// each row of 16 lanes; row_bcast 15 adds the last lane of rows 0, 2 to rows
+// 1, 3 and row_bcast 31 adds lane 31 to rows 2, 3 (gfx9-family DPP controls
+// 0x111..0x118, 0x142, 0x143).
+__device__ __forceinline__ float wave_prefix_sum(float x) {
+  x += dpp0<0x111, 0xf>(x);
+  x += dpp0<0x112, 0xf>(x);
+  x += dpp0<0x114, 0xf>(x);
+  x += dpp0<0x118, 0xf>(x);
+  x += dpp0<0x142, 0xa>(x);
+  x += dpp0<0x143, 0xc>(x);
+  return x;
+}
+
+__device__ __forceinline__ float lane_value(float x, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+}
+
 __device__ __forceinline__ float pick(float4_t v, int i) {
   return (i == 0) ? v[0] : (i == 1) ? v[1] : (i == 2) ? v[2] : v[3];
 }
@@ -274,14 +299,14 @@ struct ChunkInputs {
 
   // Registers -> LDS buffer `buf`: K and Q [t][key], V [t][col], and (scan
   // wave) the decay and beta tables of the chunk (below).
-  __device__ void store(unsigned char *lds, int buf, int tid, int lane, bool scan, float scale) const {
+  __device__ void store(unsigned char *lds, int buf, int tid, int lane, bool scan, float scale, int sc_off = 0) const {
 #pragma unroll
     for (int i = 0; i < UPT; ++i) put_unit(lds + LY::KQ + (2 * buf + mat_of(tid, i)) * LY::KQ_MAT + qk_lds[i], x[i]);
     if constexpr (WITH_V) {
       if (tid < V_UNITS) put_unit(lds + LY::V16 + buf * LY::V16_BUF + v_lds, vx);
     }
     if constexpr (WITH_SCAN) {
-      if (scan) scan_tables(reinterpret_cast<float *>(lds + LY::SC), lane, scale);
+      if (scan) scan_tables(reinterpret_cast<float *>(lds + LY::SC + sc_off), lane, scale);
     }
   }
 
@@ -294,15 +319,12 @@ struct ChunkInputs {
     const float b = bdt == PBGDN_F32    ? __uint_as_float(b32)
                     : bdt == PBGDN_BF16 ? __uint_as_float(static_cast<uint32_t>(b16) << 16)
                                         : static_cast<float>(__builtin_bit_cast(half_t, b16));
-    float x = g;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const float y = __shfl_up(x, off, 64);
-      if (lane >= off) x += y;
-    }
-    const float last = __shfl(x, 63, 64);
+    const float x = wave_prefix_sum(g);
+    const float c16 = lane_value(x, 16), c32 = lane_value(x, 32), c48 = lane_value(x, 48);
+    const float last = lane_value(x, 63);
     const int t4 = (lane & 15) * 4 + (lane >> 4);
-    const float u = __expf(x - __shfl(x, lane & ~15, 64));
+    const float row0 = lane < 16 ? lane_value(x, 0) : lane < 32 ? c16 : lane < 48 ? c32 : c48;
+    const float u = __expf(x - row0);
     sc[LY::CUM / 4 + lane] = x;
     sc[LY::GAM / 4 + lane] = __expf(x);
     sc[LY::DEC / 4 + lane] = __expf(last - x);
@@ -311,11 +333,9 @@ struct ChunkInputs {
     sc[LY::BET4 / 4 + t4] = b;
     sc[LY::BU4 / 4 + t4] = b * u;
     sc[LY::SU4 / 4 + t4] = scale * u;
-#pragma unroll
-    for (int r = 1; r < 4; ++r) {
-      const float cr = __shfl(x, 16 * r, 64);
-      sc[LY::W1 / 4 + (r - 1) * CH + lane] = (lane < 16 * r) ? __expf(cr - x) : 0.f;
-    }
+    sc[LY::W1 / 4 + lane] = (lane < 16) ? __expf(c16 - x) : 0.f;
+    sc[LY::W1 / 4 + CH + lane] = (lane < 32) ? __expf(c32 - x) : 0.f;
+    sc[LY::W1 / 4 + 2 * CH + lane] = (lane < 48) ? __expf(c48 - x) : 0.f;
   }
 };
 

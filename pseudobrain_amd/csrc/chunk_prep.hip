@@ -9,19 +9,23 @@
 //   QKD = scale (Q K^T o D), D inclusive        as 16x16x32 fp16 A fragments
 //   exp(c_t), scale exp(c_t), exp(c_63 - c_t)  fp32
 //
-// A persistent grid of 4-wave workgroups walks the (record, head) items; the
-// inputs of a workgroup's next item are loaded into registers while it works
-// on the current one. Item numbering keeps the value heads that share a key
-// head on one XCD, so a q/k chunk comes from HBM once per pair.
+// A persistent grid of 4-wave workgroups walks the items: a chunk record and
+// HPI value heads that share a key head (HPI = 2 when the value heads per key
+// head are even, else 1). The inputs of a workgroup's next item are loaded
+// into registers while it works on the current one, and items are numbered so
+// that neighbours share an XCD.
 //
 // Per item (barrier-separated stages):
-//   stage   K, Q -> LDS (bf16/fp16 kept, fp32 rounded to fp16); wave 3 scans g
-//           into the decay tables
-//   tiles   the 10 lower 16x16 tile pairs of A and QKD (bf16/fp16 16x16x32
-//           MFMA, fp32 accumulate), computed transposed so each lane writes 4
-//           consecutive elements of a row; off-diagonal tiles take the decay
-//           as u_t W_R[s] (two multiplies, no masks), diagonal tiles exp(c_t -
-//           c_s) with the triangular masks, in fp32 for the inverse
+//   stage   K, Q -> LDS (bf16/fp16 kept, fp32 rounded to fp16); waves 3, 2
+//           scan g of heads 0, 1 into their decay tables
+//   tiles   the 10 lower 16x16 tile pairs of K K^T and Q K^T (bf16/fp16
+//           16x16x32 MFMA, fp32 accumulate) once for the key head, kept in
+//           registers, formed transposed so each lane holds 4 consecutive
+//           elements of a row
+// then for each value head:
+//   decay   A = beta K K^T o D, QKD = scale Q K^T o D; off-diagonal tiles take
+//           the decay as u_t W_R[s] (two multiplies, no masks), diagonal tiles
+//           exp(c_t - c_s) with the triangular masks, in fp32 for the inverse
 //   diag    the 4 diagonal blocks of T as (I+M)(I+M^2)(I+M^4)(I+M^8), M = -A_ww
 //           strictly lower (nilpotent), on fp16 high/low MFMAs (~22-bit products)
 //   offdiag the off-diagonal blocks of T by block forward substitution
@@ -33,7 +37,6 @@ namespace pbgdn {
 namespace {
 
 constexpr int PNT = 256;          // threads per prep workgroup
-constexpr int PREP_SCAN_WAVE = 3; // wave that loads g, beta and scans them
 constexpr int PREP_WG_PER_CU = 2;
 constexpr int NUM_CU = 256;
 
@@ -47,10 +50,11 @@ struct PrepLayout {
   static constexpr int ATP = 4 * 16 + 16;               // fp32 16-column rows + pad
   static constexpr int KQ_MAT = CH * KPB;
   static constexpr int KQ = 0;                          // [K, Q][64 t][K] operand type (swz)
-  static constexpr int SC = KQ + 2 * KQ_MAT;            // [11][64] fp32 decay tables
+  static constexpr int SC = KQ + 2 * KQ_MAT;            // [2 heads][11][64] fp32 decay tables
+  static constexpr int SC_HEAD = 11 * CH * 4;
   static constexpr int CUM = 0, GAM = 256, DEC = 512, BET = 768, CUM4 = 1024, BET4 = 1280, BU4 = 1536,
                        SU4 = 1792, W1 = 2048;
-  static constexpr int AT = SC + 11 * CH * 4;           // [4 tiles][16][16] fp32 diagonal tiles of A
+  static constexpr int AT = SC + 2 * SC_HEAD;           // [4 tiles][16][16] fp32 diagonal tiles of A
   static constexpr int TB = AT + 4 * 16 * ATP;          // [64 t][64 s] fp16 Tb (swz)
   static constexpr int QKD = TB + CH * SPB;             // [64 t][64 s] fp16 (swz)
   static constexpr int A16 = QKD + CH * SPB;            // [64 t][64 s] fp16: off-diagonal A, diagonal D (swz)
@@ -69,8 +73,9 @@ struct PrepBlock {
 
   unsigned char *lds;
   const ChunkParams &p;
-  int tid, lane, c16, g4, wave, group_heads;
+  int tid, lane, c16, g4, wave, group_heads, hpi, hgroups, jscan;
   Inputs in;
+  float4_t rk[3], rq[3];  // raw K K^T and Q K^T of this wave's tile pairs
   uint32_t kp_frag, sp_frag, sp_tile, at_lane, tr_a;
 
   __device__ PrepBlock(unsigned char *l, const ChunkParams &prm) : lds(l), p(prm) {
@@ -80,6 +85,9 @@ struct PrepBlock {
     c16 = lane & 15;
     g4 = lane >> 4;
     group_heads = p.Hv / p.Hk;
+    hpi = (group_heads % 2 == 0) ? 2 : 1;
+    hgroups = p.Hv / hpi;
+    jscan = (3 - wave) < hpi ? 3 - wave : 0;  // head whose g this wave loads (waves 3, 2 scan)
     in.init(p, tid, lane);
     const uint32_t s4 = ((c16 >> 2) & 1) << 4;
     kp_frag = c16 * L::KPB + ((16 * g4) ^ s4);                         // row c, 16 bytes at 16 g
@@ -99,15 +107,16 @@ struct PrepBlock {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t *)(lds + off));
   }
 
-  // Item = (chunk record, value head) -> sequence, first token, tokens left.
+  // Item = (chunk record, group of hpi value heads) -> first head, sequence,
+  // first token, tokens left.
   // Returns false for a record that no sequence's chunk maps to. Everything
   // here is wave-uniform and kept in scalar registers (readfirstlane), so the
   // lookups are scalar loads that do not wait for outstanding vector memory
   // operations.
   __device__ bool locate(int item, int &h, long &rec, long &t0, long &len) const {
-    const int r32 = __builtin_amdgcn_readfirstlane(item / p.Hv);
+    const int r32 = __builtin_amdgcn_readfirstlane(item / hgroups);
     rec = r32;
-    h = __builtin_amdgcn_readfirstlane(item - r32 * p.Hv);
+    h = __builtin_amdgcn_readfirstlane((item - r32 * hgroups) * hpi);  // first value head of the item
     int lo = 0, hi = p.num_seqs - 1;  // largest s with rec_base(s) <= rec
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
@@ -131,67 +140,77 @@ struct PrepBlock {
     return items;
   }
 
-  // Tile (R, S), S <= R, of A = strict_lower(b_t K K^T o D) and of
-  // QKD = scale (Q K^T o D) (inclusive). The products are formed transposed
-  // (rows s from K_S, columns t from K_R and Q_R), so lane (g, c) holds row
-  // t = 16R + c, columns s = 16S + 4g..4g+3 and writes them at once. Off the
-  // diagonal, s < 16R <= t and exp(c_t - c_s) = u_t W_R[s], both factors <= 1
-  // (an underflow only drops a product that is itself below the fp32 range).
-  __device__ void tile_pair(int R, int S) {
+  // Raw products of tile pair (R, S), S <= R, formed transposed (rows s from
+  // K_S, columns t from K_R and Q_R): lane (g, c) holds row t = 16R + c,
+  // columns s = 16S + 4g..4g+3 of K K^T (ak) and Q K^T (aq).
+  __device__ void raw_pair(int R, int S, float4_t &ak, float4_t &aq) const {
     const uint32_t kmat = L::KQ + kp_frag;
     const uint32_t qmat = kmat + L::KQ_MAT;
-    const bool diag_tile = R == S;
     O8 kr[KS], qr[KS], ks[KS];
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
       kr[kk] = ld<O8>(kmat + 16 * R * L::KPB + 64 * kk);
       qr[kk] = ld<O8>(qmat + 16 * R * L::KPB + 64 * kk);
+      ks[kk] = ld<O8>(kmat + 16 * S * L::KPB + 64 * kk);
     }
-    if (diag_tile) {
-#pragma unroll
-      for (int kk = 0; kk < KS; ++kk) ks[kk] = kr[kk];
-    } else {
-#pragma unroll
-      for (int kk = 0; kk < KS; ++kk) ks[kk] = ld<O8>(kmat + 16 * S * L::KPB + 64 * kk);
-    }
-    const int s0 = 16 * S + 4 * g4;
-    float4_t acck = {0.f, 0.f, 0.f, 0.f}, accq = acck;
+    ak = float4_t{0.f, 0.f, 0.f, 0.f};
+    aq = ak;
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
-      acck = mma(ks[kk], kr[kk], acck);
-      accq = mma(ks[kk], qr[kk], accq);
-    }
-    const uint32_t qkd_out = L::QKD + 16 * R * L::SPB + 32 * S + sp_tile;
-    if (diag_tile) {
-      const int t = 16 * R + c16;
-      const float ct = pick(ld<float4_t>(L::SC + L::CUM4 + c16 * 16), R);
-      const float bt = pick(ld<float4_t>(L::SC + L::BET4 + c16 * 16), R);
-      const float4_t cs = ld<float4_t>(L::SC + L::CUM + s0 * 4);
-      float4_t av, qv;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float d = __expf(ct - cs[i]);
-        av[i] = (s0 + i < t) ? bt * acck[i] * d : 0.f;
-        qv[i] = (s0 + i <= t) ? p.scale * accq[i] * d : 0.f;
-      }
-      st(L::AT + 16 * R * L::ATP + at_lane, av);
-      st(qkd_out, to_half4(qv));
-    } else {
-      const float bu = pick(ld<float4_t>(L::SC + L::BU4 + c16 * 16), R);
-      const float su = pick(ld<float4_t>(L::SC + L::SU4 + c16 * 16), R);
-      const float4_t w = ld<float4_t>(L::SC + L::W1 + ((R - 1) * CH + s0) * 4);
-      st(L::A16 + 16 * R * L::SPB + 32 * S + sp_tile, to_half4(acck * bu * w));
-      st(qkd_out, to_half4(accq * su * w));
+      ak = mma(ks[kk], kr[kk], ak);
+      aq = mma(ks[kk], qr[kk], aq);
     }
   }
 
-  // Tile pairs i = wave, wave + 4, wave + 8 of the list (3,0) (3,1) (3,2)
-  // (3,3) (2,0) (2,1) (2,2) (1,0) (1,1) (0,0): 3, 3, 2, 2 per wave.
+  // Tile pair i of the list (3,0) (3,1) (3,2) (3,3) (2,0) (2,1) (2,2) (1,0)
+  // (1,1) (0,0); wave w takes i = w, w + 4, w + 8 (3, 3, 2, 2 pairs).
+  __device__ static int pair_r(int i) { return (i < 4) ? 3 : (i < 7) ? 2 : (i < 9) ? 1 : 0; }
+  __device__ static int pair_s(int i) { return i - ((i < 4) ? 0 : (i < 7) ? 4 : (i < 9) ? 7 : 9); }
+
   __device__ void tiles() {
-    for (int i = wave; i < 10; i += 4) {
-      const int R = (i < 4) ? 3 : (i < 7) ? 2 : (i < 9) ? 1 : 0;
-      const int S = i - ((i < 4) ? 0 : (i < 7) ? 4 : (i < 9) ? 7 : 9);
-      tile_pair(R, S);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int i = wave + 4 * j;
+      if (i < 10) raw_pair(pair_r(i), pair_s(i), rk[j], rq[j]);
+    }
+  }
+
+  // Decays of value head jh on the raw tile pairs: tile (R, S) of
+  // A = strict_lower(b_t K K^T o D) and QKD = scale (Q K^T o D) (inclusive).
+  // Off the diagonal, s < 16R <= t and exp(c_t - c_s) = u_t W_R[s], both
+  // factors <= 1 (an underflow only drops a product that is itself below the
+  // fp32 range). Diagonal tiles go to AT (fp32, for the inverse), off-diagonal
+  // A tiles to A16.
+  __device__ void decay(int jh) const {
+    const uint32_t sc = L::SC + jh * L::SC_HEAD;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int i = wave + 4 * j;
+      if (i >= 10) continue;
+      const int R = pair_r(i), S = pair_s(i);
+      const int s0 = 16 * S + 4 * g4;
+      const uint32_t qkd_out = L::QKD + 16 * R * L::SPB + 32 * S + sp_tile;
+      if (R == S) {
+        const int t = 16 * R + c16;
+        const float ct = pick(ld<float4_t>(sc + L::CUM4 + c16 * 16), R);
+        const float bt = pick(ld<float4_t>(sc + L::BET4 + c16 * 16), R);
+        const float4_t cs = ld<float4_t>(sc + L::CUM + s0 * 4);
+        float4_t av, qv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float d = __expf(ct - cs[e]);
+          av[e] = (s0 + e < t) ? bt * rk[j][e] * d : 0.f;
+          qv[e] = (s0 + e <= t) ? p.scale * rq[j][e] * d : 0.f;
+        }
+        st(L::AT + 16 * R * L::ATP + at_lane, av);
+        st(qkd_out, to_half4(qv));
+      } else {
+        const float bu = pick(ld<float4_t>(sc + L::BU4 + c16 * 16), R);
+        const float su = pick(ld<float4_t>(sc + L::SU4 + c16 * 16), R);
+        const float4_t w = ld<float4_t>(sc + L::W1 + ((R - 1) * CH + s0) * 4);
+        st(L::A16 + 16 * R * L::SPB + 32 * S + sp_tile, to_half4(rk[j] * bu * w));
+        st(qkd_out, to_half4(rq[j] * su * w));
+      }
     }
   }
 
@@ -219,11 +238,11 @@ struct PrepBlock {
   // in registers; tile(M) comes from tile(M^T) as MFMA(tile(M^T), tile(I)).
   // Y = D is built transposed: Y^T <- Y^T + P_k^T Y^T. D goes to A16 (fp16)
   // for the off-diagonal blocks, D diag(beta) to the diagonal block of Tb.
-  __device__ void diag() {
+  __device__ void diag(int jh) {
     const int w = wave;
     const float4_t z = {0.f, 0.f, 0.f, 0.f};
     const float4_t p1t = -ld<float4_t>(L::AT + 16 * w * L::ATP + at_lane);  // tile(M^T)
-    const float4_t bw = ld<float4_t>(L::SC + L::BET + (16 * w + 4 * g4) * 4);
+    const float4_t bw = ld<float4_t>(L::SC + jh * L::SC_HEAD + L::BET + (16 * w + 4 * g4) * 4);
     half4_t eye;
 #pragma unroll
     for (int j = 0; j < 4; ++j) eye[j] = static_cast<half_t>((4 * g4 + j == c16) ? 1.f : 0.f);
@@ -253,14 +272,14 @@ struct PrepBlock {
   // also formed transposed (MFMA(tile(Y), A op D_r) = tile((D_r Y)^T)) and
   // written as Tb rows T_rs diag(beta). Chains: T10 -> T20 -> T30; T21 -> T31;
   // T32.
-  __device__ void offdiag(int chain) {
+  __device__ void offdiag(int chain, int jh) {
     const float4_t z = {0.f, 0.f, 0.f, 0.f};
     auto aop = [&](int r, int s) { return ld<half4_t>(L::A16 + 16 * r * L::SPB + 32 * s + sp_tile); };
     auto dop = [&](int s) {  // tile(D_s) via a transposing read
       return __builtin_bit_cast(half4_t, ld_tr(L::A16 + 16 * s * L::SPB + 32 * s + tr_a));
     };
     auto put = [&](int r, int s, float4_t mt) {  // mt = tile((D_r Y_rs)^T) = -tile(T_rs^T)
-      const float4_t bs = ld<float4_t>(L::SC + L::BET + (16 * s + 4 * g4) * 4);
+      const float4_t bs = ld<float4_t>(L::SC + jh * L::SC_HEAD + L::BET + (16 * s + 4 * g4) * 4);
       st(L::TB + 16 * r * L::SPB + 32 * s + sp_tile, to_half4(-mt * bs));
     };
     if (chain == 0) {
@@ -291,7 +310,7 @@ struct PrepBlock {
 
   // Fragments f = wave, wave + 4, wave + 8 of Tb (f < 6) and QKD (f >= 6) and
   // one decay vector per wave (wave 3: c itself) -> the workspace record. rec < 0 issues the same stores with a zero-size resource.
-  __device__ void out(long rec, int h) const {
+  __device__ void out(long rec, int h, int jh) const {
     const __amdgpu_buffer_rsrc_t rr =
         rsrc(p.ws + (rec * p.Hv + h) * static_cast<long>(REC_BYTES), rec >= 0 ? REC_BYTES : 0);
 #pragma unroll
@@ -304,10 +323,11 @@ struct PrepBlock {
       const uint32_t dst = (f < NFRAG ? REC_TB : REC_QKD) + fi * FRAG_BYTES + lane * 16;
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, ld<half8_t>(src)), rr, dst, 0, 0);
     }
-    const float gam = ld<float>(L::SC + L::GAM + lane * 4);
+    const uint32_t sc = L::SC + jh * L::SC_HEAD;
+    const float gam = ld<float>(sc + L::GAM + lane * 4);
     const float val = wave == 0 ? gam
                       : wave == 1 ? p.scale * gam
-                      : ld<float>(L::SC + (wave == 2 ? L::DEC : L::CUM) + lane * 4);
+                      : ld<float>(sc + (wave == 2 ? L::DEC : L::CUM) + lane * 4);
     const uint32_t dst = REC_SC + 256 * wave + lane * 4;  // SC_GAM, SC_GSC, SC_DEC, c
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, val), rr, dst, 0, 0);
   }
@@ -328,23 +348,27 @@ struct PrepBlock {
     // Every wave issues the same memory operations on every path (loads of an
     // absent next item have zero length; the stores before the first item go
     // nowhere), so waits for the item's inputs never cover newer stores.
-    in.load(p, t0, len, h / group_heads, h, 0);
-    out(-1, 0);
+    in.load(p, t0, len, h / group_heads, h + jscan, 0);
+    out(-1, 0, 0);
     while (true) {
       int h_n = 0;
       long rec_n = 0, t0_n = 0, len_n = 0;
       const int next = next_valid(item + stride, stride, items, h_n, rec_n, t0_n, len_n);
       block_sync();  // the previous item's readers of K, Q, the tables and Tb/QKD are done
-      in.store(lds, 0, tid, lane, wave == PREP_SCAN_WAVE, p.scale);
-      in.load(p, t0_n, next < items ? len_n : 0, h_n / group_heads, h_n, 0);
+      in.store(lds, 0, tid, lane, wave >= 4 - hpi, p.scale, jscan * L::SC_HEAD);
+      in.load(p, t0_n, next < items ? len_n : 0, h_n / group_heads, h_n + jscan, 0);
       block_sync();
       tiles();
-      block_sync();
-      diag();
-      block_sync();
-      if (wave < 3) offdiag(wave);
-      block_sync();
-      out(rec, h);
+      for (int jh = 0; jh < hpi; ++jh) {
+        if (jh > 0) block_sync();  // out() of the previous head has read Tb, QKD
+        decay(jh);
+        block_sync();
+        diag(jh);
+        block_sync();
+        if (wave < 3) offdiag(wave, jh);
+        block_sync();
+        out(rec, h + jh, jh);
+      }
       if (next >= items) break;
       item = next;
       h = h_n;
@@ -376,7 +400,8 @@ int launch_prep(const ChunkParams &p, long records, hipStream_t stream) {
     }
     configured = true;
   }
-  const long items = records * p.Hv;
+  const int hpi = ((p.Hv / p.Hk) % 2 == 0) ? 2 : 1;  // value heads per item (PrepBlock::hpi)
+  const long items = records * (p.Hv / hpi);
   if (items > 0x3fffffffL) return PBGDN_ERR_UNSUPPORTED;  // item numbers are 32-bit
   long grid = static_cast<long>(NUM_CU) * PREP_WG_PER_CU;
   if (items < grid) grid = (items + 7) / 8 * 8;
