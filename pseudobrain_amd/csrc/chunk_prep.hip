@@ -37,12 +37,18 @@ namespace pbgdn {
 namespace {
 
 constexpr int PNT = 256;          // threads per prep workgroup
-constexpr int PREP_WG_PER_CU = 2;
 constexpr int NUM_CU = 256;
+// Resident workgroups per CU: three when the registers allow it (16-bit
+// inputs); fp32 inputs hold more registers and keep two.
+template <typename TIn>
+constexpr int prep_wg_per_cu() { return sizeof(TIn) == 4 ? 2 : 3; }
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
-// LDS layout (byte offsets); (swz) as in chunk.hpp.
+// LDS layout (byte offsets); (swz) as in chunk.hpp. K and Q are read only by
+// the tiles stage, and Tb, QKD, A16, AT live from the decay stage to the
+// record stores, so the two groups share bytes (a barrier separates the two
+// uses); the decay tables follow the larger of the two.
 template <int K>
 struct PrepLayout {
   static constexpr int KPB = 2 * K + 32;
@@ -50,15 +56,16 @@ struct PrepLayout {
   static constexpr int ATP = 4 * 16 + 16;               // fp32 16-column rows + pad
   static constexpr int KQ_MAT = CH * KPB;
   static constexpr int KQ = 0;                          // [K, Q][64 t][K] operand type (swz)
-  static constexpr int SC = KQ + 2 * KQ_MAT;            // [2 heads][11][64] fp32 decay tables
+  static constexpr int TB = 0;                          // [64 t][64 s] fp16 Tb (swz), over K
+  static constexpr int QKD = TB + CH * SPB;             // [64 t][64 s] fp16 (swz)
+  static constexpr int A16 = QKD + CH * SPB;            // [64 t][64 s] fp16: off-diagonal A, diagonal D (swz)
+  static constexpr int AT = A16 + CH * SPB;             // [4 tiles][16][16] fp32 diagonal tiles of A
+  static constexpr int AT_END = AT + 4 * 16 * ATP;
+  static constexpr int SC = AT_END > 2 * KQ_MAT ? AT_END : 2 * KQ_MAT;  // [2 heads][11][64] fp32 decay tables
   static constexpr int SC_HEAD = 11 * CH * 4;
   static constexpr int CUM = 0, GAM = 256, DEC = 512, BET = 768, CUM4 = 1024, BET4 = 1280, BU4 = 1536,
                        SU4 = 1792, W1 = 2048;
-  static constexpr int AT = SC + 2 * SC_HEAD;           // [4 tiles][16][16] fp32 diagonal tiles of A
-  static constexpr int TB = AT + 4 * 16 * ATP;          // [64 t][64 s] fp16 Tb (swz)
-  static constexpr int QKD = TB + CH * SPB;             // [64 t][64 s] fp16 (swz)
-  static constexpr int A16 = QKD + CH * SPB;            // [64 t][64 s] fp16: off-diagonal A, diagonal D (swz)
-  static constexpr int BYTES = A16 + CH * SPB;
+  static constexpr int BYTES = SC + 2 * SC_HEAD;
 };
 
 template <int K, typename TIn>
@@ -69,7 +76,7 @@ struct PrepBlock {
   using Inputs = ChunkInputs<K, TIn, PNT, L, false, true>;
   static constexpr int KS = K / 32;  // contraction steps over keys
   static_assert(K == 64 || K == 128, "K must be 64 or 128");
-  static_assert(L::BYTES * PREP_WG_PER_CU <= 160 * 1024, "prep LDS");
+  static_assert(L::BYTES * prep_wg_per_cu<TIn>() <= 160 * 1024, "prep LDS");
 
   unsigned char *lds;
   const ChunkParams &p;
@@ -332,9 +339,16 @@ struct PrepBlock {
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, val), rr, dst, 0, 0);
   }
 
+  // Blocks (0, 1) and (2, 3) of Tb and QKD lie above the diagonal inside the
+  // fragments the record holds and must read as zero; the staging of K and Q
+  // overwrote them, so each wave clears one of the four per item.
+  __device__ void clear_upper() const {
+    const int r = (wave & 1) ? 2 : 0;
+    const uint32_t base = (wave & 2) ? L::QKD : L::TB;
+    st(base + 16 * r * L::SPB + 32 * (r + 1) + sp_tile, half4_t{});
+  }
+
   __device__ void run(int items) {
-    // Blocks of Tb and QKD above the diagonal stay zero (never written).
-    for (int i = tid; i < 2 * CH * L::SPB / 4; i += PNT) reinterpret_cast<uint32_t *>(lds + L::TB)[i] = 0u;
     const int stride = gridDim.x;
     const int nx = stride / 8;
     // Workgroups are dispatched round-robin over the 8 XCDs: number the items
@@ -359,6 +373,8 @@ struct PrepBlock {
       in.load(p, t0_n, next < items ? len_n : 0, h_n / group_heads, h_n + jscan, 0);
       block_sync();
       tiles();
+      block_sync();  // K, Q are read; Tb, QKD, A16, AT take their bytes
+      clear_upper();
       for (int jh = 0; jh < hpi; ++jh) {
         if (jh > 0) block_sync();  // out() of the previous head has read Tb, QKD
         decay(jh);
@@ -380,7 +396,7 @@ struct PrepBlock {
 };
 
 template <int K, typename TIn>
-__global__ __launch_bounds__(PNT) void prep_kernel(ChunkParams p, int items) {
+__global__ __launch_bounds__(PNT, prep_wg_per_cu<TIn>()) void prep_kernel(ChunkParams p, int items) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   PrepBlock<K, TIn> blk(smem_raw, p);
   blk.run(items);
@@ -403,7 +419,7 @@ int launch_prep(const ChunkParams &p, long records, hipStream_t stream) {
   const int hpi = ((p.Hv / p.Hk) % 2 == 0) ? 2 : 1;  // value heads per item (PrepBlock::hpi)
   const long items = records * (p.Hv / hpi);
   if (items > 0x3fffffffL) return PBGDN_ERR_UNSUPPORTED;  // item numbers are 32-bit
-  long grid = static_cast<long>(NUM_CU) * PREP_WG_PER_CU;
+  long grid = static_cast<long>(NUM_CU) * prep_wg_per_cu<TIn>();
   if (items < grid) grid = (items + 7) / 8 * 8;
   hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(PNT), smem, stream, p, static_cast<int>(items));
   return hipGetLastError() == hipSuccess ? PBGDN_OK : PBGDN_ERR_LAUNCH;
