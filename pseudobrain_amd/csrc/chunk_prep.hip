@@ -348,17 +348,40 @@ struct PrepBlock {
     st(base + 16 * r * L::SPB + 32 * (r + 1) + sp_tile, half4_t{});
   }
 
+  // Items of this workgroup: the grid is resident from the start with
+  // tiers = grid / NUM_CU workgroups per CU, and the k-th workgroup dispatched
+  // to a CU (block index / NUM_CU) runs slower than the ones before it (the
+  // oldest waves win issue arbitration): at T = 32K the second and third go
+  // at about 0.85 and 0.74 of the first one's pace. The items are split into one
+  // contiguous segment per tier in proportion to these paces; within a
+  // segment the tier's workgroups take every `stride`-th item from `first`.
+  __device__ void share(int items, int &first, int &stride, int &end) const {
+    constexpr int PACE[3] = {100, 85, 74};
+    const int grid = gridDim.x;
+    const int tiers = (grid % NUM_CU == 0 && grid / NUM_CU <= 3) ? grid / NUM_CU : 1;
+    stride = grid / tiers;
+    const int tier = static_cast<int>(blockIdx.x) / stride;
+    const int j = static_cast<int>(blockIdx.x) % stride;
+    int total = 0, before = 0;
+    for (int t = 0; t < tiers; ++t) {
+      total += PACE[t];
+      if (t < tier) before += PACE[t];
+    }
+    const int begin = static_cast<int>(static_cast<long>(items) * before / total);
+    end = static_cast<int>(static_cast<long>(items) * (before + PACE[tier]) / total);
+    // Workgroups are dispatched round-robin over the 8 XCDs: number the
+    // items so that consecutive ones (the value heads of one key head) share
+    // an XCD.
+    first = begin + ((stride % 8 == 0) ? (j & 7) * (stride / 8) + (j >> 3) : j);
+  }
+
   __device__ void run(int items) {
-    const int stride = gridDim.x;
-    const int nx = stride / 8;
-    // Workgroups are dispatched round-robin over the 8 XCDs: number the items
-    // so that consecutive ones (the value heads of one key head) share an XCD.
-    const int first = (stride % 8 == 0) ? static_cast<int>(blockIdx.x & 7) * nx + static_cast<int>(blockIdx.x >> 3)
-                                        : static_cast<int>(blockIdx.x);
+    int first, stride, end;
+    share(items, first, stride, end);
     int h;
     long rec, t0, len;
-    int item = next_valid(first, stride, items, h, rec, t0, len);
-    if (item >= items) return;
+    int item = next_valid(first, stride, end, h, rec, t0, len);
+    if (item >= end) return;
     // Every wave issues the same memory operations on every path (loads of an
     // absent next item have zero length; the stores before the first item go
     // nowhere), so waits for the item's inputs never cover newer stores.
@@ -367,10 +390,10 @@ struct PrepBlock {
     while (true) {
       int h_n = 0;
       long rec_n = 0, t0_n = 0, len_n = 0;
-      const int next = next_valid(item + stride, stride, items, h_n, rec_n, t0_n, len_n);
+      const int next = next_valid(item + stride, stride, end, h_n, rec_n, t0_n, len_n);
       block_sync();  // the previous item's readers of K, Q, the tables and Tb/QKD are done
       in.store(lds, 0, tid, lane, wave >= 4 - hpi, p.scale, jscan * L::SC_HEAD);
-      in.load(p, t0_n, next < items ? len_n : 0, h_n / group_heads, h_n + jscan, 0);
+      in.load(p, t0_n, next < end ? len_n : 0, h_n / group_heads, h_n + jscan, 0);
       block_sync();
       tiles();
       block_sync();  // K, Q are read; Tb, QKD, A16, AT take their bytes
@@ -385,7 +408,7 @@ struct PrepBlock {
         block_sync();
         out(rec, h + jh, jh);
       }
-      if (next >= items) break;
+      if (next >= end) break;
       item = next;
       h = h_n;
       rec = rec_n;
