@@ -12,6 +12,13 @@
  *   pbgdn_recurrent_fwd  per-token recurrence (decode steps, T <= SEQUENTIAL_MAX);
  *                        replaces delta_rule_sequential (gated_deltanet.py:93-107).
  *
+ * Two more carry the layer-side work on either side of the recurrence:
+ *
+ *   pbgdn_prologue_fwd   short convolution + SiLU, q/k L2 norm, decay/beta
+ *                        gates (GatedDeltaNetLayer.forward, gated_deltanet.py:415-429,
+ *                        short_convolution :314-338, l2_normalize :59-70);
+ *   pbgdn_epilogue_fwd   per-head RMSNorm x o_norm x SiLU(gate) (:439-441).
+ *
  * Conventions (all entry points):
  *   - every pointer is device memory owned by the caller; nothing is allocated
  *     (scratch memory comes in as a caller-provided workspace);
@@ -38,7 +45,7 @@
 extern "C" {
 #endif
 
-#define PBGDN_ABI_VERSION 2
+#define PBGDN_ABI_VERSION 3
 
 /* element types */
 #define PBGDN_F32 0
@@ -134,6 +141,62 @@ int pbgdn_recurrent_fwd(const void *q, const void *k, const void *v,
                         int num_states, void *o, int out_dtype, int B, int T,
                         int Hk, int Hv, int K, int V, float scale,
                         void *stream);
+
+/*
+ * Layer prologue: from the input projection of a GatedDeltaNetLayer to the
+ * operator's inputs, in one pass (gated_deltanet.py:415-429):
+ *   y = SiLU(causal depthwise conv of tail ++ qkv)            (:314-338)
+ *   q, k = l2_normalize(y[q], y[k]) per key head, mode 'max' or 'hf' (:59-70)
+ *   v = y[v]
+ *   g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b)   (:425-427)
+ * The GQA repeat (:422-424) is not materialised: the operator maps heads.
+ *
+ *   qkv         [B, T, 2 Hk K + Hv V] rows of qkv_stride elements, in_dtype
+ *               (the [q | k | v] columns of the projection)
+ *   decay       [B, T, 2 Hv] rows of decay_stride elements, in_dtype
+ *               (the [a | b] columns of the projection)
+ *   tail        [B, conv-1, 2 Hk K + Hv V] tail_dtype: the last conv-1 inputs
+ *               before qkv (NULL when conv <= 1); cast to in_dtype before the
+ *               convolution, as the reference does
+ *   tail_out    same shape: the last conv-1 inputs of tail ++ qkv; must not
+ *               be `tail` (NULL when conv <= 1)
+ *   conv_weight [2 Hk K + Hv V, conv] float32, tap conv-1 on the current input
+ *               (NULL when conv == 0: SiLU only)
+ *   a_log, dt_bias [Hv] float32
+ *   q, k        [B, T, Hk, K] out_dtype      v [B, T, Hv, V] out_dtype
+ *   g, beta     [B, T, Hv] float32
+ *   l2_mode     0 'max' (x / max(|x|, 1e-6)), 1 'hf' (x rsqrt(|x|^2 + 1e-6))
+ *
+ * Supported: K in {64, 128}; V a multiple of 8; conv in 0..4. qkv, q, k, v,
+ * tail and tail_out 16-byte aligned; qkv_stride a multiple of 8.
+ */
+int pbgdn_prologue_fwd(const void *qkv, long qkv_stride, const void *decay,
+                       long decay_stride, int in_dtype, const void *tail,
+                       void *tail_out, int tail_dtype, const float *conv_weight,
+                       int conv, const float *a_log, const float *dt_bias,
+                       void *q, void *k, void *v, int out_dtype, float *g,
+                       float *beta, int B, int T, int Hk, int Hv, int K, int V,
+                       int l2_mode, void *stream);
+
+/*
+ * Layer epilogue (gated_deltanet.py:439-441), one pass:
+ *   out = o rsqrt(mean_V(o^2) + eps) o_norm SiLU(gate)   per (token, value head)
+ *
+ *   o           [B, T, Hv, V] o_dtype (the operator's output)
+ *   gate        [B, T, Hv V] rows of gate_stride elements, gate_dtype (the
+ *               output-gate columns of the projection)
+ *   o_norm      [V] float32
+ *   eps         the per-head RMSNorm epsilon (the reference's norm_eps, 1e-5)
+ *   out         [B, T, Hv V] out_dtype (the reference's hs before the out
+ *               projection, in the hidden dtype)
+ *
+ * Supported: V in {64, 128}. o, gate, out 16-byte aligned; gate_stride a
+ * multiple of 8.
+ */
+int pbgdn_epilogue_fwd(const void *o, int o_dtype, const void *gate,
+                       long gate_stride, int gate_dtype, const float *o_norm,
+                       float eps, void *out, int out_dtype, int B, int T,
+                       int Hv, int V, void *stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,146 @@
+"""The layer-side work around the recurrence on MI355X: the fused prologue and
+epilogue of GatedDeltaNetLayer.forward (pseudobrain/gated_deltanet.py:403-441).
+
+    z = proj(norm(x))                                 [q | k | v | gate | a | b]
+    layer_prologue(z, tail, ...)  ->  q, k, v, g, beta, gate, new tail   (:415-427)
+        one kernel (pbgdn_prologue_fwd): causal depthwise convolution over
+        tail ++ [q | k | v] then SiLU (short_convolution, :314-338), q/k L2
+        normalisation per key head (l2_normalize, :59-70), the gates
+        g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b)
+    o, S = gated_delta_rule(q, k, v, g, beta, K ** -0.5, S, "hip")    (:433-438)
+    layer_epilogue(o, gate, o_norm, eps)  ->  hs                      (:439-441)
+        one kernel (pbgdn_epilogue_fwd): per-head RMSNorm x o_norm x SiLU(gate)
+
+q and k come out [B,T,Hk,K] without the GQA repeat (:422-424): the operator
+maps value head h to key head h // (Hv // Hk) itself. Both kernels run on the
+GPU only; a missing library or a CPU tensor raises.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+NORM_EPS = 1e-5           # gated_deltanet.py:72
+L2_MODES = ("max", "hf")  # gated_deltanet.py:57
+PROLOGUE_KEY_DIMS = (64, 128)
+EPILOGUE_VALUE_DIMS = (64, 128)
+MAX_CONV = 4
+
+
+def _rows(x: torch.Tensor, name: str) -> int:
+    """Row stride (elements per token) of a [B,T,C] tensor or column slice of one."""
+    if x.ndim != 3 or x.stride(-1) != 1 or x.stride(0) != x.shape[1] * x.stride(1):
+        raise ValueError(f"{name} must be a [B,T,C] tensor with unit column stride and dense rows "
+                         "(a column slice of a contiguous projection is fine)")
+    return x.stride(1)
+
+
+def layer_prologue(z: torch.Tensor, tail: torch.Tensor | None, conv_weight: torch.Tensor | None,
+                   A_log: torch.Tensor, dt_bias: torch.Tensor, heads: int, key_dim: int, value_heads: int,
+                   value_dim: int, l2norm: str = "max", *, out_dtype: torch.dtype | None = None):
+    """GatedDeltaNetLayer.forward from the projection to the operator's inputs
+    (gated_deltanet.py:415-427) in one kernel.
+
+    z [B,T,2*heads*key_dim + 2*value_heads*value_dim + 2*value_heads], split as
+    the reference splits it (qkv, gate, decay); tail [B,conv-1,channels] (the
+    last conv-1 inputs of q|k|v; any float dtype, kept); conv_weight
+    [channels, conv] or None (SiLU only); A_log, dt_bias [value_heads].
+
+    Returns (q [B,T,heads,key_dim], k, v [B,T,value_heads,value_dim] in
+    out_dtype (default z's dtype, the operator's matmul precision), g, beta
+    [B,T,value_heads] float32, gate (the [B,T,value_heads*value_dim] view of z
+    the epilogue takes), new tail [B,conv-1,channels] in the tail's dtype)."""
+    if l2norm not in L2_MODES:
+        raise ValueError(f"l2 normalization mode must be one of {L2_MODES}")
+    if heads < 1 or value_heads % heads:
+        raise ValueError("gated deltanet value heads must be a multiple of the key heads")
+    if key_dim not in PROLOGUE_KEY_DIMS or value_dim % 8:
+        raise ValueError(f"layer_prologue supports key widths {PROLOGUE_KEY_DIMS} and value widths "
+                         "that are multiples of 8")
+    channels = 2 * heads * key_dim + value_heads * value_dim
+    vwidth = value_heads * value_dim
+    if z.ndim != 3 or z.shape[-1] != channels + vwidth + 2 * value_heads:
+        raise ValueError(f"z must be [B,T,{channels + vwidth + 2 * value_heads}] "
+                         "([q | k | v | gate | a | b])")
+    if z.stride(-1) != 1 or z.stride(0) != z.shape[1] * z.stride(1):
+        z = z.contiguous()  # the kernel addresses token rows of one stride across the batch
+    qkv, gate, decay = z.split((channels, vwidth, 2 * value_heads), dim=-1)
+    batch, length, _ = z.shape
+    dev = z.device
+    if dev.type != "cuda":
+        raise RuntimeError(f"pbgdn kernels run on ROCm devices only (got a tensor on '{dev}'); "
+                           "this package has no CPU path")
+    conv = 0 if conv_weight is None else conv_weight.shape[1]
+    if conv_weight is not None:
+        if conv_weight.shape != (channels, conv) or not 1 <= conv <= MAX_CONV:
+            raise ValueError(f"conv_weight must be [{channels}, conv] with 1 <= conv <= {MAX_CONV}")
+        conv_weight = conv_weight.to(device=dev, dtype=torch.float32).contiguous()
+    tail_rows = max(conv - 1, 0)
+    new_tail = tail
+    if tail_rows:
+        if tail is None or tail.shape != (batch, tail_rows, channels):
+            raise ValueError(f"tail must be [B, conv-1, channels] = {(batch, tail_rows, channels)}")
+        tail = tail.contiguous()
+        new_tail = torch.empty_like(tail)
+    out_dtype = z.dtype if out_dtype is None else out_dtype
+    codes = _lib.DTYPE_CODES
+    if z.dtype not in codes or out_dtype not in codes or (tail_rows and tail.dtype not in codes):
+        raise ValueError("z, the tail and out_dtype must be float32, bfloat16 or float16")
+    q = torch.empty(batch, length, heads, key_dim, dtype=out_dtype, device=dev)
+    k = torch.empty_like(q)
+    v = torch.empty(batch, length, value_heads, value_dim, dtype=out_dtype, device=dev)
+    g = torch.empty(batch, length, value_heads, dtype=torch.float32, device=dev)
+    beta = torch.empty_like(g)
+    a_log = A_log.to(device=dev, dtype=torch.float32).contiguous()
+    dtb = dt_bias.to(device=dev, dtype=torch.float32).contiguous()
+    if a_log.shape != (value_heads,) or dtb.shape != (value_heads,):
+        raise ValueError(f"A_log and dt_bias must be [{value_heads}]")
+    if _rows(qkv, "z") % 8 or qkv.data_ptr() % 16:  # the kernel reads 16-byte row pieces
+        qkv = qkv.contiguous()
+    status = _lib.lib().pbgdn_prologue_fwd(
+        _lib.ptr(qkv), _rows(qkv, "z"), _lib.ptr(decay), _rows(decay, "z"), codes[z.dtype],
+        _lib.ptr(tail) if tail_rows else None, _lib.ptr(new_tail) if tail_rows else None,
+        codes[tail.dtype] if tail_rows else _lib.F32, _lib.ptr(conv_weight), conv, _lib.ptr(a_log),
+        _lib.ptr(dtb), _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), codes[out_dtype], _lib.ptr(g), _lib.ptr(beta),
+        batch, length, heads, value_heads, key_dim, value_dim, L2_MODES.index(l2norm), _lib.stream_handle(dev))
+    _lib.check(status, "pbgdn_prologue_fwd")
+    return q, k, v, g, beta, gate, new_tail
+
+
+def layer_epilogue(o: torch.Tensor, gate: torch.Tensor, o_norm: torch.Tensor, eps: float = NORM_EPS, *,
+                   out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """hs = o rsqrt(mean(o^2) + eps) o_norm SiLU(gate) per (token, value head),
+    reshaped to [B,T,Hv*V] in out_dtype (the reference's hidden dtype), as
+    gated_deltanet.py:439-441 computes it, in one kernel. o [B,T,Hv,V] (the
+    operator's output, any float dtype); gate [B,T,Hv*V] (the projection's
+    gate columns, e.g. the view layer_prologue returns); o_norm [V]."""
+    if o.ndim != 4:
+        raise ValueError("o must be [B,T,Hv,V]")
+    batch, length, hv, dv = o.shape
+    if dv not in EPILOGUE_VALUE_DIMS:
+        raise ValueError(f"layer_epilogue supports value widths {EPILOGUE_VALUE_DIMS}")
+    if gate.shape != (batch, length, hv * dv):
+        raise ValueError(f"gate must be [B,T,Hv*V] = {(batch, length, hv * dv)}")
+    if not eps >= 0:
+        raise ValueError("eps must be >= 0")
+    dev = o.device
+    if dev.type != "cuda":
+        raise RuntimeError(f"pbgdn kernels run on ROCm devices only (got a tensor on '{dev}'); "
+                           "this package has no CPU path")
+    codes = _lib.DTYPE_CODES
+    if o.dtype not in codes or gate.dtype not in codes or out_dtype not in codes:
+        raise ValueError("o, gate and out_dtype must be float32, bfloat16 or float16")
+    o = o.contiguous()
+    norm = o_norm.to(device=dev, dtype=torch.float32).contiguous()
+    if norm.shape != (dv,):
+        raise ValueError(f"o_norm must be [{dv}]")
+    out = torch.empty(batch, length, hv * dv, dtype=out_dtype, device=dev)
+    if (gate.stride(-1) != 1 or gate.stride(0) != gate.shape[1] * gate.stride(1) or gate.stride(1) % 8
+            or gate.data_ptr() % 16):  # one row stride across the batch, 16-byte row pieces
+        gate = gate.contiguous()
+    status = _lib.lib().pbgdn_epilogue_fwd(
+        _lib.ptr(o), codes[o.dtype], _lib.ptr(gate), _rows(gate, "gate"), codes[gate.dtype], _lib.ptr(norm),
+        float(eps), _lib.ptr(out), codes[out_dtype], batch, length, hv, dv, _lib.stream_handle(dev))
+    _lib.check(status, "pbgdn_epilogue_fwd")
+    return out

@@ -28,7 +28,9 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version_and_status_strings():
-    assert _lib.lib().pbgdn_abi_version() == _lib.ABI_VERSION == 2
+    assert _lib.lib().pbgdn_abi_version() == _lib.ABI_VERSION == 3
+    header = open(HEADER).read()
+    assert re.search(r"#define PBGDN_ABI_VERSION (\d+)", header).group(1) == str(_lib.ABI_VERSION)
     assert _lib.status_string(0) == "ok"
     for code in (1, 2, 3, 99):
         assert _lib.status_string(code)
@@ -110,3 +112,65 @@ def test_chunk_workspace_size():
     assert lib.pbgdn_chunk_workspace_size(1, 0, 4, 1) == 2 * 4 * rec
     assert lib.pbgdn_chunk_workspace_size(-1, 10, 4, 1) == 0
     assert lib.pbgdn_chunk_workspace_size(1, 10, 0, 1) == 0
+
+
+CH = 2 * 16 * 128 + 32 * 128  # q, k, v channels of the Qwen3-Next layer
+
+
+def prologue_call(**over):
+    args = dict(qkv=FAKE, qkv_stride=CH + 4096 + 64, decay=FAKE, decay_stride=CH + 4096 + 64, in_dtype=1,
+                tail=FAKE, tail_out=FAKE + 4096, tail_dtype=0, w=FAKE, conv=4, a_log=FAKE, dt_bias=FAKE,
+                q=FAKE, k=FAKE, v=FAKE, out_dtype=1, g=FAKE, beta=FAKE, B=1, T=64, Hk=16, Hv=32, K=128,
+                V=128, l2=0, stream=None)
+    args.update(over)
+    return _lib.lib().pbgdn_prologue_fwd(*args.values())
+
+
+def epilogue_call(**over):
+    args = dict(o=FAKE, o_dtype=1, gate=FAKE, gate_stride=4096, gate_dtype=1, o_norm=FAKE, eps=1e-5,
+                out=FAKE, out_dtype=1, B=1, T=64, Hv=32, V=128, stream=None)
+    args.update(over)
+    return _lib.lib().pbgdn_epilogue_fwd(*args.values())
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(in_dtype=3), _lib.ERR_INVALID_ARGUMENT),
+    (dict(tail_dtype=-1), _lib.ERR_INVALID_ARGUMENT),
+    (dict(l2=2), _lib.ERR_INVALID_ARGUMENT),
+    (dict(Hv=24), _lib.ERR_INVALID_ARGUMENT),           # not a multiple of Hk
+    (dict(conv=-1), _lib.ERR_INVALID_ARGUMENT),
+    (dict(qkv_stride=CH - 8), _lib.ERR_INVALID_ARGUMENT),  # rows shorter than q, k, v
+    (dict(qkv_stride=CH + 4), _lib.ERR_INVALID_ARGUMENT),  # not a multiple of 8
+    (dict(decay_stride=63), _lib.ERR_INVALID_ARGUMENT),
+    (dict(tail_out=FAKE), _lib.ERR_INVALID_ARGUMENT),       # in place: the tail would race
+    (dict(tail=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(w=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(qkv=FAKE + 8), _lib.ERR_INVALID_ARGUMENT),        # 16-byte alignment
+    (dict(g=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(K=96), _lib.ERR_UNSUPPORTED),
+    (dict(V=100), _lib.ERR_UNSUPPORTED),
+    (dict(conv=5), _lib.ERR_UNSUPPORTED),
+])
+def test_prologue_fwd_rejects(over, code):
+    assert prologue_call(**over) == code
+
+
+def test_prologue_and_epilogue_empty_are_ok():
+    assert prologue_call(B=0) == _lib.OK
+    assert prologue_call(T=0) == _lib.OK
+    assert epilogue_call(T=0) == _lib.OK
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(o_dtype=4), _lib.ERR_INVALID_ARGUMENT),
+    (dict(out_dtype=-2), _lib.ERR_INVALID_ARGUMENT),
+    (dict(eps=-1.0), _lib.ERR_INVALID_ARGUMENT),
+    (dict(eps=float("nan")), _lib.ERR_INVALID_ARGUMENT),
+    (dict(gate_stride=4000), _lib.ERR_INVALID_ARGUMENT),  # shorter than Hv * V
+    (dict(gate=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(out=FAKE + 4), _lib.ERR_INVALID_ARGUMENT),
+    (dict(V=96), _lib.ERR_UNSUPPORTED),
+    (dict(V=256), _lib.ERR_UNSUPPORTED),
+])
+def test_epilogue_fwd_rejects(over, code):
+    assert epilogue_call(**over) == code
