@@ -1,7 +1,7 @@
 """Benchmark of the Gated DeltaNet operator on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
-                    [--no-b256] [--copy-probe]
+                    [--no-b256] [--no-layer] [--copy-probe]
 
 Prints ONE JSON line. The headline workload is the Qwen3-Next-shaped prefill
 (B=1, T=32768, Hk=16 -> Hv=32, K=V=128, bf16 q/k/v, fp32 state, chunk 64):
@@ -10,7 +10,9 @@ a step is one chunk-kernel call over those inputs, resident in HBM, writing o
 The same line carries the decode step (64 sequences x 1 token, state
 [64,32,128,128] fp32 updated in place, 1000 chained steps) in µs/step and as a
 fraction of HBM bandwidth, an ungraded 256-sequence decode (state larger than
-the 256 MB Infinity Cache), the roofline of the prefill kernel measured with
+the 256 MB Infinity Cache), the fused layer prologue and epilogue kernels at
+the same T and head shape with their HBM rooflines, the roofline of the
+prefill kernel measured with
 HIP events on the stream it runs on, and the CPU baseline: the numpy oracle
 (oracle/gdn.py) on a bounded sample of the same prefill, run first, before the
 GPU is touched, as one single-threaded process per core over the heads.
@@ -188,6 +190,55 @@ def bench_decode(batch, steps, warmup=10):
     }
 
 
+def layer_inputs(length):
+    """Synthetic layer inputs at the Qwen3-Next layer shape (Hk=16, Hv=32,
+    K=V=128, conv 4): a bf16 projection z [1, T, q|k|v|gate|a|b], fp32 tail,
+    conv weight, A_log, dt_bias, o_norm, and a bf16 operator output o."""
+    import torch
+    gen = torch.Generator().manual_seed(0)
+    hk, hv, dk, dv, conv = 16, 32, 128, 128, 4
+    channels = 2 * hk * dk + hv * dv
+    z = torch.randn(1, length, channels + hv * dv + 2 * hv, generator=gen).to(torch.bfloat16).cuda()
+    tail = torch.randn(1, conv - 1, channels, generator=gen).cuda()
+    weight = ((torch.rand(channels, conv, generator=gen) * 2 - 1) / 2).cuda()
+    a_log = torch.empty(hv).uniform_(0, 16, generator=gen).log().cuda()
+    dt_bias = (torch.randn(hv, generator=gen) - 4).cuda()
+    o = (torch.randn(1, length, hv, dv, generator=gen) * 0.1).to(torch.bfloat16).cuda()
+    o_norm = torch.ones(dv).cuda()
+    return dict(hk=hk, hv=hv, dk=dk, dv=dv, conv=conv, channels=channels, z=z, tail=tail, weight=weight,
+                a_log=a_log, dt_bias=dt_bias, o=o, o_norm=o_norm)
+
+
+def bench_layer(length, steps, warmup=3):
+    """The fused prologue and epilogue kernels over T tokens of the layer shape:
+    HBM-bound; algorithmic bytes = what each must read and write once."""
+    import torch
+    from pseudobrain_amd.layer import layer_epilogue, layer_prologue
+    x = layer_inputs(length)
+    hk, hv, dk, dv, ch = x["hk"], x["hv"], x["dk"], x["dv"], x["channels"]
+
+    def pro():
+        layer_prologue(x["z"], x["tail"], x["weight"], x["a_log"], x["dt_bias"], hk, dk, hv, dv)
+
+    gate = x["z"][..., ch:ch + hv * dv]
+
+    def epi():
+        layer_epilogue(x["o"], gate, x["o_norm"], out_dtype=torch.float32)
+
+    out = {}
+    # prologue: q|k|v bf16 in and out, a|b bf16 in, g, beta fp32 out, the tail fp32 in and out
+    pro_bytes = length * (ch * 2 * 2 + 2 * hv * 2 + 2 * hv * 4) + 2 * (x["conv"] - 1) * ch * 4
+    # epilogue: o bf16 and gate bf16 in, hs fp32 out
+    epi_bytes = length * hv * dv * (2 + 2 + 4)
+    for name, fn, nbytes in (("layer_prologue", pro, pro_bytes), ("layer_epilogue", epi, epi_bytes)):
+        sec, ksec = timed_steps(fn, steps, warmup)
+        gbs = nbytes / ksec / 1e9
+        out[name] = {"T": length, "us_per_call": sec * 1e6, "kernel_us": ksec * 1e6, "bytes_per_call": nbytes,
+                     "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                  "frac": gbs / HBM_PEAK_GBS}}
+    return out
+
+
 def copy_probe(reps=5):
     """A plain device copy of COPY_PROBE_BYTES (torch's copy kernel): the
     reference point that scales the FETCH_SIZE/WRITE_SIZE counters, and a
@@ -216,6 +267,7 @@ def main(argv=None):
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-b256", action="store_true", help="skip the ungraded 256-sequence decode")
     ap.add_argument("--copy-probe", action="store_true", help="also time a plain 256 MiB device copy")
+    ap.add_argument("--no-layer", action="store_true", help="skip the layer prologue/epilogue kernels")
     args = ap.parse_args(argv)
     world = int(os.environ.get("WORLD_SIZE", args.gpus))
     if args.gpus != 1 or world != 1:
@@ -265,6 +317,8 @@ def main(argv=None):
                                                "traffic": measured_traffic("recurrent_b64")})
         if not args.no_b256:
             result["decode_b256_ungraded"] = bench_decode(256, 200)
+    if not args.no_layer:
+        result.update(bench_layer(shape.length, 20))
     if args.copy_probe:
         result["copy_probe"] = copy_probe()
     print(json.dumps(result), flush=True)
