@@ -10,7 +10,9 @@
  *                        (gated_deltanet.py:280-285), and computes the same
  *                        recurrence as delta_rule_chunked (gated_deltanet.py:110-165).
  *   pbgdn_recurrent_fwd  per-token recurrence (decode steps, T <= SEQUENTIAL_MAX);
- *                        replaces delta_rule_sequential (gated_deltanet.py:93-107).
+ *                        replaces delta_rule_sequential (gated_deltanet.py:93-107);
+ *                        pbgdn_recurrent_verify_fwd is its speculative-verify
+ *                        form (the state after every token kept in a slot).
  *
  * Two more carry the layer-side work on either side of the recurrence:
  *
@@ -141,6 +143,35 @@ int pbgdn_recurrent_fwd(const void *q, const void *k, const void *v,
                         int num_states, void *o, int out_dtype, int B, int T,
                         int Hk, int Hv, int K, int V, float scale,
                         void *stream);
+
+/*
+ * Speculative verify: the recurrent steps of pbgdn_recurrent_fwd over the T
+ * tokens of each sequence (the accepted token and T-1 draft tokens), writing
+ * the state after every token to its own slot, so that the state after the
+ * last accepted token can be kept (vLLM keeps conv-1+num_spec rows of the
+ * conv state and a slot per draft token of the recurrent state,
+ * serving/pb27_vllm/pb27_vllm/universal_models.py:147-165).
+ * No reference counterpart: the reference's serving path delegates it to vLLM.
+ *
+ *   state_in         [S, Hv, K, V] float32 states read
+ *   states           [S, Hv, K, V] float32 states written (may equal state_in)
+ *   state_idx        [B] int32 slot of each sequence's starting state, or
+ *                    NULL for slot b; a slot outside [0, S) gives zero output
+ *                    and writes nothing
+ *   token_state_idx  [B, T] int32 slot that receives the state after token t
+ *                    of sequence b; a slot outside [0, S) is skipped. The
+ *                    starting states are read whole before anything is
+ *                    written; the slots a call writes must be distinct and
+ *                    must not be another sequence's starting slot
+ *   q, k, v, g, beta, o, scale: as pbgdn_recurrent_fwd
+ */
+int pbgdn_recurrent_verify_fwd(const void *q, const void *k, const void *v,
+                               int in_dtype, const float *g, const void *beta,
+                               int beta_dtype, const float *state_in,
+                               float *states, const int32_t *state_idx,
+                               const int32_t *token_state_idx, int num_states,
+                               void *o, int out_dtype, int B, int T, int Hk,
+                               int Hv, int K, int V, float scale, void *stream);
 
 /*
  * Layer prologue: from the input projection of a GatedDeltaNetLayer to the

@@ -30,6 +30,8 @@ SIGNATURES = {
     "pbgdn_chunk_workspace_size": ([_i, _i, _i, _i], ctypes.c_size_t),
     "pbgdn_recurrent_fwd": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _i,
                              _i, _i, _i, _i, _i, _i, _f, _vp], _i),
+    "pbgdn_recurrent_verify_fwd": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _i, _vp, _i,
+                                    _i, _i, _i, _i, _i, _i, _f, _vp], _i),
     "pbgdn_prologue_fwd": ([_vp, _l, _vp, _l, _i, _vp, _vp, _i, _vp, _i, _vp, _vp,
                             _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp], _i),
     "pbgdn_epilogue_fwd": ([_vp, _i, _vp, _l, _i, _vp, _f, _vp, _i, _i, _i, _i, _i, _vp], _i),

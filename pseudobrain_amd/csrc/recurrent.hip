@@ -10,6 +10,9 @@
 // sweep over the registers (wavefront shuffles, then 4 partials per column
 // through LDS), and then the update and o = a S^T q + u (k.q) need no second
 // sweep. The kernel is HBM-bound: K*V*8 bytes of state traffic per head.
+// In verify mode (speculative decoding) the state after every token is also
+// written, to a slot per token, so that the state after the last accepted
+// draft token can be kept.
 #include "common.hpp"
 
 namespace pbgdn {
@@ -23,6 +26,7 @@ struct RecurrentParams {
   const float *state_in;
   float *state_out;
   const int32_t *state_idx;
+  const int32_t *token_state_idx;  // [B, T] slot of the state after each token, or NULL
   int num_states;
   void *o;
   int out_dtype;
@@ -136,12 +140,24 @@ __global__ __launch_bounds__(256) void recurrent_kernel(RecurrentParams p) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) store_elem(p.o, o_base + c, p.out_dtype, out[c]);
     }
+    if (p.token_state_idx) {  // verify mode: the state after this token goes to its own slot
+      const long ts = p.token_state_idx[tok];
+      if (ts >= 0 && ts < p.num_states) {
+        float *dst = p.state_out + (ts * p.Hv + h) * static_cast<long>(K) * V;
+#pragma unroll
+        for (int j = 0; j < RPT; ++j) {
+          *reinterpret_cast<float4_t *>(dst + static_cast<long>(rg + RG * j) * V + 4 * cg) = s[j];
+        }
+      }
+    }
     __syncthreads();  // sk, sq and the partials are rewritten by the next token
   }
 
+  if (!p.token_state_idx) {
 #pragma unroll
-  for (int j = 0; j < RPT; ++j) {
-    *reinterpret_cast<float4_t *>(sout + static_cast<long>(rg + RG * j) * V + 4 * cg) = s[j];
+    for (int j = 0; j < RPT; ++j) {
+      *reinterpret_cast<float4_t *>(sout + static_cast<long>(rg + RG * j) * V + 4 * cg) = s[j];
+    }
   }
 }
 
@@ -199,6 +215,29 @@ extern "C" int pbgdn_recurrent_fwd(const void *q, const void *k, const void *v, 
   if (T > 0 && (!q || !k || !v || !g || !beta || !o)) return PBGDN_ERR_INVALID_ARGUMENT;
   if (B > 65535) return PBGDN_ERR_UNSUPPORTED;
   pbgdn::RecurrentParams p{q, k, v, in_dtype, g, beta, beta_dtype, state_in, state_out,
-                           state_idx, num_states, o, out_dtype, T, Hk, Hv, scale};
+                           state_idx, nullptr, num_states, o, out_dtype, T, Hk, Hv, scale};
+  return pbgdn::recurrent_fwd(p, B, K, V, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int pbgdn_recurrent_verify_fwd(const void *q, const void *k, const void *v, int in_dtype,
+                                          const float *g, const void *beta, int beta_dtype,
+                                          const float *state_in, float *states,
+                                          const int32_t *state_idx, const int32_t *token_state_idx,
+                                          int num_states, void *o, int out_dtype, int B, int T, int Hk,
+                                          int Hv, int K, int V, float scale, void *stream) {
+  if (B < 0 || T < 0 || Hk <= 0 || Hv <= 0 || K <= 0 || V <= 0 || Hv % Hk != 0) {
+    return PBGDN_ERR_INVALID_ARGUMENT;
+  }
+  if (!valid_dtype(in_dtype) || !valid_dtype(out_dtype) ||
+      !(beta_dtype == PBGDN_F32 || beta_dtype == in_dtype)) {
+    return PBGDN_ERR_INVALID_ARGUMENT;
+  }
+  if (B == 0 || T == 0) return PBGDN_OK;
+  if (!state_in || !states || !token_state_idx || num_states < 0) return PBGDN_ERR_INVALID_ARGUMENT;
+  if (!state_idx && num_states < B) return PBGDN_ERR_INVALID_ARGUMENT;
+  if (!q || !k || !v || !g || !beta || !o) return PBGDN_ERR_INVALID_ARGUMENT;
+  if (B > 65535) return PBGDN_ERR_UNSUPPORTED;
+  pbgdn::RecurrentParams p{q, k, v, in_dtype, g, beta, beta_dtype, state_in, states,
+                           state_idx, token_state_idx, num_states, o, out_dtype, T, Hk, Hv, scale};
   return pbgdn::recurrent_fwd(p, B, K, V, static_cast<hipStream_t>(stream));
 }

@@ -126,11 +126,18 @@ def chunk_fwd(q, k, v, g, beta, scale: float, h0=None, cu_seqlens=None, *,
 
 
 def recurrent_fwd(q, k, v, g, beta, scale: float, state_in, state_out=None, state_idx=None, *,
-                  out_dtype: torch.dtype = torch.float32, out: torch.Tensor | None = None):
+                  out_dtype: torch.dtype = torch.float32, out: torch.Tensor | None = None,
+                  token_state_idx: torch.Tensor | None = None):
     """Launch pbgdn_recurrent_fwd: all T tokens through the per-step recurrence.
     state_out may be state_in (in place) or None (a new tensor). state_idx [B]
     int32 maps sequences to state slots (distinct; a slot outside the state
-    tensor, e.g. -1, is skipped and its o is zero). Returns (o, state_out)."""
+    tensor, e.g. -1, is skipped and its o is zero). Returns (o, state_out).
+
+    token_state_idx [B,T] int32 selects the speculative-verify form
+    (pbgdn_recurrent_verify_fwd): sequence b starts from slot state_idx[b] and
+    the state after its token t is written to slot token_state_idx[b, t] of
+    state_out (skipped when outside the state tensor); nothing else is
+    written."""
     batch, length, hk, hv, dk, dv = _shapes(q, k, v, g, beta)
     dev = _require_device(q, k, v, g, beta, state_in, state_out, state_idx)
     if dk not in RECURRENT_HEAD_DIMS or dv not in RECURRENT_HEAD_DIMS:
@@ -153,6 +160,17 @@ def recurrent_fwd(q, k, v, g, beta, scale: float, state_in, state_out=None, stat
     if out is None:
         out = torch.empty(batch, length, hv, dv, dtype=out_dtype, device=dev)
     codes = _lib.DTYPE_CODES
+    if token_state_idx is not None:
+        if token_state_idx.shape != (batch, length):
+            raise ValueError("token_state_idx must be [B,T]")
+        token_state_idx = token_state_idx.to(torch.int32).contiguous()
+        status = _lib.lib().pbgdn_recurrent_verify_fwd(
+            _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), codes[q.dtype], _lib.ptr(g), _lib.ptr(beta),
+            codes[beta.dtype], _lib.ptr(state_in), _lib.ptr(state_out), _lib.ptr(state_idx),
+            _lib.ptr(token_state_idx), state_in.shape[0], _lib.ptr(out), codes[out.dtype], batch, length, hk,
+            hv, dk, dv, float(scale), _lib.stream_handle(dev))
+        _lib.check(status, "pbgdn_recurrent_verify_fwd")
+        return out, state_out
     status = _lib.lib().pbgdn_recurrent_fwd(
         _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), codes[q.dtype], _lib.ptr(g), _lib.ptr(beta),
         codes[beta.dtype], _lib.ptr(state_in), _lib.ptr(state_out), _lib.ptr(state_idx),

@@ -174,3 +174,29 @@ def test_prologue_and_epilogue_empty_are_ok():
 ])
 def test_epilogue_fwd_rejects(over, code):
     assert epilogue_call(**over) == code
+
+
+def verify_call(**over):
+    args = dict(q=FAKE, k=FAKE, v=FAKE, in_dtype=1, g=FAKE, beta=FAKE, beta_dtype=0, sin=FAKE,
+                states=FAKE, idx=None, tidx=FAKE, nstates=8, o=FAKE, out_dtype=1, B=2, T=4, Hk=16, Hv=32,
+                K=128, V=128, scale=0.1, stream=None)
+    args.update(over)
+    return _lib.lib().pbgdn_recurrent_verify_fwd(*args.values())
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(tidx=None), _lib.ERR_INVALID_ARGUMENT),        # the per-token slot table is required
+    (dict(states=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(nstates=1), _lib.ERR_INVALID_ARGUMENT),        # without state_idx, slot b must exist
+    (dict(beta_dtype=2), _lib.ERR_INVALID_ARGUMENT),
+    (dict(Hv=20), _lib.ERR_INVALID_ARGUMENT),
+    (dict(K=48), _lib.ERR_UNSUPPORTED),
+    (dict(B=70000, nstates=70000), _lib.ERR_UNSUPPORTED),
+])
+def test_recurrent_verify_fwd_rejects(over, code):
+    assert verify_call(**over) == code
+
+
+def test_recurrent_verify_fwd_empty_is_ok():
+    assert verify_call(B=0) == _lib.OK
+    assert verify_call(T=0) == _lib.OK

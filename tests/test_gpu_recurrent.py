@@ -75,3 +75,42 @@ def test_already_repeated_heads_and_bf16_beta():
     o, s = gd.delta_rule_sequential(*to_dev(q, k, v, g, beta), SCALE, h0.to(DEV))
     torch.cuda.synchronize()
     assert_parity("Hk == Hv, bf16 beta", o, o_ref, s, s_ref, o_tol=1e-4, s_tol=1e-4)
+
+
+def test_speculative_verify_keeps_the_state_after_every_token():
+    """Verify mode: 6 sequences x 4 tokens (one accepted + 3 drafts) from
+    pooled starting slots; the state after token t lands in its own slot and
+    equals the oracle's state after the first t+1 tokens; o matches the
+    sequential oracle; slots not named are untouched, a -1 token slot is
+    skipped, and a -1 starting slot gives zero output and writes nothing."""
+    batch, length, hk, hv, dk, dv = 6, 4, 16, 32, 128, 128
+    q, k, v, g, beta, _ = generate(batch, length, hk, hv, dk, dv, torch.bfloat16, 0.0, seed=21)
+    pool = torch.randn(40, hv, dk, dv, generator=torch.Generator().manual_seed(22)) * 0.02
+    start = torch.tensor([3, 11, 0, 39, -1, 7], dtype=torch.int32)
+    slots = torch.arange(12, 12 + batch * length, dtype=torch.int32).view(batch, length)
+    slots[1, 2] = -1  # a draft position whose state is not kept
+    dq, dk_, dv_, dg, db, dpool, dstart, dslots = to_dev(q, k, v, g, beta, pool.clone(), start, slots)
+    o, states = gd.recurrent_fwd(dq, dk_, dv_, dg, db, SCALE, dpool, dpool, dstart,
+                                 out_dtype=torch.bfloat16, token_state_idx=dslots)
+    torch.cuda.synchronize()
+    states = states.cpu()
+    live = [b for b in range(batch) if start[b] >= 0]
+    h0 = pool[start[live].long()]
+    o_ref, _ = oracle(q[live], k[live], v[live], g[live], beta[live], SCALE, h0, "sequential")
+    for t in range(length):
+        _, s_t = oracle(q[live, :t + 1], k[live, :t + 1], v[live, :t + 1], g[live, :t + 1],
+                        beta[live, :t + 1], SCALE, h0, "sequential")
+        for i, b in enumerate(live):
+            if slots[b, t] >= 0:
+                assert_parity(f"verify b={b} t={t}", o[b:b + 1, t:t + 1], o_ref[i:i + 1, t:t + 1],
+                              states[slots[b, t]][None], s_t[i:i + 1])
+    named = set(slots[slots >= 0].tolist()) | set(start[start >= 0].tolist())
+    assert torch.equal(states[[s for s in range(40) if s not in named]], pool[[s for s in range(40) if s not in named]])
+    assert torch.equal(states[start[start >= 0].long()], pool[start[start >= 0].long()])  # starting slots are only read
+    assert torch.equal(states[slots[4].long()], pool[slots[4].long()])  # the -1 start writes nothing
+    assert not o[4].float().abs().any()
+    # the last kept state equals the plain recurrent call's final state, bit for bit
+    _, final = gd.recurrent_fwd(dq, dk_, dv_, dg, db, SCALE, dpool.clone(), None, dstart, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    for b in live:
+        assert torch.equal(states[slots[b, -1]], final.cpu()[start[b]])
