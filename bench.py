@@ -1,7 +1,7 @@
 """Benchmark of the Gated DeltaNet operator on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
-                    [--no-b256] [--no-layer] [--copy-probe]
+                    [--no-b256] [--no-layer] [--no-long] [--copy-probe]
 
 Prints ONE JSON line. The headline workload is the Qwen3-Next-shaped prefill
 (B=1, T=32768, Hk=16 -> Hv=32, K=V=128, bf16 q/k/v, fp32 state, chunk 64):
@@ -11,8 +11,9 @@ The same line carries the decode step (64 sequences x 1 token, state
 [64,32,128,128] fp32 updated in place, 1000 chained steps) in µs/step and as a
 fraction of HBM bandwidth, an ungraded 256-sequence decode (state larger than
 the 256 MB Infinity Cache), the fused layer prologue and epilogue kernels at
-the same T and head shape with their HBM rooflines, the roofline of the
-prefill kernel measured with
+the same T and head shape with their HBM rooflines, the varlen (8 packed
+sequences, 262,144 tokens) and streamed (1,048,576 tokens in 16 segments)
+prefill workloads, the roofline of the prefill kernel measured with
 HIP events on the stream it runs on, and the CPU baseline: the numpy oracle
 (oracle/gdn.py) on a bounded sample of the same prefill, run first, before the
 GPU is touched, as one single-threaded process per core over the heads.
@@ -190,6 +191,48 @@ def bench_decode(batch, steps, warmup=10):
     }
 
 
+def bench_long(steps=5, warmup=1):
+    """The varlen (8 packed sequences, 262,144 tokens, per-sequence states) and
+    streamed (1,048,576 tokens as 16 segments of 65,536 with the state carried)
+    prefill workloads: Mtok/s and the MFMA roofline of each whole pass."""
+    import torch
+    from pseudobrain_amd import gated_deltanet as gd
+    from pseudobrain_amd.workloads import STREAM_SEGMENT, WORKLOADS, generate, varlen_workload
+    out = {}
+    s = WORKLOADS["varlen_8seq"]
+    q, k, v, g, beta, h0, cu = varlen_workload(seed=0, device="cuda")
+    scale = s.dk ** -0.5
+    o = torch.empty(1, s.length, s.hv, s.dv, dtype=torch.bfloat16, device="cuda")
+
+    def varlen():
+        gd.chunk_fwd(q, k, v, g, beta, scale, h0, cu, out=o)
+
+    sec, ksec = timed_steps(varlen, steps, warmup)
+    flops = prefill_flops(s.length, s.hv, s.dk, s.dv)
+    out["varlen_8seq"] = {"T": s.length, "sequences": cu.numel() - 1, "value": s.length / sec / 1e6,
+                          "unit": "Mtok/s", "ms_per_call": sec * 1e3,
+                          "roofline": {"bound": "mfma", "achieved": flops / ksec / 1e12, "peak": MFMA_PEAK_TFLOPS,
+                                       "unit": "TFLOP/s", "frac": flops / ksec / 1e12 / MFMA_PEAK_TFLOPS}}
+    del q, k, v, g, beta, h0, o
+    s = WORKLOADS["stream_1m"]
+    q, k, v, g, beta, h0 = generate(1, s.length, s.hk, s.hv, s.dk, s.dv, s.dtype, s.h0_std, seed=0, device="cuda")
+    o = torch.empty(1, STREAM_SEGMENT, s.hv, s.dv, dtype=torch.bfloat16, device="cuda")
+
+    def stream():
+        state = h0
+        for lo in range(0, s.length, STREAM_SEGMENT):
+            sl = slice(lo, lo + STREAM_SEGMENT)
+            _, state = gd.chunk_fwd(q[:, sl], k[:, sl], v[:, sl], g[:, sl], beta[:, sl], scale, state, out=o)
+
+    sec, ksec = timed_steps(stream, max(1, steps // 2), warmup)
+    flops = prefill_flops(s.length, s.hv, s.dk, s.dv)
+    out["stream_1m"] = {"T": s.length, "segments": s.length // STREAM_SEGMENT, "value": s.length / sec / 1e6,
+                        "unit": "Mtok/s", "ms_per_pass": sec * 1e3,
+                        "roofline": {"bound": "mfma", "achieved": flops / ksec / 1e12, "peak": MFMA_PEAK_TFLOPS,
+                                     "unit": "TFLOP/s", "frac": flops / ksec / 1e12 / MFMA_PEAK_TFLOPS}}
+    return out
+
+
 def layer_inputs(length):
     """Synthetic layer inputs at the Qwen3-Next layer shape (Hk=16, Hv=32,
     K=V=128, conv 4): a bf16 projection z [1, T, q|k|v|gate|a|b], fp32 tail,
@@ -268,6 +311,7 @@ def main(argv=None):
     ap.add_argument("--no-b256", action="store_true", help="skip the ungraded 256-sequence decode")
     ap.add_argument("--copy-probe", action="store_true", help="also time a plain 256 MiB device copy")
     ap.add_argument("--no-layer", action="store_true", help="skip the layer prologue/epilogue kernels")
+    ap.add_argument("--no-long", action="store_true", help="skip the varlen and streamed prefill workloads")
     args = ap.parse_args(argv)
     world = int(os.environ.get("WORLD_SIZE", args.gpus))
     if args.gpus != 1 or world != 1:
@@ -319,6 +363,8 @@ def main(argv=None):
             result["decode_b256_ungraded"] = bench_decode(256, 200)
     if not args.no_layer:
         result.update(bench_layer(shape.length, 20))
+    if not args.no_long:
+        result.update(bench_long())
     if args.copy_probe:
         result["copy_probe"] = copy_probe()
     print(json.dumps(result), flush=True)
