@@ -84,6 +84,25 @@ def test_slow_decay_long_range():
     assert_parity("slow decay", o, o_ref, s, s_ref)
 
 
+@pytest.mark.parametrize("case", ["strong_decay", "no_decay", "beta_zero", "beta_one"])
+def test_gate_extremes(case):
+    """Gates at their edges: g about 30x the usual log decay (in-chunk decays
+    underflow to zero; nothing may become NaN or inf), g = 0 (no decay), beta = 0
+    (pure decay: S_t = exp(c_t) S_0) and beta = 1."""
+    q, k, v, g, beta, h0 = generate(1, 1000, 16, 32, 128, 128, torch.bfloat16, 0.02, seed=31,
+                                    g_scale=30.0 if case == "strong_decay" else 1.0)
+    if case == "no_decay":
+        g = torch.zeros_like(g)
+    if case == "beta_zero":
+        beta = torch.zeros_like(beta)
+    if case == "beta_one":
+        beta = torch.ones_like(beta)
+    o_ref, s_ref = oracle(q, k, v, g, beta, SCALE, h0)
+    o, s = run(q, k, v, g, beta, SCALE, h0)
+    assert torch.isfinite(o.float()).all() and torch.isfinite(s).all()
+    assert_parity(f"gates {case}", o, o_ref, s, s_ref)
+
+
 def test_beta_in_input_dtype_and_fp32_output():
     q, k, v, g, beta, h0 = generate(1, 300, 2, 4, 128, 64, torch.bfloat16, 0.02, seed=8)
     beta = beta.to(torch.bfloat16)
