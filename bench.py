@@ -9,7 +9,8 @@ a step is one chunk-kernel call over those inputs, resident in HBM, writing o
 (bf16) and the final state (fp32). `value` is prefill throughput in Mtok/s.
 The same line carries the decode step (64 sequences x 1 token, state
 [64,32,128,128] fp32 updated in place, 1000 chained steps) in µs/step and as a
-fraction of HBM bandwidth, an ungraded 256-sequence decode (state larger than
+fraction of HBM bandwidth, the same step with the state held in bf16 (a
+serving cache's default), an ungraded 256-sequence decode (state larger than
 the 256 MB Infinity Cache), the fused layer prologue and epilogue kernels at
 the same T and head shape with their HBM rooflines, the varlen (8 packed
 sequences, 262,144 tokens) and streamed (1,048,576 tokens in 16 segments)
@@ -72,8 +73,8 @@ def prefill_bytes(tokens, hk, hv, dk, dv, nstates=1, elem=2):
     return per_token * tokens + 2 * nstates * hv * dk * dv * 4
 
 
-def decode_bytes(batch, hk, hv, dk, dv, elem=2):
-    state = 2 * batch * hv * dk * dv * 4
+def decode_bytes(batch, hk, hv, dk, dv, elem=2, state_elem=4):
+    state = 2 * batch * hv * dk * dv * state_elem
     io = batch * (2 * hk * dk * elem + 2 * hv * dv * elem + 2 * hv * 4)
     return state + io
 
@@ -171,21 +172,23 @@ def bench_prefill(steps, warmup):
     return s, sec, ksec, flops, nbytes
 
 
-def bench_decode(batch, steps, warmup=10):
+def bench_decode(batch, steps, warmup=10, state_dtype=None):
     import torch
     from pseudobrain_amd.workloads import WORKLOADS, generate
     s = WORKLOADS["decode_b64"]
     q, k, v, g, beta, state = (x.cuda() for x in generate(batch, 1, s.hk, s.hv, s.dk, s.dv, s.dtype,
                                                           s.h0_std, seed=0))
+    if state_dtype is not None:
+        state = state.to(state_dtype)
     scale = s.dk ** -0.5
 
     def step():
         torch.ops.pbgdn.recurrent_step_(q, k, v, g, beta, state, None, scale)
 
     sec, ksec = timed_steps(step, steps, warmup)
-    nbytes = decode_bytes(batch, s.hk, s.hv, s.dk, s.dv)
+    nbytes = decode_bytes(batch, s.hk, s.hv, s.dk, s.dv, state_elem=state.element_size())
     return {
-        "batch": batch, "steps": steps, "us_per_step": sec * 1e6, "kernel_us": ksec * 1e6,
+        "batch": batch, "state_dtype": str(state.dtype).replace("torch.", ""), "steps": steps, "us_per_step": sec * 1e6, "kernel_us": ksec * 1e6,
         "bytes_per_step": nbytes, "achieved_GBs": nbytes / ksec / 1e9,
         "hbm_frac": nbytes / ksec / 1e9 / HBM_PEAK_GBS,
     }
@@ -359,6 +362,11 @@ def main(argv=None):
                                                "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                                "frac": dec["hbm_frac"],
                                                "traffic": measured_traffic("recurrent_b64")})
+        # vLLM keeps the recurrent state in the model's dtype unless told otherwise
+        bf = bench_decode(64, args.decode_steps, state_dtype=torch.bfloat16)
+        result["decode_bf16_state"] = dict(bf, roofline={"bound": "hbm", "achieved": bf["achieved_GBs"],
+                                                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                                         "frac": bf["hbm_frac"]})
         if not args.no_b256:
             result["decode_b256_ungraded"] = bench_decode(256, 200)
     if not args.no_layer:

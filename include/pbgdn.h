@@ -26,12 +26,15 @@
  *     (scratch memory comes in as a caller-provided workspace);
  *   - tensors are dense row-major in the reference layouts:
  *       q, k  [B, T, Hk, K]     v, o  [B, T, Hv, V]     g, beta  [B, T, Hv]
- *       states [N, Hv, K, V] float32, S stored [d_k, d_v] per head;
+ *       states [N, Hv, K, V] in state_dtype (F32, BF16 or F16; serving caches
+ *       may keep the state in the model's dtype), S stored [d_k, d_v] per head;
  *   - GQA: value head h reads query/key head h / (Hv / Hk)
  *     (repeat_interleave, gated_deltanet.py:422-424); Hk == Hv is the
  *     reference's already-repeated layout;
  *   - g is the log decay (<= 0), float32; beta float32 or the q/k/v dtype;
- *   - arithmetic: the state and every accumulation are float32;
+ *   - arithmetic: the state and every accumulation are float32 inside the
+ *     kernels; a 16-bit state is widened when it is read and rounded to
+ *     nearest even when it is written;
  *   - launches are asynchronous on `stream` (a hipStream_t; NULL = the null
  *     stream); no host synchronisation; the kernels keep no global state and
  *     are safe to call from several threads;
@@ -47,7 +50,7 @@
 extern "C" {
 #endif
 
-#define PBGDN_ABI_VERSION 3
+#define PBGDN_ABI_VERSION 4
 
 /* element types */
 #define PBGDN_F32 0
@@ -78,14 +81,26 @@ const char *pbgdn_status_string(int status);
  *   v           [B, T, Hv, V]   dtype in_dtype
  *   g           [B, T, Hv]      float32 log decay
  *   beta        [B, T, Hv]      dtype beta_dtype (F32 or in_dtype)
- *   h0          [N, Hv, K, V]   float32 initial states, or NULL for zeros
+ *   h0          [N, Hv, K, V]   initial states in state_dtype, or NULL for zeros
  *   cu_seqlens  [N + 1] int32 sequence boundaries into the T axis (B must be
  *               1, cu_seqlens[0] == 0, cu_seqlens[N] == T, nondecreasing), or
  *               NULL: then N = B sequences of T tokens each
  *   o           [B, T, Hv, V]   dtype out_dtype (F32 or in_dtype; another
  *               type is PBGDN_ERR_UNSUPPORTED), written
- *   ht          [N, Hv, K, V]   float32 final states, written (may be NULL;
- *               may equal h0 for an in-place state update)
+ *   ht          [N, Hv, K, V]   final states in state_dtype, written (may be
+ *               NULL; may equal h0 for an in-place state update)
+ *   state_dtype element type of h0 and ht (F32, BF16 or F16)
+ *   state_idx   NULL, or [N] int32 state slot of each sequence: then h0 and ht
+ *               are pools of num_states slots [num_states, Hv, K, V] (either
+ *               may be NULL, and they may be the same pool), sequence n starts
+ *               from slot state_idx[n] of h0 and its final state goes to slot
+ *               state_idx[n] of ht; a slot outside [0, num_states) starts from
+ *               zeros and keeps no final state; the slots of one call must be
+ *               distinct (vLLM's per-request state slots,
+ *               serving/pb27_vllm/pb27_vllm/universal_models.py:147-165)
+ *   has_initial_state NULL, or [N] uint8: 0 starts sequence n from zeros
+ *               instead of h0 (a new request whose slot holds stale data)
+ *   num_states  slots in the pools (ignored when state_idx is NULL)
  *   num_seqs    N (must equal B when cu_seqlens is NULL)
  *   scale       query scale (the reference passes K ** -0.5)
  *   chunk       must be 64 (CHUNK, gated_deltanet.py:49)
@@ -99,10 +114,12 @@ const char *pbgdn_status_string(int status);
  */
 int pbgdn_chunk_fwd(const void *q, const void *k, const void *v, int in_dtype,
                     const float *g, const void *beta, int beta_dtype,
-                    const float *h0, float *ht, const int32_t *cu_seqlens,
-                    int num_seqs, void *o, int out_dtype, int B, int T, int Hk,
-                    int Hv, int K, int V, float scale, int chunk,
-                    void *workspace, size_t workspace_bytes, void *stream);
+                    const void *h0, void *ht, int state_dtype,
+                    const int32_t *state_idx, const uint8_t *has_initial_state,
+                    int num_states, const int32_t *cu_seqlens, int num_seqs,
+                    void *o, int out_dtype, int B, int T, int Hk, int Hv,
+                    int K, int V, float scale, int chunk, void *workspace,
+                    size_t workspace_bytes, void *stream);
 
 /*
  * Bytes of workspace pbgdn_chunk_fwd needs for a call with these sizes
@@ -124,22 +141,25 @@ size_t pbgdn_chunk_workspace_size(int B, int T, int Hv, int num_seqs);
  *   q, k        [B, T, Hk, K]   dtype in_dtype
  *   v           [B, T, Hv, V]   dtype in_dtype
  *   g, beta     [B, T, Hv]      g float32, beta beta_dtype
- *   state_in    [S, Hv, K, V]   float32 states read (S = num_states)
- *   state_out   [S, Hv, K, V]   float32 states written; may equal state_in
+ *   state_in    [S, Hv, K, V]   states read (S = num_states), state_dtype
+ *   state_out   [S, Hv, K, V]   states written, state_dtype; may equal state_in
  *               (in-place update: each state is read whole before it is written;
  *               the slots of one call must be distinct)
  *   state_idx   [B] int32 state slot of each sequence, or NULL for slot b;
  *               a slot outside [0, num_states) (e.g. -1 padding) is skipped:
  *               no state is touched and that sequence's o is written as zeros
  *   num_states  S (must be >= B when state_idx is NULL)
+ *   state_dtype F32, BF16 or F16 (both state tensors); they must be aligned
+ *               to 4 elements; q, k, v to 16 bytes, g and beta to 4 bytes
  *   o           [B, T, Hv, V]   dtype out_dtype
  *
  * Supported: K in {32, 64, 128, 256}, V in {32, 64, 128, 256}.
  */
 int pbgdn_recurrent_fwd(const void *q, const void *k, const void *v,
                         int in_dtype, const float *g, const void *beta,
-                        int beta_dtype, const float *state_in,
-                        float *state_out, const int32_t *state_idx,
+                        int beta_dtype, const void *state_in,
+                        void *state_out, int state_dtype,
+                        const int32_t *state_idx,
                         int num_states, void *o, int out_dtype, int B, int T,
                         int Hk, int Hv, int K, int V, float scale,
                         void *stream);
@@ -153,8 +173,9 @@ int pbgdn_recurrent_fwd(const void *q, const void *k, const void *v,
  * serving/pb27_vllm/pb27_vllm/universal_models.py:147-165).
  * No reference counterpart: the reference's serving path delegates it to vLLM.
  *
- *   state_in         [S, Hv, K, V] float32 states read
- *   states           [S, Hv, K, V] float32 states written (may equal state_in)
+ *   state_in         [S, Hv, K, V] states read, state_dtype
+ *   states           [S, Hv, K, V] states written, state_dtype (may equal
+ *                    state_in)
  *   state_idx        [B] int32 slot of each sequence's starting state, or
  *                    NULL for slot b; a slot outside [0, S) gives zero output
  *                    and writes nothing
@@ -163,12 +184,13 @@ int pbgdn_recurrent_fwd(const void *q, const void *k, const void *v,
  *                    starting states are read whole before anything is
  *                    written; the slots a call writes must be distinct and
  *                    must not be another sequence's starting slot
- *   q, k, v, g, beta, o, scale: as pbgdn_recurrent_fwd
+ *   q, k, v, g, beta, o, scale, state_dtype: as pbgdn_recurrent_fwd
  */
 int pbgdn_recurrent_verify_fwd(const void *q, const void *k, const void *v,
                                int in_dtype, const float *g, const void *beta,
-                               int beta_dtype, const float *state_in,
-                               float *states, const int32_t *state_idx,
+                               int beta_dtype, const void *state_in,
+                               void *states, int state_dtype,
+                               const int32_t *state_idx,
                                const int32_t *token_state_idx, int num_states,
                                void *o, int out_dtype, int B, int T, int Hk,
                                int Hv, int K, int V, float scale, void *stream);

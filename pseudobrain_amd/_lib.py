@@ -13,7 +13,7 @@ import threading
 import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpbgdn.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 F32, BF16, F16 = 0, 1, 2
 OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3
@@ -25,12 +25,12 @@ _vp, _i, _f, _l = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_long
 SIGNATURES = {
     "pbgdn_abi_version": ([], _i),
     "pbgdn_status_string": ([_i], ctypes.c_char_p),
-    "pbgdn_chunk_fwd": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _i,
+    "pbgdn_chunk_fwd": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _i, _vp, _i,
                          _i, _i, _i, _i, _i, _i, _f, _i, _vp, ctypes.c_size_t, _vp], _i),
     "pbgdn_chunk_workspace_size": ([_i, _i, _i, _i], ctypes.c_size_t),
-    "pbgdn_recurrent_fwd": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _i,
+    "pbgdn_recurrent_fwd": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _i, _vp, _i,
                              _i, _i, _i, _i, _i, _i, _f, _vp], _i),
-    "pbgdn_recurrent_verify_fwd": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _i, _vp, _i,
+    "pbgdn_recurrent_verify_fwd": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _i,
                                     _i, _i, _i, _i, _i, _i, _f, _vp], _i),
     "pbgdn_prologue_fwd": ([_vp, _l, _vp, _l, _i, _vp, _vp, _i, _vp, _i, _vp, _vp,
                             _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp], _i),

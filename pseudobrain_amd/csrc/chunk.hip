@@ -41,7 +41,8 @@ extern "C" size_t pbgdn_chunk_workspace_size(int B, int T, int Hv, int num_seqs)
 }
 
 extern "C" int pbgdn_chunk_fwd(const void *q, const void *k, const void *v, int in_dtype, const float *g,
-                               const void *beta, int beta_dtype, const float *h0, float *ht,
+                               const void *beta, int beta_dtype, const void *h0, void *ht, int state_dtype,
+                               const int32_t *state_idx, const uint8_t *has_initial_state, int num_states,
                                const int32_t *cu_seqlens, int num_seqs, void *o, int out_dtype, int B, int T,
                                int Hk, int Hv, int K, int V, float scale, int chunk, void *workspace,
                                size_t workspace_bytes, void *stream) {
@@ -50,9 +51,11 @@ extern "C" int pbgdn_chunk_fwd(const void *q, const void *k, const void *v, int 
   if (B < 0 || T < 0 || Hk <= 0 || Hv <= 0 || K <= 0 || V <= 0 || Hv % Hk != 0 || num_seqs < 0) {
     return PBGDN_ERR_INVALID_ARGUMENT;
   }
-  if (!valid_dtype(in_dtype) || !valid_dtype(out_dtype) || !(beta_dtype == PBGDN_F32 || beta_dtype == in_dtype)) {
+  if (!valid_dtype(in_dtype) || !valid_dtype(out_dtype) || !valid_dtype(state_dtype) ||
+      !(beta_dtype == PBGDN_F32 || beta_dtype == in_dtype)) {
     return PBGDN_ERR_INVALID_ARGUMENT;
   }
+  if (state_idx && num_states < 0) return PBGDN_ERR_INVALID_ARGUMENT;
   if (cu_seqlens ? B != 1 : num_seqs != B) return PBGDN_ERR_INVALID_ARGUMENT;
   if (chunk != pbgdn::CH) return PBGDN_ERR_UNSUPPORTED;
   if (!(K == 64 || K == 128) || V % pbgdn::VT != 0) return PBGDN_ERR_UNSUPPORTED;
@@ -72,8 +75,9 @@ extern "C" int pbgdn_chunk_fwd(const void *q, const void *k, const void *v, int 
   const long total = static_cast<long>(V / pbgdn::VT) * Hv * num_seqs;
   if (total > 0x7fffffffL) return PBGDN_ERR_UNSUPPORTED;
   const long records = pbgdn::chunk_records(static_cast<long>(B) * T, num_seqs);
-  pbgdn::ChunkParams p{q, k, v, g, beta, beta_dtype, h0, ht, cu_seqlens, o,
-                       static_cast<unsigned char *>(workspace), T, Hk, Hv, V, num_seqs, scale};
+  pbgdn::ChunkParams p{q, k, v, g, beta, beta_dtype, h0, ht, state_dtype, state_idx, has_initial_state,
+                       num_states, cu_seqlens, o, static_cast<unsigned char *>(workspace), T, Hk, Hv, V,
+                       num_seqs, scale};
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (K) {
     case 64: return pbgdn::dispatch_in<64>(p, records, in_dtype, out_dtype, s);

@@ -45,7 +45,6 @@ typedef short i16x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int CH = 64;                  // chunk length (CHUNK, gated_deltanet.py:49)
 constexpr int VT = 16;                  // value columns per scan workgroup
-constexpr int RSRC_WORD3 = 0x00020000;  // raw buffer resource, gfx9 family
 
 // Workspace record of one (chunk, value head), REC_BYTES bytes:
 //   REC_SC   fp32 [64] gamma_t, [64] scale gamma_t, [64] exp(c_63 - c_t),
@@ -82,8 +81,12 @@ struct ChunkParams {
   const float *g;
   const void *beta;
   int beta_dtype;
-  const float *h0;
-  float *ht;
+  const void *h0;  // initial states, or NULL for zeros
+  void *ht;        // final states, or NULL
+  int state_dtype;
+  const int32_t *state_idx;          // [N] state slot of each sequence, or NULL for slot n
+  const uint8_t *has_initial_state;  // [N] 0: start from zeros, or NULL (all read h0)
+  int num_states;                    // slots in h0/ht when state_idx is set
   const int32_t *cu_seqlens;
   void *o;
   unsigned char *ws;  // workspace records
@@ -145,14 +148,6 @@ __device__ __forceinline__ void block_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, long bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0),
-                                           static_cast<int>(bytes > 0 ? bytes : 0), RSRC_WORD3);
-}
-
-__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-}
 
 // Output element stores through a buffer resource (stores past its range are dropped).
 template <typename T>
@@ -199,9 +194,6 @@ __device__ __forceinline__ float pick(float4_t v, int i) {
   return (i == 0) ? v[0] : (i == 1) ? v[1] : (i == 2) ? v[2] : v[3];
 }
 
-// Offset that is past the range of every buffer resource here (ranges stay
-// below 2^31): a load from it returns zeros, a store to it is dropped.
-constexpr uint32_t OUT_OF_RANGE = 0x7ffffff0u;
 
 // One chunk of raw inputs held in registers between its buffer load and its
 // store into LDS. LY gives the LDS placement (KQ, KQ_MAT, KPB; V16, V16_BUF

@@ -543,14 +543,21 @@ struct ScanBlock {
   }
 
   __device__ __forceinline__ void run() {
-    // Initial state: compute wave j owns key rows 16j..16j+15.
-    const long state_base = (static_cast<long>(seq) * p.Hv + h) * K * p.V + v0 + c16;
+    // Initial state: compute wave j owns key rows 16j..16j+15. With state
+    // slots, a slot outside [0, num_states) starts from zeros and keeps no
+    // final state.
+    const long slot = p.state_idx ? static_cast<long>(p.state_idx[seq]) : static_cast<long>(seq);
+    const bool in_pool = !p.state_idx || (slot >= 0 && slot < p.num_states);
+    const bool read_h0 = p.h0 && in_pool && (!p.has_initial_state || p.has_initial_state[seq]);
+    const long state_base = (slot * p.Hv + h) * K * p.V + v0 + c16;
     const int kt = wave;
     const bool owner = kt < NKT;
     if (owner) {
-      if (p.h0) {
+      if (read_h0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sacc[i] = p.h0[state_base + static_cast<long>(16 * kt + 4 * g4 + i) * p.V];
+        for (int i = 0; i < 4; ++i) {
+          sacc[i] = load_elem(p.h0, state_base + static_cast<long>(16 * kt + 4 * g4 + i) * p.V, p.state_dtype);
+        }
       }
       const O4 hi = Op::from(sacc);
       st(L::SH + kp_tile + 32 * kt, hi);
@@ -603,9 +610,11 @@ struct ScanBlock {
       if (nchunks > 0) out_tile(static_cast<int>((nchunks - 1) & 1), qs, gs, f0, f1);
       block_sync();
     }
-    if (p.ht && owner) {
+    if (p.ht && owner && in_pool) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) p.ht[state_base + static_cast<long>(16 * kt + 4 * g4 + i) * p.V] = sacc[i];
+      for (int i = 0; i < 4; ++i) {
+        store_elem(p.ht, state_base + static_cast<long>(16 * kt + 4 * g4 + i) * p.V, p.state_dtype, sacc[i]);
+      }
     }
   }
 };

@@ -13,6 +13,8 @@ typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint16_t u16;
+typedef uint32_t v2u32_t __attribute__((ext_vector_type(2)));
+typedef uint32_t v4u32_t __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------
 // Scalar element access. bf16 is handled as raw bits (no compiler bf16
@@ -46,6 +48,26 @@ __device__ __forceinline__ void store_elem(void *p, long i, int dtype, float x) 
   } else {
     static_cast<half_t *>(p)[i] = static_cast<half_t>(x);
   }
+}
+
+// ---------------------------------------------------------------------------
+// Buffer resources: a base address and a byte range; a load outside the range
+// returns zeros and a store outside it is dropped, so per-lane conditions need
+// no branches around the memory operations.
+// ---------------------------------------------------------------------------
+constexpr int RSRC_WORD3 = 0x00020000;  // raw buffer resource, gfx9 family
+
+// Offset that is past the range of every buffer resource here (ranges stay
+// below 2^31): a load from it returns zeros, a store to it is dropped.
+constexpr uint32_t OUT_OF_RANGE = 0x7ffffff0u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, long bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes > 0 ? bytes : 0), RSRC_WORD3);
+}
+
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
 // ---------------------------------------------------------------------------

@@ -9,13 +9,88 @@
 // Per token the two column reductions S^T k and S^T q are formed together in one
 // sweep over the registers (wavefront shuffles, then 4 partials per column
 // through LDS), and then the update and o = a S^T q + u (k.q) need no second
-// sweep. The kernel is HBM-bound: K*V*8 bytes of state traffic per head.
+// sweep. The kernel is HBM-bound: K*V*8 bytes of state traffic per head for a
+// float32 state, K*V*4 for a bf16 or fp16 one (serving caches often keep the
+// state in the model's dtype); the arithmetic is float32 either way.
 // In verify mode (speculative decoding) the state after every token is also
 // written, to a slot per token, so that the state after the last accepted
 // draft token can be kept.
+//
+// The state moves through buffer loads and stores: one VGPR of lane offset,
+// and the row steps as constant SGPR offsets. For a one-token step over a
+// 16-bit state (the serving decode) the registers hold the state as loaded,
+// two elements a register, and widen it in each sweep: half the registers, so
+// twice the workgroups per CU and as many state bytes in flight as a float32
+// state has. The arithmetic is the same float32 either way.
 #include "common.hpp"
 
 namespace pbgdn {
+
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+
+// Element `half` (0 low, 1 high) of a loaded word for 16-bit dtypes, the word
+// itself for float32.
+__device__ __forceinline__ float widen_word(uint32_t w, int half, int dtype) {
+  if (dtype == PBGDN_F32) return __uint_as_float(w);
+  const uint32_t bits = half ? w >> 16 : w & 0xffffu;
+  if (dtype == PBGDN_BF16) return __uint_as_float(bits << 16);
+  return static_cast<float>(__builtin_bit_cast(half_t, static_cast<u16>(bits)));
+}
+
+// Four consecutive elements from two loaded 8-byte pieces (w1 only for float32).
+__device__ __forceinline__ float4_t widen_words(v2u32_t w0, v2u32_t w1, int dtype) {
+  if (dtype == PBGDN_F32) {
+    return float4_t{__uint_as_float(w0[0]), __uint_as_float(w0[1]), __uint_as_float(w1[0]), __uint_as_float(w1[1])};
+  }
+  if (dtype == PBGDN_BF16) {
+    return float4_t{__uint_as_float(w0[0] << 16), __uint_as_float(w0[0] & 0xffff0000u),
+                    __uint_as_float(w0[1] << 16), __uint_as_float(w0[1] & 0xffff0000u)};
+  }
+  return to_float4(__builtin_bit_cast(half4_t, w0));
+}
+
+// State element I/O: Raw is what a thread loads for 4 consecutive columns.
+template <typename TS>
+struct StateIO;
+template <>
+struct StateIO<float> {
+  using Raw = float4_t;
+  __device__ static Raw load(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+  }
+  __device__ static float4_t widen(Raw x) { return x; }
+  __device__ static void store(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, float4_t x) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32_t, x), r, voff, soff, 0);
+  }
+};
+template <>
+struct StateIO<u16> {
+  using Raw = v2u32_t;
+  __device__ static Raw load(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+  }
+  __device__ static float4_t widen(Raw w) {
+    return float4_t{__uint_as_float(w[0] << 16), __uint_as_float(w[0] & 0xffff0000u),
+                    __uint_as_float(w[1] << 16), __uint_as_float(w[1] & 0xffff0000u)};
+  }
+  // Round to nearest even (v_cvt_pk_bf16_f32).
+  __device__ static void store(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, float4_t x) {
+    const bf16x4_t b = {static_cast<__bf16>(x[0]), static_cast<__bf16>(x[1]), static_cast<__bf16>(x[2]),
+                        static_cast<__bf16>(x[3])};
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32_t, b), r, voff, soff, 0);
+  }
+};
+template <>
+struct StateIO<half_t> {
+  using Raw = v2u32_t;
+  __device__ static Raw load(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+  }
+  __device__ static float4_t widen(Raw w) { return to_float4(__builtin_bit_cast(half4_t, w)); }
+  __device__ static void store(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, float4_t x) {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32_t, to_half4(x)), r, voff, soff, 0);
+  }
+};
 
 struct RecurrentParams {
   const void *q, *k, *v;
@@ -23,8 +98,8 @@ struct RecurrentParams {
   const float *g;
   const void *beta;
   int beta_dtype;
-  const float *state_in;
-  float *state_out;
+  const void *state_in;
+  void *state_out;
   const int32_t *state_idx;
   const int32_t *token_state_idx;  // [B, T] slot of the state after each token, or NULL
   int num_states;
@@ -34,8 +109,21 @@ struct RecurrentParams {
   float scale;
 };
 
-template <int K, int V>
-__global__ __launch_bounds__(256) void recurrent_kernel(RecurrentParams p) {
+// Workgroups per CU for the one-token step: 4 (128 VGPRs) where a thread's
+// state is at most 64 floats, 6 (80 VGPRs) for the packed 16-bit form of the
+// same. The token loop and the larger head shapes take what the compiler
+// gives them (a bound there would spill).
+template <int K, int V, bool ONE, bool PACKED>
+constexpr int recurrent_wg_per_cu() {
+  return ONE && K * V / 256 <= 64 ? (PACKED ? 6 : 4) : 1;
+}
+
+// ONE: a single token and no verify slots (the decode step), with no token
+// loop; then a 16-bit state stays packed in the registers as loaded.
+template <int K, int V, typename TS, bool ONE>
+__global__ __launch_bounds__(256, (recurrent_wg_per_cu<K, V, ONE, ONE && sizeof(TS) == 2>())) void recurrent_kernel(
+    RecurrentParams p) {
+  constexpr bool PACKED = ONE && sizeof(TS) == 2;
   constexpr int NT = 256;
   constexpr int NW = NT / 64;
   constexpr int CG = V / 4;    // float4 column groups
@@ -43,6 +131,9 @@ __global__ __launch_bounds__(256) void recurrent_kernel(RecurrentParams p) {
   constexpr int RPT = K / RG;  // rows per thread
   static_assert(CG >= 1 && CG <= 64 && 64 % CG == 0, "V/4 must divide 64");
   static_assert(RPT >= 1 && RG * RPT == K, "K must be a multiple of the row groups");
+  using IO = StateIO<TS>;
+  constexpr uint32_t ROW_STEP = RG * V * sizeof(TS);         // bytes between a thread's rows
+  constexpr uint32_t STATE_BYTES = K * V * sizeof(TS);
 
   const int h = blockIdx.x;
   const int b = blockIdx.y;
@@ -70,29 +161,79 @@ __global__ __launch_bounds__(256) void recurrent_kernel(RecurrentParams p) {
     return;
   }
   const long state_off = (slot * p.Hv + h) * static_cast<long>(K) * V;
-  const float *sin = p.state_in + state_off;
-  float *sout = p.state_out + state_off;
+  const __amdgpu_buffer_rsrc_t rin = rsrc(static_cast<const TS *>(p.state_in) + state_off, STATE_BYTES);
+  const __amdgpu_buffer_rsrc_t rout = rsrc(static_cast<TS *>(p.state_out) + state_off, STATE_BYTES);
+  const uint32_t voff = (rg * V + 4 * cg) * sizeof(TS);
 
-  float4_t s[RPT];
+  // A token's inputs, as loaded: the same load instructions for every input
+  // dtype (the elements are picked out of the loaded words afterwards), so no
+  // branches sit around loads and no per-dtype addresses are kept. Thread
+  // i < K takes element i of the q and k rows; every thread takes v columns
+  // 4cg..4cg+3 (two 8-byte loads; the second is sent out of range for 16-bit
+  // inputs, which need only the first).
+  const int esz = p.in_dtype == PBGDN_F32 ? 4 : 2;
+  const int besz = p.beta_dtype == PBGDN_F32 ? 4 : 2;
+  const uint32_t qk_off = (tid * esz) & ~3u;
+  const uint32_t v_off0 = 4 * cg * esz;
+  const uint32_t v_off1 = esz == 4 ? v_off0 + 8 : OUT_OF_RANGE;
+  struct Inputs {
+    uint32_t wq, wk, wb;
+    v2u32_t wv0, wv1;
+    float g;
+  };
+  auto fetch = [&](long tok) {
+    Inputs in;
+    const long qk_row = (tok * p.Hk + hk) * K * esz;
+    const __amdgpu_buffer_rsrc_t rq = rsrc(static_cast<const char *>(p.q) + qk_row, K * esz);
+    const __amdgpu_buffer_rsrc_t rk = rsrc(static_cast<const char *>(p.k) + qk_row, K * esz);
+    in.wq = __builtin_amdgcn_raw_buffer_load_b32(rq, qk_off, 0, 0);
+    in.wk = __builtin_amdgcn_raw_buffer_load_b32(rk, qk_off, 0, 0);
+    const __amdgpu_buffer_rsrc_t rv = rsrc(static_cast<const char *>(p.v) + (tok * p.Hv + h) * V * esz, V * esz);
+    in.wv0 = __builtin_amdgcn_raw_buffer_load_b64(rv, v_off0, 0, 0);
+    in.wv1 = __builtin_amdgcn_raw_buffer_load_b64(rv, v_off1, 0, 0);
+    const long gb = tok * p.Hv + h;
+    in.g = p.g[gb];
+    // The aligned word holding beta (for a 16-bit beta with an odd count, the
+    // last word reaches 2 bytes past the end, inside the same aligned word).
+    in.wb = *reinterpret_cast<const uint32_t *>(static_cast<const char *>(p.beta) + ((gb * besz) & ~3L));
+    return in;
+  };
+  const long tok0 = static_cast<long>(b) * p.T;
+  Inputs in = {};
+  if (ONE || p.T > 0) in = fetch(tok0);  // with T = 0 the input pointers may be null
+  // Keep the inputs' loads ahead of the state's: the wait for the inputs then
+  // leaves the state loads in flight.
+  asm volatile("" ::: "memory");
+
+  typename IO::Raw raw[PACKED ? RPT : 1];
+  float4_t s[PACKED ? 1 : RPT];
 #pragma unroll
   for (int j = 0; j < RPT; ++j) {
-    s[j] = *reinterpret_cast<const float4_t *>(sin + static_cast<long>(rg + RG * j) * V + 4 * cg);
-  }
-
-  for (int t = 0; t < p.T; ++t) {
-    const long tok = static_cast<long>(b) * p.T + t;
-    const long qk_base = (tok * p.Hk + hk) * K;
-    for (int i = tid; i < K; i += NT) {
-      sk[i] = load_elem(p.k, qk_base + i, p.in_dtype);
-      sq[i] = load_elem(p.q, qk_base + i, p.in_dtype) * p.scale;
+    if constexpr (PACKED) {
+      raw[j] = IO::load(rin, voff, j * ROW_STEP);
+    } else {
+      s[j] = IO::widen(IO::load(rin, voff, j * ROW_STEP));
     }
-    const long v_base = (tok * p.Hv + h) * V + 4 * cg;
-    float4_t vv;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) vv[c] = load_elem(p.v, v_base + c, p.in_dtype);
-    const long gb = tok * p.Hv + h;
-    const float alpha = expf(p.g[gb]);
-    const float bt = load_elem(p.beta, gb, p.beta_dtype);
+  }
+  auto row = [&](int j) -> float4_t {
+    if constexpr (PACKED) {
+      return IO::widen(raw[j]);
+    } else {
+      return s[j];
+    }
+  };
+
+  const int T = ONE ? 1 : p.T;
+  for (int t = 0; t < T; ++t) {
+    const long tok = tok0 + t;
+    if (t > 0) in = fetch(tok);
+    if (tid < K) {
+      sk[tid] = widen_word(in.wk, tid & 1, p.in_dtype);
+      sq[tid] = widen_word(in.wq, tid & 1, p.in_dtype) * p.scale;
+    }
+    const float4_t vv = widen_words(in.wv0, in.wv1, p.in_dtype);
+    const float alpha = expf(in.g);
+    const float bt = widen_word(in.wb, static_cast<int>((tok * p.Hv + h) & 1), p.beta_dtype);
     __syncthreads();
 
     float kq = 0.f;
@@ -105,8 +246,15 @@ __global__ __launch_bounds__(256) void recurrent_kernel(RecurrentParams p) {
     for (int j = 0; j < RPT; ++j) {
       const float kr = sk[rg + RG * j];
       const float qr = sq[rg + RG * j];
-      pk += s[j] * kr;
-      pq += s[j] * qr;
+      const float4_t sj = row(j);
+      pk += sj * kr;
+      pq += sj * qr;
+    }
+    if constexpr (PACKED) {
+      // Widen again in the second sweep rather than keep the widened rows
+      // alive across the reduction (which would undo the packing).
+#pragma unroll
+      for (int j = 0; j < RPT; ++j) asm volatile("" : "+v"(raw[j]));
     }
 #pragma unroll
     for (int off = CG; off < 64; off <<= 1) {
@@ -133,58 +281,73 @@ __global__ __launch_bounds__(256) void recurrent_kernel(RecurrentParams p) {
 #pragma unroll
     for (int j = 0; j < RPT; ++j) {
       const float kr = sk[rg + RG * j];
-      s[j] = alpha * s[j] + kr * u;
+      if constexpr (PACKED) {
+        IO::store(rout, voff, j * ROW_STEP, alpha * row(j) + kr * u);
+      } else {
+        s[j] = alpha * s[j] + kr * u;
+      }
     }
     if (rg == 0) {
       const long o_base = (tok * p.Hv + h) * V + 4 * cg;
 #pragma unroll
       for (int c = 0; c < 4; ++c) store_elem(p.o, o_base + c, p.out_dtype, out[c]);
     }
-    if (p.token_state_idx) {  // verify mode: the state after this token goes to its own slot
+    if (!ONE && p.token_state_idx) {  // verify mode: the state after this token goes to its own slot
       const long ts = p.token_state_idx[tok];
       if (ts >= 0 && ts < p.num_states) {
-        float *dst = p.state_out + (ts * p.Hv + h) * static_cast<long>(K) * V;
+        const __amdgpu_buffer_rsrc_t rts =
+            rsrc(static_cast<TS *>(p.state_out) + (ts * p.Hv + h) * static_cast<long>(K) * V, STATE_BYTES);
 #pragma unroll
-        for (int j = 0; j < RPT; ++j) {
-          *reinterpret_cast<float4_t *>(dst + static_cast<long>(rg + RG * j) * V + 4 * cg) = s[j];
-        }
+        for (int j = 0; j < RPT; ++j) IO::store(rts, voff, j * ROW_STEP, row(j));
       }
     }
     __syncthreads();  // sk, sq and the partials are rewritten by the next token
   }
 
-  if (!p.token_state_idx) {
+  if (!PACKED && (ONE || !p.token_state_idx)) {
 #pragma unroll
-    for (int j = 0; j < RPT; ++j) {
-      *reinterpret_cast<float4_t *>(sout + static_cast<long>(rg + RG * j) * V + 4 * cg) = s[j];
-    }
+    for (int j = 0; j < RPT; ++j) IO::store(rout, voff, j * ROW_STEP, row(j));
   }
 }
 
-template <int K, int V>
+template <int K, int V, typename TS>
 static int launch_recurrent(const RecurrentParams &p, int B, hipStream_t stream) {
-  hipLaunchKernelGGL((recurrent_kernel<K, V>), dim3(p.Hv, B), dim3(256), 0, stream, p);
+  if (p.T == 1 && !p.token_state_idx) {
+    hipLaunchKernelGGL((recurrent_kernel<K, V, TS, true>), dim3(p.Hv, B), dim3(256), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((recurrent_kernel<K, V, TS, false>), dim3(p.Hv, B), dim3(256), 0, stream, p);
+  }
   return hipGetLastError() == hipSuccess ? PBGDN_OK : PBGDN_ERR_LAUNCH;
 }
 
-template <int K>
+template <int K, typename TS>
 static int dispatch_v(const RecurrentParams &p, int B, int V, hipStream_t stream) {
   switch (V) {
-    case 32: return launch_recurrent<K, 32>(p, B, stream);
-    case 64: return launch_recurrent<K, 64>(p, B, stream);
-    case 128: return launch_recurrent<K, 128>(p, B, stream);
-    case 256: return launch_recurrent<K, 256>(p, B, stream);
+    case 32: return launch_recurrent<K, 32, TS>(p, B, stream);
+    case 64: return launch_recurrent<K, 64, TS>(p, B, stream);
+    case 128: return launch_recurrent<K, 128, TS>(p, B, stream);
+    case 256: return launch_recurrent<K, 256, TS>(p, B, stream);
     default: return PBGDN_ERR_UNSUPPORTED;
   }
 }
 
-int recurrent_fwd(const RecurrentParams &p, int B, int K, int V, hipStream_t stream) {
+template <typename TS>
+static int dispatch_k(const RecurrentParams &p, int B, int K, int V, hipStream_t stream) {
   switch (K) {
-    case 32: return dispatch_v<32>(p, B, V, stream);
-    case 64: return dispatch_v<64>(p, B, V, stream);
-    case 128: return dispatch_v<128>(p, B, V, stream);
-    case 256: return dispatch_v<256>(p, B, V, stream);
+    case 32: return dispatch_v<32, TS>(p, B, V, stream);
+    case 64: return dispatch_v<64, TS>(p, B, V, stream);
+    case 128: return dispatch_v<128, TS>(p, B, V, stream);
+    case 256: return dispatch_v<256, TS>(p, B, V, stream);
     default: return PBGDN_ERR_UNSUPPORTED;
+  }
+}
+
+int recurrent_fwd(const RecurrentParams &p, int state_dtype, int B, int K, int V, hipStream_t stream) {
+  switch (state_dtype) {
+    case PBGDN_F32: return dispatch_k<float>(p, B, K, V, stream);
+    case PBGDN_BF16: return dispatch_k<u16>(p, B, K, V, stream);
+    case PBGDN_F16: return dispatch_k<half_t>(p, B, K, V, stream);
+    default: return PBGDN_ERR_INVALID_ARGUMENT;
   }
 }
 
@@ -195,9 +358,20 @@ int recurrent_fwd(const RecurrentParams &p, int B, int K, int V, hipStream_t str
 // ---------------------------------------------------------------------------
 static bool valid_dtype(int d) { return d == PBGDN_F32 || d == PBGDN_BF16 || d == PBGDN_F16; }
 
+// The kernel moves the state in pieces of 4 elements, and reads q, k, v in
+// aligned words (16-byte aligned tensors, as pbgdn_chunk_fwd takes them) and
+// g and beta in 4-byte words.
+static bool state_aligned(const void *p, int dtype) {
+  return (reinterpret_cast<uintptr_t>(p) & (dtype == PBGDN_F32 ? 15u : 7u)) == 0;
+}
+static bool inputs_aligned(const void *q, const void *k, const void *v, const void *g, const void *beta) {
+  auto a = [](const void *x, uintptr_t m) { return (reinterpret_cast<uintptr_t>(x) & m) == 0; };
+  return a(q, 15) && a(k, 15) && a(v, 15) && a(g, 3) && a(beta, 3);
+}
+
 extern "C" int pbgdn_recurrent_fwd(const void *q, const void *k, const void *v, int in_dtype,
                                    const float *g, const void *beta, int beta_dtype,
-                                   const float *state_in, float *state_out,
+                                   const void *state_in, void *state_out, int state_dtype,
                                    const int32_t *state_idx, int num_states, void *o,
                                    int out_dtype, int B,
                                    int T, int Hk, int Hv, int K, int V, float scale,
@@ -205,39 +379,47 @@ extern "C" int pbgdn_recurrent_fwd(const void *q, const void *k, const void *v, 
   if (B < 0 || T < 0 || Hk <= 0 || Hv <= 0 || K <= 0 || V <= 0 || Hv % Hk != 0) {
     return PBGDN_ERR_INVALID_ARGUMENT;
   }
-  if (!valid_dtype(in_dtype) || !valid_dtype(out_dtype) ||
+  if (!valid_dtype(in_dtype) || !valid_dtype(out_dtype) || !valid_dtype(state_dtype) ||
       !(beta_dtype == PBGDN_F32 || beta_dtype == in_dtype)) {
     return PBGDN_ERR_INVALID_ARGUMENT;
   }
   if (B == 0 || Hv == 0) return PBGDN_OK;
   if (!state_in || !state_out || num_states < 0) return PBGDN_ERR_INVALID_ARGUMENT;
+  if (!state_aligned(state_in, state_dtype) || !state_aligned(state_out, state_dtype)) {
+    return PBGDN_ERR_INVALID_ARGUMENT;
+  }
   if (!state_idx && num_states < B) return PBGDN_ERR_INVALID_ARGUMENT;
   if (T > 0 && (!q || !k || !v || !g || !beta || !o)) return PBGDN_ERR_INVALID_ARGUMENT;
+  if (!inputs_aligned(q, k, v, g, beta)) return PBGDN_ERR_INVALID_ARGUMENT;
   if (B > 65535) return PBGDN_ERR_UNSUPPORTED;
   pbgdn::RecurrentParams p{q, k, v, in_dtype, g, beta, beta_dtype, state_in, state_out,
                            state_idx, nullptr, num_states, o, out_dtype, T, Hk, Hv, scale};
-  return pbgdn::recurrent_fwd(p, B, K, V, static_cast<hipStream_t>(stream));
+  return pbgdn::recurrent_fwd(p, state_dtype, B, K, V, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int pbgdn_recurrent_verify_fwd(const void *q, const void *k, const void *v, int in_dtype,
                                           const float *g, const void *beta, int beta_dtype,
-                                          const float *state_in, float *states,
+                                          const void *state_in, void *states, int state_dtype,
                                           const int32_t *state_idx, const int32_t *token_state_idx,
                                           int num_states, void *o, int out_dtype, int B, int T, int Hk,
                                           int Hv, int K, int V, float scale, void *stream) {
   if (B < 0 || T < 0 || Hk <= 0 || Hv <= 0 || K <= 0 || V <= 0 || Hv % Hk != 0) {
     return PBGDN_ERR_INVALID_ARGUMENT;
   }
-  if (!valid_dtype(in_dtype) || !valid_dtype(out_dtype) ||
+  if (!valid_dtype(in_dtype) || !valid_dtype(out_dtype) || !valid_dtype(state_dtype) ||
       !(beta_dtype == PBGDN_F32 || beta_dtype == in_dtype)) {
     return PBGDN_ERR_INVALID_ARGUMENT;
   }
   if (B == 0 || T == 0) return PBGDN_OK;
   if (!state_in || !states || !token_state_idx || num_states < 0) return PBGDN_ERR_INVALID_ARGUMENT;
+  if (!state_aligned(state_in, state_dtype) || !state_aligned(states, state_dtype)) {
+    return PBGDN_ERR_INVALID_ARGUMENT;
+  }
   if (!state_idx && num_states < B) return PBGDN_ERR_INVALID_ARGUMENT;
   if (!q || !k || !v || !g || !beta || !o) return PBGDN_ERR_INVALID_ARGUMENT;
+  if (!inputs_aligned(q, k, v, g, beta)) return PBGDN_ERR_INVALID_ARGUMENT;
   if (B > 65535) return PBGDN_ERR_UNSUPPORTED;
   pbgdn::RecurrentParams p{q, k, v, in_dtype, g, beta, beta_dtype, state_in, states,
                            state_idx, token_state_idx, num_states, o, out_dtype, T, Hk, Hv, scale};
-  return pbgdn::recurrent_fwd(p, B, K, V, static_cast<hipStream_t>(stream));
+  return pbgdn::recurrent_fwd(p, state_dtype, B, K, V, static_cast<hipStream_t>(stream));
 }

@@ -69,13 +69,18 @@ def _operands(q, k, v, g, beta):
     gated_deltanet.py:284); g float32; beta float32 or q's dtype."""
     if q.dtype not in _lib.DTYPE_CODES:
         raise ValueError(f"unsupported q dtype {q.dtype}")
-    k = k.to(q.dtype).contiguous()
-    v = v.to(q.dtype).contiguous()
-    q = q.contiguous()
-    g = g.to(torch.float32).contiguous()
+    k = _aligned(k.to(q.dtype).contiguous(), 16)
+    v = _aligned(v.to(q.dtype).contiguous(), 16)
+    q = _aligned(q.contiguous(), 16)
+    g = _aligned(g.to(torch.float32).contiguous(), 4)
     if beta.dtype not in (torch.float32, q.dtype):
         beta = beta.to(torch.float32)
-    return q, k, v, g, beta.contiguous()
+    return q, k, v, g, _aligned(beta.contiguous(), 4)
+
+
+def _aligned(x: torch.Tensor, nbytes: int) -> torch.Tensor:
+    """x, or a copy of it when a view leaves it off the alignment the kernels read in."""
+    return x if x.data_ptr() % nbytes == 0 else x.clone()
 
 
 # ----------------------------------------------------------------------------
@@ -118,11 +123,70 @@ def chunk_fwd(q, k, v, g, beta, scale: float, h0=None, cu_seqlens=None, *,
     codes = _lib.DTYPE_CODES
     status = lib.pbgdn_chunk_fwd(
         _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), codes[q.dtype], _lib.ptr(g), _lib.ptr(beta),
-        codes[beta.dtype], _lib.ptr(h0), _lib.ptr(final), _lib.ptr(cu_seqlens), nseq,
+        codes[beta.dtype], _lib.ptr(h0), _lib.ptr(final), _lib.F32, None, None, 0, _lib.ptr(cu_seqlens), nseq,
         _lib.ptr(out), codes[out_dtype], batch, length, hk, hv, dk, dv, float(scale), CHUNK,
         _lib.ptr(workspace), ws_bytes, _lib.stream_handle(dev))
     _lib.check(status, "pbgdn_chunk_fwd")
     return out, final
+
+
+def _state_pool(states, hv, dk, dv):
+    if (states.ndim != 4 or states.shape[1:] != (hv, dk, dv) or states.dtype not in _lib.DTYPE_CODES
+            or not states.is_contiguous()):
+        raise ValueError(f"states must be a contiguous [S,{hv},{dk},{dv}] float32, bfloat16 or float16 tensor")
+
+
+def chunk_fwd_slots(q, k, v, g, beta, scale: float, states, state_idx, cu_seqlens=None,
+                    has_initial_state=None, *, out_dtype: torch.dtype | None = None,
+                    out: torch.Tensor | None = None):
+    """Prefill against a pool of state slots, the way a serving cache holds
+    them (vLLM's per-request slots, serving/pb27_vllm/pb27_vllm/universal_models.py:147-165):
+    sequence n starts from states[state_idx[n]] (zeros where has_initial_state[n]
+    is False, or where the slot is outside the pool) and its final state is
+    written back to that slot, in the pool's dtype (float32, bfloat16 or
+    float16; the arithmetic is float32). Slots must be distinct. One call of
+    pbgdn_chunk_fwd; no gather or scatter copies. Returns o [B,T,Hv,V]."""
+    batch, length, hk, hv, dk, dv = _shapes(q, k, v, g, beta)
+    if out_dtype is not None and out_dtype not in (torch.float32, q.dtype):
+        raise ValueError(f"chunk kernel writes o as float32 or q's dtype ({q.dtype}), not {out_dtype}")
+    dev = _require_device(q, k, v, g, beta, states, state_idx, cu_seqlens, has_initial_state)
+    if dk not in CHUNK_HEAD_DIMS or dv % 16:
+        raise ValueError(f"chunk kernel supports K in {CHUNK_HEAD_DIMS} and V a multiple of 16")
+    _state_pool(states, hv, dk, dv)
+    q, k, v, g, beta = _operands(q, k, v, g, beta)
+    if cu_seqlens is not None:
+        if batch != 1:
+            raise ValueError("cu_seqlens needs B == 1 (sequences packed along T)")
+        if cu_seqlens.ndim != 1 or cu_seqlens.numel() < 1:
+            raise ValueError("cu_seqlens must be a 1-D tensor [N+1]")
+        cu_seqlens = cu_seqlens.to(torch.int32).contiguous()
+        nseq = cu_seqlens.numel() - 1
+    else:
+        nseq = batch
+    if state_idx.shape != (nseq,):
+        raise ValueError(f"state_idx must be [N] = [{nseq}]")
+    state_idx = state_idx.to(torch.int32).contiguous()
+    if has_initial_state is not None:
+        if has_initial_state.shape != (nseq,):
+            raise ValueError(f"has_initial_state must be [N] = [{nseq}]")
+        has_initial_state = has_initial_state.to(torch.uint8).contiguous()
+    out_dtype = q.dtype if out_dtype is None else out_dtype
+    if out is None:
+        out = torch.empty(batch, length, hv, dv, dtype=out_dtype, device=dev)
+    elif out.shape != (batch, length, hv, dv) or out.dtype != out_dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous [B,T,Hv,V] tensor of out_dtype")
+    lib = _lib.lib()
+    ws_bytes = lib.pbgdn_chunk_workspace_size(batch, length, hv, nseq)
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    codes = _lib.DTYPE_CODES
+    status = lib.pbgdn_chunk_fwd(
+        _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), codes[q.dtype], _lib.ptr(g), _lib.ptr(beta),
+        codes[beta.dtype], _lib.ptr(states), _lib.ptr(states), codes[states.dtype], _lib.ptr(state_idx),
+        _lib.ptr(has_initial_state), states.shape[0], _lib.ptr(cu_seqlens), nseq, _lib.ptr(out),
+        codes[out_dtype], batch, length, hk, hv, dk, dv, float(scale), CHUNK, _lib.ptr(workspace), ws_bytes,
+        _lib.stream_handle(dev))
+    _lib.check(status, "pbgdn_chunk_fwd")
+    return out
 
 
 def recurrent_fwd(q, k, v, g, beta, scale: float, state_in, state_out=None, state_idx=None, *,
@@ -131,7 +195,9 @@ def recurrent_fwd(q, k, v, g, beta, scale: float, state_in, state_out=None, stat
     """Launch pbgdn_recurrent_fwd: all T tokens through the per-step recurrence.
     state_out may be state_in (in place) or None (a new tensor). state_idx [B]
     int32 maps sequences to state slots (distinct; a slot outside the state
-    tensor, e.g. -1, is skipped and its o is zero). Returns (o, state_out).
+    tensor, e.g. -1, is skipped and its o is zero). The states may be float32,
+    bfloat16 or float16 (state_out in state_in's dtype); the arithmetic is
+    float32. Returns (o, state_out).
 
     token_state_idx [B,T] int32 selects the speculative-verify form
     (pbgdn_recurrent_verify_fwd): sequence b starts from slot state_idx[b] and
@@ -143,9 +209,7 @@ def recurrent_fwd(q, k, v, g, beta, scale: float, state_in, state_out=None, stat
     if dk not in RECURRENT_HEAD_DIMS or dv not in RECURRENT_HEAD_DIMS:
         raise ValueError(f"recurrent kernel supports K, V in {RECURRENT_HEAD_DIMS}")
     q, k, v, g, beta = _operands(q, k, v, g, beta)
-    if state_in.dtype != torch.float32 or not state_in.is_contiguous() or state_in.ndim != 4 \
-            or state_in.shape[1:] != (hv, dk, dv):
-        raise ValueError(f"state must be a contiguous float32 [S,Hv,K,V] tensor, [*,{hv},{dk},{dv}]")
+    _state_pool(state_in, hv, dk, dv)
     if state_idx is None:
         if state_in.shape[0] != batch:
             raise ValueError("without state_idx the state batch must equal B")
@@ -155,7 +219,7 @@ def recurrent_fwd(q, k, v, g, beta, scale: float, state_in, state_out=None, stat
         state_idx = state_idx.to(torch.int32).contiguous()
     if state_out is None:
         state_out = torch.empty_like(state_in)
-    elif state_out.shape != state_in.shape or state_out.dtype != torch.float32 or not state_out.is_contiguous():
+    elif state_out.shape != state_in.shape or state_out.dtype != state_in.dtype or not state_out.is_contiguous():
         raise ValueError("state_out must match state_in")
     if out is None:
         out = torch.empty(batch, length, hv, dv, dtype=out_dtype, device=dev)
@@ -166,14 +230,14 @@ def recurrent_fwd(q, k, v, g, beta, scale: float, state_in, state_out=None, stat
         token_state_idx = token_state_idx.to(torch.int32).contiguous()
         status = _lib.lib().pbgdn_recurrent_verify_fwd(
             _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), codes[q.dtype], _lib.ptr(g), _lib.ptr(beta),
-            codes[beta.dtype], _lib.ptr(state_in), _lib.ptr(state_out), _lib.ptr(state_idx),
+            codes[beta.dtype], _lib.ptr(state_in), _lib.ptr(state_out), codes[state_in.dtype], _lib.ptr(state_idx),
             _lib.ptr(token_state_idx), state_in.shape[0], _lib.ptr(out), codes[out.dtype], batch, length, hk,
             hv, dk, dv, float(scale), _lib.stream_handle(dev))
         _lib.check(status, "pbgdn_recurrent_verify_fwd")
         return out, state_out
     status = _lib.lib().pbgdn_recurrent_fwd(
         _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), codes[q.dtype], _lib.ptr(g), _lib.ptr(beta),
-        codes[beta.dtype], _lib.ptr(state_in), _lib.ptr(state_out), _lib.ptr(state_idx),
+        codes[beta.dtype], _lib.ptr(state_in), _lib.ptr(state_out), codes[state_in.dtype], _lib.ptr(state_idx),
         state_in.shape[0], _lib.ptr(out), codes[out.dtype], batch, length, hk, hv, dk, dv, float(scale),
         _lib.stream_handle(dev))
     _lib.check(status, "pbgdn_recurrent_fwd")
@@ -212,6 +276,20 @@ def recurrent_step_(q, k, v, g, beta, state, state_idx, scale):
 
 @recurrent_step_.register_fake
 def _(q, k, v, g, beta, state, state_idx, scale):
+    return q.new_empty(q.shape[0], q.shape[1], v.shape[2], v.shape[3])
+
+
+@torch.library.custom_op("pbgdn::chunk_slots_", mutates_args=("states",),
+                         schema="(Tensor q, Tensor k, Tensor v, Tensor g, Tensor beta, Tensor(a!) states, "
+                                "Tensor state_idx, Tensor? cu_seqlens, Tensor? has_initial_state, "
+                                "float scale) -> Tensor")
+def chunk_slots_(q, k, v, g, beta, states, state_idx, cu_seqlens, has_initial_state, scale):
+    """Prefill against state slots (chunk_fwd_slots), updating `states` in place; o in q's dtype."""
+    return chunk_fwd_slots(q, k, v, g, beta, scale, states, state_idx, cu_seqlens, has_initial_state)
+
+
+@chunk_slots_.register_fake
+def _(q, k, v, g, beta, states, state_idx, cu_seqlens, has_initial_state, scale):
     return q.new_empty(q.shape[0], q.shape[1], v.shape[2], v.shape[3])
 
 

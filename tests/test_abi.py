@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version_and_status_strings():
-    assert _lib.lib().pbgdn_abi_version() == _lib.ABI_VERSION == 3
+    assert _lib.lib().pbgdn_abi_version() == _lib.ABI_VERSION == 4
     header = open(HEADER).read()
     assert re.search(r"#define PBGDN_ABI_VERSION (\d+)", header).group(1) == str(_lib.ABI_VERSION)
     assert _lib.status_string(0) == "ok"
@@ -43,7 +43,7 @@ FAKE = 0x1000  # never dereferenced: every call below fails validation first
 
 def chunk_call(**over):
     args = dict(q=FAKE, k=FAKE, v=FAKE, in_dtype=1, g=FAKE, beta=FAKE, beta_dtype=0, h0=None,
-                ht=None, cu=None, nseq=1, o=FAKE, out_dtype=1, B=1, T=64, Hk=16, Hv=32, K=128,
+                ht=None, sdt=0, sidx=None, has_init=None, nstates=0, cu=None, nseq=1, o=FAKE, out_dtype=1, B=1, T=64, Hk=16, Hv=32, K=128,
                 V=128, scale=0.1, chunk=64, ws=FAKE, ws_bytes=1 << 40, stream=None)
     args.update(over)
     return _lib.lib().pbgdn_chunk_fwd(*args.values())
@@ -51,7 +51,7 @@ def chunk_call(**over):
 
 def recurrent_call(**over):
     args = dict(q=FAKE, k=FAKE, v=FAKE, in_dtype=1, g=FAKE, beta=FAKE, beta_dtype=0, sin=FAKE,
-                sout=FAKE, idx=None, nstates=1, o=FAKE, out_dtype=1, B=1, T=1, Hk=16, Hv=32, K=128,
+                sout=FAKE, sdt=0, idx=None, nstates=1, o=FAKE, out_dtype=1, B=1, T=1, Hk=16, Hv=32, K=128,
                 V=128, scale=0.1, stream=None)
     args.update(over)
     return _lib.lib().pbgdn_recurrent_fwd(*args.values())
@@ -73,6 +73,8 @@ def recurrent_call(**over):
     (dict(ws=None), _lib.ERR_INVALID_ARGUMENT),
     (dict(ws=FAKE + 8), _lib.ERR_INVALID_ARGUMENT),     # workspace must be 16-byte aligned
     (dict(ws_bytes=1000), _lib.ERR_INVALID_ARGUMENT),  # smaller than pbgdn_chunk_workspace_size
+    (dict(sdt=3), _lib.ERR_INVALID_ARGUMENT),           # state dtype code
+    (dict(sidx=FAKE, nstates=-1), _lib.ERR_INVALID_ARGUMENT),
 ])
 def test_chunk_fwd_rejects(over, code):
     assert chunk_call(**over) == code
@@ -90,6 +92,11 @@ def test_chunk_fwd_empty_is_ok():
     (dict(o=None), _lib.ERR_INVALID_ARGUMENT),
     (dict(nstates=-1), _lib.ERR_INVALID_ARGUMENT),
     (dict(B=4, nstates=3), _lib.ERR_INVALID_ARGUMENT),  # without state_idx, slot b must exist
+    (dict(sdt=4), _lib.ERR_INVALID_ARGUMENT),           # state dtype code
+    (dict(sin=FAKE + 8), _lib.ERR_INVALID_ARGUMENT),    # a float32 state moves in 16-byte pieces
+    (dict(sout=FAKE + 4, sdt=1), _lib.ERR_INVALID_ARGUMENT),  # a 16-bit state in 8-byte pieces
+    (dict(v=FAKE + 8), _lib.ERR_INVALID_ARGUMENT),      # q, k, v are read in aligned words
+    (dict(beta=FAKE + 2), _lib.ERR_INVALID_ARGUMENT),   # beta in 4-byte words
     (dict(K=48), _lib.ERR_UNSUPPORTED),
     (dict(V=512), _lib.ERR_UNSUPPORTED),
     (dict(B=70000, nstates=70000), _lib.ERR_UNSUPPORTED),
@@ -178,7 +185,7 @@ def test_epilogue_fwd_rejects(over, code):
 
 def verify_call(**over):
     args = dict(q=FAKE, k=FAKE, v=FAKE, in_dtype=1, g=FAKE, beta=FAKE, beta_dtype=0, sin=FAKE,
-                states=FAKE, idx=None, tidx=FAKE, nstates=8, o=FAKE, out_dtype=1, B=2, T=4, Hk=16, Hv=32,
+                states=FAKE, sdt=0, idx=None, tidx=FAKE, nstates=8, o=FAKE, out_dtype=1, B=2, T=4, Hk=16, Hv=32,
                 K=128, V=128, scale=0.1, stream=None)
     args.update(over)
     return _lib.lib().pbgdn_recurrent_verify_fwd(*args.values())
@@ -188,6 +195,8 @@ def verify_call(**over):
     (dict(tidx=None), _lib.ERR_INVALID_ARGUMENT),        # the per-token slot table is required
     (dict(states=None), _lib.ERR_INVALID_ARGUMENT),
     (dict(nstates=1), _lib.ERR_INVALID_ARGUMENT),        # without state_idx, slot b must exist
+    (dict(sdt=-1), _lib.ERR_INVALID_ARGUMENT),
+    (dict(states=FAKE + 2, sdt=2), _lib.ERR_INVALID_ARGUMENT),
     (dict(beta_dtype=2), _lib.ERR_INVALID_ARGUMENT),
     (dict(Hv=20), _lib.ERR_INVALID_ARGUMENT),
     (dict(K=48), _lib.ERR_UNSUPPORTED),

@@ -58,6 +58,7 @@ def test_custom_ops_are_registered_with_shape_inference():
     from torch._subclasses.fake_tensor import FakeTensorMode
     assert hasattr(torch.ops.pbgdn, "gated_delta_chunk")
     assert hasattr(torch.ops.pbgdn, "recurrent_step_")
+    assert hasattr(torch.ops.pbgdn, "chunk_slots_")
     with FakeTensorMode():
         q, k, v, g, beta, h0 = inputs(batch=1, length=300, hk=2, hv=4, dk=128, dv=64)
         cu = torch.zeros(4, dtype=torch.int32)
@@ -69,3 +70,7 @@ def test_custom_ops_are_registered_with_shape_inference():
         o2 = torch.ops.pbgdn.recurrent_step_(q[:, :1], k[:, :1], v[:, :1], g[:, :1], beta[:, :1],
                                              state, None, 0.1)
         assert o2.shape == (1, 1, 4, 64)
+        pool = torch.zeros(6, 4, 128, 64, dtype=torch.bfloat16)
+        o3 = torch.ops.pbgdn.chunk_slots_(q, k, v, g, beta, pool, torch.zeros(1, dtype=torch.int32), None, None,
+                                          0.1)
+        assert o3.shape == (1, 300, 4, 64) and o3.dtype == torch.bfloat16
