@@ -12,7 +12,9 @@ The same line carries the decode step (64 sequences x 1 token, state
 fraction of HBM bandwidth, the same step with the state held in bf16 (a
 serving cache's default), an ungraded 256-sequence decode (state larger than
 the 256 MB Infinity Cache), the fused layer prologue and epilogue kernels at
-the same T and head shape with their HBM rooflines, the varlen (8 packed
+the same T and head shape with their HBM rooflines, the fused one-kernel
+decode step of the whole layer (64 sequences; against the same step as three
+launches), the varlen (8 packed
 sequences, 262,144 tokens) and streamed (1,048,576 tokens in 16 segments)
 prefill workloads, the roofline of the prefill kernel measured with
 HIP events on the stream it runs on, and the CPU baseline: the numpy oracle
@@ -285,6 +287,49 @@ def bench_layer(length, steps, warmup=3):
     return out
 
 
+def bench_decode_layer(batch, steps, warmup=10, state_dtype=None):
+    """The fused decode step of the whole layer (pbgdn_decode_layer_fwd) at the
+    Qwen3-Next layer shape for `batch` sequences of one token, state and conv
+    pools updated in place, against the same step as three launches (the
+    layer prologue, the recurrent step, the epilogue). HBM roofline of the
+    fused step: the state read and written, the projection row read, the conv
+    tail read and written, hs written."""
+    import torch
+    from pseudobrain_amd.layer import decode_layer_step, layer_epilogue, layer_prologue
+    gen = torch.Generator().manual_seed(1)
+    hk, hv, dk, dv, conv = 16, 32, 128, 128, 4
+    channels = 2 * hk * dk + hv * dv
+    width = channels + hv * dv + 2 * hv
+    z = torch.randn(batch, width, generator=gen).to(torch.bfloat16).cuda()
+    pool = torch.randn(batch, conv - 1, channels, generator=gen).cuda()
+    weight = ((torch.rand(channels, conv, generator=gen) * 2 - 1) / 2).cuda()
+    a_log = torch.empty(hv).uniform_(0, 16, generator=gen).log().cuda()
+    dt_bias = (torch.randn(hv, generator=gen) - 4).cuda()
+    state = (torch.randn(batch, hv, dk, dv, generator=gen) * 0.02).cuda()
+    if state_dtype is not None:
+        state = state.to(state_dtype)
+    o_norm = torch.ones(dv).cuda()
+
+    def fused():
+        decode_layer_step(z, pool, weight, a_log, dt_bias, state, o_norm, hk, dk, hv, dv)
+
+    def three():
+        q, k, v, g, beta, gate, new_tail = layer_prologue(z[:, None], pool, weight, a_log, dt_bias, hk, dk, hv, dv)
+        o = torch.ops.pbgdn.recurrent_step_(q, k, v, g, beta, state, None, dk ** -0.5)
+        layer_epilogue(o, gate, o_norm)
+
+    sec, ksec = timed_steps(fused, steps, warmup)
+    sec3, ksec3 = timed_steps(three, steps, warmup)
+    nbytes = (2 * batch * hv * dk * dv * state.element_size() + batch * width * 2 + 2 * batch * (conv - 1) * channels * 4
+              + batch * hv * dv * 4)
+    gbs = nbytes / ksec / 1e9
+    return {"batch": batch, "state_dtype": str(state.dtype).replace("torch.", ""), "steps": steps,
+            "us_per_step": sec * 1e6, "kernel_us": ksec * 1e6, "bytes_per_step": nbytes,
+            "three_launches_us_per_step": ksec3 * 1e6,
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs / HBM_PEAK_GBS}}
+
+
 def copy_probe(reps=5):
     """A plain device copy of COPY_PROBE_BYTES (torch's copy kernel): the
     reference point that scales the FETCH_SIZE/WRITE_SIZE counters, and a
@@ -371,6 +416,9 @@ def main(argv=None):
             result["decode_b256_ungraded"] = bench_decode(256, 200)
     if not args.no_layer:
         result.update(bench_layer(shape.length, 20))
+        if not args.no_decode:
+            result["decode_layer_b64"] = bench_decode_layer(64, 200)
+            result["decode_layer_b64_bf16_state"] = bench_decode_layer(64, 200, state_dtype=torch.bfloat16)
     if not args.no_long:
         result.update(bench_long())
     if args.copy_probe:

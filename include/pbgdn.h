@@ -21,6 +21,12 @@
  *                        short_convolution :314-338, l2_normalize :59-70);
  *   pbgdn_epilogue_fwd   per-head RMSNorm x o_norm x SiLU(gate) (:439-441).
  *
+ * and one fuses all three for the decode step (one token per sequence):
+ *
+ *   pbgdn_decode_layer_fwd  projection row -> conv, norms, gates -> recurrent
+ *                        step -> RMSNorm/gate output, conv tail and state
+ *                        updated in place in their slot pools.
+ *
  * Conventions (all entry points):
  *   - every pointer is device memory owned by the caller; nothing is allocated
  *     (scratch memory comes in as a caller-provided workspace);
@@ -50,7 +56,7 @@
 extern "C" {
 #endif
 
-#define PBGDN_ABI_VERSION 4
+#define PBGDN_ABI_VERSION 5
 
 /* element types */
 #define PBGDN_F32 0
@@ -250,6 +256,46 @@ int pbgdn_epilogue_fwd(const void *o, int o_dtype, const void *gate,
                        long gate_stride, int gate_dtype, const float *o_norm,
                        float eps, void *out, int out_dtype, int B, int T,
                        int Hv, int V, void *stream);
+
+/*
+ * Fused decode step of a GatedDeltaNetLayer: one token per sequence, from the
+ * input projection to the layer output, in one launch (GatedDeltaNetLayer.forward
+ * at T = 1, gated_deltanet.py:415-441: short_convolution :314-338,
+ * l2_normalize :59-70, the gates :425-427, delta_rule_sequential :93-107, the
+ * epilogue :439-441). q, k and v stay float32 between the convolution and the
+ * recurrence, as on the reference's sequential path. No reference counterpart
+ * as one call: the reference runs these as separate torch steps.
+ *
+ *   z           [B, z_stride] in_dtype rows of the projection, the columns
+ *               [q | k | v | gate | a | b] (2 Hk K + 2 Hv V + 2 Hv of them)
+ *   conv_state  pool of conv tails, conv_dtype: row j (0 = oldest) of channel c
+ *               of slot s at element s * conv_slot_stride + j * conv_row_stride
+ *               + c * conv_chan_stride (so [S, conv-1, C] and vLLM's
+ *               channel-major [S, C, conv-1] both work); the tail shifts by one
+ *               row in place; NULL when conv <= 1
+ *   conv_weight [2 Hk K + Hv V, conv] float32 (NULL when conv == 0)
+ *   a_log, dt_bias [Hv] float32; l2_mode as pbgdn_prologue_fwd
+ *   state       pool [S, Hv, K, V] state_dtype, updated in place (aligned to
+ *               4 elements)
+ *   state_idx   [B] int32 slot of each sequence in both pools, or NULL for
+ *               slot b; a slot outside [0, num_states) touches no pool and its
+ *               output is zeros; the slots of one call must be distinct
+ *   o_norm      [V] float32; eps the RMSNorm epsilon (the reference's 1e-5)
+ *   hs          [B, Hv V] out_dtype, written
+ *   scale       query scale (K ** -0.5)
+ *
+ * Supported: K, V in {64, 128}; conv 0..4; Hv a multiple of Hk, at most 8 Hk.
+ */
+int pbgdn_decode_layer_fwd(const void *z, long z_stride, int in_dtype,
+                           void *conv_state, int conv_dtype,
+                           long conv_slot_stride, long conv_row_stride,
+                           long conv_chan_stride, const float *conv_weight,
+                           int conv, const float *a_log, const float *dt_bias,
+                           int l2_mode, void *state, int state_dtype,
+                           const int32_t *state_idx, int num_states,
+                           const float *o_norm, float eps, void *hs,
+                           int out_dtype, int B, int Hk, int Hv, int K, int V,
+                           float scale, void *stream);
 
 #ifdef __cplusplus
 }

@@ -13,6 +13,7 @@ typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint16_t u16;
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t v2u32_t __attribute__((ext_vector_type(2)));
 typedef uint32_t v4u32_t __attribute__((ext_vector_type(4)));
 

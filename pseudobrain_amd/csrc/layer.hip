@@ -14,6 +14,7 @@
 // Epilogue: V/8 lanes per (token, value head) row, 8 elements each; the mean
 // square over the head is a shuffle reduction inside the row group.
 #include "chunk.hpp"  // buffer-resource helpers (rsrc, buf_load16, OUT_OF_RANGE)
+#include "layer_math.hpp"
 
 namespace pbgdn {
 namespace {
@@ -142,24 +143,6 @@ __device__ __forceinline__ Raw8 load_raw8(__amdgpu_buffer_rsrc_t r, uint32_t off
   x.b = WIDE ? buf_load16(r, off + 16) : uint4{0u, 0u, 0u, 0u};
   return x;
 }
-
-// The value a float takes after a round trip through `dtype` (the reference
-// casts the carried tail to the input's dtype before the convolution).
-__device__ __forceinline__ float through(float x, int dtype) {
-  if (dtype == PBGDN_BF16) return bf16_bits_to_float(float_to_bf16_bits(x));
-  if (dtype == PBGDN_F16) return static_cast<float>(static_cast<half_t>(x));
-  return x;
-}
-
-__device__ __forceinline__ float sigmoidf(float x) { return 1.f / (1.f + expf(-x)); }
-// x sigmoid(x) on v_exp_f32 and v_rcp_f32 (about 1e-7 relative error; the
-// IEEE-exact forms cost ~25 VALU operations per element and made both
-// kernels VALU-bound)
-__device__ __forceinline__ float siluf(float x) {
-  return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
-}
-// torch.nn.functional.softplus with beta 1, threshold 20
-__device__ __forceinline__ float softplusf(float x) { return x > 20.f ? x : log1pf(expf(x)); }
 
 // Sum over groups of `width` lanes (a power of two up to 16), inside a
 // 16-lane row.

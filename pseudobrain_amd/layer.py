@@ -11,6 +11,10 @@ epilogue of GatedDeltaNetLayer.forward (pseudobrain/gated_deltanet.py:403-441).
     layer_epilogue(o, gate, o_norm, eps)  ->  hs                      (:439-441)
         one kernel (pbgdn_epilogue_fwd): per-head RMSNorm x o_norm x SiLU(gate)
 
+For decode (one token per sequence), decode_layer_step does all of it in one
+kernel (pbgdn_decode_layer_fwd), against slot pools of conv tails and states
+updated in place, the way a serving cache holds them.
+
 q and k come out [B,T,Hk,K] without the GQA repeat (:422-424): the operator
 maps value head h to key head h // (Hv // Hk) itself. Both kernels run on the
 GPU only; a missing library or a CPU tensor raises.
@@ -25,6 +29,7 @@ NORM_EPS = 1e-5           # gated_deltanet.py:72
 L2_MODES = ("max", "hf")  # gated_deltanet.py:57
 PROLOGUE_KEY_DIMS = (64, 128)
 EPILOGUE_VALUE_DIMS = (64, 128)
+DECODE_HEAD_DIMS = (64, 128)
 MAX_CONV = 4
 
 
@@ -144,3 +149,87 @@ def layer_epilogue(o: torch.Tensor, gate: torch.Tensor, o_norm: torch.Tensor, ep
         float(eps), _lib.ptr(out), codes[out_dtype], batch, length, hv, dv, _lib.stream_handle(dev))
     _lib.check(status, "pbgdn_epilogue_fwd")
     return out
+
+
+def decode_layer_step(z: torch.Tensor, conv_state: torch.Tensor | None, conv_weight: torch.Tensor | None,
+                      A_log: torch.Tensor, dt_bias: torch.Tensor, state: torch.Tensor, o_norm: torch.Tensor,
+                      heads: int, key_dim: int, value_heads: int, value_dim: int,
+                      state_idx: torch.Tensor | None = None, l2norm: str = "max", eps: float = NORM_EPS, *,
+                      scale: float | None = None, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """One decode token per sequence through GatedDeltaNetLayer.forward from the
+    projection to hs (gated_deltanet.py:415-441) in one kernel: the short
+    convolution against the carried tail, SiLU, q/k L2 norms, the gates, the
+    recurrent step (delta_rule_sequential, :93-107, with q, k, v kept float32
+    as on that path), and the RMSNorm x o_norm x SiLU(gate) epilogue.
+
+    z [B, 2*heads*key_dim + 2*value_heads*value_dim + 2*value_heads] (or
+    [B, 1, ...]) is the projection of the token; conv_state [S, conv-1,
+    channels] is the pool of tails (any strides: a channel-major pool viewed as
+    [S, conv-1, channels] works) and state [S, Hv, K, V] the pool of recurrent
+    states (float32, bfloat16 or float16), both updated in place at slot
+    state_idx[b] (int32 [B], or None for slot b; a slot outside the pools
+    touches nothing and gives zeros). Returns hs [B, value_heads*value_dim] in
+    out_dtype."""
+    if l2norm not in L2_MODES:
+        raise ValueError(f"l2 normalization mode must be one of {L2_MODES}")
+    if heads < 1 or value_heads % heads:
+        raise ValueError("gated deltanet value heads must be a multiple of the key heads")
+    if key_dim not in DECODE_HEAD_DIMS or value_dim not in DECODE_HEAD_DIMS:
+        raise ValueError(f"decode_layer_step supports key and value widths {DECODE_HEAD_DIMS}")
+    if z.ndim == 3 and z.shape[1] == 1:
+        z = z[:, 0]
+    channels = 2 * heads * key_dim + value_heads * value_dim
+    width = channels + value_heads * value_dim + 2 * value_heads
+    if z.ndim != 2 or z.shape[1] != width:
+        raise ValueError(f"z must be [B, {width}] ([q | k | v | gate | a | b] of one token)")
+    if z.stride(1) != 1:
+        z = z.contiguous()
+    dev = z.device
+    if dev.type != "cuda":
+        raise RuntimeError(f"pbgdn kernels run on ROCm devices only (got a tensor on '{dev}'); "
+                           "this package has no CPU path")
+    codes = _lib.DTYPE_CODES
+    batch = z.shape[0]
+    if (state.ndim != 4 or state.shape[1:] != (value_heads, key_dim, value_dim) or state.dtype not in codes
+            or not state.is_contiguous()):
+        raise ValueError(f"state must be a contiguous [S,{value_heads},{key_dim},{value_dim}] float32, bfloat16 "
+                         "or float16 pool")
+    conv = 0 if conv_weight is None else conv_weight.shape[1]
+    if conv_weight is not None:
+        if conv_weight.shape != (channels, conv) or not 1 <= conv <= MAX_CONV:
+            raise ValueError(f"conv_weight must be [{channels}, conv] with 1 <= conv <= {MAX_CONV}")
+        conv_weight = conv_weight.to(device=dev, dtype=torch.float32).contiguous()
+    if conv > 1:
+        if (conv_state is None or conv_state.ndim != 3 or conv_state.shape[1:] != (conv - 1, channels)
+                or conv_state.shape[0] != state.shape[0] or conv_state.dtype not in codes):
+            raise ValueError(f"conv_state must be a [S, conv-1, channels] = [{state.shape[0]}, {conv - 1}, "
+                             f"{channels}] pool with the state pool's slots")
+        strides = conv_state.stride()
+    else:
+        conv_state, strides = None, (0, 0, 0)
+    if state_idx is None:
+        if state.shape[0] < batch:
+            raise ValueError("without state_idx the pools need a slot per sequence")
+    else:
+        if state_idx.shape != (batch,):
+            raise ValueError("state_idx must be [B]")
+        state_idx = state_idx.to(device=dev, dtype=torch.int32).contiguous()
+    if z.dtype not in codes or out_dtype not in codes:
+        raise ValueError("z and out_dtype must be float32, bfloat16 or float16")
+    a_log = A_log.to(device=dev, dtype=torch.float32).contiguous()
+    dtb = dt_bias.to(device=dev, dtype=torch.float32).contiguous()
+    norm = o_norm.to(device=dev, dtype=torch.float32).contiguous()
+    if a_log.shape != (value_heads,) or dtb.shape != (value_heads,) or norm.shape != (value_dim,):
+        raise ValueError(f"A_log and dt_bias must be [{value_heads}], o_norm [{value_dim}]")
+    if not eps >= 0:
+        raise ValueError("eps must be >= 0")
+    hs = torch.empty(batch, value_heads * value_dim, dtype=out_dtype, device=dev)
+    status = _lib.lib().pbgdn_decode_layer_fwd(
+        _lib.ptr(z), z.stride(0), codes[z.dtype], _lib.ptr(conv_state),
+        codes[conv_state.dtype] if conv_state is not None else _lib.F32, *strides, _lib.ptr(conv_weight), conv,
+        _lib.ptr(a_log), _lib.ptr(dtb), L2_MODES.index(l2norm), _lib.ptr(state), codes[state.dtype],
+        _lib.ptr(state_idx), state.shape[0], _lib.ptr(norm), float(eps), _lib.ptr(hs), codes[out_dtype], batch,
+        heads, value_heads, key_dim, value_dim, float(key_dim ** -0.5 if scale is None else scale),
+        _lib.stream_handle(dev))
+    _lib.check(status, "pbgdn_decode_layer_fwd")
+    return hs

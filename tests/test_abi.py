@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version_and_status_strings():
-    assert _lib.lib().pbgdn_abi_version() == _lib.ABI_VERSION == 4
+    assert _lib.lib().pbgdn_abi_version() == _lib.ABI_VERSION == 5
     header = open(HEADER).read()
     assert re.search(r"#define PBGDN_ABI_VERSION (\d+)", header).group(1) == str(_lib.ABI_VERSION)
     assert _lib.status_string(0) == "ok"
@@ -209,3 +209,36 @@ def test_recurrent_verify_fwd_rejects(over, code):
 def test_recurrent_verify_fwd_empty_is_ok():
     assert verify_call(B=0) == _lib.OK
     assert verify_call(T=0) == _lib.OK
+
+
+def decode_layer_call(**over):
+    width = 2 * 16 * 128 + 2 * 32 * 128 + 64
+    args = dict(z=FAKE, z_stride=width, in_dtype=1, conv_state=FAKE, conv_dtype=0, css=3 * CH, crs=CH, ccs=1,
+                w=FAKE, conv=4, a_log=FAKE, dt_bias=FAKE, l2=0, state=FAKE, sdt=0, idx=None, nstates=64,
+                o_norm=FAKE, eps=1e-5, hs=FAKE, out_dtype=0, B=64, Hk=16, Hv=32, K=128, V=128, scale=0.1,
+                stream=None)
+    args.update(over)
+    return _lib.lib().pbgdn_decode_layer_fwd(*args.values())
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(z_stride=1000), _lib.ERR_INVALID_ARGUMENT),     # rows narrower than q|k|v|gate|a|b
+    (dict(conv=5), _lib.ERR_INVALID_ARGUMENT),
+    (dict(conv_state=None), _lib.ERR_INVALID_ARGUMENT),   # conv > 1 needs the tail pool
+    (dict(w=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(l2=2), _lib.ERR_INVALID_ARGUMENT),
+    (dict(eps=-1.0), _lib.ERR_INVALID_ARGUMENT),
+    (dict(state=FAKE + 8), _lib.ERR_INVALID_ARGUMENT),    # a float32 state moves in 16-byte pieces
+    (dict(nstates=10), _lib.ERR_INVALID_ARGUMENT),        # without state_idx, slot b must exist
+    (dict(sdt=3), _lib.ERR_INVALID_ARGUMENT),
+    (dict(Hv=24), _lib.ERR_INVALID_ARGUMENT),
+    (dict(Hk=2, z_stride=1 << 20), _lib.ERR_UNSUPPORTED),  # 16 value heads per key head: more than 8
+    (dict(K=96), _lib.ERR_UNSUPPORTED),
+    (dict(V=256, z_stride=1 << 20), _lib.ERR_UNSUPPORTED),
+])
+def test_decode_layer_fwd_rejects(over, code):
+    assert decode_layer_call(**over) == code
+
+
+def test_decode_layer_fwd_empty_is_ok():
+    assert decode_layer_call(B=0) == _lib.OK
