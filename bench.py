@@ -54,7 +54,7 @@ TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profile
 
 
 def measured_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` ("chunk" or "recurrent_b64") from the
+    """HBM bytes per launch of `kernel` ("chunk", "recurrent_b64", ...) from the
     committed counter summary: lines of the form `traffic_bytes[<kernel>]: <int>`."""
     try:
         with open(TRAFFIC_FILE) as f:
@@ -411,13 +411,15 @@ def main(argv=None):
         bf = bench_decode(64, args.decode_steps, state_dtype=torch.bfloat16)
         result["decode_bf16_state"] = dict(bf, roofline={"bound": "hbm", "achieved": bf["achieved_GBs"],
                                                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                                         "frac": bf["hbm_frac"]})
+                                                         "frac": bf["hbm_frac"],
+                                                         "traffic": measured_traffic("recurrent_b64_bf16_state")})
         if not args.no_b256:
             result["decode_b256_ungraded"] = bench_decode(256, 200)
     if not args.no_layer:
         result.update(bench_layer(shape.length, 20))
         if not args.no_decode:
             result["decode_layer_b64"] = bench_decode_layer(64, 200)
+            result["decode_layer_b64"]["roofline"]["traffic"] = measured_traffic("decode_layer_b64")
             result["decode_layer_b64_bf16_state"] = bench_decode_layer(64, 200, state_dtype=torch.bfloat16)
     if not args.no_long:
         result.update(bench_long())
