@@ -113,6 +113,17 @@ def test_beta_in_input_dtype_and_fp32_output():
     assert_parity("bf16 beta, fp32 o", o, o_ref, s, s_ref)
 
 
+@pytest.mark.parametrize("dk,dv,hk,hv", [(64, 16, 1, 8), (128, 48, 2, 2), (128, 256, 1, 4), (64, 256, 2, 4)])
+def test_value_widths_and_gqa_groups(dk, dv, hk, hv):
+    """Every value width the ABI takes (multiples of 16: one to sixteen column
+    tiles per head), eight value heads on one key head, B = 2 without
+    cu_seqlens, a length that is not a multiple of the chunk."""
+    q, k, v, g, beta, h0 = generate(2, 300, hk, hv, dk, dv, torch.bfloat16, 0.02, seed=dk + dv + hv)
+    o_ref, s_ref = oracle(q, k, v, g, beta, dk ** -0.5, h0)
+    o, s = run(q, k, v, g, beta, dk ** -0.5, h0)
+    assert_parity(f"K={dk} V={dv} {hk}->{hv}", o, o_ref, s, s_ref)
+
+
 def test_varlen_small():
     """8 packed sequences (ragged, one empty, lengths not multiples of 64)."""
     lengths = [700, 64, 0, 1, 1500, 333, 129, 2000]
