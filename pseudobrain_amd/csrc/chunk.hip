@@ -4,6 +4,8 @@
 // state recurrence, chunk_scan.hip). The workspace carries the prep kernel's
 // records to the scan kernel; see chunk.hpp for the algorithm and the record
 // format.
+#include <algorithm>
+
 #include "chunk.hpp"
 
 namespace pbgdn {
@@ -75,9 +77,14 @@ extern "C" int pbgdn_chunk_fwd(const void *q, const void *k, const void *v, int 
   const long total = static_cast<long>(V / pbgdn::VT) * Hv * num_seqs;
   if (total > 0x7fffffffL) return PBGDN_ERR_UNSUPPORTED;
   const long records = pbgdn::chunk_records(static_cast<long>(B) * T, num_seqs);
+  // The scan's sequence groups: one (value head, column tile) pair per CU
+  // needs one group; fewer pairs than CUs split the sequences into groups
+  // to fill them.
+  const int pairs = (V / pbgdn::VT) * Hv;
+  const int groups = std::max(1, std::min(num_seqs, pbgdn::SCAN_CUS / pairs));
   pbgdn::ChunkParams p{q, k, v, g, beta, beta_dtype, h0, ht, state_dtype, state_idx, has_initial_state,
                        num_states, cu_seqlens, o, static_cast<unsigned char *>(workspace), T, Hk, Hv, V,
-                       num_seqs, scale};
+                       num_seqs, groups, scale};
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (K) {
     case 64: return pbgdn::dispatch_in<64>(p, records, in_dtype, out_dtype, s);

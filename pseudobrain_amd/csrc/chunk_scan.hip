@@ -2,9 +2,14 @@
 // chunk (the serial loop of delta_rule_chunked, pseudobrain/gated_deltanet.py:158-165).
 //
 // The recurrence is separable along the value columns, so a workgroup owns
-// one (sequence, value head, 16-column tile of V): grid = V/16 x Hv x N. The
-// fp32 state tile S [K, 16] lives in MFMA accumulators for the whole sequence
-// (compute wave j owns key rows 16j..16j+15) and is read and written once.
+// one (value head, 16-column tile of V) of a group of sequences: grid = V/16
+// x Hv x G. It runs the chunks of the group's sequences back to back as one
+// stream (the pipeline below does not drain between sequences, so many short
+// sequences cost what one long one of the same total does); at the end of a
+// sequence's last chunk the owners write its final state and load the next
+// one's initial state. The fp32 state tile S [K, 16] lives in MFMA
+// accumulators (compute wave j owns key rows 16j..16j+15) and is read and
+// written once per sequence.
 // Everything that does not involve S (Tb, QKD, the decay vectors) comes from
 // the prep kernel's workspace records.
 //
@@ -215,7 +220,7 @@ struct ScanStage {
 // group is kept on one XCD (workgroups are dispatched round-robin over the 8
 // XCDs) so that its q/k chunks and Tb/QKD records are fetched into that XCD's
 // L2 once.
-__device__ __forceinline__ void decode_block(int L, int total, int nv, int group_heads, int Hk, int &seq, int &h,
+__device__ __forceinline__ void decode_block(int L, int total, int nv, int group_heads, int Hk, int &grp_seq, int &h,
                                              int &vtile, int &member) {
   const int gsize = nv * group_heads;
   const int ngroups = total / gsize;
@@ -230,7 +235,7 @@ __device__ __forceinline__ void decode_block(int L, int total, int nv, int group
     in = L % gsize;
   }
   const int hk = grp % Hk;
-  seq = grp / Hk;
+  grp_seq = grp / Hk;
   h = hk * group_heads + in / nv;
   vtile = in % nv;
   member = in;
@@ -247,7 +252,10 @@ __device__ __forceinline__ float out_elem<float>(float x) { return x; }
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
-template <int K, typename TIn, typename TOut>
+// CHAIN: a workgroup runs more than one sequence (the stream crosses sequence
+// boundaries); without it the stream is one sequence and the cursors are
+// plain counters.
+template <int K, typename TIn, typename TOut, bool CHAIN>
 struct ScanBlock {
   using L = ScanLayout<K>;
   using Op = OpOf<TIn>;
@@ -263,8 +271,16 @@ struct ScanBlock {
 
   unsigned char *lds;
   const ChunkParams &p;
-  int tid, lane, c16, g4, wave, seq, h, hk, v0, lt;  // lt: loader thread index (loader waves)
-  long bos, eos, nchunks, rbase;
+  int tid, lane, c16, g4, wave, h, hk, v0, lt;  // lt: loader thread index (loader waves)
+  int s_begin, s_end;  // the group's sequences
+  long nchunks;        // chunks of the group's sequences (the stream's length)
+  // Stream positions: compute waves at the current chunk; loader waves at the
+  // chunk being loaded (three ahead) and at the chunk whose O goes out (one behind).
+  struct Cursor {
+    int s;     // sequence (s_end past the stream's end)
+    int left;  // chunks of s from this one on
+    long t0, eos, rec;  // this chunk's first token, s's end, this chunk's record
+  } cc, lc, oc;
   float4_t sacc;
   Stage stage;
   typename Stage::Regs regs[2];
@@ -272,7 +288,7 @@ struct ScanBlock {
   // Per-lane LDS byte offsets (see lane_offsets()).
   uint32_t kp_frag, sp_frag, kp_tile, sp_tile, tr_v, tr_k0, tr_k1;
 
-  __device__ ScanBlock(unsigned char *l, const ChunkParams &prm) : lds(l), p(prm) {
+  __device__ __forceinline__ ScanBlock(unsigned char *l, const ChunkParams &prm) : lds(l), p(prm) {
     tid = threadIdx.x;
     lane = tid & 63;
     wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -280,13 +296,12 @@ struct ScanBlock {
     g4 = lane >> 4;
     lt = tid - NCW * 64;
     const int group_heads = p.Hv / p.Hk;
-    int vtile, member;
-    decode_block(blockIdx.x, gridDim.x, p.V / VT, group_heads, p.Hk, seq, h, vtile, member);
+    int vtile, member, grp;
+    decode_block(blockIdx.x, gridDim.x, p.V / VT, group_heads, p.Hk, grp, h, vtile, member);
     hk = h / group_heads;
     v0 = vtile * VT;
-    seq_bounds(p, seq, bos, eos);
-    nchunks = (eos - bos + CH - 1) / CH;
-    rbase = rec_base(bos, seq);
+    s_begin = static_cast<int>(static_cast<long>(grp) * p.num_seqs / p.seq_groups);
+    s_end = static_cast<int>(static_cast<long>(grp + 1) * p.num_seqs / p.seq_groups);
     sacc = float4_t{0.f, 0.f, 0.f, 0.f};
     if (wave >= NCW) {
       stage.init(p, lt);
@@ -322,23 +337,122 @@ struct ScanBlock {
   }
 
   // ------------------------------------------------------------ loader waves
-  __device__ __forceinline__ void load_chunk(typename Stage::Regs &r, long n) const {
-    const long t0 = bos + n * CH;
-    const unsigned char *rec = n < nchunks ? p.ws + ((rbase + n) * p.Hv + h) * static_cast<long>(REC_BYTES) : nullptr;
-    stage.load(p, r, t0, eos - t0, hk, h, v0, rec);
+  // -------------------------------------------------------- chunk stream
+  // From sequence s on, the first sequence of the group with tokens (s_end if
+  // none). Wave-uniform; cu_seqlens reads are scalar loads.
+  __device__ __forceinline__ bool enter(Cursor &c) const {  // chunk 0 of sequence c.s, if it has tokens
+    long b, e;
+    seq_bounds(p, c.s, b, e);
+    c.t0 = b;
+    c.eos = e;
+    c.rec = rec_base(b, c.s);
+    c.left = static_cast<int>((e - b + CH - 1) / CH);
+    return e > b;
+  }
+  __device__ __forceinline__ void seek(Cursor &c, int s) const {
+    for (c.s = s; c.s < s_end; ++c.s) {
+      if (enter(c)) return;
+    }
+    c.t0 = c.eos = c.rec = 0;
+    c.left = 0;
+  }
+  __device__ __forceinline__ bool at_end(const Cursor &c) const { return c.s >= s_end; }
+  __device__ __forceinline__ long len_of(const Cursor &c) const { return c.eos - c.t0; }  // 0 at the end
+  // Next chunk of the stream: a few scalar adds except at a sequence's end.
+  __device__ __forceinline__ void advance(Cursor &c) const {
+    if constexpr (!CHAIN) {  // one sequence: past its end the loads have zero size
+      c.t0 += CH;
+      ++c.rec;
+      return;
+    }
+    if (at_end(c)) return;
+    if (--c.left > 0) {
+      c.t0 += CH;
+      ++c.rec;
+    } else {
+      seek(c, c.s + 1);
+    }
+  }
+  __device__ __forceinline__ const unsigned char *rec_of(const Cursor &c) const {
+    const bool none = CHAIN ? at_end(c) : c.t0 >= c.eos;
+    return none ? nullptr : p.ws + (c.rec * p.Hv + h) * static_cast<long>(REC_BYTES);
   }
 
-  // O tile of chunk n (LDS buffer n & 1) -> HBM, one 16-byte unit per loader
-  // thread; n < 0 issues the same store with a zero-size resource.
+  // ------------------------------------------------------------ loader waves
+  __device__ __forceinline__ void load_chunk(typename Stage::Regs &r, const Cursor &c) const {
+    stage.load(p, r, c.t0, len_of(c), hk, h, v0, rec_of(c));
+  }
+
+  // O tile of stream chunk n (LDS buffer n & 1, at cursor oc) -> HBM, one
+  // 16-byte unit per loader thread; n < 0 issues the same store with a
+  // zero-size resource.
   __device__ __forceinline__ void store_out(long n) const {
-    const long t0 = bos + n * CH;
-    const long len = eos - t0;
+    const long t0 = n >= 0 ? oc.t0 : 0;
+    const long len = n >= 0 ? len_of(oc) : 0;
     const long rows = len < CH ? len : CH;
-    const long bytes = n >= 0 ? ((rows - 1) * p.Hv * p.V + VT) * static_cast<long>(sizeof(TOut)) : 0;
+    const long bytes = rows > 0 ? ((rows - 1) * p.Hv * p.V + VT) * static_cast<long>(sizeof(TOut)) : 0;
     const __amdgpu_buffer_rsrc_t ro =
         rsrc(static_cast<TOut *>(p.o) + (t0 * p.Hv + h) * static_cast<long>(p.V) + v0, bytes);
     const uint4 x = ld<uint4>(L::ot(static_cast<int>(n & 1)) + out_src);
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, x), ro, out_dst, 0, 0);
+  }
+
+  // ------------------------------------------------------------- states
+  // Slot of sequence s in the state tensors (its index without state_idx);
+  // a slot outside [0, num_states) starts from zeros and keeps no final state.
+  __device__ __forceinline__ long slot_of(int s) const {
+    return p.state_idx ? static_cast<long>(p.state_idx[s]) : static_cast<long>(s);
+  }
+  __device__ __forceinline__ bool in_pool(long slot) const {
+    return !p.state_idx || (slot >= 0 && slot < p.num_states);
+  }
+  // This lane's 4 elements of key tile kt of sequence s's initial state.
+  __device__ __forceinline__ float4_t initial_state(int s, int kt) const {
+    float4_t x = {0.f, 0.f, 0.f, 0.f};
+    const long slot = slot_of(s);
+    if (p.h0 && in_pool(slot) && (!p.has_initial_state || p.has_initial_state[s])) {
+      const long base = (slot * p.Hv + h) * K * p.V + v0 + c16;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[i] = load_elem(p.h0, base + static_cast<long>(16 * kt + 4 * g4 + i) * p.V, p.state_dtype);
+    }
+    return x;
+  }
+  __device__ __forceinline__ void final_state(int s, int kt, float4_t x) const {
+    const long slot = slot_of(s);
+    if (p.ht && in_pool(slot)) {
+      const long base = (slot * p.Hv + h) * K * p.V + v0 + c16;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) store_elem(p.ht, base + static_cast<long>(16 * kt + 4 * g4 + i) * p.V, p.state_dtype, x[i]);
+    }
+  }
+  // sacc -> the S^T high/low operand copies in LDS (key tile kt).
+  __device__ __forceinline__ void put_state(int kt) const {
+    const O4 hi = Op::from(sacc);
+    st(L::SH + kp_tile + 32 * kt, hi);
+    st(L::SL + kp_tile + 32 * kt, Op::from(sacc - Op::to(hi)));
+  }
+  // Owners, from sequence s on: pass the empty sequences' initial states to
+  // their final states, and stop at the first one with tokens.
+  __device__ __forceinline__ void seek_owner(Cursor &c, int s, int kt) const {
+    for (c.s = s; c.s < s_end; ++c.s) {
+      if (enter(c)) return;
+      final_state(c.s, kt, initial_state(c.s, kt));
+    }
+    c.left = 0;
+  }
+  // Owners, phase 3 of each tick, after the state update of the cursor's
+  // chunk: at a sequence's last chunk its final state goes out and the next
+  // sequence's initial state (loaded first) replaces it; then the cursor
+  // moves on.
+  __device__ __forceinline__ void next_chunk(int kt) {
+    if constexpr (!CHAIN) return;  // the one sequence's final state goes out after the loop
+    if (--cc.left > 0) return;
+    const int done = cc.s;
+    const float4_t fin = sacc;
+    seek_owner(cc, done + 1, kt);
+    sacc = at_end(cc) ? float4_t{0.f, 0.f, 0.f, 0.f} : initial_state(cc.s, kt);
+    final_state(done, kt, fin);
+    put_state(kt);
   }
 
   // ------------------------------------------------------------ compute waves
@@ -457,6 +571,7 @@ struct ScanBlock {
       const float4_t nvv = Op::bits_to_float(ld_tr(L::v16(b ^ 1) + 16 * r * 32 + tr_v));
       const float4_t ngg = rec_rows(b ^ 1, SC_GAM, r);
       update_state(b, kt);
+      next_chunk(wave);
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk) mf[kk] = nmf[kk];
       vv = nvv;
@@ -514,7 +629,10 @@ struct ScanBlock {
     {
       O8 nmf[KS];
       fetch_rows(b ^ 1, 1, nmf);
-      if constexpr (NKT > 4) update_state(b, kt);
+      if constexpr (NKT > 4) {
+        update_state(b, kt);
+        next_chunk(wave);
+      }
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk) mf[kk] = nmf[kk];
     }
@@ -528,49 +646,71 @@ struct ScanBlock {
   // phase 2) also goes out.
   template <int P>
   __device__ __forceinline__ void tick_loader(long n) {
-    const long m = n + 3;
-    const long t0 = bos + m * CH;
-    const unsigned char *rec = m < nchunks ? p.ws + ((rbase + m) * p.Hv + h) * static_cast<long>(REC_BYTES) : nullptr;
-    stage.template restage<0, Stage::SLOT_P2>(p, lds, L::kq(P ^ 1), regs[P], lt, t0, eos - t0, hk, h, v0, rec);
+    const long t0 = lc.t0;  // chunk n + 3
+    const long len = len_of(lc);
+    const unsigned char *rec = rec_of(lc);
+    stage.template restage<0, Stage::SLOT_P2>(p, lds, L::kq(P ^ 1), regs[P], lt, t0, len, hk, h, v0, rec);
     block_sync();
-    stage.template restage<Stage::SLOT_P2, Stage::SLOT_P3>(p, lds, L::kq(P ^ 1), regs[P], lt, t0, eos - t0, hk, h,
-                                                            v0, rec);
+    stage.template restage<Stage::SLOT_P2, Stage::SLOT_P3>(p, lds, L::kq(P ^ 1), regs[P], lt, t0, len, hk, h, v0,
+                                                            rec);
     block_sync();
     store_out(n - 1);
-    stage.template restage<Stage::SLOT_P3, Stage::UPT>(p, lds, L::kq(P ^ 1), regs[P], lt, t0, eos - t0, hk, h, v0,
-                                                        rec);
+    if (n > 0) advance(oc);
+    stage.template restage<Stage::SLOT_P3, Stage::UPT>(p, lds, L::kq(P ^ 1), regs[P], lt, t0, len, hk, h, v0, rec);
+    advance(lc);
     block_sync();
   }
 
-  __device__ __forceinline__ void run() {
-    // Initial state: compute wave j owns key rows 16j..16j+15. With state
-    // slots, a slot outside [0, num_states) starts from zeros and keeps no
-    // final state.
-    const long slot = p.state_idx ? static_cast<long>(p.state_idx[seq]) : static_cast<long>(seq);
-    const bool in_pool = !p.state_idx || (slot >= 0 && slot < p.num_states);
-    const bool read_h0 = p.h0 && in_pool && (!p.has_initial_state || p.has_initial_state[seq]);
-    const long state_base = (slot * p.Hv + h) * K * p.V + v0 + c16;
-    const int kt = wave;
-    const bool owner = kt < NKT;
-    if (owner) {
-      if (read_h0) {
+  // Chunks of the group's sequences, summed over the whole workgroup (one
+  // sequence: read directly, with no barrier before the first loads).
+  __device__ __forceinline__ long group_chunks() {
+    if (s_end - s_begin == 1) {
+      long b, e;
+      seq_bounds(p, s_begin, b, e);
+      return (e - b + CH - 1) / CH;
+    }
+    int c = 0;
+    for (int s = s_begin + tid; s < s_end; s += NT) {
+      long b, e;
+      seq_bounds(p, s, b, e);
+      c += static_cast<int>((e - b + CH - 1) / CH);
+    }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          sacc[i] = load_elem(p.h0, state_base + static_cast<long>(16 * kt + 4 * g4 + i) * p.V, p.state_dtype);
-        }
-      }
-      const O4 hi = Op::from(sacc);
-      st(L::SH + kp_tile + 32 * kt, hi);
-      st(L::SL + kp_tile + 32 * kt, Op::from(sacc - Op::to(hi)));
+    for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, 64);
+    int *part = reinterpret_cast<int *>(lds + L::OT);  // the O tiles are not in use yet
+    if (lane == 0) part[wave] = c;
+    block_sync();
+    long total = 0;
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) total += part[w];
+    block_sync();
+    return total;
+  }
+
+  __device__ __forceinline__ void run() {
+    nchunks = group_chunks();
+    // Initial state of the group's first sequence with tokens (the empty ones
+    // before it pass their initial states through): compute wave j owns key
+    // rows 16j..16j+15.
+    const int kt = wave;
+    if (kt < NKT) {
+      seek_owner(cc, s_begin, kt);
+      if (!at_end(cc)) sacc = initial_state(cc.s, kt);
+      put_state(kt);
     }
     if (wave >= NCW) {
       // Chunk 0 into buffer 0; chunks 1 and 2 in flight into register sets 0
       // and 1, each followed by a store that goes nowhere, as in a tick.
-      load_chunk(regs[1], 0);
+      seek(lc, s_begin);
+      oc = lc;
+      load_chunk(regs[1], lc);
+      advance(lc);
       stage.store(lds, L::kq(0), regs[1], lt);
-      load_chunk(regs[0], 1);
+      load_chunk(regs[0], lc);
+      advance(lc);
       store_out(-1);
-      load_chunk(regs[1], 2);
+      load_chunk(regs[1], lc);
+      advance(lc);
       store_out(-1);
       block_sync();
       long n = 0;
@@ -610,29 +750,23 @@ struct ScanBlock {
       if (nchunks > 0) out_tile(static_cast<int>((nchunks - 1) & 1), qs, gs, f0, f1);
       block_sync();
     }
-    if (p.ht && owner && in_pool) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        store_elem(p.ht, state_base + static_cast<long>(16 * kt + 4 * g4 + i) * p.V, p.state_dtype, sacc[i]);
-      }
-    }
+    // With CHAIN, final states went out at each sequence's last chunk (next_chunk).
+    if (!CHAIN && kt < NKT && !at_end(cc)) final_state(cc.s, kt, sacc);
   }
 };
 
-template <int K, typename TIn, typename TOut>
+template <int K, typename TIn, typename TOut, bool CHAIN>
 __global__ __launch_bounds__(NT) void scan_kernel(ChunkParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  ScanBlock<K, TIn, TOut> blk(smem_raw, p);
+  ScanBlock<K, TIn, TOut, CHAIN> blk(smem_raw, p);
   blk.run();
 }
 
-}  // namespace
-
-template <int K, typename TIn, typename TOut>
-int launch_scan(const ChunkParams &p, hipStream_t stream) {
+template <int K, typename TIn, typename TOut, bool CHAIN>
+int launch_scan_kernel(const ChunkParams &p, hipStream_t stream) {
   static bool configured = false;  // benign race: the attribute call is idempotent
   const size_t smem = ScanLayout<K>::BYTES;
-  auto kernel = scan_kernel<K, TIn, TOut>;
+  auto kernel = scan_kernel<K, TIn, TOut, CHAIN>;
   if (!configured) {
     if (hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(smem)) != hipSuccess) {
@@ -640,9 +774,17 @@ int launch_scan(const ChunkParams &p, hipStream_t stream) {
     }
     configured = true;
   }
-  const int total = (p.V / VT) * p.Hv * p.num_seqs;
+  const int total = (p.V / VT) * p.Hv * p.seq_groups;
   hipLaunchKernelGGL(kernel, dim3(total), dim3(NT), smem, stream, p);
   return hipGetLastError() == hipSuccess ? PBGDN_OK : PBGDN_ERR_LAUNCH;
+}
+
+}  // namespace
+
+template <int K, typename TIn, typename TOut>
+int launch_scan(const ChunkParams &p, hipStream_t stream) {
+  if (p.num_seqs > p.seq_groups) return launch_scan_kernel<K, TIn, TOut, true>(p, stream);
+  return launch_scan_kernel<K, TIn, TOut, false>(p, stream);
 }
 
 template int launch_scan<64, u16, u16>(const ChunkParams &, hipStream_t);

@@ -136,6 +136,26 @@ def test_varlen_small():
     assert torch.equal(s[2].cpu(), h0[2])  # the empty sequence returns its initial state
 
 
+@pytest.mark.parametrize("nseq,hk,hv,dv", [(300, 2, 4, 64), (40, 16, 32, 128)])
+def test_many_short_sequences(nseq, hk, hv, dv):
+    """Serving-style packing: many short sequences (0 to 150 tokens, some
+    empty), each from its own initial state. A workgroup of the scan runs a
+    group of sequences back to back (16 groups of ~19 sequences for the small
+    heads, one group of all 40 at the Qwen3-Next heads), swapping states at
+    every boundary."""
+    lengths = torch.randint(0, 151, (nseq,), generator=torch.Generator().manual_seed(nseq)).tolist()
+    lengths[3] = 0
+    lengths[nseq - 1] = 0
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lengths)]), dtype=torch.int32)
+    q, k, v, g, beta, h0 = generate(1, int(cu[-1]), hk, hv, 128, dv, torch.bfloat16, 0.02, seed=nseq + 1,
+                                    nstates=nseq)
+    o_ref, s_ref = oracle(q, k, v, g, beta, SCALE, h0, cu_seqlens=cu)
+    o, s = run(q, k, v, g, beta, SCALE, h0, cu)
+    assert_parity(f"{nseq} short sequences", o, o_ref, s, s_ref)
+    for i in (3, nseq - 1):  # empty sequences return their initial states
+        assert torch.equal(s[i].cpu(), h0[i])
+
+
 def test_varlen_full_size_packing_equals_separate_calls():
     """262,144 packed tokens in 8 sequences: the packed call equals one call per
     sequence bit for bit, and the shortest sequence matches the oracle."""
