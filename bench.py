@@ -235,6 +235,24 @@ def bench_long(steps=5, warmup=1):
                         "unit": "Mtok/s", "ms_per_pass": sec * 1e3,
                         "roofline": {"bound": "mfma", "achieved": flops / ksec / 1e12, "peak": MFMA_PEAK_TFLOPS,
                                      "unit": "TFLOP/s", "frac": flops / ksec / 1e12 / MFMA_PEAK_TFLOPS}}
+    del q, k, v, g, beta, h0, o
+    # Serving-style batches of the same 32,768 tokens (ungraded): many packed
+    # sequences, each from its own state (the scan runs them back to back).
+    from pseudobrain_amd.workloads import cu_seqlens_of
+    o = torch.empty(1, 32768, 32, 128, dtype=torch.bfloat16, device="cuda")
+    batches = {}
+    for nseq in (64, 256):
+        length = 32768 // nseq
+        q, k, v, g, beta, h0 = generate(1, 32768, 16, 32, 128, 128, torch.bfloat16, 0.02, seed=0, nstates=nseq,
+                                        device="cuda")
+        cu = cu_seqlens_of([length] * nseq).to("cuda")
+
+        def packed():
+            gd.chunk_fwd(q, k, v, g, beta, scale, h0, cu, out=o)
+
+        sec, ksec = timed_steps(packed, steps, warmup)
+        batches[f"{nseq}x{length}"] = {"value": 32768 / ksec / 1e6, "unit": "Mtok/s", "ms_per_call": ksec * 1e3}
+    out["serving_prefill_ungraded"] = batches
     return out
 
 
