@@ -77,11 +77,16 @@ extern "C" int pbgdn_chunk_fwd(const void *q, const void *k, const void *v, int 
   const long total = static_cast<long>(V / pbgdn::VT) * Hv * num_seqs;
   if (total > 0x7fffffffL) return PBGDN_ERR_UNSUPPORTED;
   const long records = pbgdn::chunk_records(static_cast<long>(B) * T, num_seqs);
-  // The scan's sequence groups: one (value head, column tile) pair per CU
-  // needs one group; fewer pairs than CUs split the sequences into groups
-  // to fill them.
+  // The scan's sequence groups. Sequences of 2,048 tokens or more on average
+  // get a workgroup each (the unchained kernel: its step is ~10% shorter,
+  // and a sequence's pipeline fill is small next to its length). Shorter
+  // ones run back to back in groups (a chained workgroup pays ~1 µs per
+  // sequence boundary instead of a fill and drain): one group when the
+  // (value head, column tile) pairs fill the CUs, else enough groups to.
   const int pairs = (V / pbgdn::VT) * Hv;
-  const int groups = std::max(1, std::min(num_seqs, pbgdn::SCAN_CUS / pairs));
+  const long tokens = static_cast<long>(B) * T;
+  const int groups = tokens >= 2048L * num_seqs ? num_seqs
+                                                : std::max(1, std::min(num_seqs, pbgdn::SCAN_CUS / pairs));
   pbgdn::ChunkParams p{q, k, v, g, beta, beta_dtype, h0, ht, state_dtype, state_idx, has_initial_state,
                        num_states, cu_seqlens, o, static_cast<unsigned char *>(workspace), T, Hk, Hv, V,
                        num_seqs, groups, scale};

@@ -81,6 +81,12 @@ struct ScanLayout {
   static constexpr int OT = SL + VT * KPB;            // [2][64 t][16] output type
   static constexpr int OT_BUF = CH * VT * 4;
   static constexpr int BYTES = OT + 2 * OT_BUF;
+  // Chained streams only: the initial state of the sequence whose first
+  // chunk is in chunk buffer b ([K rows][16 columns] as stored), staged by the
+  // loader waves with that chunk.
+  static constexpr int H0_BYTES = K * VT * 4;
+  static constexpr int CHAIN_BYTES = BYTES + 2 * H0_BYTES;
+  __device__ static constexpr int h0(int b) { return BYTES + b * H0_BYTES; }
   __device__ static constexpr int kq(int b) { return b * BUF; }
   __device__ static constexpr int v16(int b) { return b * BUF + V16_OFF; }
   __device__ static constexpr int rec(int b) { return b * BUF + REC_OFF; }
@@ -278,12 +284,15 @@ struct ScanBlock {
   // chunk being loaded (three ahead) and at the chunk whose O goes out (one behind).
   struct Cursor {
     int s;     // sequence (s_end past the stream's end)
-    int left;  // chunks of s from this one on
+    int left;    // chunks of s from this one on
+    bool first;  // this chunk is s's first
     long t0, eos, rec;  // this chunk's first token, s's end, this chunk's record
   } cc, lc, oc;
   float4_t sacc;
   Stage stage;
   typename Stage::Regs regs[2];
+  uint4 h0r[2][2];  // chained streams: loader thread's 16-byte units of a chunk's initial state, per register set
+  bool h0v[2];      // the set holds a sequence's first chunk (its units go to LDS)
   uint32_t out_src, out_dst;  // loader thread's O unit: LDS offset in a tile, byte offset in a chunk
   // Per-lane LDS byte offsets (see lane_offsets()).
   uint32_t kp_frag, sp_frag, kp_tile, sp_tile, tr_v, tr_k0, tr_k1;
@@ -347,6 +356,7 @@ struct ScanBlock {
     c.eos = e;
     c.rec = rec_base(b, c.s);
     c.left = static_cast<int>((e - b + CH - 1) / CH);
+    c.first = true;
     return e > b;
   }
   __device__ __forceinline__ void seek(Cursor &c, int s) const {
@@ -355,6 +365,7 @@ struct ScanBlock {
     }
     c.t0 = c.eos = c.rec = 0;
     c.left = 0;
+    c.first = false;
   }
   __device__ __forceinline__ bool at_end(const Cursor &c) const { return c.s >= s_end; }
   __device__ __forceinline__ long len_of(const Cursor &c) const { return c.eos - c.t0; }  // 0 at the end
@@ -369,6 +380,7 @@ struct ScanBlock {
     if (--c.left > 0) {
       c.t0 += CH;
       ++c.rec;
+      c.first = false;
     } else {
       seek(c, c.s + 1);
     }
@@ -381,6 +393,39 @@ struct ScanBlock {
   // ------------------------------------------------------------ loader waves
   __device__ __forceinline__ void load_chunk(typename Stage::Regs &r, const Cursor &c) const {
     stage.load(p, r, c.t0, len_of(c), hk, h, v0, rec_of(c));
+  }
+
+  // Chained streams: the loads of this loader thread's part of the initial
+  // state of the sequence whose first chunk is at cursor c (zero-size when c
+  // is not a sequence's first chunk or the sequence starts from zeros), issued
+  // with the chunk's own loads: 16-byte units u = lt, lt + 256 of the
+  // [K][16] tile, esz = 16 / (elements per unit) units per row.
+  __device__ __forceinline__ void load_h0(uint4 (&r)[2], const Cursor &c, bool first) const {
+    const int esz = p.state_dtype == PBGDN_F32 ? 4 : 2;
+    long bytes = 0;
+    const unsigned char *base = nullptr;
+    if (first && !at_end(c)) {
+      const long slot = slot_of(c.s);
+      if (p.h0 && in_pool(slot) && (!p.has_initial_state || p.has_initial_state[c.s])) {
+        base = static_cast<const unsigned char *>(p.h0) + ((slot * p.Hv + h) * K * p.V + v0) * esz;
+        bytes = (static_cast<long>(K - 1) * p.V + VT) * esz;
+      }
+    }
+    const __amdgpu_buffer_rsrc_t rs = rsrc(base, bytes);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int u = lt + NLT * i;
+      const uint32_t off = u < K * esz ? ((u / esz) * p.V + (u % esz) * (16 / esz)) * esz : OUT_OF_RANGE;
+      r[i] = buf_load16(rs, off);
+    }
+  }
+  __device__ __forceinline__ void store_h0(int buf, const uint4 (&r)[2]) const {
+    const int esz = p.state_dtype == PBGDN_F32 ? 4 : 2;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int u = lt + NLT * i;
+      if (u < K * esz) st(L::h0(buf) + 16 * u, r[i]);
+    }
   }
 
   // O tile of stream chunk n (LDS buffer n & 1, at cursor oc) -> HBM, one
@@ -444,13 +489,26 @@ struct ScanBlock {
   // chunk: at a sequence's last chunk its final state goes out and the next
   // sequence's initial state (loaded first) replaces it; then the cursor
   // moves on.
-  __device__ __forceinline__ void next_chunk(int kt) {
+  // The next sequence's initial state was staged by the loader waves with its
+  // first chunk (chunk buffer nb): this lane's rows 16 kt + 4 g + i, column c.
+  __device__ __forceinline__ void next_chunk(int kt, int nb) {
     if constexpr (!CHAIN) return;  // the one sequence's final state goes out after the loop
     if (--cc.left > 0) return;
     const int done = cc.s;
     const float4_t fin = sacc;
     seek_owner(cc, done + 1, kt);
-    sacc = at_end(cc) ? float4_t{0.f, 0.f, 0.f, 0.f} : initial_state(cc.s, kt);
+    const int row0 = 16 * kt + 4 * g4;
+    if (p.state_dtype == PBGDN_F32) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sacc[i] = ld<float>(L::h0(nb) + ((row0 + i) * VT + c16) * 4);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const u16 x = ld<u16>(L::h0(nb) + ((row0 + i) * VT + c16) * 2);
+        sacc[i] = p.state_dtype == PBGDN_BF16 ? bf16_bits_to_float(x)
+                                                : static_cast<float>(__builtin_bit_cast(half_t, x));
+      }
+    }
     final_state(done, kt, fin);
     put_state(kt);
   }
@@ -571,7 +629,7 @@ struct ScanBlock {
       const float4_t nvv = Op::bits_to_float(ld_tr(L::v16(b ^ 1) + 16 * r * 32 + tr_v));
       const float4_t ngg = rec_rows(b ^ 1, SC_GAM, r);
       update_state(b, kt);
-      next_chunk(wave);
+      next_chunk(wave, b ^ 1);
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk) mf[kk] = nmf[kk];
       vv = nvv;
@@ -631,7 +689,7 @@ struct ScanBlock {
       fetch_rows(b ^ 1, 1, nmf);
       if constexpr (NKT > 4) {
         update_state(b, kt);
-        next_chunk(wave);
+        next_chunk(wave, b ^ 1);
       }
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk) mf[kk] = nmf[kk];
@@ -646,6 +704,11 @@ struct ScanBlock {
   // phase 2) also goes out.
   template <int P>
   __device__ __forceinline__ void tick_loader(long n) {
+    if constexpr (CHAIN) {  // chunk n + 1's initial-state units to its buffer; chunk n + 3's issued
+      if (h0v[P]) store_h0(P ^ 1, h0r[P]);
+      h0v[P] = lc.first && !at_end(lc);
+      load_h0(h0r[P], lc, lc.first);
+    }
     const long t0 = lc.t0;  // chunk n + 3
     const long len = len_of(lc);
     const unsigned char *rec = rec_of(lc);
@@ -706,9 +769,17 @@ struct ScanBlock {
       load_chunk(regs[1], lc);
       advance(lc);
       stage.store(lds, L::kq(0), regs[1], lt);
+      if constexpr (CHAIN) {  // initial states of chunks 1 and 2, as in a tick
+        h0v[0] = lc.first && !at_end(lc);
+        load_h0(h0r[0], lc, lc.first);
+      }
       load_chunk(regs[0], lc);
       advance(lc);
       store_out(-1);
+      if constexpr (CHAIN) {
+        h0v[1] = lc.first && !at_end(lc);
+        load_h0(h0r[1], lc, lc.first);
+      }
       load_chunk(regs[1], lc);
       advance(lc);
       store_out(-1);
@@ -765,7 +836,7 @@ __global__ __launch_bounds__(NT) void scan_kernel(ChunkParams p) {
 template <int K, typename TIn, typename TOut, bool CHAIN>
 int launch_scan_kernel(const ChunkParams &p, hipStream_t stream) {
   static bool configured = false;  // benign race: the attribute call is idempotent
-  const size_t smem = ScanLayout<K>::BYTES;
+  const size_t smem = CHAIN ? ScanLayout<K>::CHAIN_BYTES : ScanLayout<K>::BYTES;
   auto kernel = scan_kernel<K, TIn, TOut, CHAIN>;
   if (!configured) {
     if (hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
