@@ -279,7 +279,7 @@ def bench_layer(length, steps, warmup=3):
     """The fused prologue and epilogue kernels over T tokens of the layer shape:
     HBM-bound; algorithmic bytes = what each must read and write once."""
     import torch
-    from pseudobrain_amd.layer import layer_epilogue, layer_prologue
+    from pseudobrain_amd.layer import layer_epilogue, layer_prologue, layer_prologue_varlen
     x = layer_inputs(length)
     hk, hv, dk, dv, ch = x["hk"], x["hv"], x["dk"], x["dv"], x["channels"]
 
@@ -291,12 +291,23 @@ def bench_layer(length, steps, warmup=3):
     def epi():
         layer_epilogue(x["o"], gate, x["o_norm"], out_dtype=torch.float32)
 
+    # the same tokens as 64 packed sequences against a pool of 64 fp32 conv tails
+    nseq = 64
+    cu = torch.tensor([i * length // nseq for i in range(nseq + 1)], dtype=torch.int32).cuda()
+    pool = x["tail"].repeat(nseq, 1, 1).contiguous()
+    slots = torch.arange(nseq, dtype=torch.int32).cuda()
+
+    def pro_varlen():
+        layer_prologue_varlen(x["z"], cu, pool, x["weight"], x["a_log"], x["dt_bias"], hk, dk, hv, dv, slots)
+
     out = {}
     # prologue: q|k|v bf16 in and out, a|b bf16 in, g, beta fp32 out, the tail fp32 in and out
     pro_bytes = length * (ch * 2 * 2 + 2 * hv * 2 + 2 * hv * 4) + 2 * (x["conv"] - 1) * ch * 4
+    varlen_bytes = pro_bytes + (nseq - 1) * 2 * (x["conv"] - 1) * ch * 4
     # epilogue: o bf16 and gate bf16 in, hs fp32 out
     epi_bytes = length * hv * dv * (2 + 2 + 4)
-    for name, fn, nbytes in (("layer_prologue", pro, pro_bytes), ("layer_epilogue", epi, epi_bytes)):
+    for name, fn, nbytes in (("layer_prologue", pro, pro_bytes), ("layer_prologue_varlen64", pro_varlen,
+                                                                  varlen_bytes), ("layer_epilogue", epi, epi_bytes)):
         sec, ksec = timed_steps(fn, steps, warmup)
         gbs = nbytes / ksec / 1e9
         out[name] = {"T": length, "us_per_call": sec * 1e6, "kernel_us": ksec * 1e6, "bytes_per_call": nbytes,

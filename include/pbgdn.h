@@ -19,7 +19,9 @@
  *   pbgdn_prologue_fwd   short convolution + SiLU, q/k L2 norm, decay/beta
  *                        gates (GatedDeltaNetLayer.forward, gated_deltanet.py:415-429,
  *                        short_convolution :314-338, l2_normalize :59-70);
- *   pbgdn_epilogue_fwd   per-head RMSNorm x o_norm x SiLU(gate) (:439-441).
+ *   pbgdn_epilogue_fwd   per-head RMSNorm x o_norm x SiLU(gate) (:439-441);
+ *   pbgdn_prologue_varlen_fwd  the prologue over packed sequences, each with
+ *                        its own tail in a pool of slots (the serving form).
  *
  * and one fuses all three for the decode step (one token per sequence):
  *
@@ -56,7 +58,7 @@
 extern "C" {
 #endif
 
-#define PBGDN_ABI_VERSION 5
+#define PBGDN_ABI_VERSION 6
 
 /* element types */
 #define PBGDN_F32 0
@@ -217,8 +219,8 @@ int pbgdn_recurrent_verify_fwd(const void *q, const void *k, const void *v,
  *   tail        [B, conv-1, 2 Hk K + Hv V] tail_dtype: the last conv-1 inputs
  *               before qkv (NULL when conv <= 1); cast to in_dtype before the
  *               convolution, as the reference does
- *   tail_out    same shape: the last conv-1 inputs of tail ++ qkv; must not
- *               be `tail` (NULL when conv <= 1)
+ *   tail_out    same shape: the last conv-1 inputs of tail ++ qkv; may be
+ *               `tail` (NULL when conv <= 1)
  *   conv_weight [2 Hk K + Hv V, conv] float32, tap conv-1 on the current input
  *               (NULL when conv == 0: SiLU only)
  *   a_log, dt_bias [Hv] float32
@@ -256,6 +258,45 @@ int pbgdn_epilogue_fwd(const void *o, int o_dtype, const void *gate,
                        long gate_stride, int gate_dtype, const float *o_norm,
                        float eps, void *out, int out_dtype, int B, int T,
                        int Hv, int V, void *stream);
+
+/*
+ * Layer prologue over packed sequences: pbgdn_prologue_fwd with B = 1 and N
+ * sequences packed along T by cu_seqlens [N + 1], each convolving against its
+ * own carried tail, kept in a pool of slots as a serving cache keeps conv
+ * states. No reference counterpart as one call (the reference's layer works
+ * on [B, T] batches with a tail per batch row, short_convolution,
+ * gated_deltanet.py:314-338); the per-sequence arithmetic is that one.
+ *
+ *   qkv, decay, in_dtype, conv_weight, conv, a_log, dt_bias, q, k, v,
+ *   out_dtype, g, beta, Hk, Hv, K, V, l2_mode: as pbgdn_prologue_fwd, B = 1
+ *   tail        pool of tails, tail_dtype: row j (0 = oldest) of channel c of
+ *               slot s at element s * tail_slot_stride + j * tail_row_stride
+ *               + c * tail_chan_stride ([S, conv-1, C] and the channel-major
+ *               [S, C, conv-1] both work); NULL when conv <= 1
+ *   cu_seqlens  [N + 1] int32, nondecreasing from 0 to T (a bound outside
+ *               [0, T] is clamped, never followed out of the buffer)
+ *   tail_out    pool the new tails go to, same layout; may be `tail` (every
+ *               old tail element is read before the new one is written)
+ *   slot_idx    [N] int32 slot of each sequence, or NULL for slot n; a slot
+ *               outside [0, num_slots) starts from a zero tail and keeps no
+ *               new one; the slots of one call must be distinct
+ *   has_initial_state [N] uint8, or NULL: 0 starts sequence n from a zero tail
+ *
+ * Supported: as pbgdn_prologue_fwd; N <= 65535.
+ */
+int pbgdn_prologue_varlen_fwd(const void *qkv, long qkv_stride,
+                              const void *decay, long decay_stride,
+                              int in_dtype, const int32_t *cu_seqlens,
+                              int num_seqs, const void *tail, void *tail_out,
+                              int tail_dtype, long tail_slot_stride,
+                              long tail_row_stride, long tail_chan_stride,
+                              const int32_t *slot_idx,
+                              const uint8_t *has_initial_state, int num_slots,
+                              const float *conv_weight, int conv,
+                              const float *a_log, const float *dt_bias,
+                              void *q, void *k, void *v, int out_dtype,
+                              float *g, float *beta, int T, int Hk, int Hv,
+                              int K, int V, int l2_mode, void *stream);
 
 /*
  * Fused decode step of a GatedDeltaNetLayer: one token per sequence, from the

@@ -6,4 +6,4 @@ from .gated_deltanet import (  # noqa: F401
     delta_rule_sequential, gated_delta_chunk, gated_delta_rule, hip_usable, recurrent_fwd, recurrent_step_,
     select_kernel,
 )
-from .layer import decode_layer_step, layer_epilogue, layer_prologue  # noqa: F401,E402
+from .layer import decode_layer_step, layer_epilogue, layer_prologue, layer_prologue_varlen  # noqa: F401,E402

@@ -13,7 +13,7 @@ import threading
 import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpbgdn.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 F32, BF16, F16 = 0, 1, 2
 OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3
@@ -35,6 +35,9 @@ SIGNATURES = {
     "pbgdn_prologue_fwd": ([_vp, _l, _vp, _l, _i, _vp, _vp, _i, _vp, _i, _vp, _vp,
                             _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp], _i),
     "pbgdn_epilogue_fwd": ([_vp, _i, _vp, _l, _i, _vp, _f, _vp, _i, _i, _i, _i, _i, _vp], _i),
+    "pbgdn_prologue_varlen_fwd": ([_vp, _l, _vp, _l, _i, _vp, _i, _vp, _vp, _i, _l, _l, _l, _vp, _vp, _i,
+                                   _vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp],
+                                  _i),
     "pbgdn_decode_layer_fwd": ([_vp, _l, _i, _vp, _i, _l, _l, _l, _vp, _i, _vp, _vp, _i, _vp, _i, _vp, _i,
                                 _vp, _f, _vp, _i, _i, _i, _i, _i, _i, _f, _vp], _i),
 }

@@ -10,6 +10,10 @@
 // registers. A 16-lane row holds all channels of one token, so the q/k norm
 // over a key head (K/8 lanes) is a shuffle reduction inside the row. Extra
 // workgroups (blockIdx.x >= channel blocks) compute the gates of the tile.
+// Packed sequences run through the same kernel as one sequence; a second,
+// small kernel redoes the first conv-1 tokens of each sequence against its
+// own tail from a slot pool and writes the new tails, so the main pass needs
+// no per-token sequence lookup.
 //
 // Epilogue: V/8 lanes per (token, value head) row, 8 elements each; the mean
 // square over the head is a shuffle reduction inside the row group.
@@ -147,7 +151,10 @@ __device__ __forceinline__ Raw8 load_raw8(__amdgpu_buffer_rsrc_t r, uint32_t off
 // Sum over groups of `width` lanes (a power of two up to 16), inside a
 // 16-lane row.
 __device__ __forceinline__ float group_sum(float x, int width) {
-  for (int off = 1; off < width; off <<= 1) x += __shfl_xor(x, off, 64);
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) {  // a fixed trip count: no loop inside the callers' unrolled loops
+    if (off < width) x += __shfl_xor(x, off, 64);
+  }
   return x;
 }
 
@@ -161,15 +168,79 @@ struct PrologueParams {
   int in_dtype, tail_dtype, out_dtype;
   int B, T, Hk, Hv, K, V, conv, l2_mode;
   int units, ch_blocks;  // 8-channel units; channel workgroups per tile
+  // Packed sequences (B = 1): cu_seqlens [N+1] over the T axis, and the tails
+  // in a pool of slots, row j of channel c of slot s at element
+  // s * tail_ss + j * tail_rs + c * tail_cs; slot_idx [N] (NULL: slot n),
+  // has_initial [N] (NULL: all; 0: the sequence starts from a zero tail).
+  const int32_t *cu_seqlens, *slot_idx;
+  const uint8_t *has_initial;
+  int num_seqs, num_slots;
+  long tail_ss, tail_rs, tail_cs;
+  // 1: rows of channels (tail_cs == 1), 2: channels of rows (tail_rs == 1,
+  // tail_cs == conv-1), both 16-byte aligned in 8-element pieces, so a
+  // lane's eight channels move in whole vectors; 0: element by element.
+  int tail_vec;
+};
+
+// Where a lane's eight channels go: q, k (L2-normalised over the key head,
+// K/8 lanes of a 16-lane row) or v, and the element index of its first
+// channel in that output for token 0 plus the step per token.
+struct OutLane {
+  int kind;  // 0 q, 1 k, 2 v
+  int head_lanes;
+  void *ptr;
+  long step, col;
+  __device__ __forceinline__ OutLane(const PrologueParams &p, int u, int c0) {
+    const int qk_units = p.Hk * p.K / 8;
+    int head, off;
+    if (u < qk_units) {
+      kind = 0;
+      head = c0 / p.K;
+      off = c0 % p.K;
+    } else if (u < 2 * qk_units) {
+      kind = 1;
+      head = (c0 - 8 * qk_units) / p.K;
+      off = (c0 - 8 * qk_units) % p.K;
+    } else {
+      kind = 2;
+      head = (c0 - 16 * qk_units) / p.V;
+      off = (c0 - 16 * qk_units) % p.V;
+    }
+    head_lanes = p.K / 8;
+    const int width = kind < 2 ? p.K : p.V;
+    ptr = kind == 0 ? p.q : kind == 1 ? p.k : p.v;
+    step = static_cast<long>(kind < 2 ? p.Hk : p.Hv) * width;
+    col = static_cast<long>(head) * width + off;
+  }
+  // y = SiLU(conv) of one token: the q/k norm (every lane of the row takes
+  // part in its sum), then the store at element i when `store`.
+  __device__ __forceinline__ bool finish(const PrologueParams &p, float (&y)[8], bool store, long i) const {
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += y[e] * y[e];
+    ss = group_sum(ss, head_lanes);
+    if (!store) return false;
+    if (kind < 2) {
+      constexpr float l2_eps = 1e-6f;
+      const float n = p.l2_mode == 0 ? 1.f / fmaxf(sqrtf(ss), l2_eps) : rsqrtf(ss + l2_eps);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] *= n;
+    }
+    store8(ptr, i, p.out_dtype, y);
+    return true;
+  }
 };
 
 // CONV is the filter width (0: SiLU only). Every input row a lane needs (its
 // TPL tokens and the CONV-1 before them) is loaded before any is used, so the
-// loads of a lane overlap instead of following one another.
+// loads of a lane overlap instead of following one another. Rows before the
+// sequence's start read zeros: the first CONV-1 tokens of every sequence
+// (batch row or packed sequence) are redone against the sequence's own tail by
+// edge_kernel, which also writes the new tails, so this pass reads and writes
+// no tail and needs no per-token sequence lookup.
 template <int CONV, typename TIn>
 __global__ __launch_bounds__(LNT) void prologue_kernel(PrologueParams p) {
   constexpr int IN = dtype_of<TIn>();
-  constexpr int TAIL = CONV > 1 ? CONV - 1 : 0;  // rows of the carried tail
   constexpr int HALO = CONV > 1 ? CONV - 1 : 0;  // rows before a lane's first token
   const int tid = threadIdx.x;
   const int b = blockIdx.z;
@@ -194,20 +265,15 @@ __global__ __launch_bounds__(LNT) void prologue_kernel(PrologueParams p) {
   if (t_first >= p.T) return;  // the whole 16-lane row: no tokens (no shuffle partner is lost)
   const bool live = u < p.units;
   const int c0 = 8 * (live ? u : 0);
-  const int qk_units = p.Hk * p.K / 8;
   const long seq_row = static_cast<long>(b) * p.T;
-  const long tail_base = static_cast<long>(b) * TAIL;
   const long chans = static_cast<long>(p.units) * 8;
-  // Every row this lane needs is loaded unconditionally through buffer
-  // resources that span exactly this sequence's rows and its carried tail; a
-  // row outside them (or a dead lane) gets an out-of-range offset and reads
-  // zeros. No load then waits on a branch merge: they all issue back to back.
+  // Every row this lane needs is loaded unconditionally through a buffer
+  // resource that spans exactly this sequence's rows; a row outside it (or a
+  // dead lane) gets an out-of-range offset and reads zeros. No load then
+  // waits on a branch merge: they all issue back to back.
   const auto rq = rsrc(static_cast<const TIn *>(p.qkv) + seq_row * p.qkv_stride,
                        (static_cast<long>(p.T - 1) * p.qkv_stride + chans) * static_cast<long>(sizeof(TIn)));
-  const int tail_elem = p.tail_dtype == PBGDN_F32 ? 4 : 2;
-  const auto rt = rsrc(static_cast<const unsigned char *>(p.tail) + tail_base * chans * tail_elem,
-                       TAIL > 0 ? static_cast<long>(TAIL) * chans * tail_elem : 0);
-  Raw8 raw[HALO + TPL], raw_tail[HALO > 0 ? HALO : 1];  // rows t_first - HALO ..
+  Raw8 raw[HALO + TPL];  // rows t_first - HALO ..
 #pragma unroll
   for (int m = 0; m < HALO + TPL; ++m) {
     const int t = t_first - HALO + m;
@@ -216,73 +282,17 @@ __global__ __launch_bounds__(LNT) void prologue_kernel(PrologueParams p) {
                              : OUT_OF_RANGE;
     raw[m] = load_raw8<sizeof(TIn) == 4>(rq, off);
   }
-#pragma unroll
-  for (int m = 0; m < HALO; ++m) {  // tail rows: only the first lane row of the first tile has any
-    const int t = t_first - HALO + m;
-    const uint32_t off = live && t < 0 && t >= -TAIL
-                             ? (static_cast<uint32_t>(TAIL + t) * static_cast<uint32_t>(chans) + c0) * tail_elem
-                             : OUT_OF_RANGE;
-    raw_tail[m] = load_raw8<true>(rt, off);  // 32 bytes whatever the tail's type: no branch
-  }
   float xr[HALO + TPL][8];
 #pragma unroll
-  for (int m = 0; m < HALO + TPL; ++m) {
-    decode8<TIn>(raw[m], xr[m]);
-    if (m < HALO && t_first - HALO + m < 0) {
-      // the carried tail, rounded through the input dtype as in cat(tail.to(x.dtype), x)
-      float xt[8];
-      decode8(raw_tail[m < HALO ? m : 0], p.tail_dtype, xt);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) xr[m][e] = through(xt[e], IN);
-    }
-  }
-  auto input_row = [&](int t, float (&x)[8]) {  // used only for the old-tail rows of the new tail
-    if (live && t < 0 && t >= -TAIL) {
-      load8(p.tail, (tail_base + TAIL + t) * chans + c0, p.tail_dtype, x);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = through(x[e], IN);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = 0.f;
-    }
-  };
+  for (int m = 0; m < HALO + TPL; ++m) decode8<TIn>(raw[m], xr[m]);
   float w[8][CONV > 0 ? CONV : 1];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
 #pragma unroll
     for (int j = 0; j < CONV; ++j) w[e][j] = p.conv_weight[(c0 + e) * CONV + j];
   }
-  // The new tail: the last CONV-1 rows of tail ++ x. Rows that still come
-  // from the old tail (T < CONV-1) are written once, by lane row 0 of the
-  // first tile.
-  if (TAIL > 0 && live && t_tile == 0 && tl == 0) {
-    for (int r = 0; r + p.T < TAIL; ++r) {
-      float x[8];
-      input_row(p.T + r - TAIL, x);
-      store8(p.tail_out, (tail_base + r) * chans + c0, p.tail_dtype, x);
-    }
-  }
-  int kind = 2, head = 0, off = 0;  // 0 q, 1 k, 2 v
-  if (u < qk_units) {
-    kind = 0;
-    head = c0 / p.K;
-    off = c0 % p.K;
-  } else if (u < 2 * qk_units) {
-    kind = 1;
-    head = (c0 - 8 * qk_units) / p.K;
-    off = (c0 - 8 * qk_units) % p.K;
-  } else {
-    head = (c0 - 16 * qk_units) / p.V;
-    off = (c0 - 16 * qk_units) % p.V;
-  }
-  const int head_lanes = p.K / 8;
-  // Output element index of token t_first and the step per token.
-  const int out_heads = kind < 2 ? p.Hk : p.Hv;
-  const int out_width = kind < 2 ? p.K : p.V;
-  void *const out_ptr = kind == 0 ? p.q : kind == 1 ? p.k : p.v;
-  const long out_step = static_cast<long>(out_heads) * out_width;
-  const long out0 = (seq_row + t_first) * out_step + static_cast<long>(head) * out_width + off;
-  const float l2_eps = 1e-6f;
+  const OutLane out(p, u, c0);
+  const long out0 = (seq_row + t_first) * out.step + out.col;
 #pragma unroll
   for (int i = 0; i < TPL; ++i) {
     const int t = t_first + i;
@@ -294,21 +304,7 @@ __global__ __launch_bounds__(LNT) void prologue_kernel(PrologueParams p) {
       for (int j = 0; j < CONV; ++j) acc += w[e][j] * xr[HALO + i - (CONV - 1) + j][e];  // tap j: row t-(CONV-1)+j
       y[e] = siluf(acc);
     }
-    float ss = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ss += y[e] * y[e];
-    ss = group_sum(ss, head_lanes);  // every lane of the row takes part
-    if (live && t < p.T) {
-      if (kind < 2) {
-        const float n = p.l2_mode == 0 ? 1.f / fmaxf(sqrtf(ss), l2_eps) : rsqrtf(ss + l2_eps);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) y[e] *= n;
-      }
-      store8(out_ptr, out0 + i * out_step, p.out_dtype, y);
-      if (TAIL > 0 && t >= p.T - TAIL) {
-        store8(p.tail_out, (tail_base + t - (p.T - TAIL)) * chans + c0, p.tail_dtype, xr[HALO + i]);
-      }
-    }
+    out.finish(p, y, live && t < p.T, out0 + i * out.step);
   }
 }
 
@@ -320,6 +316,143 @@ void launch_prologue(int conv, dim3 grid, hipStream_t st, const PrologueParams &
     case 2: hipLaunchKernelGGL((prologue_kernel<2, TIn>), grid, dim3(LNT), 0, st, prm); break;
     case 3: hipLaunchKernelGGL((prologue_kernel<3, TIn>), grid, dim3(LNT), 0, st, prm); break;
     default: hipLaunchKernelGGL((prologue_kernel<4, TIn>), grid, dim3(LNT), 0, st, prm); break;
+  }
+}
+
+// After the prologue: thread (unit u, sequence s) redoes tokens 0 .. CONV-2
+// of sequence s for channels 8u .. 8u+7 with the sequence's own tail (the
+// prologue gave them zeros or the previous sequence's inputs), in the
+// prologue's arithmetic, and writes s's new tail: the last CONV-1 rows of
+// (its tail, rounded through the input dtype) ++ (its inputs). Sequence s is
+// packed rows cu_seqlens[s] .. cu_seqlens[s+1]-1 of T, or without cu_seqlens
+// batch row s (T rows). A thread reads every old tail row before it writes,
+// and no other thread touches its channels of that slot, so tail_out may be
+// the pool itself.
+template <int CONV, typename TIn>
+__global__ __launch_bounds__(LNT) void edge_kernel(PrologueParams p) {
+  constexpr int IN = dtype_of<TIn>();
+  constexpr int TAIL = CONV - 1;
+  const int u = blockIdx.x * LNT + threadIdx.x;
+  const int s = blockIdx.y;
+  const bool live = u < p.units;
+  const int c0 = 8 * (live ? u : 0);
+  const long chans = static_cast<long>(p.units) * 8;
+  long bos = static_cast<long>(s) * p.T, len = p.T;
+  if (p.cu_seqlens) {  // clamped to the packed rows, whatever cu_seqlens holds
+    bos = min(max(0L, static_cast<long>(p.cu_seqlens[s])), static_cast<long>(p.T));
+    len = min(max(0L, static_cast<long>(p.cu_seqlens[s + 1]) - bos), p.T - bos);
+  }
+  const long slot = p.slot_idx ? static_cast<long>(p.slot_idx[s]) : static_cast<long>(s);
+  const auto rq = rsrc(static_cast<const TIn *>(p.qkv) + bos * p.qkv_stride,
+                       len > 0 ? ((len - 1) * p.qkv_stride + chans) * static_cast<long>(sizeof(TIn)) : 0);
+  auto row_off = [&](long j) -> uint32_t {  // byte offset of the sequence's row j, channel c0
+    return live && j < len ? static_cast<uint32_t>((j * p.qkv_stride + c0) * static_cast<long>(sizeof(TIn)))
+                           : OUT_OF_RANGE;
+  };
+  float old[TAIL][8], x[TAIL][8];  // the old tail; the sequence's first TAIL inputs
+#pragma unroll
+  for (int j = 0; j < TAIL; ++j) decode8<TIn>(load_raw8<sizeof(TIn) == 4>(rq, row_off(j)), x[j]);
+  const bool from_pool = live && slot >= 0 && slot < p.num_slots && !(p.has_initial && !p.has_initial[s]);
+  if (!from_pool) {
+#pragma unroll
+    for (int j = 0; j < TAIL; ++j) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) old[j][e] = 0.f;
+    }
+  } else if (p.tail_vec == 1) {
+#pragma unroll
+    for (int j = 0; j < TAIL; ++j) load8(p.tail, slot * p.tail_ss + j * p.tail_rs + c0, p.tail_dtype, old[j]);
+  } else if (p.tail_vec == 2) {  // element m of the lane's run is channel m / TAIL, row m % TAIL
+#pragma unroll
+    for (int m = 0; m < TAIL; ++m) {
+      float v[8];
+      load8(p.tail, slot * p.tail_ss + static_cast<long>(c0) * TAIL + 8 * m, p.tail_dtype, v);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) old[(8 * m + k) % TAIL][(8 * m + k) / TAIL] = v[k];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < TAIL; ++j) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        old[j][e] = load_elem(p.tail, slot * p.tail_ss + j * p.tail_rs + (c0 + e) * p.tail_cs, p.tail_dtype);
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < TAIL; ++j) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) old[j][e] = through(old[j][e], IN);  // as cat(tail.to(x.dtype), x)
+  }
+  float w[8][CONV];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+#pragma unroll
+    for (int j = 0; j < CONV; ++j) w[e][j] = p.conv_weight[(c0 + e) * CONV + j];
+  }
+  const OutLane out(p, u, c0);
+#pragma unroll
+  for (int i = 0; i < TAIL; ++i) {  // token i: taps are rows i .. i+CONV-1 of (old tail ++ inputs)
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < CONV; ++j) acc += w[e][j] * (i + j < TAIL ? old[i + j][e] : x[i + j - TAIL][e]);
+      y[e] = siluf(acc);
+    }
+    out.finish(p, y, live && i < len, (bos + i) * out.step + out.col);
+  }
+  if (!live || slot < 0 || slot >= p.num_slots) return;
+  float nt[TAIL][8];  // the new tail
+#pragma unroll
+  for (int r = 0; r < TAIL; ++r) {
+    const long e = len + r;  // row of (old tail ++ inputs)
+    if (e < TAIL) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) nt[r][k] = old[e < TAIL ? e : 0][k];
+    } else {
+      decode8<TIn>(load_raw8<sizeof(TIn) == 4>(rq, row_off(e - TAIL)), nt[r]);
+    }
+  }
+  if (p.tail_vec == 1) {
+#pragma unroll
+    for (int r = 0; r < TAIL; ++r) store8(p.tail_out, slot * p.tail_ss + r * p.tail_rs + c0, p.tail_dtype, nt[r]);
+  } else if (p.tail_vec == 2) {
+#pragma unroll
+    for (int m = 0; m < TAIL; ++m) {
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = nt[(8 * m + k) % TAIL][(8 * m + k) / TAIL];
+      store8(p.tail_out, slot * p.tail_ss + static_cast<long>(c0) * TAIL + 8 * m, p.tail_dtype, v);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < TAIL; ++r) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        store_elem(p.tail_out, slot * p.tail_ss + r * p.tail_rs + (c0 + k) * p.tail_cs, p.tail_dtype, nt[r][k]);
+      }
+    }
+  }
+}
+
+template <typename TIn>
+void launch_edge(int conv, dim3 grid, hipStream_t st, const PrologueParams &prm) {
+  switch (conv) {
+    case 2: hipLaunchKernelGGL((edge_kernel<2, TIn>), grid, dim3(LNT), 0, st, prm); break;
+    case 3: hipLaunchKernelGGL((edge_kernel<3, TIn>), grid, dim3(LNT), 0, st, prm); break;
+    default: hipLaunchKernelGGL((edge_kernel<4, TIn>), grid, dim3(LNT), 0, st, prm); break;
+  }
+}
+
+// The prologue pass, then (conv > 1) the edge pass over `seqs` sequences.
+template <typename TIn>
+void launch_prologue_and_edges(const PrologueParams &prm, dim3 grid, int seqs, hipStream_t st) {
+  if (prm.T > 0) launch_prologue<TIn>(prm.conv, grid, st, prm);
+  if (prm.conv > 1) {
+    const dim3 egrid(static_cast<unsigned>((prm.units + LNT - 1) / LNT), static_cast<unsigned>(seqs));
+    launch_edge<TIn>(prm.conv, egrid, st, prm);
   }
 }
 
@@ -424,7 +557,7 @@ extern "C" int pbgdn_prologue_fwd(const void *qkv, long qkv_stride, const void *
   if (static_cast<long>(B) * T == 0) return PBGDN_OK;
   const bool has_tail = conv > 1;
   if (!qkv || !decay || !a_log || !dt_bias || !q || !k || !v || !g || !beta || (conv > 0 && !conv_weight) ||
-      (has_tail && (!tail || !tail_out || tail == tail_out))) {
+      (has_tail && (!tail || !tail_out))) {
     return PBGDN_ERR_INVALID_ARGUMENT;
   }
   if (!aligned16(qkv) || !aligned16(q) || !aligned16(k) || !aligned16(v) ||
@@ -434,14 +567,66 @@ extern "C" int pbgdn_prologue_fwd(const void *qkv, long qkv_stride, const void *
   if (channels / 8 > 0x7fffffffL / 16 || static_cast<long>(T) + TT > 0x7fffffffL) return PBGDN_ERR_UNSUPPORTED;
   PrologueParams prm{qkv, decay, tail, tail_out, conv_weight, a_log, dt_bias, q, k, v, g, beta, qkv_stride,
                      decay_stride, in_dtype, tail_dtype, out_dtype, B, T, Hk, Hv, K, V, conv, l2_mode,
-                     static_cast<int>(channels / 8), static_cast<int>((channels / 8 + 15) / 16)};
+                     static_cast<int>(channels / 8), static_cast<int>((channels / 8 + 15) / 16),
+                     nullptr, nullptr, nullptr, B, B, (conv - 1) * channels, channels, 1, 1};
   const dim3 grid(prm.ch_blocks + 1, (T + TT - 1) / TT, B);
   if (grid.y > 0x7fffffffu || B > 65535 || grid.y > 65535u) return PBGDN_ERR_UNSUPPORTED;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (in_dtype) {  // tails: row-major [B, conv-1, C], batch row b in slot b
+    case PBGDN_F32: launch_prologue_and_edges<float>(prm, grid, B, st); break;
+    case PBGDN_BF16: launch_prologue_and_edges<u16>(prm, grid, B, st); break;
+    default: launch_prologue_and_edges<half_t>(prm, grid, B, st); break;
+  }
+  return hipGetLastError() == hipSuccess ? PBGDN_OK : PBGDN_ERR_LAUNCH;
+}
+
+extern "C" int pbgdn_prologue_varlen_fwd(const void *qkv, long qkv_stride, const void *decay, long decay_stride,
+                                         int in_dtype, const int32_t *cu_seqlens, int num_seqs, const void *tail,
+                                         void *tail_out, int tail_dtype, long tail_slot_stride, long tail_row_stride,
+                                         long tail_chan_stride, const int32_t *slot_idx,
+                                         const uint8_t *has_initial_state, int num_slots, const float *conv_weight,
+                                         int conv, const float *a_log, const float *dt_bias, void *q, void *k,
+                                         void *v, int out_dtype, float *g, float *beta, int T, int Hk, int Hv,
+                                         int K, int V, int l2_mode, void *stream) {
+  using namespace pbgdn;
+  if (T < 0 || num_seqs < 0 || num_slots < 0 || Hk <= 0 || Hv <= 0 || K <= 0 || V <= 0 || Hv % Hk != 0 ||
+      conv < 0) {
+    return PBGDN_ERR_INVALID_ARGUMENT;
+  }
+  if (!valid_dtype(in_dtype) || !valid_dtype(out_dtype) || !valid_dtype(tail_dtype) ||
+      !(l2_mode == 0 || l2_mode == 1)) {
+    return PBGDN_ERR_INVALID_ARGUMENT;
+  }
+  if (!(K == 64 || K == 128) || V % 8 != 0 || conv > MAX_CONV) return PBGDN_ERR_UNSUPPORTED;
+  const long channels = 2L * Hk * K + static_cast<long>(Hv) * V;
+  if (qkv_stride < channels || decay_stride < 2L * Hv || qkv_stride % 8 != 0) return PBGDN_ERR_INVALID_ARGUMENT;
+  const long in_elem = in_dtype == PBGDN_F32 ? 4 : 2;
+  if (static_cast<long>(T) * qkv_stride * in_elem > 0x7ffffff0L - 64) return PBGDN_ERR_UNSUPPORTED;
+  if (num_seqs == 0) return T == 0 ? PBGDN_OK : PBGDN_ERR_INVALID_ARGUMENT;
+  const bool has_tail = conv > 1;
+  if (!cu_seqlens || !qkv || !decay || !a_log || !dt_bias || !q || !k || !v || !g || !beta ||
+      (conv > 0 && !conv_weight) ||
+      (has_tail && (!tail || !tail_out || tail_slot_stride < 0 || tail_row_stride < 0 || tail_chan_stride < 0))) {
+    return PBGDN_ERR_INVALID_ARGUMENT;
+  }
+  if (!aligned16(qkv) || !aligned16(q) || !aligned16(k) || !aligned16(v)) return PBGDN_ERR_INVALID_ARGUMENT;
+  if (channels / 8 > 0x7fffffffL / 16 || static_cast<long>(T) + TT > 0x7fffffffL) return PBGDN_ERR_UNSUPPORTED;
+  PrologueParams prm{qkv, decay, tail, tail_out, conv_weight, a_log, dt_bias, q, k, v, g, beta, qkv_stride,
+                     decay_stride, in_dtype, tail_dtype, out_dtype, 1, T, Hk, Hv, K, V, conv, l2_mode,
+                     static_cast<int>(channels / 8), static_cast<int>((channels / 8 + 15) / 16), cu_seqlens,
+                     slot_idx, has_initial_state, num_seqs, num_slots, tail_slot_stride, tail_row_stride,
+                     tail_chan_stride, 0};
+  if (has_tail && tail_slot_stride % 8 == 0 && aligned16(tail) && aligned16(tail_out)) {
+    if (tail_chan_stride == 1 && tail_row_stride % 8 == 0) prm.tail_vec = 1;
+    if (tail_row_stride == 1 && tail_chan_stride == conv - 1) prm.tail_vec = 2;
+  }
+  const dim3 grid(prm.ch_blocks + 1, (T + TT - 1) / TT, 1);
+  if (grid.y > 65535u || num_seqs > 65535) return PBGDN_ERR_UNSUPPORTED;
+  hipStream_t st = static_cast<hipStream_t>(stream);
   switch (in_dtype) {
-    case PBGDN_F32: launch_prologue<float>(conv, grid, st, prm); break;
-    case PBGDN_BF16: launch_prologue<u16>(conv, grid, st, prm); break;
-    default: launch_prologue<half_t>(conv, grid, st, prm); break;
+    case PBGDN_F32: launch_prologue_and_edges<float>(prm, grid, num_seqs, st); break;
+    case PBGDN_BF16: launch_prologue_and_edges<u16>(prm, grid, num_seqs, st); break;
+    default: launch_prologue_and_edges<half_t>(prm, grid, num_seqs, st); break;
   }
   return hipGetLastError() == hipSuccess ? PBGDN_OK : PBGDN_ERR_LAUNCH;
 }

@@ -43,7 +43,8 @@ def _rows(x: torch.Tensor, name: str) -> int:
 
 def layer_prologue(z: torch.Tensor, tail: torch.Tensor | None, conv_weight: torch.Tensor | None,
                    A_log: torch.Tensor, dt_bias: torch.Tensor, heads: int, key_dim: int, value_heads: int,
-                   value_dim: int, l2norm: str = "max", *, out_dtype: torch.dtype | None = None):
+                   value_dim: int, l2norm: str = "max", *, out_dtype: torch.dtype | None = None,
+                   tail_out: torch.Tensor | None = None):
     """GatedDeltaNetLayer.forward from the projection to the operator's inputs
     (gated_deltanet.py:415-427) in one kernel.
 
@@ -55,7 +56,9 @@ def layer_prologue(z: torch.Tensor, tail: torch.Tensor | None, conv_weight: torc
     Returns (q [B,T,heads,key_dim], k, v [B,T,value_heads,value_dim] in
     out_dtype (default z's dtype, the operator's matmul precision), g, beta
     [B,T,value_heads] float32, gate (the [B,T,value_heads*value_dim] view of z
-    the epilogue takes), new tail [B,conv-1,channels] in the tail's dtype)."""
+    the epilogue takes), new tail [B,conv-1,channels] in the tail's dtype,
+    written to tail_out when given: a contiguous tensor of the tail's shape
+    and dtype, which may be the tail itself)."""
     if l2norm not in L2_MODES:
         raise ValueError(f"l2 normalization mode must be one of {L2_MODES}")
     if heads < 1 or value_heads % heads:
@@ -86,8 +89,15 @@ def layer_prologue(z: torch.Tensor, tail: torch.Tensor | None, conv_weight: torc
     if tail_rows:
         if tail is None or tail.shape != (batch, tail_rows, channels):
             raise ValueError(f"tail must be [B, conv-1, channels] = {(batch, tail_rows, channels)}")
+        if tail_out is not None and tail_out.data_ptr() == tail.data_ptr() and not tail.is_contiguous():
+            raise ValueError("an in-place tail must be contiguous")
         tail = tail.contiguous()
-        new_tail = torch.empty_like(tail)
+        if tail_out is None:
+            new_tail = torch.empty_like(tail)
+        else:
+            if tail_out.shape != tail.shape or tail_out.dtype != tail.dtype or not tail_out.is_contiguous():
+                raise ValueError("tail_out must be a contiguous tensor of the tail's shape and dtype")
+            new_tail = tail_out
     out_dtype = z.dtype if out_dtype is None else out_dtype
     codes = _lib.DTYPE_CODES
     if z.dtype not in codes or out_dtype not in codes or (tail_rows and tail.dtype not in codes):
@@ -111,6 +121,100 @@ def layer_prologue(z: torch.Tensor, tail: torch.Tensor | None, conv_weight: torc
         batch, length, heads, value_heads, key_dim, value_dim, L2_MODES.index(l2norm), _lib.stream_handle(dev))
     _lib.check(status, "pbgdn_prologue_fwd")
     return q, k, v, g, beta, gate, new_tail
+
+
+def layer_prologue_varlen(z: torch.Tensor, cu_seqlens: torch.Tensor, tail_pool: torch.Tensor | None,
+                          conv_weight: torch.Tensor | None, A_log: torch.Tensor, dt_bias: torch.Tensor, heads: int,
+                          key_dim: int, value_heads: int, value_dim: int, slot_idx: torch.Tensor | None = None,
+                          has_initial_state: torch.Tensor | None = None, l2norm: str = "max", *,
+                          out_dtype: torch.dtype | None = None, tail_out: torch.Tensor | None = None):
+    """layer_prologue over packed sequences, the way a serving engine batches
+    prefill: z [T, width] (or [1, T, width]) holds N sequences back to back
+    (cu_seqlens int32 [N+1]); sequence n convolves against its own tail,
+    tail_pool[slot_idx[n]] ([S, conv-1, channels], any strides, e.g. a
+    channel-major pool viewed as that), or a zero tail when
+    has_initial_state[n] is False or the slot is outside the pool. The new
+    tails go to tail_out (default: the pool itself, updated in place).
+    Returns (q [1,T,heads,key_dim], k, v [1,T,value_heads,value_dim] in
+    out_dtype, g, beta [1,T,value_heads] float32, gate view of z)."""
+    if l2norm not in L2_MODES:
+        raise ValueError(f"l2 normalization mode must be one of {L2_MODES}")
+    if heads < 1 or value_heads % heads:
+        raise ValueError("gated deltanet value heads must be a multiple of the key heads")
+    if key_dim not in PROLOGUE_KEY_DIMS or value_dim % 8:
+        raise ValueError(f"layer_prologue supports key widths {PROLOGUE_KEY_DIMS} and value widths "
+                         "that are multiples of 8")
+    if z.ndim == 3:
+        if z.shape[0] != 1:
+            raise ValueError("packed sequences: z must be [T, width] or [1, T, width]")
+        z = z[0]
+    channels = 2 * heads * key_dim + value_heads * value_dim
+    vwidth = value_heads * value_dim
+    if z.ndim != 2 or z.shape[-1] != channels + vwidth + 2 * value_heads:
+        raise ValueError(f"z must be [T, {channels + vwidth + 2 * value_heads}] ([q | k | v | gate | a | b])")
+    if z.stride(-1) != 1 or z.stride(0) % 8 or z.data_ptr() % 16:
+        z = z.contiguous()
+    dev = z.device
+    if dev.type != "cuda":
+        raise RuntimeError(f"pbgdn kernels run on ROCm devices only (got a tensor on '{dev}'); "
+                           "this package has no CPU path")
+    if cu_seqlens.ndim != 1 or cu_seqlens.numel() < 1:
+        raise ValueError("cu_seqlens must be a 1-D tensor [N+1]")
+    cu = cu_seqlens.to(device=dev, dtype=torch.int32).contiguous()
+    nseq = cu.numel() - 1
+    length = z.shape[0]
+    conv = 0 if conv_weight is None else conv_weight.shape[1]
+    if conv_weight is not None:
+        if conv_weight.shape != (channels, conv) or not 1 <= conv <= MAX_CONV:
+            raise ValueError(f"conv_weight must be [{channels}, conv] with 1 <= conv <= {MAX_CONV}")
+        conv_weight = conv_weight.to(device=dev, dtype=torch.float32).contiguous()
+    codes = _lib.DTYPE_CODES
+    strides = (0, 0, 0)
+    nslots = 0
+    if conv > 1:
+        if (tail_pool is None or tail_pool.ndim != 3 or tail_pool.shape[1:] != (conv - 1, channels)
+                or tail_pool.dtype not in codes):
+            raise ValueError(f"tail_pool must be [S, conv-1, channels] = [S, {conv - 1}, {channels}]")
+        tail_out = tail_pool if tail_out is None else tail_out
+        if tail_out.shape != tail_pool.shape or tail_out.stride() != tail_pool.stride() or \
+                tail_out.dtype != tail_pool.dtype:
+            raise ValueError("tail_out must have the tail pool's shape, strides and dtype")
+        strides = tail_pool.stride()
+        nslots = tail_pool.shape[0]
+    else:
+        tail_pool = tail_out = None
+    if slot_idx is not None:
+        if slot_idx.shape != (nseq,):
+            raise ValueError(f"slot_idx must be [N] = [{nseq}]")
+        slot_idx = slot_idx.to(device=dev, dtype=torch.int32).contiguous()
+    elif conv > 1 and nslots < nseq:
+        raise ValueError("without slot_idx the tail pool needs a slot per sequence")
+    if has_initial_state is not None:
+        if has_initial_state.shape != (nseq,):
+            raise ValueError(f"has_initial_state must be [N] = [{nseq}]")
+        has_initial_state = has_initial_state.to(device=dev, dtype=torch.uint8).contiguous()
+    out_dtype = z.dtype if out_dtype is None else out_dtype
+    if z.dtype not in codes or out_dtype not in codes:
+        raise ValueError("z and out_dtype must be float32, bfloat16 or float16")
+    qkv, gate, decay = z.split((channels, vwidth, 2 * value_heads), dim=-1)
+    q = torch.empty(1, length, heads, key_dim, dtype=out_dtype, device=dev)
+    k = torch.empty_like(q)
+    v = torch.empty(1, length, value_heads, value_dim, dtype=out_dtype, device=dev)
+    g = torch.empty(1, length, value_heads, dtype=torch.float32, device=dev)
+    beta = torch.empty_like(g)
+    a_log = A_log.to(device=dev, dtype=torch.float32).contiguous()
+    dtb = dt_bias.to(device=dev, dtype=torch.float32).contiguous()
+    if a_log.shape != (value_heads,) or dtb.shape != (value_heads,):
+        raise ValueError(f"A_log and dt_bias must be [{value_heads}]")
+    status = _lib.lib().pbgdn_prologue_varlen_fwd(
+        _lib.ptr(qkv), z.stride(0), _lib.ptr(decay), z.stride(0), codes[z.dtype], _lib.ptr(cu), nseq,
+        _lib.ptr(tail_pool), _lib.ptr(tail_out), codes[tail_pool.dtype] if tail_pool is not None else _lib.F32,
+        *strides, _lib.ptr(slot_idx), _lib.ptr(has_initial_state), nslots, _lib.ptr(conv_weight), conv,
+        _lib.ptr(a_log), _lib.ptr(dtb), _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), codes[out_dtype], _lib.ptr(g),
+        _lib.ptr(beta), length, heads, value_heads, key_dim, value_dim, L2_MODES.index(l2norm),
+        _lib.stream_handle(dev))
+    _lib.check(status, "pbgdn_prologue_varlen_fwd")
+    return q, k, v, g, beta, gate[None]
 
 
 def layer_epilogue(o: torch.Tensor, gate: torch.Tensor, o_norm: torch.Tensor, eps: float = NORM_EPS, *,

@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version_and_status_strings():
-    assert _lib.lib().pbgdn_abi_version() == _lib.ABI_VERSION == 5
+    assert _lib.lib().pbgdn_abi_version() == _lib.ABI_VERSION == 6
     header = open(HEADER).read()
     assert re.search(r"#define PBGDN_ABI_VERSION (\d+)", header).group(1) == str(_lib.ABI_VERSION)
     assert _lib.status_string(0) == "ok"
@@ -149,7 +149,6 @@ def epilogue_call(**over):
     (dict(qkv_stride=CH - 8), _lib.ERR_INVALID_ARGUMENT),  # rows shorter than q, k, v
     (dict(qkv_stride=CH + 4), _lib.ERR_INVALID_ARGUMENT),  # not a multiple of 8
     (dict(decay_stride=63), _lib.ERR_INVALID_ARGUMENT),
-    (dict(tail_out=FAKE), _lib.ERR_INVALID_ARGUMENT),       # in place: the tail would race
     (dict(tail=None), _lib.ERR_INVALID_ARGUMENT),
     (dict(w=None), _lib.ERR_INVALID_ARGUMENT),
     (dict(qkv=FAKE + 8), _lib.ERR_INVALID_ARGUMENT),        # 16-byte alignment
@@ -242,3 +241,33 @@ def test_decode_layer_fwd_rejects(over, code):
 
 def test_decode_layer_fwd_empty_is_ok():
     assert decode_layer_call(B=0) == _lib.OK
+
+
+def prologue_varlen_call(**over):
+    args = dict(qkv=FAKE, qkv_stride=CH + 4096 + 64, decay=FAKE, decay_stride=CH + 4096 + 64, in_dtype=1,
+                cu=FAKE, nseq=4, tail=FAKE, tail_out=FAKE, tail_dtype=0, tss=3 * CH, trs=CH, tcs=1, slots=None,
+                has_init=None, nslots=4, w=FAKE, conv=4, a_log=FAKE, dt_bias=FAKE, q=FAKE, k=FAKE, v=FAKE,
+                out_dtype=1, g=FAKE, beta=FAKE, T=64, Hk=16, Hv=32, K=128, V=128, l2=0, stream=None)
+    args.update(over)
+    return _lib.lib().pbgdn_prologue_varlen_fwd(*args.values())
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(cu=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(nseq=0), _lib.ERR_INVALID_ARGUMENT),           # tokens but no sequences
+    (dict(tail=None), _lib.ERR_INVALID_ARGUMENT),        # conv > 1 needs the tail pool
+    (dict(tcs=-1), _lib.ERR_INVALID_ARGUMENT),
+    (dict(nslots=-1), _lib.ERR_INVALID_ARGUMENT),
+    (dict(q=FAKE + 8), _lib.ERR_INVALID_ARGUMENT),       # 16-byte rows
+    (dict(qkv_stride=CH + 4), _lib.ERR_INVALID_ARGUMENT),
+    (dict(l2=3), _lib.ERR_INVALID_ARGUMENT),
+    (dict(K=96), _lib.ERR_UNSUPPORTED),
+    (dict(conv=5), _lib.ERR_UNSUPPORTED),
+    (dict(nseq=70000), _lib.ERR_UNSUPPORTED),
+])
+def test_prologue_varlen_fwd_rejects(over, code):
+    assert prologue_varlen_call(**over) == code
+
+
+def test_prologue_varlen_fwd_empty_is_ok():
+    assert prologue_varlen_call(T=0, nseq=0) == _lib.OK

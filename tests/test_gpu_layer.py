@@ -107,6 +107,22 @@ def test_prologue_segments_equal_one_pass():
     assert torch.equal(second[6], whole[6])
 
 
+@pytest.mark.parametrize("length", [1, 2, 200])
+def test_prologue_tail_in_place(length):
+    """tail_out = tail: the tail is updated in place and every output equals
+    the call with a separate new tail, bit for bit (short inputs keep part of
+    the old tail)."""
+    z, tail, w, a_log, dtb = [None if x is None else x.to(DEV)
+                              for x in make_layer_inputs(3, length, 4, 128, 8, 128, 4, torch.bfloat16, seed=31)]
+    ref = layer_prologue(z, tail, w, a_log, dtb, 4, 128, 8, 128)
+    pool = tail.clone()
+    got = layer_prologue(z, pool, w, a_log, dtb, 4, 128, 8, 128, tail_out=pool)
+    torch.cuda.synchronize()
+    for i in range(5):
+        assert torch.equal(got[i], ref[i]), i
+    assert got[6] is pool and torch.equal(pool, ref[6])
+
+
 @pytest.mark.parametrize("dv,o_dtype,gate_dtype,out_dtype", [
     (128, torch.bfloat16, torch.bfloat16, torch.float32),
     (128, torch.float32, torch.bfloat16, torch.bfloat16),
