@@ -58,7 +58,7 @@
 extern "C" {
 #endif
 
-#define PBGDN_ABI_VERSION 6
+#define PBGDN_ABI_VERSION 7
 
 /* element types */
 #define PBGDN_F32 0
@@ -297,6 +297,45 @@ int pbgdn_prologue_varlen_fwd(const void *qkv, long qkv_stride,
                               void *q, void *k, void *v, int out_dtype,
                               float *g, float *beta, int T, int Hk, int Hv,
                               int K, int V, int l2_mode, void *stream);
+
+/*
+ * Backward of pbgdn_chunk_fwd for [B, T] batches: the gradients the
+ * reference's pseudobrain::gated_delta_chunk_backward returns
+ * (gated_deltanet.py:230-277), given the gradients of o and of the final
+ * state. It recomputes what it needs from the forward's inputs (no saved
+ * intermediates): the state at every 64-token chunk start by a forward pass,
+ * the state adjoint at every chunk end by a reverse pass, then each chunk's
+ * gradients; all arithmetic float32.
+ *
+ *   q, k, v, in_dtype, g, beta, beta_dtype, h0, B, T, Hk, Hv, K, V, scale:
+ *               as pbgdn_chunk_fwd without cu_seqlens (h0 [B, Hv, K, V]
+ *               float32, or NULL for zeros)
+ *   dout        [B, T, Hv, V] do_dtype: the gradient of o
+ *   dht         [B, Hv, K, V] float32 or NULL (zeros): the gradient of the
+ *               final state
+ *   dq, dk      [B, T, Hk, K] in_dtype (GQA: summed over the Hv/Hk value
+ *               heads of each key head)
+ *   dv          [B, T, Hv, V] in_dtype
+ *   dg          [B, T, Hv] float32
+ *   dbeta       [B, T, Hv] beta_dtype
+ *   dh0         [B, Hv, K, V] float32, or NULL when not wanted
+ *   workspace   device scratch of pbgdn_chunk_bwd_workspace_size(B, T, Hk,
+ *               Hv, K, V) bytes, 16-byte aligned, no initialisation needed
+ *               (per chunk: its start state, end adjoint, T, the dO terms)
+ *
+ * Supported: K, V in {64, 128}; at most 65,535 chunks per sequence.
+ */
+int pbgdn_chunk_bwd(const void *q, const void *k, const void *v, int in_dtype,
+                    const float *g, const void *beta, int beta_dtype,
+                    const float *h0, const void *dout, int do_dtype,
+                    const float *dht, void *dq, void *dk, void *dv, float *dg,
+                    void *dbeta, float *dh0, void *workspace,
+                    size_t workspace_bytes, int B, int T, int Hk, int Hv,
+                    int K, int V, float scale, void *stream);
+
+/* Workspace bytes pbgdn_chunk_bwd needs for these sizes. */
+size_t pbgdn_chunk_bwd_workspace_size(int B, int T, int Hk, int Hv, int K,
+                                      int V);
 
 /*
  * Fused decode step of a GatedDeltaNetLayer: one token per sequence, from the

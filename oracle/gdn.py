@@ -212,6 +212,60 @@ def streamed(q, k, v, g, beta, scale, h0, segment: int, kernel: str = "chunked")
         yield o, state
 
 
+def gated_delta_rule_backward(q, k, v, g, beta, scale, h0, do, dht):
+    """Gradients of (o, S_T) = gated_delta_rule(q, k, v, g, beta, scale, h0)
+    with respect to every input, given do [B,T,H,V] and dht [B,H,K,V]: what
+    the reference's pseudobrain::gated_delta_chunk_backward op returns
+    (gated_deltanet.py:230-277, fla's chunk backward; parity unpinned against
+    fla itself, which is absent here). Reverse mode through the per-token
+    recurrence (gated_deltanet.py:9-11, :93-107), states kept from a forward
+    pass; q, k may be un-repeated [B,T,Hk,K], and their gradients are then
+    summed over the value heads that read them.
+
+    Per token, reversed, with P = a_t S_{t-1}, r = v_t - P^T k_t, u = b_t r:
+        dS += q_t do_t^T scale          dq_t = S_t do_t scale
+        dk_t = dS u,  du = dS^T k_t     db_t = du . r,  dr = b_t du,  dv_t = dr
+        dP = dS - k_t dr^T              dk_t -= P dr
+        dg_t = a_t <dP, S_{t-1}>        dS = a_t dP
+    Returns (dq, dk, dv, dg, dbeta, dh0) in the compute dtype."""
+    dtype, qr, kr, v, g, beta, state = _prepare(q, k, v, g, beta, h0)
+    do = np.asarray(do, dtype)
+    ds = np.asarray(dht, dtype).copy()
+    length = v.shape[1]
+    decay = np.exp(g)
+    states = [state]
+    for t in range(length):  # forward, keeping S_{t-1} for every t
+        p = states[-1] * decay[:, t, :, None, None]
+        r = v[:, t] - np.einsum("bhkv,bhk->bhv", p, kr[:, t])
+        states.append(p + kr[:, t, :, :, None] * (r * beta[:, t, :, None])[:, :, None, :])
+    dq, dk, dv = np.zeros_like(qr), np.zeros_like(kr), np.zeros_like(v)
+    dg, db = np.zeros_like(g), np.zeros_like(beta)
+    sc = dtype(scale)
+    for t in reversed(range(length)):
+        prev, cur = states[t], states[t + 1]
+        kt, qt, a, b = kr[:, t], qr[:, t], decay[:, t, :, None, None], beta[:, t, :, None]
+        ds = ds + sc * qt[..., None] * do[:, t, :, None, :]
+        dq[:, t] = sc * np.einsum("bhkv,bhv->bhk", cur, do[:, t])
+        p = prev * a
+        r = v[:, t] - np.einsum("bhkv,bhk->bhv", p, kt)
+        u = b * r
+        dk[:, t] = np.einsum("bhkv,bhv->bhk", ds, u)
+        du = np.einsum("bhkv,bhk->bhv", ds, kt)
+        db[:, t] = np.sum(du * r, axis=-1)
+        dr = b * du
+        dv[:, t] = dr
+        dp = ds - kt[..., None] * dr[:, :, None, :]
+        dk[:, t] -= np.einsum("bhkv,bhv->bhk", p, dr)
+        dg[:, t] = decay[:, t] * np.sum(dp * prev, axis=(-2, -1))
+        ds = dp * a
+    heads_k = np.asarray(q).shape[2]
+    if heads_k != v.shape[2]:  # GQA: sum over the value heads of each key head
+        groups = v.shape[2] // heads_k
+        dq = dq.reshape(*dq.shape[:2], heads_k, groups, dq.shape[-1]).sum(3)
+        dk = dk.reshape(*dk.shape[:2], heads_k, groups, dk.shape[-1]).sum(3)
+    return dq, dk, dv, dg, db, ds
+
+
 def rel_inf_error(x, ref) -> float:
     """Infinity-norm relative error max|x - ref| / max|ref| (the tolerance measure)."""
     x = np.asarray(x, dtype=np.float64)

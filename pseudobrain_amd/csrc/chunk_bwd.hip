@@ -1,0 +1,729 @@
+// Backward of the chunked Gated DeltaNet operator: the gradients that
+// pseudobrain::gated_delta_chunk_backward returns (pseudobrain/
+// gated_deltanet.py:230-277), from the chunk form of the forward
+//
+//   X = V - Gamma K S,   U = Tb X,   O = scale Gamma Q S + M U,
+//   S' = gamma_C S + K^T E U,
+//   Tb = (I + A)^-1 diag(beta),  A_ts = beta_t (k_t.k_s) e^{c_t - c_s} (t > s),
+//   M_ts = scale (q_t.k_s) e^{c_t - c_s} (t >= s),  Gamma = diag(e^{c_t}),
+//   E = diag(e^{c_last - c_t}),  gamma_C = e^{c_last},
+//
+// with c the in-chunk inclusive cumulative sum of g. Reverse mode through it:
+// the state adjoint runs backward over the chunks,
+//   dU = M^T dO + E K dS',  dX = Tb^T dU,
+//   dS = gamma_C dS' + scale (Gamma Q)^T dO - (Gamma K)^T dX,
+// and each chunk's gradients follow from its start state S, its end adjoint
+// dS' and its own inputs. Five launches on the caller's stream:
+//
+//   bwd_local_kernel     per (chunk, value head): T = (I + A)^-1 by forward
+//                        substitution, dU0 = M^T dO, J = scale (Gamma Q)^T dO
+//   bwd_state_kernel     per (value head, 16 value columns), serial over the
+//                        chunks: the state at every chunk start
+//   bwd_adjoint_kernel   the same grid, chunks in reverse: the adjoint at
+//                        every chunk end, and dh0
+//   bwd_grad_kernel      per (chunk, value head): dq, dk, dv, dbeta, dg
+//   bwd_gqa_reduce_kernel  dq, dk summed over the value heads of a key head
+//
+// Everything is float32: operands staged in LDS, products on the 16x16x4 fp32
+// MFMA (the same peak as fp32 FMA on this chip, with far fewer LDS reads).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "common.hpp"
+
+namespace pbgdn {
+namespace {
+
+constexpr int BC = 64;    // chunk length
+constexpr int BNT = 256;  // threads per workgroup (4 waves)
+constexpr int LC = BC + 4;
+constexpr int LT = 16 + 4;  // row stride of 16-column tiles
+
+struct BwdParams {
+  const void *q, *k, *v;
+  const float *g;
+  const void *beta;
+  const float *h0;
+  const void *dout;
+  const float *dht;
+  void *dq, *dk, *dv;
+  float *dg;
+  void *dbeta;
+  float *dh0;
+  float *ws_T, *ws_c, *ws_dU0, *ws_J, *ws_S, *ws_dS, *ws_dq, *ws_dk;
+  int in_dtype, beta_dtype, do_dtype;
+  int B, T, Hk, Hv, K, V, n;
+  float scale;
+};
+
+// fp32 MFMA: acc (16x16) += A (16x4) B (4x16). Lane l, c = l & 15, g = l >> 4:
+// A[m=c][k=g], B[k=g][n=c]; acc[r] is D[row 4g + r][col c].
+__device__ __forceinline__ float4_t mfma_f32(float a, float b, float4_t acc) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+}
+
+// acc += sum_{k < KD} a(i, k) b(k, j) over a 16x16 tile; a(i, k) is row i of
+// the tile's A rows, b(k, j) column j of its B columns.
+template <int KD, typename FA, typename FB>
+__device__ __forceinline__ float4_t tile_mm(float4_t acc, FA a, FB b) {
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15, g = lane >> 4;
+#pragma unroll 8
+  for (int k = 0; k < KD; k += 4) acc = mfma_f32(a(c, k + g), b(k + g, c), acc);
+  return acc;
+}
+
+__device__ __forceinline__ float4_t zero4() { return float4_t{0.f, 0.f, 0.f, 0.f}; }
+
+// Sum over the 16 lanes that share lane >> 4 (the columns of one tile row).
+__device__ __forceinline__ float row16_sum(float x) {
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
+// Workspace records of (batch b, value head h, chunk i).
+__device__ __forceinline__ long rec(const BwdParams &p, int b, int h, int i) {
+  return (static_cast<long>(b) * p.Hv + h) * p.n + i;
+}
+
+// Rows t0 .. t0+63 of a [B,T,H,W] tensor (head hd, columns col0 .. col0+cols-1)
+// into LDS as float, zero past T.
+__device__ __forceinline__ void load_rows(float *dst, int ld, const void *src, int dtype, const BwdParams &p, int b,
+                                          int t0, int heads, int hd, int width, int col0, int cols) {
+  for (int e = threadIdx.x; e < BC * cols; e += BNT) {
+    const int t = e / cols, j = e % cols;
+    float x = 0.f;
+    if (t0 + t < p.T) {
+      x = load_elem(src, ((static_cast<long>(b) * p.T + t0 + t) * heads + hd) * width + col0 + j, dtype);
+    }
+    dst[t * ld + j] = x;
+  }
+}
+
+// c (in-chunk cumulative log decay), e^c, e^(c_last - c) and beta of one chunk,
+// from the workspace record (c) and beta; rows past T have beta 0.
+__device__ __forceinline__ void load_decays(const BwdParams &p, int b, int h, int i, float *sc, float *sgam, float *se,
+                                            float *sbeta) {
+  const int tid = threadIdx.x;
+  if (tid < BC) {
+    const float c = p.ws_c[rec(p, b, h, i) * BC + tid];
+    const float last = p.ws_c[rec(p, b, h, i) * BC + BC - 1];
+    const int t = i * BC + tid;
+    sc[tid] = c;
+    sgam[tid] = expf(c);
+    se[tid] = expf(last - c);
+    sbeta[tid] = t < p.T ? load_elem(p.beta, (static_cast<long>(b) * p.T + t) * p.Hv + h, p.beta_dtype) : 0.f;
+  }
+}
+
+// A (strict lower) and M (lower, scaled) of one chunk from K K^T and Q K^T;
+// wave w writes rows 16w .. 16w+15.
+template <int K>
+__device__ __forceinline__ void form_a_m(const BwdParams &p, const float *sq, const float *sk, const float *sc,
+                                         const float *sbeta, float *sa, float *sm) {
+  constexpr int LK = K + 4;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 15, g4 = lane >> 4;
+  for (int tc = 0; tc < 4; ++tc) {
+    auto bk = [&](int kk, int j) { return sk[(16 * tc + j) * LK + kk]; };
+    float4_t kk_acc = tile_mm<K>(zero4(), [&](int r, int kk) { return sk[(16 * wave + r) * LK + kk]; }, bk);
+    float4_t qk_acc = tile_mm<K>(zero4(), [&](int r, int kk) { return sq[(16 * wave + r) * LK + kk]; }, bk);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = 16 * wave + 4 * g4 + r, s = 16 * tc + c;
+      const float d = t >= s ? expf(sc[t] - sc[s]) : 0.f;
+      if (sa) sa[t * LC + s] = t > s ? sbeta[t] * kk_acc[r] * d : 0.f;
+      sm[t * LC + s] = p.scale * qk_acc[r] * d;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Per (chunk, value head): T, dU0 = M^T dO, J = scale (Gamma Q)^T dO, c.
+// ---------------------------------------------------------------------------
+template <int K, int V>
+__global__ __launch_bounds__(BNT) void bwd_local_kernel(BwdParams p) {
+  constexpr int LK = K + 4, LV = V + 4;
+  extern __shared__ __align__(16) float lds[];
+  float *sq = lds, *sk = sq + BC * LK, *sdo = sk + BC * LK, *sa = sdo + BC * LV, *sm = sa + BC * LC;
+  float *sc = sm + BC * LC, *sgam = sc + BC, *sbeta = sgam + BC;
+  const int i = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 15, g4 = lane >> 4;
+  const int hk = h / (p.Hv / p.Hk);
+  const int t0 = i * BC;
+  load_rows(sq, LK, p.q, p.in_dtype, p, b, t0, p.Hk, hk, K, 0, K);
+  load_rows(sk, LK, p.k, p.in_dtype, p, b, t0, p.Hk, hk, K, 0, K);
+  load_rows(sdo, LV, p.dout, p.do_dtype, p, b, t0, p.Hv, h, V, 0, V);
+  if (wave == 0) {  // inclusive cumulative sum of g over the chunk (zero past T)
+    const int t = t0 + lane;
+    float x = t < p.T ? p.g[(static_cast<long>(b) * p.T + t) * p.Hv + h] : 0.f;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float y = __shfl_up(x, off, 64);
+      if (lane >= off) x += y;
+    }
+    sc[lane] = x;
+    sgam[lane] = expf(x);
+    sbeta[lane] = t < p.T ? load_elem(p.beta, (static_cast<long>(b) * p.T + t) * p.Hv + h, p.beta_dtype) : 0.f;
+    p.ws_c[rec(p, b, h, i) * BC + lane] = x;
+  }
+  __syncthreads();
+  form_a_m<K>(p, sq, sk, sc, sbeta, sa, sm);
+  __syncthreads();
+  if (wave == 0) {
+    // T = (I + A)^-1, unit lower triangular, in place over A: lane j walks
+    // column j down the rows; T[t][j] = -sum_{s<t} A[t][s] T[s][j] (T[s][j] = 0
+    // above the diagonal, where A is zero too). All lanes read row t before
+    // any writes it (one wave, one instruction stream).
+    const int j = lane;
+    for (int t = 0; t < BC; ++t) {
+      float acc = 0.f;
+      for (int s = 0; s < t; ++s) acc += sa[t * LC + s] * sa[s * LC + j];
+      sa[t * LC + j] = t == j ? 1.f : (t < j ? 0.f : -acc);
+    }
+  }
+  __syncthreads();
+  float *wt = p.ws_T + rec(p, b, h, i) * BC * BC;
+  for (int e = tid; e < BC * BC; e += BNT) wt[e] = sa[(e / BC) * LC + e % BC];
+  // dU0 = M^T dO: tiles (row tile, 16-column tile)
+  float *wu = p.ws_dU0 + rec(p, b, h, i) * BC * V;
+  for (int tile = wave; tile < 4 * (V / 16); tile += 4) {
+    const int tr = tile & 3, tv = tile >> 2;
+    const float4_t acc = tile_mm<BC>(zero4(), [&](int r, int s) { return sm[s * LC + 16 * tr + r]; },
+                                     [&](int s, int col) { return sdo[s * LV + 16 * tv + col]; });
+#pragma unroll
+    for (int r = 0; r < 4; ++r) wu[(16 * tr + 4 * g4 + r) * V + 16 * tv + c] = acc[r];
+  }
+  // J = scale (Gamma Q)^T dO: K x V
+  float *wj = p.ws_J + rec(p, b, h, i) * static_cast<long>(K) * V;
+  for (int tile = wave; tile < (K / 16) * (V / 16); tile += 4) {
+    const int tk = tile % (K / 16), tv = tile / (K / 16);
+    const float4_t acc = tile_mm<BC>(zero4(), [&](int r, int t) { return sq[t * LK + 16 * tk + r] * sgam[t]; },
+                                     [&](int t, int col) { return sdo[t * LV + 16 * tv + col]; });
+#pragma unroll
+    for (int r = 0; r < 4; ++r) wj[(16 * tk + 4 * g4 + r) * V + 16 * tv + c] = p.scale * acc[r];
+  }
+}
+
+// Chunk inputs of the two scans: K rows, T, decays.
+template <int K>
+__device__ __forceinline__ void load_scan_chunk(const BwdParams &p, int b, int h, int hk, int i, float *sk, float *st,
+                                                float *sc, float *sgam, float *se, float *sbeta) {
+  constexpr int LK = K + 4;
+  load_rows(sk, LK, p.k, p.in_dtype, p, b, i * BC, p.Hk, hk, K, 0, K);
+  const float *wt = p.ws_T + rec(p, b, h, i) * BC * BC;
+  for (int e = threadIdx.x; e < BC * BC; e += BNT) st[(e / BC) * LC + e % BC] = wt[e];
+  load_decays(p, b, h, i, sc, sgam, se, sbeta);
+}
+
+// ---------------------------------------------------------------------------
+// Forward over the chunks for 16 value columns: the state at every chunk
+// start. Wave w holds key-row tiles w, w+4 (K/64 of them) of the state.
+// ---------------------------------------------------------------------------
+template <int K>
+__global__ __launch_bounds__(BNT) void bwd_state_kernel(BwdParams p) {
+  constexpr int LK = K + 4, PER = K / 64;
+  extern __shared__ __align__(16) float lds[];
+  float *sk = lds, *st = sk + BC * LK, *ss = st + BC * LC, *sx = ss + K * LT, *su = sx + BC * LT;
+  float *sc = su + BC * LT, *sgam = sc + BC, *se = sgam + BC, *sbeta = se + BC;
+  const int v0 = 16 * blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 15, g4 = lane >> 4;
+  const int hk = h / (p.Hv / p.Hk);
+  const long kv = (static_cast<long>(b) * p.Hv + h) * K * p.V;
+  float4_t s[PER];
+#pragma unroll
+  for (int m = 0; m < PER; ++m) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int kk = 16 * (wave + 4 * m) + 4 * g4 + r;
+      s[m][r] = p.h0 ? p.h0[kv + static_cast<long>(kk) * p.V + v0 + c] : 0.f;
+    }
+  }
+  for (int i = 0; i < p.n; ++i) {
+    float *ws = p.ws_S + rec(p, b, h, i) * K * p.V;
+#pragma unroll
+    for (int m = 0; m < PER; ++m) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int kk = 16 * (wave + 4 * m) + 4 * g4 + r;
+        ws[static_cast<long>(kk) * p.V + v0 + c] = s[m][r];
+        ss[kk * LT + c] = s[m][r];
+      }
+    }
+    load_scan_chunk<K>(p, b, h, hk, i, sk, st, sc, sgam, se, sbeta);
+    load_rows(sx, LT, p.v, p.in_dtype, p, b, i * BC, p.Hv, h, p.V, v0, 16);
+    __syncthreads();
+    // X = V - Gamma K S (rows 16w ..)
+    const float4_t ks = tile_mm<K>(zero4(), [&](int r, int kk) { return sk[(16 * wave + r) * LK + kk]; },
+                                   [&](int kk, int col) { return ss[kk * LT + col]; });
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = 16 * wave + 4 * g4 + r;
+      sx[t * LT + c] -= sgam[t] * ks[r];
+    }
+    __syncthreads();
+    // U = T diag(beta) X
+    const float4_t u = tile_mm<BC>(zero4(), [&](int r, int s2) { return st[(16 * wave + r) * LC + s2] * sbeta[s2]; },
+                                   [&](int s2, int col) { return sx[s2 * LT + col]; });
+#pragma unroll
+    for (int r = 0; r < 4; ++r) su[(16 * wave + 4 * g4 + r) * LT + c] = u[r];
+    __syncthreads();
+    // S = gamma_C S + K^T E U
+    const float gam_c = sgam[BC - 1];
+#pragma unroll
+    for (int m = 0; m < PER; ++m) {
+      const int k0 = 16 * (wave + 4 * m);
+      const float4_t y = tile_mm<BC>(zero4(), [&](int r, int t) { return sk[t * LK + k0 + r] * se[t]; },
+                                     [&](int t, int col) { return su[t * LT + col]; });
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[m][r] = gam_c * s[m][r] + y[r];
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward over the chunks for 16 value columns: the adjoint dS' at every
+// chunk end (the input of that chunk's gradients), then dh0.
+// ---------------------------------------------------------------------------
+template <int K>
+__global__ __launch_bounds__(BNT) void bwd_adjoint_kernel(BwdParams p) {
+  constexpr int LK = K + 4, PER = K / 64;
+  extern __shared__ __align__(16) float lds[];
+  float *sk = lds, *st = sk + BC * LK, *sds = st + BC * LC, *sdu = sds + K * LT, *sdx = sdu + BC * LT;
+  float *sc = sdx + BC * LT, *sgam = sc + BC, *se = sgam + BC, *sbeta = se + BC;
+  const int v0 = 16 * blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 15, g4 = lane >> 4;
+  const int hk = h / (p.Hv / p.Hk);
+  const long kv = (static_cast<long>(b) * p.Hv + h) * K * p.V;
+  float4_t ds[PER];
+#pragma unroll
+  for (int m = 0; m < PER; ++m) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int kk = 16 * (wave + 4 * m) + 4 * g4 + r;
+      ds[m][r] = p.dht ? p.dht[kv + static_cast<long>(kk) * p.V + v0 + c] : 0.f;
+    }
+  }
+  for (int i = p.n - 1; i >= 0; --i) {
+    float *wds = p.ws_dS + rec(p, b, h, i) * K * p.V;
+    const float *wj = p.ws_J + rec(p, b, h, i) * K * p.V;
+    float4_t jv[PER];
+#pragma unroll
+    for (int m = 0; m < PER; ++m) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int kk = 16 * (wave + 4 * m) + 4 * g4 + r;
+        wds[static_cast<long>(kk) * p.V + v0 + c] = ds[m][r];
+        sds[kk * LT + c] = ds[m][r];
+        jv[m][r] = wj[static_cast<long>(kk) * p.V + v0 + c];
+      }
+    }
+    load_scan_chunk<K>(p, b, h, hk, i, sk, st, sc, sgam, se, sbeta);
+    const float *wu = p.ws_dU0 + rec(p, b, h, i) * BC * p.V;
+    for (int e = tid; e < BC * 16; e += BNT) sdu[(e >> 4) * LT + (e & 15)] = wu[(e >> 4) * p.V + v0 + (e & 15)];
+    __syncthreads();
+    // dU = dU0 + E K dS'
+    const float4_t kd = tile_mm<K>(zero4(), [&](int r, int kk) { return sk[(16 * wave + r) * LK + kk]; },
+                                   [&](int kk, int col) { return sds[kk * LT + col]; });
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = 16 * wave + 4 * g4 + r;
+      sdu[t * LT + c] += se[t] * kd[r];
+    }
+    __syncthreads();
+    // dX = (T diag(beta))^T dU
+    const float4_t dx = tile_mm<BC>(
+        zero4(), [&](int r, int s2) { return st[s2 * LC + 16 * wave + r] * sbeta[16 * wave + r]; },
+        [&](int s2, int col) { return sdu[s2 * LT + col]; });
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sdx[(16 * wave + 4 * g4 + r) * LT + c] = dx[r];
+    __syncthreads();
+    // dS = gamma_C dS' + J - (Gamma K)^T dX
+    const float gam_c = sgam[BC - 1];
+#pragma unroll
+    for (int m = 0; m < PER; ++m) {
+      const int k0 = 16 * (wave + 4 * m);
+      const float4_t y = tile_mm<BC>(zero4(), [&](int r, int t) { return sk[t * LK + k0 + r] * sgam[t]; },
+                                     [&](int t, int col) { return sdx[t * LT + col]; });
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ds[m][r] = gam_c * ds[m][r] + jv[m][r] - y[r];
+    }
+    __syncthreads();
+  }
+  if (p.dh0) {
+#pragma unroll
+    for (int m = 0; m < PER; ++m) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int kk = 16 * (wave + 4 * m) + 4 * g4 + r;
+        p.dh0[kv + static_cast<long>(kk) * p.V + v0 + c] = ds[m][r];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Per (chunk, value head): the gradients, from the chunk's start state S and
+// end adjoint dS'. Wave w owns token rows 16w .. 16w+15 of every product.
+// ---------------------------------------------------------------------------
+template <int K, int V>
+__global__ __launch_bounds__(BNT) void bwd_grad_kernel(BwdParams p) {
+  constexpr int LK = K + 4, KT = K / 16;
+  extern __shared__ __align__(16) float lds[];
+  float *sq = lds, *sk = sq + BC * LK, *st = sk + BC * LK, *sm = st + BC * LC;
+  float *area = sm + BC * LC;  // the value-column tiles, then three C x C matrices
+  float *ss = area, *sds = ss + K * LT, *sx = sds + K * LT, *sdo = sx + BC * LT, *su = sdo + BC * LT;
+  float *sdu = su + BC * LT, *sdx = sdu + BC * LT;
+  float *b1 = area, *b2 = b1 + BC * LC, *b3 = b2 + BC * LC;
+  float *vec = area + (3 * BC * LC > 2 * K * LT + 5 * BC * LT ? 3 * BC * LC : 2 * K * LT + 5 * BC * LT);
+  float *sc = vec, *sgam = sc + BC, *se = sgam + BC, *sbeta = se + BC;
+  float *sdgam = sbeta + BC, *sde = sdgam + BC, *sdc = sde + BC, *sdb = sdc + BC, *sred = sdb + BC;
+  const int i = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 15, g4 = lane >> 4;
+  const int hk = h / (p.Hv / p.Hk);
+  const int t0 = i * BC;
+  load_rows(sq, LK, p.q, p.in_dtype, p, b, t0, p.Hk, hk, K, 0, K);
+  load_rows(sk, LK, p.k, p.in_dtype, p, b, t0, p.Hk, hk, K, 0, K);
+  const float *wt = p.ws_T + rec(p, b, h, i) * BC * BC;
+  for (int e = tid; e < BC * BC; e += BNT) st[(e / BC) * LC + e % BC] = wt[e];
+  load_decays(p, b, h, i, sc, sgam, se, sbeta);
+  if (tid < BC) {
+    sdgam[tid] = 0.f;
+    sde[tid] = 0.f;
+    sdc[tid] = 0.f;
+    sdb[tid] = 0.f;
+  }
+  __syncthreads();
+  form_a_m<K>(p, sq, sk, sc, sbeta, nullptr, sm);
+
+  float4_t dq[KT], dk[KT], dtb[4], dm[4];
+#pragma unroll
+  for (int m = 0; m < KT; ++m) dq[m] = dk[m] = zero4();
+#pragma unroll
+  for (int m = 0; m < 4; ++m) dtb[m] = dm[m] = zero4();
+  float dgam_r[4] = {0.f, 0.f, 0.f, 0.f}, de_r[4] = {0.f, 0.f, 0.f, 0.f}, dgc = 0.f;
+  const long kv = rec(p, b, h, i) * K * V;
+  const int tw = 16 * wave;  // this wave's token rows
+  for (int v0 = 0; v0 < V; v0 += 16) {
+    __syncthreads();  // the previous tile's readers are done (and sm is complete)
+    for (int e = tid; e < K * 16; e += BNT) {
+      const int kk = e >> 4, j = e & 15;
+      ss[kk * LT + j] = p.ws_S[kv + static_cast<long>(kk) * V + v0 + j];
+      sds[kk * LT + j] = p.ws_dS[kv + static_cast<long>(kk) * V + v0 + j];
+    }
+    load_rows(sx, LT, p.v, p.in_dtype, p, b, t0, p.Hv, h, V, v0, 16);
+    load_rows(sdo, LT, p.dout, p.do_dtype, p, b, t0, p.Hv, h, V, v0, 16);
+    __syncthreads();
+    auto rows_of = [&](const float *m2, int ld) { return [=](int r, int kk) { return m2[(tw + r) * ld + kk]; }; };
+    auto state_cols = [&](const float *m2) { return [=](int kk, int col) { return m2[kk * LT + col]; }; };
+    const float4_t ks = tile_mm<K>(zero4(), rows_of(sk, LK), state_cols(ss));
+    const float4_t qs = tile_mm<K>(zero4(), rows_of(sq, LK), state_cols(ss));
+    const float4_t kd = tile_mm<K>(zero4(), rows_of(sk, LK), state_cols(sds));
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = tw + 4 * g4 + r;
+      sx[t * LT + c] -= sgam[t] * ks[r];  // X = V - Gamma K S
+    }
+    __syncthreads();
+    const float4_t u = tile_mm<BC>(zero4(), [&](int r, int s2) { return st[(tw + r) * LC + s2] * sbeta[s2]; },
+                                   [&](int s2, int col) { return sx[s2 * LT + col]; });
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      su[(tw + 4 * g4 + r) * LT + c] = u[r];
+      de_r[r] += kd[r] * u[r];
+    }
+    float4_t du = tile_mm<BC>(zero4(), [&](int r, int s2) { return sm[s2 * LC + tw + r]; },
+                              [&](int s2, int col) { return sdo[s2 * LT + col]; });
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = tw + 4 * g4 + r;
+      du[r] += se[t] * kd[r];
+      sdu[t * LT + c] = du[r];
+    }
+    __syncthreads();
+    const float4_t dx = tile_mm<BC>(
+        zero4(), [&](int r, int s2) { return st[s2 * LC + tw + r] * sbeta[tw + r]; },
+        [&](int s2, int col) { return sdu[s2 * LT + col]; });
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = tw + 4 * g4 + r;
+      sdx[t * LT + c] = dx[r];
+      if (t0 + t < p.T) {
+        store_elem(p.dv, ((static_cast<long>(b) * p.T + t0 + t) * p.Hv + h) * V + v0 + c, p.in_dtype, dx[r]);
+      }
+      dgam_r[r] += p.scale * qs[r] * sdo[t * LT + c] - ks[r] * dx[r];
+    }
+    for (int e = tid; e < K * 16; e += BNT) dgc += ss[(e >> 4) * LT + (e & 15)] * sds[(e >> 4) * LT + (e & 15)];
+    __syncthreads();
+    // C x C products over these 16 columns: dTb += dU X^T, dM += dO U^T
+#pragma unroll
+    for (int tc = 0; tc < 4; ++tc) {
+      dtb[tc] = tile_mm<16>(dtb[tc], rows_of(sdu, LT), [&](int j, int col) { return sx[(16 * tc + col) * LT + j]; });
+      dm[tc] = tile_mm<16>(dm[tc], rows_of(sdo, LT), [&](int j, int col) { return su[(16 * tc + col) * LT + j]; });
+    }
+    // dQ += scale Gamma dO S^T;  dK += E U dS'^T - Gamma dX S^T
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+      auto s_t = [&](int j, int col) { return ss[(16 * kt + col) * LT + j]; };
+      dq[kt] = tile_mm<16>(dq[kt], [&](int r, int j) { return sdo[(tw + r) * LT + j] * sgam[tw + r] * p.scale; }, s_t);
+      dk[kt] = tile_mm<16>(dk[kt], [&](int r, int j) { return su[(tw + r) * LT + j] * se[tw + r]; },
+                           [&](int j, int col) { return sds[(16 * kt + col) * LT + j]; });
+      dk[kt] = tile_mm<16>(dk[kt], [&](int r, int j) { return -sdx[(tw + r) * LT + j] * sgam[tw + r]; }, s_t);
+    }
+  }
+  // per-token sums over the value columns
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float a = row16_sum(dgam_r[r]), e2 = row16_sum(de_r[r]);
+    if (c == 0) {
+      sdgam[tw + 4 * g4 + r] = a;
+      sde[tw + 4 * g4 + r] = e2;
+    }
+  }
+  dgc = wave_sum(dgc);
+  if (lane == 0) sred[wave] = dgc;
+  __syncthreads();  // the value tiles are dead: the area now holds b1, b2, b3
+  // dM o Mt into b1 (and its dc terms); dT = dTb diag(beta) into b2 (and dbeta)
+#pragma unroll
+  for (int tc = 0; tc < 4; ++tc) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = tw + 4 * g4 + r, s2 = 16 * tc + c;
+      const float d = t >= s2 ? p.scale * expf(sc[t] - sc[s2]) : 0.f;
+      const float dmv = t >= s2 ? dm[tc][r] : 0.f;
+      b1[t * LC + s2] = dmv * d;
+      const float dcv = dmv * sm[t * LC + s2];
+      atomicAdd(&sdc[t], dcv);
+      atomicAdd(&sdc[s2], -dcv);
+      b2[t * LC + s2] = dtb[tc][r] * sbeta[s2];
+      atomicAdd(&sdb[s2], dtb[tc][r] * st[t * LC + s2]);
+    }
+  }
+  __syncthreads();
+  // W = T^T dT (rows of this wave), then into b2 once every wave has read dT
+  float4_t w4[4];
+#pragma unroll
+  for (int tc = 0; tc < 4; ++tc) {
+    w4[tc] = tile_mm<BC>(zero4(), [&](int r, int u2) { return st[u2 * LC + tw + r]; },
+                         [&](int u2, int col) { return b2[u2 * LC + 16 * tc + col]; });
+  }
+  __syncthreads();
+#pragma unroll
+  for (int tc = 0; tc < 4; ++tc) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) b2[(tw + 4 * g4 + r) * LC + 16 * tc + c] = w4[tc][r];
+  }
+  __syncthreads();
+  // dA = -W T^T (strict lower): H = dA beta_t D into b3; dbeta_t, dc terms
+#pragma unroll
+  for (int tc = 0; tc < 4; ++tc) {
+    const float4_t da = tile_mm<BC>(zero4(), [&](int r, int u2) { return b2[(tw + r) * LC + u2]; },
+                                    [&](int u2, int col) { return st[(16 * tc + col) * LC + u2]; });
+    const float4_t gk = tile_mm<K>(zero4(), [&](int r, int kk) { return sk[(tw + r) * LK + kk]; },
+                                   [&](int kk, int col) { return sk[(16 * tc + col) * LK + kk]; });
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = tw + 4 * g4 + r, s2 = 16 * tc + c;
+      float hv = 0.f;
+      if (t > s2) {
+        const float d = expf(sc[t] - sc[s2]);
+        const float dav = -da[r];
+        const float av = sbeta[t] * gk[r] * d;
+        hv = dav * sbeta[t] * d;
+        atomicAdd(&sdb[t], dav * gk[r] * d);
+        atomicAdd(&sdc[t], dav * av);
+        atomicAdd(&sdc[s2], -dav * av);
+      }
+      b3[t * LC + s2] = hv;
+    }
+  }
+  __syncthreads();
+  // dQ += (dM o Mt) K;  dK += (dM o Mt)^T Q + H K + H^T K
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) {
+    auto kcol = [&](int s2, int col) { return sk[s2 * LK + 16 * kt + col]; };
+    dq[kt] = tile_mm<BC>(dq[kt], [&](int r, int s2) { return b1[(tw + r) * LC + s2]; }, kcol);
+    dk[kt] = tile_mm<BC>(dk[kt], [&](int r, int s2) { return b1[s2 * LC + tw + r]; },
+                         [&](int s2, int col) { return sq[s2 * LK + 16 * kt + col]; });
+    dk[kt] = tile_mm<BC>(dk[kt], [&](int r, int s2) { return b3[(tw + r) * LC + s2]; }, kcol);
+    dk[kt] = tile_mm<BC>(dk[kt], [&](int r, int s2) { return b3[s2 * LC + tw + r]; }, kcol);
+  }
+  // dq, dk: straight to the output without GQA, else per value head in float32
+  const bool direct = p.Hk == p.Hv;
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = t0 + tw + 4 * g4 + r, kk = 16 * kt + c;
+      if (t >= p.T) continue;
+      if (direct) {
+        const long o = ((static_cast<long>(b) * p.T + t) * p.Hk + hk) * K + kk;
+        store_elem(p.dq, o, p.in_dtype, dq[kt][r]);
+        store_elem(p.dk, o, p.in_dtype, dk[kt][r]);
+      } else {
+        const long o = ((static_cast<long>(b) * p.T + t) * p.Hv + h) * K + kk;
+        p.ws_dq[o] = dq[kt][r];
+        p.ws_dk[o] = dk[kt][r];
+      }
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {  // dc -> dg = reverse cumulative sum within the chunk
+    const int t = lane;
+    float dcv = sdc[t] + sdgam[t] * sgam[t] - sde[t] * se[t];
+    const float tail = wave_sum(sde[t] * se[t]);
+    if (t == BC - 1) dcv += tail + (sred[0] + sred[1] + sred[2] + sred[3]) * sgam[BC - 1];
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float y = __shfl_down(dcv, off, 64);
+      if (lane + off < 64) dcv += y;
+    }
+    if (t0 + t < p.T) {
+      const long o = (static_cast<long>(b) * p.T + t0 + t) * p.Hv + h;
+      p.dg[o] = dcv;
+      store_elem(p.dbeta, o, p.beta_dtype, sdb[t]);
+    }
+  }
+}
+
+// dq, dk [B,T,Hk,K] = sum over the Hv/Hk value heads of each key head.
+__global__ __launch_bounds__(BNT) void bwd_gqa_reduce_kernel(BwdParams p) {
+  const long total = static_cast<long>(p.B) * p.T * p.Hk * p.K;
+  const int group = p.Hv / p.Hk;
+  for (long e = static_cast<long>(blockIdx.x) * BNT + threadIdx.x; e < total; e += static_cast<long>(gridDim.x) * BNT) {
+    const long kk = e % p.K, rest = e / p.K;
+    const long hk = rest % p.Hk, bt = rest / p.Hk;
+    const long base = (bt * p.Hv + hk * group) * p.K + kk;
+    float sq = 0.f, sk = 0.f;
+    for (int m = 0; m < group; ++m) {
+      sq += p.ws_dq[base + static_cast<long>(m) * p.K];
+      sk += p.ws_dk[base + static_cast<long>(m) * p.K];
+    }
+    store_elem(p.dq, e, p.in_dtype, sq);
+    store_elem(p.dk, e, p.in_dtype, sk);
+  }
+}
+
+// LDS bytes of each kernel.
+template <int K, int V>
+constexpr size_t local_lds() { return sizeof(float) * (2 * BC * (K + 4) + BC * (V + 4) + 2 * BC * LC + 3 * BC); }
+template <int K>
+constexpr size_t scan_lds() { return sizeof(float) * (BC * (K + 4) + BC * LC + K * LT + 2 * BC * LT + 4 * BC); }
+template <int K>
+constexpr size_t grad_lds() {
+  return sizeof(float) * (2 * BC * (K + 4) + 2 * BC * LC +
+                          (3 * BC * LC > 2 * K * LT + 5 * BC * LT ? 3 * BC * LC : 2 * K * LT + 5 * BC * LT) +
+                          8 * BC + 4);
+}
+
+template <typename Kern>
+int launch(Kern kernel, dim3 grid, size_t lds, hipStream_t st, const BwdParams &p) {
+  if (hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          static_cast<int>(lds)) != hipSuccess) {
+    return PBGDN_ERR_LAUNCH;
+  }
+  hipLaunchKernelGGL(kernel, grid, dim3(BNT), lds, st, p);
+  return hipGetLastError() == hipSuccess ? PBGDN_OK : PBGDN_ERR_LAUNCH;
+}
+
+template <int K, int V>
+int run_backward(const BwdParams &p, hipStream_t st) {
+  static_assert(grad_lds<K>() <= 160 * 1024 && local_lds<K, V>() <= 160 * 1024, "LDS budget");
+  const dim3 per_chunk(p.n, p.Hv, p.B), per_tile(V / 16, p.Hv, p.B);
+  int rc = PBGDN_OK;
+  if (p.n > 0) rc = launch(bwd_local_kernel<K, V>, per_chunk, local_lds<K, V>(), st, p);
+  if (rc == PBGDN_OK && p.n > 0) rc = launch(bwd_state_kernel<K>, per_tile, scan_lds<K>(), st, p);
+  if (rc == PBGDN_OK) rc = launch(bwd_adjoint_kernel<K>, per_tile, scan_lds<K>(), st, p);
+  if (rc == PBGDN_OK && p.n > 0) rc = launch(bwd_grad_kernel<K, V>, per_chunk, grad_lds<K>(), st, p);
+  if (rc == PBGDN_OK && p.n > 0 && p.Hk != p.Hv) {
+    const long total = static_cast<long>(p.B) * p.T * p.Hk * K;
+    const unsigned blocks = static_cast<unsigned>(std::min<long>((total + BNT - 1) / BNT, 65535L));
+    hipLaunchKernelGGL(bwd_gqa_reduce_kernel, dim3(blocks), dim3(BNT), 0, st, p);
+    rc = hipGetLastError() == hipSuccess ? PBGDN_OK : PBGDN_ERR_LAUNCH;
+  }
+  return rc;
+}
+
+// Workspace floats per (batch, value head, chunk), and the GQA scratch.
+long ws_record_floats(int K, int V) {
+  return static_cast<long>(BC) * BC + BC + static_cast<long>(BC) * V + 3L * K * V;
+}
+
+}  // namespace
+}  // namespace pbgdn
+
+extern "C" size_t pbgdn_chunk_bwd_workspace_size(int B, int T, int Hk, int Hv, int K, int V) {
+  using namespace pbgdn;
+  if (B < 0 || T < 0 || Hk <= 0 || Hv <= 0 || K <= 0 || V <= 0) return 0;
+  const long n = (static_cast<long>(T) + BC - 1) / BC;
+  long floats = static_cast<long>(B) * Hv * n * ws_record_floats(K, V);
+  if (Hk != Hv) floats += 2L * B * T * Hv * K;
+  return static_cast<size_t>(floats) * sizeof(float) + 256;
+}
+
+extern "C" int pbgdn_chunk_bwd(const void *q, const void *k, const void *v, int in_dtype, const float *g,
+                               const void *beta, int beta_dtype, const float *h0, const void *dout, int do_dtype,
+                               const float *dht, void *dq, void *dk, void *dv, float *dg, void *dbeta, float *dh0,
+                               void *workspace, size_t workspace_bytes, int B, int T, int Hk, int Hv, int K, int V,
+                               float scale, void *stream) {
+  using namespace pbgdn;
+  if (B < 0 || T < 0 || Hk <= 0 || Hv <= 0 || K <= 0 || V <= 0 || Hv % Hk != 0) return PBGDN_ERR_INVALID_ARGUMENT;
+  auto dtype_ok = [](int d) { return d == PBGDN_F32 || d == PBGDN_BF16 || d == PBGDN_F16; };
+  if (!dtype_ok(in_dtype) || !dtype_ok(beta_dtype) || !dtype_ok(do_dtype)) return PBGDN_ERR_INVALID_ARGUMENT;
+  if (!((K == 64 || K == 128) && (V == 64 || V == 128))) return PBGDN_ERR_UNSUPPORTED;
+  if (static_cast<long>(B) * T == 0) {
+    if (B > 0 && dh0 == nullptr) return PBGDN_OK;
+  }
+  const long n = (static_cast<long>(T) + BC - 1) / BC;
+  if (n > 0 && (!q || !k || !v || !g || !beta || !dout || !dq || !dk || !dv || !dg || !dbeta)) {
+    return PBGDN_ERR_INVALID_ARGUMENT;
+  }
+  if (B == 0) return PBGDN_OK;
+  if (n > 65535 || Hv > 65535 || B > 65535) return PBGDN_ERR_UNSUPPORTED;
+  if (!workspace || workspace_bytes < pbgdn_chunk_bwd_workspace_size(B, T, Hk, Hv, K, V) ||
+      reinterpret_cast<uintptr_t>(workspace) % 16 != 0) {
+    return PBGDN_ERR_INVALID_ARGUMENT;
+  }
+  float *ws = static_cast<float *>(workspace);
+  const long recs = static_cast<long>(B) * Hv * n;
+  BwdParams p{};
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.g = g;
+  p.beta = beta;
+  p.h0 = h0;
+  p.dout = dout;
+  p.dht = dht;
+  p.dq = dq;
+  p.dk = dk;
+  p.dv = dv;
+  p.dg = dg;
+  p.dbeta = dbeta;
+  p.dh0 = dh0;
+  p.ws_T = ws;
+  p.ws_c = p.ws_T + recs * BC * BC;
+  p.ws_dU0 = p.ws_c + recs * BC;
+  p.ws_J = p.ws_dU0 + recs * BC * V;
+  p.ws_S = p.ws_J + recs * K * V;
+  p.ws_dS = p.ws_S + recs * K * V;
+  p.ws_dq = p.ws_dS + recs * K * V;
+  p.ws_dk = Hk != Hv ? p.ws_dq + static_cast<long>(B) * T * Hv * K : nullptr;
+  if (Hk == Hv) p.ws_dq = nullptr;
+  p.in_dtype = in_dtype;
+  p.beta_dtype = beta_dtype;
+  p.do_dtype = do_dtype;
+  p.B = B;
+  p.T = T;
+  p.Hk = Hk;
+  p.Hv = Hv;
+  p.K = K;
+  p.V = V;
+  p.n = static_cast<int>(n);
+  p.scale = scale;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (K == 64) return V == 64 ? run_backward<64, 64>(p, st) : run_backward<64, 128>(p, st);
+  return V == 64 ? run_backward<128, 64>(p, st) : run_backward<128, 128>(p, st);
+}

@@ -244,6 +244,53 @@ def recurrent_fwd(q, k, v, g, beta, scale: float, state_in, state_out=None, stat
     return out, state_out
 
 
+BACKWARD_HEAD_DIMS = (64, 128)
+
+
+def chunk_bwd(q, k, v, g, beta, scale: float, h0, do, dht=None):
+    """Launch pbgdn_chunk_bwd: the gradients of (o, final) = chunk_fwd(q, k, v,
+    g, beta, scale, h0) given do [B,T,Hv,V] and dht [B,Hv,K,V] (None: zeros),
+    as the reference's gated_delta_chunk_backward returns them
+    (gated_deltanet.py:230-277). Returns (dq, dk [B,T,Hk,K], dv [B,T,Hv,V] in
+    q's dtype, dg [B,T,Hv] float32, dbeta in beta's operand dtype, dh0
+    [B,Hv,K,V] float32)."""
+    batch, length, hk, hv, dk, dv = _shapes(q, k, v, g, beta)
+    dev = _require_device(q, k, v, g, beta, h0, do, dht)
+    if dk not in BACKWARD_HEAD_DIMS or dv not in BACKWARD_HEAD_DIMS:
+        raise ValueError(f"chunk backward supports K and V in {BACKWARD_HEAD_DIMS}")
+    q, k, v, g, beta = _operands(q, k, v, g, beta)
+    if do.shape != (batch, length, hv, dv):
+        raise ValueError(f"grad of o must be [B,T,Hv,V] = {(batch, length, hv, dv)}")
+    if do.dtype not in _lib.DTYPE_CODES:
+        do = do.to(torch.float32)
+    do = _aligned(do.contiguous(), 4)
+    state_shape = (batch, hv, dk, dv)
+    if h0 is not None:
+        if h0.shape != state_shape:
+            raise ValueError(f"initial state must be [B,Hv,K,V] = {state_shape}")
+        h0 = h0.to(torch.float32).contiguous()
+    if dht is not None:
+        if dht.shape != state_shape:
+            raise ValueError(f"grad of the final state must be [B,Hv,K,V] = {state_shape}")
+        dht = dht.to(torch.float32).contiguous()
+    dq, dk_ = torch.empty_like(q), torch.empty_like(k)
+    dv_ = torch.empty_like(v)
+    dg = torch.empty(batch, length, hv, dtype=torch.float32, device=dev)
+    dbeta = torch.empty_like(beta)
+    dh0 = torch.empty(state_shape, dtype=torch.float32, device=dev)
+    lib = _lib.lib()
+    ws_bytes = lib.pbgdn_chunk_bwd_workspace_size(batch, length, hk, hv, dk, dv)
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    codes = _lib.DTYPE_CODES
+    status = lib.pbgdn_chunk_bwd(
+        _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), codes[q.dtype], _lib.ptr(g), _lib.ptr(beta), codes[beta.dtype],
+        _lib.ptr(h0), _lib.ptr(do), codes[do.dtype], _lib.ptr(dht), _lib.ptr(dq), _lib.ptr(dk_), _lib.ptr(dv_),
+        _lib.ptr(dg), _lib.ptr(dbeta), _lib.ptr(dh0), _lib.ptr(workspace), ws_bytes, batch, length, hk, hv, dk, dv,
+        float(scale), _lib.stream_handle(dev))
+    _lib.check(status, "pbgdn_chunk_bwd")
+    return dq, dk_, dv_, dg, dbeta, dh0
+
+
 # ----------------------------------------------------------------------------
 # torch custom ops (functional prefill, mutating decode step) with fake impls,
 # the form of pseudobrain::gated_delta_chunk (gated_deltanet.py:200-227).
@@ -263,6 +310,49 @@ def _(q, k, v, g, beta, h0, cu_seqlens, scale):
     nseq = batch if cu_seqlens is None else cu_seqlens.shape[0] - 1
     return (q.new_empty(batch, length, hv, dv),
             q.new_empty(nseq, hv, dk, dv, dtype=torch.float32))
+
+
+@torch.library.custom_op("pbgdn::gated_delta_chunk_backward", mutates_args=(),
+                         schema="(Tensor q, Tensor k, Tensor v, Tensor g, Tensor beta, Tensor? h0, "
+                                "Tensor grad_o, Tensor? grad_final, float scale) "
+                                "-> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)")
+def gated_delta_chunk_backward(q, k, v, g, beta, h0, grad_o, grad_final, scale):
+    """(dq, dk, dv, dg fp32, dbeta, dh0 fp32): pseudobrain::gated_delta_chunk_backward
+    (gated_deltanet.py:230-256) without fla's saved gc and A (recomputed)."""
+    return chunk_bwd(q, k, v, g, beta, scale, h0, grad_o, grad_final)
+
+
+@gated_delta_chunk_backward.register_fake
+def _(q, k, v, g, beta, h0, grad_o, grad_final, scale):
+    beta_dtype = beta.dtype if beta.dtype in (torch.float32, q.dtype) else torch.float32
+    batch, hv, dk, dv = q.shape[0], v.shape[2], q.shape[3], v.shape[3]
+    return (torch.empty_like(q), q.new_empty(k.shape), q.new_empty(v.shape),
+            g.new_empty(g.shape, dtype=torch.float32), beta.new_empty(beta.shape, dtype=beta_dtype),
+            q.new_empty(batch, hv, dk, dv, dtype=torch.float32))
+
+
+def _chunk_setup(ctx, inputs, output):
+    q, k, v, g, beta, h0, cu_seqlens, scale = inputs
+    ctx.save_for_backward(q, k, v, g, beta, h0)
+    ctx.scale = scale
+    ctx.packed = cu_seqlens is not None
+
+
+def _chunk_grad(ctx, grad_o, grad_final):
+    """The reference's _fla_grad (gated_deltanet.py:266-275): zeros for a
+    missing output gradient, each gradient in its input's dtype."""
+    if ctx.packed:
+        raise NotImplementedError("the chunk backward takes [B,T] batches; packed sequences (cu_seqlens) "
+                                  "have no backward here")
+    q, k, v, g, beta, h0 = ctx.saved_tensors
+    if grad_o is None:
+        grad_o = torch.zeros(*q.shape[:2], v.shape[2], v.shape[3], dtype=q.dtype, device=q.device)
+    dq, dk, dv, dg, dbeta, dh0 = gated_delta_chunk_backward(q, k, v, g, beta, h0, grad_o, grad_final, ctx.scale)
+    return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg.to(g.dtype), dbeta.to(beta.dtype),
+            None if h0 is None else dh0.to(h0.dtype), None, None)
+
+
+gated_delta_chunk.register_autograd(_chunk_grad, setup_context=_chunk_setup)
 
 
 @torch.library.custom_op("pbgdn::recurrent_step_", mutates_args=("state",),

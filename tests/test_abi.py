@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version_and_status_strings():
-    assert _lib.lib().pbgdn_abi_version() == _lib.ABI_VERSION == 6
+    assert _lib.lib().pbgdn_abi_version() == _lib.ABI_VERSION == 7
     header = open(HEADER).read()
     assert re.search(r"#define PBGDN_ABI_VERSION (\d+)", header).group(1) == str(_lib.ABI_VERSION)
     assert _lib.status_string(0) == "ok"
@@ -271,3 +271,42 @@ def test_prologue_varlen_fwd_rejects(over, code):
 
 def test_prologue_varlen_fwd_empty_is_ok():
     assert prologue_varlen_call(T=0, nseq=0) == _lib.OK
+
+
+def chunk_bwd_call(**over):
+    args = dict(q=FAKE, k=FAKE, v=FAKE, in_dtype=1, g=FAKE, beta=FAKE, beta_dtype=0, h0=None, do=FAKE,
+                do_dtype=1, dht=None, dq=FAKE, dk=FAKE, dv=FAKE, dg=FAKE, dbeta=FAKE, dh0=None, ws=FAKE,
+                ws_bytes=1 << 40, B=1, T=64, Hk=16, Hv=32, K=128, V=128, scale=0.1, stream=None)
+    args.update(over)
+    return _lib.lib().pbgdn_chunk_bwd(*args.values())
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(in_dtype=3), _lib.ERR_INVALID_ARGUMENT),
+    (dict(beta_dtype=-1), _lib.ERR_INVALID_ARGUMENT),
+    (dict(do_dtype=5), _lib.ERR_INVALID_ARGUMENT),
+    (dict(Hv=24), _lib.ERR_INVALID_ARGUMENT),            # not a multiple of Hk
+    (dict(T=-1), _lib.ERR_INVALID_ARGUMENT),
+    (dict(K=96), _lib.ERR_UNSUPPORTED),
+    (dict(V=256), _lib.ERR_UNSUPPORTED),
+    (dict(dq=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(do=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(ws=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(ws_bytes=1024), _lib.ERR_INVALID_ARGUMENT),    # smaller than the workspace size
+    (dict(ws=FAKE + 4), _lib.ERR_INVALID_ARGUMENT),      # 16-byte alignment
+    (dict(T=64 * 65536), _lib.ERR_UNSUPPORTED),          # more chunks than a grid axis holds
+])
+def test_chunk_bwd_rejects_bad_arguments(over, code):
+    assert chunk_bwd_call(**over) == code
+
+
+def test_chunk_bwd_workspace_size():
+    """Per (batch, value head, chunk): T (64 x 64), c (64), dU0 (64 x V) and
+    the start state, end adjoint and J (K x V each) in float32; with GQA also
+    dq and dk per value head; plus 256 bytes of slack."""
+    size = _lib.lib().pbgdn_chunk_bwd_workspace_size
+    per_record = 64 * 64 + 64 + 64 * 128 + 3 * 128 * 128
+    assert size(2, 100, 4, 4, 128, 128) == 2 * 4 * 2 * per_record * 4 + 256
+    assert size(1, 64, 2, 4, 128, 128) == (4 * per_record + 2 * 64 * 4 * 128) * 4 + 256
+    assert size(1, 0, 1, 1, 64, 64) == 256
+    assert size(-1, 64, 1, 1, 64, 64) == 0

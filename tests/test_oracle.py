@@ -293,3 +293,83 @@ def test_chunked_pins_catch_mutants(old, new, monkeypatch):
     o1, s1 = gdn.delta_rule_chunked(q, k, v, g, beta, 0.5, h0)
     o2, s2 = gdn.delta_rule_sequential(q, k, v, g, beta, 0.5, h0)
     assert not (close(o1, o2, 1e-6) and close(s1, s2, 1e-6))
+
+
+# ---------------------------------------------------------------------------
+# Backward (gated_deltanet.py:230-277): gradients of <do, o> + <dht, S_T>
+# ---------------------------------------------------------------------------
+def numeric_gradients(inputs, scale, do, dht, eps=1e-6):
+    """Central differences of L = <do, o> + <dht, S_T> (float64, sequential
+    kernel) with respect to every element of every input."""
+    def loss(args):
+        o, s = gdn.delta_rule_sequential(*args[:5], scale, args[5])
+        return float(np.sum(o * do) + np.sum(s * dht))
+    grads = []
+    for i in range(6):
+        grad = np.zeros_like(inputs[i])
+        for idx in np.ndindex(inputs[i].shape):
+            args = [x.copy() for x in inputs]
+            args[i][idx] += eps
+            up = loss(args)
+            args[i][idx] -= 2 * eps
+            grad[idx] = (up - loss(args)) / (2 * eps)
+        grads.append(grad)
+    return grads
+
+
+def fd_case(seed=7):
+    rng = np.random.default_rng(seed)
+    q, k, v, g, beta, h0 = rand_inputs(1, 6, 2, 3, 2, hk=1, rng=rng, unit=False)
+    do = rng.standard_normal(v.shape)
+    dht = rng.standard_normal(h0.shape)
+    return (q, k, v, g, beta, h0), do, dht
+
+
+def test_backward_matches_finite_differences():
+    """Every gradient (GQA: q, k summed over their two value heads) equals
+    central differences of the loss through the sequential recurrence."""
+    inputs, do, dht = fd_case()
+    got = gdn.gated_delta_rule_backward(*inputs[:5], 0.8, inputs[5], do, dht)
+    want = numeric_gradients(list(inputs), 0.8, do, dht)
+    names = ("dq", "dk", "dv", "dg", "dbeta", "dh0")
+    for name, a, b in zip(names, got, want):
+        assert a.shape == b.shape, name
+        assert close(a, b, 1e-7), f"{name}: {gdn.rel_inf_error(a, b):.2e}"
+
+
+def test_backward_of_the_chunked_kernel_is_the_same():
+    """The chunked kernel computes the same function, so central differences
+    through it give the same gradients (a second route to the same numbers)."""
+    inputs, do, dht = fd_case(8)
+    q, k, v, g, beta, h0 = inputs
+    eps = 1e-6
+    got = gdn.gated_delta_rule_backward(q, k, v, g, beta, 0.6, h0, do, dht)
+
+    def loss(gv):
+        o, s = gdn.delta_rule_chunked(q, k, v, gv, beta, 0.6, h0, chunk=4)
+        return float(np.sum(o * do) + np.sum(s * dht))
+    dg = np.zeros_like(g)
+    for idx in np.ndindex(g.shape):
+        up, down = g.copy(), g.copy()
+        up[idx] += eps
+        down[idx] -= eps
+        dg[idx] = (loss(up) - loss(down)) / (2 * eps)
+    assert close(got[3], dg, 1e-7)
+
+
+BACKWARD_MUTANTS = [
+    ("ds = dp * a", "ds = dp"),                                                        # dropped decay of the adjoint
+    ("dk[:, t] -= np.einsum", "dk[:, t] += np.einsum"),                                # wrong sign
+    ("dg[:, t] = decay[:, t] * np.sum(dp * prev", "dg[:, t] = decay[:, t] * np.sum(ds * prev"),  # dS for dP
+    ("db[:, t] = np.sum(du * r, axis=-1)", "db[:, t] = np.sum(du * u, axis=-1)"),      # u for r
+    ("dq[:, t] = sc * np.einsum(\"bhkv,bhv->bhk\", cur,", "dq[:, t] = sc * np.einsum(\"bhkv,bhv->bhk\", prev,"),
+]
+
+
+@pytest.mark.parametrize("old,new", BACKWARD_MUTANTS)
+def test_backward_pins_catch_mutants(old, new):
+    bad = _mutant(gdn.gated_delta_rule_backward, old, new)
+    inputs, do, dht = fd_case()
+    got = bad(*inputs[:5], 0.8, inputs[5], do, dht)
+    want = numeric_gradients(list(inputs), 0.8, do, dht)
+    assert not all(close(a, b, 1e-7) for a, b in zip(got, want))
