@@ -1,7 +1,7 @@
 """Benchmark of the Gated DeltaNet operator on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
-                    [--no-b256] [--no-layer] [--no-long] [--copy-probe]
+                    [--no-b256] [--no-layer] [--no-long] [--no-backward] [--copy-probe]
 
 Prints ONE JSON line. The headline workload is the Qwen3-Next-shaped prefill
 (B=1, T=32768, Hk=16 -> Hv=32, K=V=128, bf16 q/k/v, fp32 state, chunk 64):
@@ -68,6 +68,46 @@ def measured_traffic(kernel: str):
 def prefill_flops(tokens, hv, dk, dv, chunk=64):
     per = 2 * chunk * (3 * dk + 2 * dv) + 6 * dk * dv + (2.0 / 3.0) * chunk * chunk
     return per * tokens * hv
+
+
+def backward_flops(tokens, hv, dk, dv, chunk=64):
+    """The chunk backward's products per token per value head: the recomputed
+    forward states and nine K x V-sized products in all (K S, K^T E U, J, K dS',
+    (Gamma K)^T dX, dO S^T, U dS'^T, dX S^T, Q S: 2KV each), five C x V-sized
+    (Tb X, M^T dO, Tb^T dU, dU X^T, dO U^T: 2CV), six C x K-sized (K K^T,
+    Q K^T, (dM o Mt) K and its transpose with Q, H K, H^T K: 2CK) and the
+    triangular terms (T^T dT, W T^T, the solve: (14/3) C^2)."""
+    per = 18 * dk * dv + 10 * chunk * dv + 12 * chunk * dk + (14.0 / 3.0) * chunk * chunk
+    return per * tokens * hv
+
+
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 MFMA
+
+
+def bench_backward(steps=3, warmup=1):
+    """pbgdn_chunk_bwd at the prefill shape (bf16 q, k, v; the gradients of o
+    and of the final state given): float32 MFMA roofline of the algorithmic
+    flops above."""
+    import torch
+    from pseudobrain_amd import gated_deltanet as gd
+    from pseudobrain_amd.workloads import WORKLOADS, workload
+    s = WORKLOADS["prefill_qwen3next"]
+    q, k, v, g, beta, h0 = (x.cuda() for x in workload("prefill_qwen3next", seed=0))
+    gen = torch.Generator().manual_seed(1)
+    do = (torch.randn(1, s.length, s.hv, s.dv, generator=gen) * 0.1).to(torch.bfloat16).cuda()
+    dht = (torch.randn(1, s.hv, s.dk, s.dv, generator=gen) * 0.1).cuda()
+    scale = s.dk ** -0.5
+
+    def step():
+        gd.chunk_bwd(q, k, v, g, beta, scale, h0, do, dht)
+
+    sec, ksec = timed_steps(step, steps, warmup)
+    flops = backward_flops(s.length, s.hv, s.dk, s.dv)
+    achieved = flops / ksec / 1e12
+    return {"workload": "prefill_qwen3next backward", "T": s.length, "ms_per_call": sec * 1e3,
+            "kernel_ms": ksec * 1e3, "Mtok_s": s.length / sec / 1e6, "algorithmic_flops": flops,
+            "roofline": {"bound": "mfma", "achieved": achieved, "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": achieved / FP32_MFMA_PEAK_TFLOPS}}
 
 
 def prefill_bytes(tokens, hk, hv, dk, dv, nstates=1, elem=2):
@@ -389,6 +429,7 @@ def main(argv=None):
     ap.add_argument("--copy-probe", action="store_true", help="also time a plain 256 MiB device copy")
     ap.add_argument("--no-layer", action="store_true", help="skip the layer prologue/epilogue kernels")
     ap.add_argument("--no-long", action="store_true", help="skip the varlen and streamed prefill workloads")
+    ap.add_argument("--no-backward", action="store_true", help="skip the chunk backward")
     args = ap.parse_args(argv)
     world = int(os.environ.get("WORLD_SIZE", args.gpus))
     if args.gpus != 1 or world != 1:
@@ -450,6 +491,8 @@ def main(argv=None):
             result["decode_layer_b64"] = bench_decode_layer(64, 200)
             result["decode_layer_b64"]["roofline"]["traffic"] = measured_traffic("decode_layer_b64")
             result["decode_layer_b64_bf16_state"] = bench_decode_layer(64, 200, state_dtype=torch.bfloat16)
+    if not args.no_backward:
+        result["backward"] = bench_backward()
     if not args.no_long:
         result.update(bench_long())
     if args.copy_probe:

@@ -310,7 +310,8 @@ int pbgdn_prologue_varlen_fwd(const void *qkv, long qkv_stride,
  *   q, k, v, in_dtype, g, beta, beta_dtype, h0, B, T, Hk, Hv, K, V, scale:
  *               as pbgdn_chunk_fwd without cu_seqlens (h0 [B, Hv, K, V]
  *               float32, or NULL for zeros)
- *   dout        [B, T, Hv, V] do_dtype: the gradient of o
+ *   dout        [B, T, Hv, V] do_dtype: the gradient of o; do_dtype must be
+ *               in_dtype (the reference casts it to q's dtype)
  *   dht         [B, Hv, K, V] float32 or NULL (zeros): the gradient of the
  *               final state
  *   dq, dk      [B, T, Hk, K] in_dtype (GQA: summed over the Hv/Hk value
@@ -323,7 +324,8 @@ int pbgdn_prologue_varlen_fwd(const void *qkv, long qkv_stride,
  *               Hv, K, V) bytes, 16-byte aligned, no initialisation needed
  *               (per chunk: its start state, end adjoint, T, the dO terms)
  *
- * Supported: K, V in {64, 128}; at most 65,535 chunks per sequence.
+ * Supported: K, V in {64, 128}; at most 65,535 chunks per sequence and
+ * 32,767 batch rows.
  */
 int pbgdn_chunk_bwd(const void *q, const void *k, const void *v, int in_dtype,
                     const float *g, const void *beta, int beta_dtype,

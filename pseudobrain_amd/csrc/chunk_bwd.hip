@@ -13,14 +13,14 @@
 //   dU = M^T dO + E K dS',  dX = Tb^T dU,
 //   dS = gamma_C dS' + scale (Gamma Q)^T dO - (Gamma K)^T dX,
 // and each chunk's gradients follow from its start state S, its end adjoint
-// dS' and its own inputs. Five launches on the caller's stream:
+// dS' and its own inputs. Four launches on the caller's stream:
 //
 //   bwd_local_kernel     per (chunk, value head): T = (I + A)^-1 by forward
 //                        substitution, dU0 = M^T dO, J = scale (Gamma Q)^T dO
-//   bwd_state_kernel     per (value head, 16 value columns), serial over the
-//                        chunks: the state at every chunk start
-//   bwd_adjoint_kernel   the same grid, chunks in reverse: the adjoint at
-//                        every chunk end, and dh0
+//   bwd_scans_kernel     per (value head, 16 value columns), serial over the
+//                        chunks, two independent roles in one launch: the
+//                        state at every chunk start (forward), and the
+//                        adjoint at every chunk end and dh0 (reverse)
 //   bwd_grad_kernel      per (chunk, value head): dq, dk, dv, dbeta, dg
 //   bwd_gqa_reduce_kernel  dq, dk summed over the value heads of a key head
 //
@@ -29,6 +29,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -52,7 +53,7 @@ struct BwdParams {
   void *dbeta;
   float *dh0;
   float *ws_T, *ws_c, *ws_dU0, *ws_J, *ws_S, *ws_dS, *ws_dq, *ws_dk;
-  int in_dtype, beta_dtype, do_dtype;
+  int in_dtype, beta_dtype;
   int B, T, Hk, Hv, K, V, n;
   float scale;
 };
@@ -76,6 +77,11 @@ __device__ __forceinline__ float4_t tile_mm(float4_t acc, FA a, FB b) {
 
 __device__ __forceinline__ float4_t zero4() { return float4_t{0.f, 0.f, 0.f, 0.f}; }
 
+template <typename T>
+constexpr int dtype_of_bwd() {
+  return sizeof(T) == 4 ? PBGDN_F32 : (std::is_same<T, u16>::value ? PBGDN_BF16 : PBGDN_F16);
+}
+
 // Sum over the 16 lanes that share lane >> 4 (the columns of one tile row).
 __device__ __forceinline__ float row16_sum(float x) {
 #pragma unroll
@@ -83,22 +89,72 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x;
 }
 
+// Eight (four for float32) consecutive elements of TIn in a 16-byte piece, as float.
+template <typename TIn>
+__device__ __forceinline__ void decode16(const uint4 &u, float *x) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+  if constexpr (sizeof(TIn) == 4) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = __uint_as_float(w[e]);
+  } else if constexpr (dtype_of_bwd<TIn>() == PBGDN_BF16) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = __uint_as_float(w[e] << 16);
+      x[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = static_cast<float>(__builtin_bit_cast(half_t, static_cast<u16>(w[e] & 0xffffu)));
+      x[2 * e + 1] = static_cast<float>(__builtin_bit_cast(half_t, static_cast<u16>(w[e] >> 16)));
+    }
+  }
+}
+
 // Workspace records of (batch b, value head h, chunk i).
 __device__ __forceinline__ long rec(const BwdParams &p, int b, int h, int i) {
   return (static_cast<long>(b) * p.Hv + h) * p.n + i;
 }
 
-// Rows t0 .. t0+63 of a [B,T,H,W] tensor (head hd, columns col0 .. col0+cols-1)
-// into LDS as float, zero past T.
-__device__ __forceinline__ void load_rows(float *dst, int ld, const void *src, int dtype, const BwdParams &p, int b,
-                                          int t0, int heads, int hd, int width, int col0, int cols) {
-  for (int e = threadIdx.x; e < BC * cols; e += BNT) {
-    const int t = e / cols, j = e % cols;
-    float x = 0.f;
-    if (t0 + t < p.T) {
-      x = load_elem(src, ((static_cast<long>(b) * p.T + t0 + t) * heads + hd) * width + col0 + j, dtype);
+// Rows t0 .. t0+63 of a [B,T,H,W] tensor of TIn (head hd, columns col0 ..
+// col0+COLS-1) into LDS as float, zero past T: 16-byte loads, all issued
+// before the first LDS write. W and col0 keep every row piece 16-byte aligned.
+template <typename TIn, int COLS>
+__device__ __forceinline__ void load_rows_vec(float *dst, int ld, const void *src, const BwdParams &p, int b, int t0,
+                                              int heads, int hd, int width, int col0) {
+  constexpr int EPP = 16 / sizeof(TIn), PPR = COLS / EPP, TOTAL = BC * PPR, PER = (TOTAL + BNT - 1) / BNT;
+  const unsigned char *base = static_cast<const unsigned char *>(src);
+  uint4 raw[PER];
+#pragma unroll
+  for (int m = 0; m < PER; ++m) {
+    const int e = threadIdx.x + BNT * m, row = e / PPR, part = e % PPR, t = t0 + row;
+    const long off = (((static_cast<long>(b) * p.T + t) * heads + hd) * width + col0) * static_cast<long>(sizeof(TIn));
+    raw[m] = e < TOTAL && t < p.T ? *reinterpret_cast<const uint4 *>(base + off + part * 16) : uint4{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int m = 0; m < PER; ++m) {
+    const int e = threadIdx.x + BNT * m, row = e / PPR, part = e % PPR;
+    if (e < TOTAL) {
+      float x[EPP];
+      decode16<TIn>(raw[m], x);
+#pragma unroll
+      for (int j = 0; j < EPP; j += 4) {
+        *reinterpret_cast<float4_t *>(&dst[row * ld + part * EPP + j]) = float4_t{x[j], x[j + 1], x[j + 2], x[j + 3]};
+      }
     }
-    dst[t * ld + j] = x;
+  }
+}
+
+// A 64 x 64 float32 record (T) into LDS rows of LC floats.
+__device__ __forceinline__ void load_t(float *st, const float *src) {
+  const float4_t *w = reinterpret_cast<const float4_t *>(src);
+  float4_t raw[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) raw[m] = w[threadIdx.x + BNT * m];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int e = threadIdx.x + BNT * m;
+    *reinterpret_cast<float4_t *>(&st[(e >> 4) * LC + 4 * (e & 15)]) = raw[m];
   }
 }
 
@@ -120,20 +176,21 @@ __device__ __forceinline__ void load_decays(const BwdParams &p, int b, int h, in
 
 // A (strict lower) and M (lower, scaled) of one chunk from K K^T and Q K^T;
 // wave w writes rows 16w .. 16w+15.
-template <int K>
+template <int K, bool WITH_A>
 __device__ __forceinline__ void form_a_m(const BwdParams &p, const float *sq, const float *sk, const float *sc,
                                          const float *sbeta, float *sa, float *sm) {
   constexpr int LK = K + 4;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 15, g4 = lane >> 4;
   for (int tc = 0; tc < 4; ++tc) {
     auto bk = [&](int kk, int j) { return sk[(16 * tc + j) * LK + kk]; };
-    float4_t kk_acc = tile_mm<K>(zero4(), [&](int r, int kk) { return sk[(16 * wave + r) * LK + kk]; }, bk);
-    float4_t qk_acc = tile_mm<K>(zero4(), [&](int r, int kk) { return sq[(16 * wave + r) * LK + kk]; }, bk);
+    float4_t kk_acc = zero4();
+    if constexpr (WITH_A) kk_acc = tile_mm<K>(kk_acc, [&](int r, int kk) { return sk[(16 * wave + r) * LK + kk]; }, bk);
+    const float4_t qk_acc = tile_mm<K>(zero4(), [&](int r, int kk) { return sq[(16 * wave + r) * LK + kk]; }, bk);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = 16 * wave + 4 * g4 + r, s = 16 * tc + c;
       const float d = t >= s ? expf(sc[t] - sc[s]) : 0.f;
-      if (sa) sa[t * LC + s] = t > s ? sbeta[t] * kk_acc[r] * d : 0.f;
+      if constexpr (WITH_A) sa[t * LC + s] = t > s ? sbeta[t] * kk_acc[r] * d : 0.f;
       sm[t * LC + s] = p.scale * qk_acc[r] * d;
     }
   }
@@ -142,19 +199,19 @@ __device__ __forceinline__ void form_a_m(const BwdParams &p, const float *sq, co
 // ---------------------------------------------------------------------------
 // Per (chunk, value head): T, dU0 = M^T dO, J = scale (Gamma Q)^T dO, c.
 // ---------------------------------------------------------------------------
-template <int K, int V>
+template <int K, int V, typename TIn>
 __global__ __launch_bounds__(BNT) void bwd_local_kernel(BwdParams p) {
   constexpr int LK = K + 4, LV = V + 4;
   extern __shared__ __align__(16) float lds[];
   float *sq = lds, *sk = sq + BC * LK, *sdo = sk + BC * LK, *sa = sdo + BC * LV, *sm = sa + BC * LC;
-  float *sc = sm + BC * LC, *sgam = sc + BC, *sbeta = sgam + BC;
+  float *sc = sm + BC * LC, *sgam = sc + BC, *sbeta = sgam + BC, *sr = sbeta + BC;
   const int i = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 15, g4 = lane >> 4;
   const int hk = h / (p.Hv / p.Hk);
   const int t0 = i * BC;
-  load_rows(sq, LK, p.q, p.in_dtype, p, b, t0, p.Hk, hk, K, 0, K);
-  load_rows(sk, LK, p.k, p.in_dtype, p, b, t0, p.Hk, hk, K, 0, K);
-  load_rows(sdo, LV, p.dout, p.do_dtype, p, b, t0, p.Hv, h, V, 0, V);
+  load_rows_vec<TIn, K>(sq, LK, p.q, p, b, t0, p.Hk, hk, K, 0);
+  load_rows_vec<TIn, K>(sk, LK, p.k, p, b, t0, p.Hk, hk, K, 0);
+  load_rows_vec<TIn, V>(sdo, LV, p.dout, p, b, t0, p.Hv, h, V, 0);
   if (wave == 0) {  // inclusive cumulative sum of g over the chunk (zero past T)
     const int t = t0 + lane;
     float x = t < p.T ? p.g[(static_cast<long>(b) * p.T + t) * p.Hv + h] : 0.f;
@@ -169,21 +226,46 @@ __global__ __launch_bounds__(BNT) void bwd_local_kernel(BwdParams p) {
     p.ws_c[rec(p, b, h, i) * BC + lane] = x;
   }
   __syncthreads();
-  form_a_m<K>(p, sq, sk, sc, sbeta, sa, sm);
+  form_a_m<K, true>(p, sq, sk, sc, sbeta, sa, sm);
   __syncthreads();
-  if (wave == 0) {
-    // T = (I + A)^-1, unit lower triangular, in place over A: lane j walks
-    // column j down the rows; T[t][j] = -sum_{s<t} A[t][s] T[s][j] (T[s][j] = 0
-    // above the diagonal, where A is zero too). All lanes read row t before
-    // any writes it (one wave, one instruction stream).
-    const int j = lane;
-    for (int t = 0; t < BC; ++t) {
+  // T = (I + A)^-1 (unit lower triangular) in place over A, by 16 x 16
+  // blocks. Wave w inverts diagonal block w by forward substitution: lane
+  // (column j, part) sums the terms s = part mod 4 of
+  // T[t][j] = -sum_{s<t} A[t][s] T[s][j] (T is zero above the diagonal, A
+  // too), and two shuffles add the parts; every lane reads row t before it is
+  // written (one wave, one instruction stream).
+  {
+    const int j = lane & 15, part = lane >> 4, base = 16 * wave;
+    for (int t = 0; t < 16; ++t) {
       float acc = 0.f;
-      for (int s = 0; s < t; ++s) acc += sa[t * LC + s] * sa[s * LC + j];
-      sa[t * LC + j] = t == j ? 1.f : (t < j ? 0.f : -acc);
+      for (int s2 = part; s2 < t; s2 += 4) acc += sa[(base + t) * LC + base + s2] * sa[(base + s2) * LC + base + j];
+      acc += __shfl_xor(acc, 16, 64);
+      acc += __shfl_xor(acc, 32, 64);
+      if (part == 0) sa[(base + t) * LC + base + j] = t == j ? 1.f : (t < j ? 0.f : -acc);
     }
   }
   __syncthreads();
+  // Off-diagonal blocks, one block row at a time:
+  // T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj, wave j forming block (i, j).
+  for (int bi = 1; bi < 4; ++bi) {
+    if (wave < bi) {
+      float4_t racc = zero4();
+      for (int bk = wave; bk < bi; ++bk) {
+        racc = tile_mm<16>(racc, [&](int r, int kk) { return sa[(16 * bi + r) * LC + 16 * bk + kk]; },
+                           [&](int kk, int col) { return sa[(16 * bk + kk) * LC + 16 * wave + col]; });
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sr[wave * 256 + (4 * g4 + r) * 16 + c] = racc[r];
+    }
+    __syncthreads();  // block row bi of A is read by every wave before any T of it is written
+    if (wave < bi) {
+      const float4_t tacc = tile_mm<16>(zero4(), [&](int r, int kk) { return sa[(16 * bi + r) * LC + 16 * bi + kk]; },
+                                        [&](int kk, int col) { return sr[wave * 256 + kk * 16 + col]; });
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sa[(16 * bi + 4 * g4 + r) * LC + 16 * wave + c] = -tacc[r];
+    }
+    __syncthreads();
+  }
   float *wt = p.ws_T + rec(p, b, h, i) * BC * BC;
   for (int e = tid; e < BC * BC; e += BNT) wt[e] = sa[(e / BC) * LC + e % BC];
   // dU0 = M^T dO: tiles (row tile, 16-column tile)
@@ -206,28 +288,114 @@ __global__ __launch_bounds__(BNT) void bwd_local_kernel(BwdParams p) {
   }
 }
 
-// Chunk inputs of the two scans: K rows, T, decays.
-template <int K>
-__device__ __forceinline__ void load_scan_chunk(const BwdParams &p, int b, int h, int hk, int i, float *sk, float *st,
-                                                float *sc, float *sgam, float *se, float *sbeta) {
-  constexpr int LK = K + 4;
-  load_rows(sk, LK, p.k, p.in_dtype, p, b, i * BC, p.Hk, hk, K, 0, K);
-  const float *wt = p.ws_T + rec(p, b, h, i) * BC * BC;
-  for (int e = threadIdx.x; e < BC * BC; e += BNT) st[(e / BC) * LC + e % BC] = wt[e];
-  load_decays(p, b, h, i, sc, sgam, se, sbeta);
-}
+// One chunk's inputs to a scan step, held in registers a step ahead: K rows
+// (16-byte pieces of TIn), T, c and beta, and the step's 16-column tile (V for
+// the forward pass; dU0 and J, the latter in the accumulator layout, for the
+// reverse pass). Loaded while the previous step computes, written to LDS
+// between steps.
+template <int K, typename TIn, bool ADJ>
+struct ScanStage {
+  static constexpr int EPP = 16 / sizeof(TIn);  // elements per 16-byte piece
+  static constexpr int ROW16 = K / EPP;         // pieces per K row
+  static constexpr int KP = BC * ROW16 / BNT;   // K pieces per thread
+  static constexpr int TILE16 = 16 / EPP;       // pieces per row of a 16-column tile
+  uint4 kr[KP];
+  float4_t tr[4];
+  float cv, bv;
+  uint4 xr;
+  float4_t dur;
+  float jr[K / 64][4];
+
+  __device__ __forceinline__ void load(const BwdParams &p, int b, int h, int hk, int i, int v0) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = lane & 15, g4 = lane >> 4;
+    const int t0 = i * BC;
+    const long r = rec(p, b, h, i);
+    const unsigned char *kb = static_cast<const unsigned char *>(p.k);
+#pragma unroll
+    for (int m = 0; m < KP; ++m) {
+      const int e = tid + BNT * m, row = e / ROW16, part = e % ROW16, t = t0 + row;
+      const long off = ((static_cast<long>(b) * p.T + t) * p.Hk + hk) * K * static_cast<long>(sizeof(TIn)) + part * 16;
+      kr[m] = t < p.T ? *reinterpret_cast<const uint4 *>(kb + off) : uint4{0u, 0u, 0u, 0u};
+    }
+    const float4_t *wt = reinterpret_cast<const float4_t *>(p.ws_T + r * BC * BC);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) tr[m] = wt[tid + BNT * m];
+    if (tid < BC) {
+      cv = p.ws_c[r * BC + tid];
+      bv = t0 + tid < p.T ? load_elem(p.beta, (static_cast<long>(b) * p.T + t0 + tid) * p.Hv + h, p.beta_dtype)
+                          : 0.f;
+    }
+    if constexpr (!ADJ) {
+      const int row = tid / TILE16, part = tid % TILE16, t = t0 + row;
+      const unsigned char *vb = static_cast<const unsigned char *>(p.v);
+      const long off = (((static_cast<long>(b) * p.T + t) * p.Hv + h) * p.V + v0) * static_cast<long>(sizeof(TIn)) +
+                       part * 16;
+      xr = tid < BC * TILE16 && t < p.T ? *reinterpret_cast<const uint4 *>(vb + off) : uint4{0u, 0u, 0u, 0u};
+    } else {
+      dur = *reinterpret_cast<const float4_t *>(p.ws_dU0 + r * BC * p.V + (tid >> 2) * p.V + v0 + 4 * (tid & 3));
+      const float *wj = p.ws_J + r * K * p.V;
+#pragma unroll
+      for (int m = 0; m < K / 64; ++m) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) jr[m][q] = wj[static_cast<long>(16 * (wave + 4 * m) + 4 * g4 + q) * p.V + v0 + c];
+      }
+    }
+  }
+
+  // K rows, T, the decays and the tile into LDS (sk, st, vectors, tile).
+  __device__ __forceinline__ void store(float *sk, float *st, float *sc, float *sgam, float *se, float *sbeta,
+                                        float *tile) const {
+    constexpr int LK = K + 4;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int m = 0; m < KP; ++m) {
+      const int e = tid + BNT * m, row = e / ROW16, part = e % ROW16;
+      float x[EPP];
+      decode16<TIn>(kr[m], x);
+#pragma unroll
+      for (int j = 0; j < EPP; j += 4) {
+        *reinterpret_cast<float4_t *>(&sk[row * LK + part * EPP + j]) = float4_t{x[j], x[j + 1], x[j + 2], x[j + 3]};
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int e = tid + BNT * m;
+      *reinterpret_cast<float4_t *>(&st[(e >> 4) * LC + 4 * (e & 15)]) = tr[m];
+    }
+    if (tid < BC) {
+      const float last = __shfl(cv, BC - 1, 64);
+      sc[tid] = cv;
+      sgam[tid] = expf(cv);
+      se[tid] = expf(last - cv);
+      sbeta[tid] = bv;
+    }
+    if constexpr (!ADJ) {
+      if (tid < BC * TILE16) {
+        float x[EPP];
+        decode16<TIn>(xr, x);
+#pragma unroll
+        for (int j = 0; j < EPP; j += 4) {
+          *reinterpret_cast<float4_t *>(&tile[(tid / TILE16) * LT + (tid % TILE16) * EPP + j]) =
+              float4_t{x[j], x[j + 1], x[j + 2], x[j + 3]};
+        }
+      }
+    } else {
+      *reinterpret_cast<float4_t *>(&tile[(tid >> 2) * LT + 4 * (tid & 3)]) = dur;
+    }
+  }
+};
 
 // ---------------------------------------------------------------------------
 // Forward over the chunks for 16 value columns: the state at every chunk
-// start. Wave w holds key-row tiles w, w+4 (K/64 of them) of the state.
+// start. Wave w holds key-row tiles w, w+4 (K/64 of them) of the state. The
+// next chunk's inputs load during each step.
 // ---------------------------------------------------------------------------
-template <int K>
-__global__ __launch_bounds__(BNT) void bwd_state_kernel(BwdParams p) {
+template <int K, typename TIn>
+__device__ __forceinline__ void state_pass(const BwdParams &p, float *lds, int b) {
   constexpr int LK = K + 4, PER = K / 64;
-  extern __shared__ __align__(16) float lds[];
   float *sk = lds, *st = sk + BC * LK, *ss = st + BC * LC, *sx = ss + K * LT, *su = sx + BC * LT;
   float *sc = su + BC * LT, *sgam = sc + BC, *se = sgam + BC, *sbeta = se + BC;
-  const int v0 = 16 * blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int v0 = 16 * blockIdx.x, h = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 15, g4 = lane >> 4;
   const int hk = h / (p.Hv / p.Hk);
   const long kv = (static_cast<long>(b) * p.Hv + h) * K * p.V;
@@ -240,6 +408,8 @@ __global__ __launch_bounds__(BNT) void bwd_state_kernel(BwdParams p) {
       s[m][r] = p.h0 ? p.h0[kv + static_cast<long>(kk) * p.V + v0 + c] : 0.f;
     }
   }
+  ScanStage<K, TIn, false> stage;
+  if (p.n > 0) stage.load(p, b, h, hk, 0, v0);
   for (int i = 0; i < p.n; ++i) {
     float *ws = p.ws_S + rec(p, b, h, i) * K * p.V;
 #pragma unroll
@@ -251,8 +421,8 @@ __global__ __launch_bounds__(BNT) void bwd_state_kernel(BwdParams p) {
         ss[kk * LT + c] = s[m][r];
       }
     }
-    load_scan_chunk<K>(p, b, h, hk, i, sk, st, sc, sgam, se, sbeta);
-    load_rows(sx, LT, p.v, p.in_dtype, p, b, i * BC, p.Hv, h, p.V, v0, 16);
+    stage.store(sk, st, sc, sgam, se, sbeta, sx);
+    if (i + 1 < p.n) stage.load(p, b, h, hk, i + 1, v0);
     __syncthreads();
     // X = V - Gamma K S (rows 16w ..)
     const float4_t ks = tile_mm<K>(zero4(), [&](int r, int kk) { return sk[(16 * wave + r) * LK + kk]; },
@@ -287,13 +457,12 @@ __global__ __launch_bounds__(BNT) void bwd_state_kernel(BwdParams p) {
 // Backward over the chunks for 16 value columns: the adjoint dS' at every
 // chunk end (the input of that chunk's gradients), then dh0.
 // ---------------------------------------------------------------------------
-template <int K>
-__global__ __launch_bounds__(BNT) void bwd_adjoint_kernel(BwdParams p) {
+template <int K, typename TIn>
+__device__ __forceinline__ void adjoint_pass(const BwdParams &p, float *lds, int b) {
   constexpr int LK = K + 4, PER = K / 64;
-  extern __shared__ __align__(16) float lds[];
   float *sk = lds, *st = sk + BC * LK, *sds = st + BC * LC, *sdu = sds + K * LT, *sdx = sdu + BC * LT;
   float *sc = sdx + BC * LT, *sgam = sc + BC, *se = sgam + BC, *sbeta = se + BC;
-  const int v0 = 16 * blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int v0 = 16 * blockIdx.x, h = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 15, g4 = lane >> 4;
   const int hk = h / (p.Hv / p.Hk);
   const long kv = (static_cast<long>(b) * p.Hv + h) * K * p.V;
@@ -306,10 +475,10 @@ __global__ __launch_bounds__(BNT) void bwd_adjoint_kernel(BwdParams p) {
       ds[m][r] = p.dht ? p.dht[kv + static_cast<long>(kk) * p.V + v0 + c] : 0.f;
     }
   }
+  ScanStage<K, TIn, true> stage;
+  if (p.n > 0) stage.load(p, b, h, hk, p.n - 1, v0);
   for (int i = p.n - 1; i >= 0; --i) {
     float *wds = p.ws_dS + rec(p, b, h, i) * K * p.V;
-    const float *wj = p.ws_J + rec(p, b, h, i) * K * p.V;
-    float4_t jv[PER];
 #pragma unroll
     for (int m = 0; m < PER; ++m) {
 #pragma unroll
@@ -317,12 +486,16 @@ __global__ __launch_bounds__(BNT) void bwd_adjoint_kernel(BwdParams p) {
         const int kk = 16 * (wave + 4 * m) + 4 * g4 + r;
         wds[static_cast<long>(kk) * p.V + v0 + c] = ds[m][r];
         sds[kk * LT + c] = ds[m][r];
-        jv[m][r] = wj[static_cast<long>(kk) * p.V + v0 + c];
       }
     }
-    load_scan_chunk<K>(p, b, h, hk, i, sk, st, sc, sgam, se, sbeta);
-    const float *wu = p.ws_dU0 + rec(p, b, h, i) * BC * p.V;
-    for (int e = tid; e < BC * 16; e += BNT) sdu[(e >> 4) * LT + (e & 15)] = wu[(e >> 4) * p.V + v0 + (e & 15)];
+    stage.store(sk, st, sc, sgam, se, sbeta, sdu);
+    float jv[PER][4];
+#pragma unroll
+    for (int m = 0; m < PER; ++m) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) jv[m][r] = stage.jr[m][r];
+    }
+    if (i > 0) stage.load(p, b, h, hk, i - 1, v0);
     __syncthreads();
     // dU = dU0 + E K dS'
     const float4_t kd = tile_mm<K>(zero4(), [&](int r, int kk) { return sk[(16 * wave + r) * LK + kk]; },
@@ -364,11 +537,26 @@ __global__ __launch_bounds__(BNT) void bwd_adjoint_kernel(BwdParams p) {
   }
 }
 
+// The two scans are independent (the reverse one needs the per-chunk records
+// and dht, not the states), so one launch runs both: blockIdx.z < B the
+// forward pass of batch row z, else the reverse pass of row z - B. Two
+// workgroups fit a CU, so each CU overlaps a forward and a reverse scan.
+template <int K, typename TIn>
+__global__ __launch_bounds__(BNT) void bwd_scans_kernel(BwdParams p) {
+  extern __shared__ __align__(16) float lds[];
+  const int z = blockIdx.z;
+  if (z < p.B) {
+    state_pass<K, TIn>(p, lds, z);
+  } else {
+    adjoint_pass<K, TIn>(p, lds, z - p.B);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Per (chunk, value head): the gradients, from the chunk's start state S and
 // end adjoint dS'. Wave w owns token rows 16w .. 16w+15 of every product.
 // ---------------------------------------------------------------------------
-template <int K, int V>
+template <int K, int V, typename TIn>
 __global__ __launch_bounds__(BNT) void bwd_grad_kernel(BwdParams p) {
   constexpr int LK = K + 4, KT = K / 16;
   extern __shared__ __align__(16) float lds[];
@@ -384,10 +572,9 @@ __global__ __launch_bounds__(BNT) void bwd_grad_kernel(BwdParams p) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 15, g4 = lane >> 4;
   const int hk = h / (p.Hv / p.Hk);
   const int t0 = i * BC;
-  load_rows(sq, LK, p.q, p.in_dtype, p, b, t0, p.Hk, hk, K, 0, K);
-  load_rows(sk, LK, p.k, p.in_dtype, p, b, t0, p.Hk, hk, K, 0, K);
-  const float *wt = p.ws_T + rec(p, b, h, i) * BC * BC;
-  for (int e = tid; e < BC * BC; e += BNT) st[(e / BC) * LC + e % BC] = wt[e];
+  load_rows_vec<TIn, K>(sq, LK, p.q, p, b, t0, p.Hk, hk, K, 0);
+  load_rows_vec<TIn, K>(sk, LK, p.k, p, b, t0, p.Hk, hk, K, 0);
+  load_t(st, p.ws_T + rec(p, b, h, i) * BC * BC);
   load_decays(p, b, h, i, sc, sgam, se, sbeta);
   if (tid < BC) {
     sdgam[tid] = 0.f;
@@ -396,7 +583,7 @@ __global__ __launch_bounds__(BNT) void bwd_grad_kernel(BwdParams p) {
     sdb[tid] = 0.f;
   }
   __syncthreads();
-  form_a_m<K>(p, sq, sk, sc, sbeta, nullptr, sm);
+  form_a_m<K, false>(p, sq, sk, sc, sbeta, nullptr, sm);
 
   float4_t dq[KT], dk[KT], dtb[4], dm[4];
 #pragma unroll
@@ -406,15 +593,52 @@ __global__ __launch_bounds__(BNT) void bwd_grad_kernel(BwdParams p) {
   float dgam_r[4] = {0.f, 0.f, 0.f, 0.f}, de_r[4] = {0.f, 0.f, 0.f, 0.f}, dgc = 0.f;
   const long kv = rec(p, b, h, i) * K * V;
   const int tw = 16 * wave;  // this wave's token rows
+  // Columns v0 .. v0+15 of the start state and end adjoint (K rows of four
+  // float4) and of V and dO (16-byte pieces of TIn), fetched into registers a
+  // tile ahead and placed in LDS between tiles.
+  constexpr int SP = K * 4 / BNT, EPP = 16 / sizeof(TIn), PPR = 16 / EPP;
+  float4_t rs[SP], rd[SP];
+  uint4 rv, ro;
+  auto fetch = [&](int v0) {
+#pragma unroll
+    for (int m = 0; m < SP; ++m) {
+      const int e = tid + BNT * m;
+      const long o = kv + static_cast<long>(e >> 2) * V + v0 + 4 * (e & 3);
+      rs[m] = *reinterpret_cast<const float4_t *>(p.ws_S + o);
+      rd[m] = *reinterpret_cast<const float4_t *>(p.ws_dS + o);
+    }
+    const int row = tid / PPR, part = tid % PPR, t = t0 + row;
+    const long off = (((static_cast<long>(b) * p.T + t) * p.Hv + h) * V + v0) * static_cast<long>(sizeof(TIn)) +
+                     part * 16;
+    const bool ok = tid < BC * PPR && t < p.T;
+    rv = ok ? *reinterpret_cast<const uint4 *>(static_cast<const unsigned char *>(p.v) + off) : uint4{0u, 0u, 0u, 0u};
+    ro = ok ? *reinterpret_cast<const uint4 *>(static_cast<const unsigned char *>(p.dout) + off)
+            : uint4{0u, 0u, 0u, 0u};
+  };
+  auto place = [&]() {
+#pragma unroll
+    for (int m = 0; m < SP; ++m) {
+      const int e = tid + BNT * m;
+      *reinterpret_cast<float4_t *>(&ss[(e >> 2) * LT + 4 * (e & 3)]) = rs[m];
+      *reinterpret_cast<float4_t *>(&sds[(e >> 2) * LT + 4 * (e & 3)]) = rd[m];
+    }
+    if (tid < BC * PPR) {
+      float x[EPP], y[EPP];
+      decode16<TIn>(rv, x);
+      decode16<TIn>(ro, y);
+      const int row = tid / PPR, part = tid % PPR;
+#pragma unroll
+      for (int j = 0; j < EPP; j += 4) {
+        *reinterpret_cast<float4_t *>(&sx[row * LT + part * EPP + j]) = float4_t{x[j], x[j + 1], x[j + 2], x[j + 3]};
+        *reinterpret_cast<float4_t *>(&sdo[row * LT + part * EPP + j]) = float4_t{y[j], y[j + 1], y[j + 2], y[j + 3]};
+      }
+    }
+  };
+  fetch(0);
   for (int v0 = 0; v0 < V; v0 += 16) {
     __syncthreads();  // the previous tile's readers are done (and sm is complete)
-    for (int e = tid; e < K * 16; e += BNT) {
-      const int kk = e >> 4, j = e & 15;
-      ss[kk * LT + j] = p.ws_S[kv + static_cast<long>(kk) * V + v0 + j];
-      sds[kk * LT + j] = p.ws_dS[kv + static_cast<long>(kk) * V + v0 + j];
-    }
-    load_rows(sx, LT, p.v, p.in_dtype, p, b, t0, p.Hv, h, V, v0, 16);
-    load_rows(sdo, LT, p.dout, p.do_dtype, p, b, t0, p.Hv, h, V, v0, 16);
+    place();
+    if (v0 + 16 < V) fetch(v0 + 16);
     __syncthreads();
     auto rows_of = [&](const float *m2, int ld) { return [=](int r, int kk) { return m2[(tw + r) * ld + kk]; }; };
     auto state_cols = [&](const float *m2) { return [=](int kk, int col) { return m2[kk * LT + col]; }; };
@@ -536,19 +760,24 @@ __global__ __launch_bounds__(BNT) void bwd_grad_kernel(BwdParams p) {
         atomicAdd(&sdc[t], dav * av);
         atomicAdd(&sdc[s2], -dav * av);
       }
-      b3[t * LC + s2] = hv;
+      // H is strictly lower: store H + H^T (symmetric) so one product gives H K + H^T K
+      if (t > s2) {
+        b3[t * LC + s2] = hv;
+        b3[s2 * LC + t] = hv;
+      } else if (t == s2) {
+        b3[t * LC + s2] = 0.f;
+      }
     }
   }
   __syncthreads();
-  // dQ += (dM o Mt) K;  dK += (dM o Mt)^T Q + H K + H^T K
+  // dQ += (dM o Mt) K;  dK += (dM o Mt)^T Q + (H + H^T) K
 #pragma unroll
   for (int kt = 0; kt < KT; ++kt) {
     auto kcol = [&](int s2, int col) { return sk[s2 * LK + 16 * kt + col]; };
     dq[kt] = tile_mm<BC>(dq[kt], [&](int r, int s2) { return b1[(tw + r) * LC + s2]; }, kcol);
     dk[kt] = tile_mm<BC>(dk[kt], [&](int r, int s2) { return b1[s2 * LC + tw + r]; },
                          [&](int s2, int col) { return sq[s2 * LK + 16 * kt + col]; });
-    dk[kt] = tile_mm<BC>(dk[kt], [&](int r, int s2) { return b3[(tw + r) * LC + s2]; }, kcol);
-    dk[kt] = tile_mm<BC>(dk[kt], [&](int r, int s2) { return b3[s2 * LC + tw + r]; }, kcol);
+    dk[kt] = tile_mm<BC>(dk[kt], [&](int r, int s2) { return b3[(tw + r) * LC + s2]; }, kcol);  // (H + H^T) K
   }
   // dq, dk: straight to the output without GQA, else per value head in float32
   const bool direct = p.Hk == p.Hv;
@@ -608,7 +837,9 @@ __global__ __launch_bounds__(BNT) void bwd_gqa_reduce_kernel(BwdParams p) {
 
 // LDS bytes of each kernel.
 template <int K, int V>
-constexpr size_t local_lds() { return sizeof(float) * (2 * BC * (K + 4) + BC * (V + 4) + 2 * BC * LC + 3 * BC); }
+constexpr size_t local_lds() {
+  return sizeof(float) * (2 * BC * (K + 4) + BC * (V + 4) + 2 * BC * LC + 3 * BC + 3 * 256);
+}
 template <int K>
 constexpr size_t scan_lds() { return sizeof(float) * (BC * (K + 4) + BC * LC + K * LT + 2 * BC * LT + 4 * BC); }
 template <int K>
@@ -631,12 +862,29 @@ int launch(Kern kernel, dim3 grid, size_t lds, hipStream_t st, const BwdParams &
 template <int K, int V>
 int run_backward(const BwdParams &p, hipStream_t st) {
   static_assert(grad_lds<K>() <= 160 * 1024 && local_lds<K, V>() <= 160 * 1024, "LDS budget");
-  const dim3 per_chunk(p.n, p.Hv, p.B), per_tile(V / 16, p.Hv, p.B);
+  const dim3 per_chunk(p.n, p.Hv, p.B), per_tile2(V / 16, p.Hv, 2 * p.B);
   int rc = PBGDN_OK;
-  if (p.n > 0) rc = launch(bwd_local_kernel<K, V>, per_chunk, local_lds<K, V>(), st, p);
-  if (rc == PBGDN_OK && p.n > 0) rc = launch(bwd_state_kernel<K>, per_tile, scan_lds<K>(), st, p);
-  if (rc == PBGDN_OK) rc = launch(bwd_adjoint_kernel<K>, per_tile, scan_lds<K>(), st, p);
-  if (rc == PBGDN_OK && p.n > 0) rc = launch(bwd_grad_kernel<K, V>, per_chunk, grad_lds<K>(), st, p);
+  if (p.n > 0) {
+    switch (p.in_dtype) {
+      case PBGDN_F32: rc = launch(bwd_local_kernel<K, V, float>, per_chunk, local_lds<K, V>(), st, p); break;
+      case PBGDN_BF16: rc = launch(bwd_local_kernel<K, V, u16>, per_chunk, local_lds<K, V>(), st, p); break;
+      default: rc = launch(bwd_local_kernel<K, V, half_t>, per_chunk, local_lds<K, V>(), st, p); break;
+    }
+  }
+  if (rc == PBGDN_OK) {  // both scans in one launch (with T = 0 only the reverse one writes: dh0 = dht)
+    switch (p.in_dtype) {
+      case PBGDN_F32: rc = launch(bwd_scans_kernel<K, float>, per_tile2, scan_lds<K>(), st, p); break;
+      case PBGDN_BF16: rc = launch(bwd_scans_kernel<K, u16>, per_tile2, scan_lds<K>(), st, p); break;
+      default: rc = launch(bwd_scans_kernel<K, half_t>, per_tile2, scan_lds<K>(), st, p); break;
+    }
+  }
+  if (rc == PBGDN_OK && p.n > 0) {
+    switch (p.in_dtype) {
+      case PBGDN_F32: rc = launch(bwd_grad_kernel<K, V, float>, per_chunk, grad_lds<K>(), st, p); break;
+      case PBGDN_BF16: rc = launch(bwd_grad_kernel<K, V, u16>, per_chunk, grad_lds<K>(), st, p); break;
+      default: rc = launch(bwd_grad_kernel<K, V, half_t>, per_chunk, grad_lds<K>(), st, p); break;
+    }
+  }
   if (rc == PBGDN_OK && p.n > 0 && p.Hk != p.Hv) {
     const long total = static_cast<long>(p.B) * p.T * p.Hk * K;
     const unsigned blocks = static_cast<unsigned>(std::min<long>((total + BNT - 1) / BNT, 65535L));
@@ -672,7 +920,7 @@ extern "C" int pbgdn_chunk_bwd(const void *q, const void *k, const void *v, int 
   if (B < 0 || T < 0 || Hk <= 0 || Hv <= 0 || K <= 0 || V <= 0 || Hv % Hk != 0) return PBGDN_ERR_INVALID_ARGUMENT;
   auto dtype_ok = [](int d) { return d == PBGDN_F32 || d == PBGDN_BF16 || d == PBGDN_F16; };
   if (!dtype_ok(in_dtype) || !dtype_ok(beta_dtype) || !dtype_ok(do_dtype)) return PBGDN_ERR_INVALID_ARGUMENT;
-  if (!((K == 64 || K == 128) && (V == 64 || V == 128))) return PBGDN_ERR_UNSUPPORTED;
+  if (!((K == 64 || K == 128) && (V == 64 || V == 128)) || do_dtype != in_dtype) return PBGDN_ERR_UNSUPPORTED;
   if (static_cast<long>(B) * T == 0) {
     if (B > 0 && dh0 == nullptr) return PBGDN_OK;
   }
@@ -681,7 +929,7 @@ extern "C" int pbgdn_chunk_bwd(const void *q, const void *k, const void *v, int 
     return PBGDN_ERR_INVALID_ARGUMENT;
   }
   if (B == 0) return PBGDN_OK;
-  if (n > 65535 || Hv > 65535 || B > 65535) return PBGDN_ERR_UNSUPPORTED;
+  if (n > 65535 || Hv > 65535 || B > 32767) return PBGDN_ERR_UNSUPPORTED;
   if (!workspace || workspace_bytes < pbgdn_chunk_bwd_workspace_size(B, T, Hk, Hv, K, V) ||
       reinterpret_cast<uintptr_t>(workspace) % 16 != 0) {
     return PBGDN_ERR_INVALID_ARGUMENT;
@@ -714,7 +962,6 @@ extern "C" int pbgdn_chunk_bwd(const void *q, const void *k, const void *v, int 
   if (Hk == Hv) p.ws_dq = nullptr;
   p.in_dtype = in_dtype;
   p.beta_dtype = beta_dtype;
-  p.do_dtype = do_dtype;
   p.B = B;
   p.T = T;
   p.Hk = Hk;

@@ -261,9 +261,7 @@ def chunk_bwd(q, k, v, g, beta, scale: float, h0, do, dht=None):
     q, k, v, g, beta = _operands(q, k, v, g, beta)
     if do.shape != (batch, length, hv, dv):
         raise ValueError(f"grad of o must be [B,T,Hv,V] = {(batch, length, hv, dv)}")
-    if do.dtype not in _lib.DTYPE_CODES:
-        do = do.to(torch.float32)
-    do = _aligned(do.contiguous(), 4)
+    do = _aligned(do.to(q.dtype).contiguous(), 16)  # the reference passes grad_o.to(q.dtype) (:272)
     state_shape = (batch, hv, dk, dv)
     if h0 is not None:
         if h0.shape != state_shape:

@@ -285,6 +285,7 @@ def chunk_bwd_call(**over):
     (dict(in_dtype=3), _lib.ERR_INVALID_ARGUMENT),
     (dict(beta_dtype=-1), _lib.ERR_INVALID_ARGUMENT),
     (dict(do_dtype=5), _lib.ERR_INVALID_ARGUMENT),
+    (dict(do_dtype=0), _lib.ERR_UNSUPPORTED),            # not q's dtype
     (dict(Hv=24), _lib.ERR_INVALID_ARGUMENT),            # not a multiple of Hk
     (dict(T=-1), _lib.ERR_INVALID_ARGUMENT),
     (dict(K=96), _lib.ERR_UNSUPPORTED),
