@@ -65,12 +65,12 @@ __device__ __forceinline__ float4_t mfma_f32(float a, float b, float4_t acc) {
 }
 
 // acc += sum_{k < KD} a(i, k) b(k, j) over a 16x16 tile; a(i, k) is row i of
-// the tile's A rows, b(k, j) column j of its B columns.
-template <int KD, typename FA, typename FB>
+// the tile's A rows, b(k, j) column j of its B columns; U k-steps unrolled.
+template <int KD, int U = 8, typename FA, typename FB>
 __device__ __forceinline__ float4_t tile_mm(float4_t acc, FA a, FB b) {
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, g = lane >> 4;
-#pragma unroll 8
+#pragma unroll U
   for (int k = 0; k < KD; k += 4) acc = mfma_f32(a(c, k + g), b(k + g, c), acc);
   return acc;
 }
@@ -554,11 +554,16 @@ __global__ __launch_bounds__(BNT) void bwd_scans_kernel(BwdParams p) {
 
 // ---------------------------------------------------------------------------
 // Per (chunk, value head): the gradients, from the chunk's start state S and
-// end adjoint dS'. Wave w owns token rows 16w .. 16w+15 of every product.
+// end adjoint dS'. Eight waves, two per SIMD: waves w and w+4 share token rows
+// 16w .. 16w+15 (w = wave & 3) and split the column tiles of every product
+// that has more than one; the chain X -> U -> dU -> dX (one 16-column tile per
+// row block) runs on waves 0-3 while waves 4-7 form Q S and its dgamma term.
 // ---------------------------------------------------------------------------
+constexpr int GNT = 512;
+
 template <int K, int V, typename TIn>
-__global__ __launch_bounds__(BNT) void bwd_grad_kernel(BwdParams p) {
-  constexpr int LK = K + 4, KT = K / 16;
+__global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
+  constexpr int LK = K + 4, KT = K / 16, KH = KT / 2;
   extern __shared__ __align__(16) float lds[];
   float *sq = lds, *sk = sq + BC * LK, *st = sk + BC * LK, *sm = st + BC * LC;
   float *area = sm + BC * LC;  // the value-column tiles, then three C x C matrices
@@ -570,36 +575,49 @@ __global__ __launch_bounds__(BNT) void bwd_grad_kernel(BwdParams p) {
   float *sdgam = sbeta + BC, *sde = sdgam + BC, *sdc = sde + BC, *sdb = sdc + BC, *sred = sdb + BC;
   const int i = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 15, g4 = lane >> 4;
+  const int half = wave >> 2, tw = 16 * (wave & 3);  // column half; this wave's token rows
+  const bool chain = half == 0;
   const int hk = h / (p.Hv / p.Hk);
   const int t0 = i * BC;
-  load_rows_vec<TIn, K>(sq, LK, p.q, p, b, t0, p.Hk, hk, K, 0);
-  load_rows_vec<TIn, K>(sk, LK, p.k, p, b, t0, p.Hk, hk, K, 0);
-  load_t(st, p.ws_T + rec(p, b, h, i) * BC * BC);
-  load_decays(p, b, h, i, sc, sgam, se, sbeta);
-  if (tid < BC) {
-    sdgam[tid] = 0.f;
-    sde[tid] = 0.f;
-    sdc[tid] = 0.f;
-    sdb[tid] = 0.f;
+  if (tid < BNT) {  // the loads run on the first four waves
+    load_rows_vec<TIn, K>(sq, LK, p.q, p, b, t0, p.Hk, hk, K, 0);
+    load_rows_vec<TIn, K>(sk, LK, p.k, p, b, t0, p.Hk, hk, K, 0);
+    load_t(st, p.ws_T + rec(p, b, h, i) * BC * BC);
+    load_decays(p, b, h, i, sc, sgam, se, sbeta);
+    if (tid < BC) {
+      sdgam[tid] = 0.f;
+      sde[tid] = 0.f;
+      sdc[tid] = 0.f;
+      sdb[tid] = 0.f;
+    }
   }
   __syncthreads();
-  form_a_m<K, false>(p, sq, sk, sc, sbeta, nullptr, sm);
+  // M = scale (Q K^T) o D, this wave's rows and column tiles 2 half, 2 half + 1
+  for (int tc = 2 * half; tc < 2 * half + 2; ++tc) {
+    const float4_t qk = tile_mm<K, 4>(zero4(), [&](int r, int kk) { return sq[(tw + r) * LK + kk]; },
+                                   [&](int kk, int j) { return sk[(16 * tc + j) * LK + kk]; });
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = tw + 4 * g4 + r, s2 = 16 * tc + c;
+      sm[t * LC + s2] = t >= s2 ? p.scale * qk[r] * expf(sc[t] - sc[s2]) : 0.f;
+    }
+  }
 
-  float4_t dq[KT], dk[KT], dtb[4], dm[4];
+  float4_t dq[KH], dk[KH], dtb[2], dm[2];
 #pragma unroll
-  for (int m = 0; m < KT; ++m) dq[m] = dk[m] = zero4();
+  for (int m = 0; m < KH; ++m) dq[m] = dk[m] = zero4();
 #pragma unroll
-  for (int m = 0; m < 4; ++m) dtb[m] = dm[m] = zero4();
+  for (int m = 0; m < 2; ++m) dtb[m] = dm[m] = zero4();
   float dgam_r[4] = {0.f, 0.f, 0.f, 0.f}, de_r[4] = {0.f, 0.f, 0.f, 0.f}, dgc = 0.f;
   const long kv = rec(p, b, h, i) * K * V;
-  const int tw = 16 * wave;  // this wave's token rows
   // Columns v0 .. v0+15 of the start state and end adjoint (K rows of four
   // float4) and of V and dO (16-byte pieces of TIn), fetched into registers a
-  // tile ahead and placed in LDS between tiles.
+  // tile ahead by the first four waves and placed in LDS between tiles.
   constexpr int SP = K * 4 / BNT, EPP = 16 / sizeof(TIn), PPR = 16 / EPP;
   float4_t rs[SP], rd[SP];
   uint4 rv, ro;
   auto fetch = [&](int v0) {
+    if (tid >= BNT) return;
 #pragma unroll
     for (int m = 0; m < SP; ++m) {
       const int e = tid + BNT * m;
@@ -616,6 +634,7 @@ __global__ __launch_bounds__(BNT) void bwd_grad_kernel(BwdParams p) {
             : uint4{0u, 0u, 0u, 0u};
   };
   auto place = [&]() {
+    if (tid >= BNT) return;
 #pragma unroll
     for (int m = 0; m < SP; ++m) {
       const int e = tid + BNT * m;
@@ -634,76 +653,86 @@ __global__ __launch_bounds__(BNT) void bwd_grad_kernel(BwdParams p) {
       }
     }
   };
+  auto rows_of = [&](const float *m2, int ld) { return [=](int r, int kk) { return m2[(tw + r) * ld + kk]; }; };
+  auto state_cols = [&](const float *m2) { return [=](int kk, int col) { return m2[kk * LT + col]; }; };
   fetch(0);
   for (int v0 = 0; v0 < V; v0 += 16) {
     __syncthreads();  // the previous tile's readers are done (and sm is complete)
     place();
     if (v0 + 16 < V) fetch(v0 + 16);
     __syncthreads();
-    auto rows_of = [&](const float *m2, int ld) { return [=](int r, int kk) { return m2[(tw + r) * ld + kk]; }; };
-    auto state_cols = [&](const float *m2) { return [=](int kk, int col) { return m2[kk * LT + col]; }; };
-    const float4_t ks = tile_mm<K>(zero4(), rows_of(sk, LK), state_cols(ss));
-    const float4_t qs = tile_mm<K>(zero4(), rows_of(sq, LK), state_cols(ss));
-    const float4_t kd = tile_mm<K>(zero4(), rows_of(sk, LK), state_cols(sds));
+    float4_t ks = zero4(), kd = zero4();
+    if (chain) {
+      ks = tile_mm<K, 4>(zero4(), rows_of(sk, LK), state_cols(ss));
+      kd = tile_mm<K, 4>(zero4(), rows_of(sk, LK), state_cols(sds));
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = tw + 4 * g4 + r;
-      sx[t * LT + c] -= sgam[t] * ks[r];  // X = V - Gamma K S
-    }
-    __syncthreads();
-    const float4_t u = tile_mm<BC>(zero4(), [&](int r, int s2) { return st[(tw + r) * LC + s2] * sbeta[s2]; },
-                                   [&](int s2, int col) { return sx[s2 * LT + col]; });
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      su[(tw + 4 * g4 + r) * LT + c] = u[r];
-      de_r[r] += kd[r] * u[r];
-    }
-    float4_t du = tile_mm<BC>(zero4(), [&](int r, int s2) { return sm[s2 * LC + tw + r]; },
-                              [&](int s2, int col) { return sdo[s2 * LT + col]; });
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = tw + 4 * g4 + r;
-      du[r] += se[t] * kd[r];
-      sdu[t * LT + c] = du[r];
-    }
-    __syncthreads();
-    const float4_t dx = tile_mm<BC>(
-        zero4(), [&](int r, int s2) { return st[s2 * LC + tw + r] * sbeta[tw + r]; },
-        [&](int s2, int col) { return sdu[s2 * LT + col]; });
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = tw + 4 * g4 + r;
-      sdx[t * LT + c] = dx[r];
-      if (t0 + t < p.T) {
-        store_elem(p.dv, ((static_cast<long>(b) * p.T + t0 + t) * p.Hv + h) * V + v0 + c, p.in_dtype, dx[r]);
+      for (int r = 0; r < 4; ++r) {
+        const int t = tw + 4 * g4 + r;
+        sx[t * LT + c] -= sgam[t] * ks[r];  // X = V - Gamma K S
       }
-      dgam_r[r] += p.scale * qs[r] * sdo[t * LT + c] - ks[r] * dx[r];
+    } else {
+      const float4_t qs = tile_mm<K, 4>(zero4(), rows_of(sq, LK), state_cols(ss));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dgam_r[r] += p.scale * qs[r] * sdo[(tw + 4 * g4 + r) * LT + c];
     }
-    for (int e = tid; e < K * 16; e += BNT) dgc += ss[(e >> 4) * LT + (e & 15)] * sds[(e >> 4) * LT + (e & 15)];
     __syncthreads();
-    // C x C products over these 16 columns: dTb += dU X^T, dM += dO U^T
+    if (chain) {
+      const float4_t u = tile_mm<BC, 4>(zero4(), [&](int r, int s2) { return st[(tw + r) * LC + s2] * sbeta[s2]; },
+                                     [&](int s2, int col) { return sx[s2 * LT + col]; });
+      float4_t du = tile_mm<BC, 4>(zero4(), [&](int r, int s2) { return sm[s2 * LC + tw + r]; },
+                                [&](int s2, int col) { return sdo[s2 * LT + col]; });
 #pragma unroll
-    for (int tc = 0; tc < 4; ++tc) {
-      dtb[tc] = tile_mm<16>(dtb[tc], rows_of(sdu, LT), [&](int j, int col) { return sx[(16 * tc + col) * LT + j]; });
-      dm[tc] = tile_mm<16>(dm[tc], rows_of(sdo, LT), [&](int j, int col) { return su[(16 * tc + col) * LT + j]; });
+      for (int r = 0; r < 4; ++r) {
+        const int t = tw + 4 * g4 + r;
+        su[t * LT + c] = u[r];
+        de_r[r] += kd[r] * u[r];
+        du[r] += se[t] * kd[r];
+        sdu[t * LT + c] = du[r];
+      }
     }
-    // dQ += scale Gamma dO S^T;  dK += E U dS'^T - Gamma dX S^T
+    __syncthreads();
+    if (chain) {
+      const float4_t dx = tile_mm<BC, 4>(
+          zero4(), [&](int r, int s2) { return st[s2 * LC + tw + r] * sbeta[tw + r]; },
+          [&](int s2, int col) { return sdu[s2 * LT + col]; });
 #pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
+      for (int r = 0; r < 4; ++r) {
+        const int t = tw + 4 * g4 + r;
+        sdx[t * LT + c] = dx[r];
+        if (t0 + t < p.T) {
+          store_elem(p.dv, ((static_cast<long>(b) * p.T + t0 + t) * p.Hv + h) * V + v0 + c, p.in_dtype, dx[r]);
+        }
+        dgam_r[r] -= ks[r] * dx[r];
+      }
+    }
+    for (int e = tid; e < K * 16; e += GNT) dgc += ss[(e >> 4) * LT + (e & 15)] * sds[(e >> 4) * LT + (e & 15)];
+    __syncthreads();
+    // C x C products over these 16 columns (this wave's two column tiles):
+    // dTb += dU X^T, dM += dO U^T
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const int tc = 2 * half + m;
+      dtb[m] = tile_mm<16, 4>(dtb[m], rows_of(sdu, LT), [&](int j, int col) { return sx[(16 * tc + col) * LT + j]; });
+      dm[m] = tile_mm<16, 4>(dm[m], rows_of(sdo, LT), [&](int j, int col) { return su[(16 * tc + col) * LT + j]; });
+    }
+    // dQ += scale Gamma dO S^T;  dK += E U dS'^T - Gamma dX S^T (this wave's half of the key tiles)
+#pragma unroll
+    for (int m = 0; m < KH; ++m) {
+      const int kt = half * KH + m;
       auto s_t = [&](int j, int col) { return ss[(16 * kt + col) * LT + j]; };
-      dq[kt] = tile_mm<16>(dq[kt], [&](int r, int j) { return sdo[(tw + r) * LT + j] * sgam[tw + r] * p.scale; }, s_t);
-      dk[kt] = tile_mm<16>(dk[kt], [&](int r, int j) { return su[(tw + r) * LT + j] * se[tw + r]; },
-                           [&](int j, int col) { return sds[(16 * kt + col) * LT + j]; });
-      dk[kt] = tile_mm<16>(dk[kt], [&](int r, int j) { return -sdx[(tw + r) * LT + j] * sgam[tw + r]; }, s_t);
+      dq[m] = tile_mm<16, 4>(dq[m], [&](int r, int j) { return sdo[(tw + r) * LT + j] * sgam[tw + r] * p.scale; }, s_t);
+      dk[m] = tile_mm<16, 4>(dk[m], [&](int r, int j) { return su[(tw + r) * LT + j] * se[tw + r]; },
+                          [&](int j, int col) { return sds[(16 * kt + col) * LT + j]; });
+      dk[m] = tile_mm<16, 4>(dk[m], [&](int r, int j) { return -sdx[(tw + r) * LT + j] * sgam[tw + r]; }, s_t);
     }
   }
-  // per-token sums over the value columns
+  // per-token sums over the value columns (both halves add into sdgam)
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const float a = row16_sum(dgam_r[r]), e2 = row16_sum(de_r[r]);
     if (c == 0) {
-      sdgam[tw + 4 * g4 + r] = a;
-      sde[tw + 4 * g4 + r] = e2;
+      atomicAdd(&sdgam[tw + 4 * g4 + r], a);
+      if (chain) sde[tw + 4 * g4 + r] = e2;
     }
   }
   dgc = wave_sum(dgc);
@@ -711,57 +740,57 @@ __global__ __launch_bounds__(BNT) void bwd_grad_kernel(BwdParams p) {
   __syncthreads();  // the value tiles are dead: the area now holds b1, b2, b3
   // dM o Mt into b1 (and its dc terms); dT = dTb diag(beta) into b2 (and dbeta)
 #pragma unroll
-  for (int tc = 0; tc < 4; ++tc) {
+  for (int m = 0; m < 2; ++m) {
+    const int tc = 2 * half + m;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = tw + 4 * g4 + r, s2 = 16 * tc + c;
       const float d = t >= s2 ? p.scale * expf(sc[t] - sc[s2]) : 0.f;
-      const float dmv = t >= s2 ? dm[tc][r] : 0.f;
+      const float dmv = t >= s2 ? dm[m][r] : 0.f;
       b1[t * LC + s2] = dmv * d;
       const float dcv = dmv * sm[t * LC + s2];
       atomicAdd(&sdc[t], dcv);
       atomicAdd(&sdc[s2], -dcv);
-      b2[t * LC + s2] = dtb[tc][r] * sbeta[s2];
-      atomicAdd(&sdb[s2], dtb[tc][r] * st[t * LC + s2]);
+      b2[t * LC + s2] = dtb[m][r] * sbeta[s2];
+      atomicAdd(&sdb[s2], dtb[m][r] * st[t * LC + s2]);
     }
   }
   __syncthreads();
-  // W = T^T dT (rows of this wave), then into b2 once every wave has read dT
-  float4_t w4[4];
+  // W = T^T dT (this wave's tiles), then into b2 once every wave has read dT
+  float4_t w4[2];
 #pragma unroll
-  for (int tc = 0; tc < 4; ++tc) {
-    w4[tc] = tile_mm<BC>(zero4(), [&](int r, int u2) { return st[u2 * LC + tw + r]; },
-                         [&](int u2, int col) { return b2[u2 * LC + 16 * tc + col]; });
+  for (int m = 0; m < 2; ++m) {
+    const int tc = 2 * half + m;
+    w4[m] = tile_mm<BC, 4>(zero4(), [&](int r, int u2) { return st[u2 * LC + tw + r]; },
+                        [&](int u2, int col) { return b2[u2 * LC + 16 * tc + col]; });
   }
   __syncthreads();
 #pragma unroll
-  for (int tc = 0; tc < 4; ++tc) {
+  for (int m = 0; m < 2; ++m) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) b2[(tw + 4 * g4 + r) * LC + 16 * tc + c] = w4[tc][r];
+    for (int r = 0; r < 4; ++r) b2[(tw + 4 * g4 + r) * LC + 16 * (2 * half + m) + c] = w4[m][r];
   }
   __syncthreads();
-  // dA = -W T^T (strict lower): H = dA beta_t D into b3; dbeta_t, dc terms
+  // dA = -W T^T (strict lower): H = dA beta_t D, stored as H + H^T in b3
+  // (symmetric, so one product gives H K + H^T K); dbeta_t, dc terms
 #pragma unroll
-  for (int tc = 0; tc < 4; ++tc) {
-    const float4_t da = tile_mm<BC>(zero4(), [&](int r, int u2) { return b2[(tw + r) * LC + u2]; },
+  for (int m = 0; m < 2; ++m) {
+    const int tc = 2 * half + m;
+    const float4_t da = tile_mm<BC, 4>(zero4(), [&](int r, int u2) { return b2[(tw + r) * LC + u2]; },
                                     [&](int u2, int col) { return st[(16 * tc + col) * LC + u2]; });
-    const float4_t gk = tile_mm<K>(zero4(), [&](int r, int kk) { return sk[(tw + r) * LK + kk]; },
+    const float4_t gk = tile_mm<K, 4>(zero4(), [&](int r, int kk) { return sk[(tw + r) * LK + kk]; },
                                    [&](int kk, int col) { return sk[(16 * tc + col) * LK + kk]; });
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = tw + 4 * g4 + r, s2 = 16 * tc + c;
-      float hv = 0.f;
       if (t > s2) {
         const float d = expf(sc[t] - sc[s2]);
         const float dav = -da[r];
         const float av = sbeta[t] * gk[r] * d;
-        hv = dav * sbeta[t] * d;
+        const float hv = dav * sbeta[t] * d;
         atomicAdd(&sdb[t], dav * gk[r] * d);
         atomicAdd(&sdc[t], dav * av);
         atomicAdd(&sdc[s2], -dav * av);
-      }
-      // H is strictly lower: store H + H^T (symmetric) so one product gives H K + H^T K
-      if (t > s2) {
         b3[t * LC + s2] = hv;
         b3[s2 * LC + t] = hv;
       } else if (t == s2) {
@@ -772,29 +801,30 @@ __global__ __launch_bounds__(BNT) void bwd_grad_kernel(BwdParams p) {
   __syncthreads();
   // dQ += (dM o Mt) K;  dK += (dM o Mt)^T Q + (H + H^T) K
 #pragma unroll
-  for (int kt = 0; kt < KT; ++kt) {
+  for (int m = 0; m < KH; ++m) {
+    const int kt = half * KH + m;
     auto kcol = [&](int s2, int col) { return sk[s2 * LK + 16 * kt + col]; };
-    dq[kt] = tile_mm<BC>(dq[kt], [&](int r, int s2) { return b1[(tw + r) * LC + s2]; }, kcol);
-    dk[kt] = tile_mm<BC>(dk[kt], [&](int r, int s2) { return b1[s2 * LC + tw + r]; },
-                         [&](int s2, int col) { return sq[s2 * LK + 16 * kt + col]; });
-    dk[kt] = tile_mm<BC>(dk[kt], [&](int r, int s2) { return b3[(tw + r) * LC + s2]; }, kcol);  // (H + H^T) K
+    dq[m] = tile_mm<BC, 4>(dq[m], [&](int r, int s2) { return b1[(tw + r) * LC + s2]; }, kcol);
+    dk[m] = tile_mm<BC, 4>(dk[m], [&](int r, int s2) { return b1[s2 * LC + tw + r]; },
+                        [&](int s2, int col) { return sq[s2 * LK + 16 * kt + col]; });
+    dk[m] = tile_mm<BC, 4>(dk[m], [&](int r, int s2) { return b3[(tw + r) * LC + s2]; }, kcol);
   }
   // dq, dk: straight to the output without GQA, else per value head in float32
   const bool direct = p.Hk == p.Hv;
 #pragma unroll
-  for (int kt = 0; kt < KT; ++kt) {
+  for (int m = 0; m < KH; ++m) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int t = t0 + tw + 4 * g4 + r, kk = 16 * kt + c;
+      const int t = t0 + tw + 4 * g4 + r, kk = 16 * (half * KH + m) + c;
       if (t >= p.T) continue;
       if (direct) {
         const long o = ((static_cast<long>(b) * p.T + t) * p.Hk + hk) * K + kk;
-        store_elem(p.dq, o, p.in_dtype, dq[kt][r]);
-        store_elem(p.dk, o, p.in_dtype, dk[kt][r]);
+        store_elem(p.dq, o, p.in_dtype, dq[m][r]);
+        store_elem(p.dk, o, p.in_dtype, dk[m][r]);
       } else {
         const long o = ((static_cast<long>(b) * p.T + t) * p.Hv + h) * K + kk;
-        p.ws_dq[o] = dq[kt][r];
-        p.ws_dk[o] = dk[kt][r];
+        p.ws_dq[o] = dq[m][r];
+        p.ws_dk[o] = dk[m][r];
       }
     }
   }
@@ -803,7 +833,10 @@ __global__ __launch_bounds__(BNT) void bwd_grad_kernel(BwdParams p) {
     const int t = lane;
     float dcv = sdc[t] + sdgam[t] * sgam[t] - sde[t] * se[t];
     const float tail = wave_sum(sde[t] * se[t]);
-    if (t == BC - 1) dcv += tail + (sred[0] + sred[1] + sred[2] + sred[3]) * sgam[BC - 1];
+    float gc = 0.f;
+#pragma unroll
+    for (int w = 0; w < GNT / 64; ++w) gc += sred[w];
+    if (t == BC - 1) dcv += tail + gc * sgam[BC - 1];
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
       const float y = __shfl_down(dcv, off, 64);
@@ -846,16 +879,16 @@ template <int K>
 constexpr size_t grad_lds() {
   return sizeof(float) * (2 * BC * (K + 4) + 2 * BC * LC +
                           (3 * BC * LC > 2 * K * LT + 5 * BC * LT ? 3 * BC * LC : 2 * K * LT + 5 * BC * LT) +
-                          8 * BC + 4);
+                          8 * BC + GNT / 64);
 }
 
 template <typename Kern>
-int launch(Kern kernel, dim3 grid, size_t lds, hipStream_t st, const BwdParams &p) {
+int launch(Kern kernel, dim3 grid, size_t lds, hipStream_t st, const BwdParams &p, int threads = BNT) {
   if (hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                           static_cast<int>(lds)) != hipSuccess) {
     return PBGDN_ERR_LAUNCH;
   }
-  hipLaunchKernelGGL(kernel, grid, dim3(BNT), lds, st, p);
+  hipLaunchKernelGGL(kernel, grid, dim3(threads), lds, st, p);
   return hipGetLastError() == hipSuccess ? PBGDN_OK : PBGDN_ERR_LAUNCH;
 }
 
@@ -880,9 +913,9 @@ int run_backward(const BwdParams &p, hipStream_t st) {
   }
   if (rc == PBGDN_OK && p.n > 0) {
     switch (p.in_dtype) {
-      case PBGDN_F32: rc = launch(bwd_grad_kernel<K, V, float>, per_chunk, grad_lds<K>(), st, p); break;
-      case PBGDN_BF16: rc = launch(bwd_grad_kernel<K, V, u16>, per_chunk, grad_lds<K>(), st, p); break;
-      default: rc = launch(bwd_grad_kernel<K, V, half_t>, per_chunk, grad_lds<K>(), st, p); break;
+      case PBGDN_F32: rc = launch(bwd_grad_kernel<K, V, float>, per_chunk, grad_lds<K>(), st, p, GNT); break;
+      case PBGDN_BF16: rc = launch(bwd_grad_kernel<K, V, u16>, per_chunk, grad_lds<K>(), st, p, GNT); break;
+      default: rc = launch(bwd_grad_kernel<K, V, half_t>, per_chunk, grad_lds<K>(), st, p, GNT); break;
     }
   }
   if (rc == PBGDN_OK && p.n > 0 && p.Hk != p.Hv) {
