@@ -391,11 +391,10 @@ struct ScanStage {
 // next chunk's inputs load during each step.
 // ---------------------------------------------------------------------------
 template <int K, typename TIn>
-__device__ __forceinline__ void state_pass(const BwdParams &p, float *lds, int b) {
+__device__ __forceinline__ void state_pass(const BwdParams &p, float *lds, int b, int h, int v0) {
   constexpr int LK = K + 4, PER = K / 64;
   float *sk = lds, *st = sk + BC * LK, *ss = st + BC * LC, *sx = ss + K * LT, *su = sx + BC * LT;
   float *sc = su + BC * LT, *sgam = sc + BC, *se = sgam + BC, *sbeta = se + BC;
-  const int v0 = 16 * blockIdx.x, h = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 15, g4 = lane >> 4;
   const int hk = h / (p.Hv / p.Hk);
   const long kv = (static_cast<long>(b) * p.Hv + h) * K * p.V;
@@ -458,11 +457,10 @@ __device__ __forceinline__ void state_pass(const BwdParams &p, float *lds, int b
 // chunk end (the input of that chunk's gradients), then dh0.
 // ---------------------------------------------------------------------------
 template <int K, typename TIn>
-__device__ __forceinline__ void adjoint_pass(const BwdParams &p, float *lds, int b) {
+__device__ __forceinline__ void adjoint_pass(const BwdParams &p, float *lds, int b, int h, int v0) {
   constexpr int LK = K + 4, PER = K / 64;
   float *sk = lds, *st = sk + BC * LK, *sds = st + BC * LC, *sdu = sds + K * LT, *sdx = sdu + BC * LT;
   float *sc = sdx + BC * LT, *sgam = sc + BC, *se = sgam + BC, *sbeta = se + BC;
-  const int v0 = 16 * blockIdx.x, h = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 15, g4 = lane >> 4;
   const int hk = h / (p.Hv / p.Hk);
   const long kv = (static_cast<long>(b) * p.Hv + h) * K * p.V;
@@ -538,17 +536,32 @@ __device__ __forceinline__ void adjoint_pass(const BwdParams &p, float *lds, int
 }
 
 // The two scans are independent (the reverse one needs the per-chunk records
-// and dht, not the states), so one launch runs both: blockIdx.z < B the
-// forward pass of batch row z, else the reverse pass of row z - B. Two
+// and dht, not the states), so one launch runs both: pair z = (role, batch
+// row, value head), role 0 the forward pass, 1 the reverse pass. Two
 // workgroups fit a CU, so each CU overlaps a forward and a reverse scan.
+// Workgroups go to the 8 XCDs round-robin by linear index; the V/16 tiles of
+// one pair read the same K rows and T records every step, so when the pairs
+// fill the XCDs evenly all tiles of a pair are given indices on one XCD and
+// those reads come from its L2 after the first.
 template <int K, typename TIn>
 __global__ __launch_bounds__(BNT) void bwd_scans_kernel(BwdParams p) {
   extern __shared__ __align__(16) float lds[];
-  const int z = blockIdx.z;
-  if (z < p.B) {
-    state_pass<K, TIn>(p, lds, z);
+  const int tiles = p.V / 16, pairs = 2 * p.B * p.Hv;
+  const int l = blockIdx.x;
+  int pair, tile;
+  if (pairs % 8 == 0) {
+    const int rest = l >> 3;
+    tile = rest % tiles;
+    pair = (rest / tiles) * 8 + (l & 7);
   } else {
-    adjoint_pass<K, TIn>(p, lds, z - p.B);
+    tile = l % tiles;
+    pair = l / tiles;
+  }
+  const int role_b = pair / p.Hv, h = pair % p.Hv;
+  if (role_b < p.B) {
+    state_pass<K, TIn>(p, lds, role_b, h, 16 * tile);
+  } else {
+    adjoint_pass<K, TIn>(p, lds, role_b - p.B, h, 16 * tile);
   }
 }
 
@@ -895,7 +908,7 @@ int launch(Kern kernel, dim3 grid, size_t lds, hipStream_t st, const BwdParams &
 template <int K, int V>
 int run_backward(const BwdParams &p, hipStream_t st) {
   static_assert(grad_lds<K>() <= 160 * 1024 && local_lds<K, V>() <= 160 * 1024, "LDS budget");
-  const dim3 per_chunk(p.n, p.Hv, p.B), per_tile2(V / 16, p.Hv, 2 * p.B);
+  const dim3 per_chunk(p.n, p.Hv, p.B), per_tile2((V / 16) * p.Hv * 2 * p.B);
   int rc = PBGDN_OK;
   if (p.n > 0) {
     switch (p.in_dtype) {
