@@ -7,7 +7,7 @@ differences in tests/test_oracle.py), on the same input values.
 Tolerances (infinity-norm relative error against the float64 oracle): 2e-4 for
 everything computed and returned in float32 (dg, a float32 dbeta, dh0, and all
 gradients of float32 inputs: the kernels run float32 sums of up to 128 terms
-through every chunk); 1e-2 for gradients returned in bf16 (their rounding)."""
+through every chunk); 1e-2 for gradients returned in bf16 or fp16 (their rounding)."""
 import numpy as np
 import pytest
 import torch
@@ -44,7 +44,7 @@ def check(name, got, ref, dtypes):
     errs = {n: rel_err(x, r) for n, x, r in zip(NAMES, got, ref)}
     print(f"[{name}] " + " ".join(f"{n}={e:.2e}" for n, e in errs.items()), flush=True)
     for n, x in zip(NAMES, got):
-        tol = BF16_TOL if x.dtype == torch.bfloat16 else F32_TOL
+        tol = BF16_TOL if x.dtype in (torch.bfloat16, torch.float16) else F32_TOL
         assert errs[n] <= tol, f"{name}: {n} error {errs[n]:.3e} > {tol}"
         assert x.dtype == dtypes[n], f"{name}: {n} is {x.dtype}"
 
@@ -55,6 +55,7 @@ def check(name, got, ref, dtypes):
     (1, 333, 1, 4, 128, 64, torch.bfloat16),     # GQA 1 -> 4, bf16 inputs
     (2, 200, 2, 4, 64, 128, torch.bfloat16),
     (1, 1000, 2, 2, 128, 128, torch.float32),    # 16 chunks
+    (1, 260, 2, 2, 128, 128, torch.float16),     # fp16 inputs
 ])
 def test_backward_matches_the_oracle(batch, length, hk, hv, dk, dv, dtype):
     name = f"bwd B={batch} T={length} {hk}->{hv} K={dk} V={dv} {dtype}"
