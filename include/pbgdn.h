@@ -68,7 +68,7 @@ extern "C" {
 /* status codes */
 #define PBGDN_OK 0
 #define PBGDN_ERR_INVALID_ARGUMENT 1 /* a null pointer, a bad size or dtype code */
-#define PBGDN_ERR_UNSUPPORTED 2      /* valid, but a head width / chunk this build has no kernel for */
+#define PBGDN_ERR_UNSUPPORTED 2      /* valid, but a head width / chunk this library has no kernel for */
 #define PBGDN_ERR_LAUNCH 3           /* the HIP launch failed (hipGetLastError) */
 
 /* Version of this ABI (PBGDN_ABI_VERSION). */

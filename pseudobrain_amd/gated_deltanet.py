@@ -404,7 +404,7 @@ def delta_rule_sequential(q, k, v, g, beta, scale, h0):
 
 def hip_usable(*tensors: torch.Tensor) -> bool:
     """The chunk kernel applies (the fla_usable gate, gated_deltanet.py:189-197):
-    device tensors and head widths this build has kernels for. tensors[0] is the
+    device tensors and head widths this library has kernels for. tensors[0] is the
     matrix state [..., K, V]. Raises if the tensors are on a GPU but the library
     is missing: a GPU caller never silently loses the kernel."""
     if not tensors or not all(t.is_cuda for t in tensors):
