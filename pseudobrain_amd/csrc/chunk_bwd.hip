@@ -976,6 +976,7 @@ extern "C" int pbgdn_chunk_bwd(const void *q, const void *k, const void *v, int 
   }
   if (B == 0) return PBGDN_OK;
   if (n > 65535 || Hv > 65535 || B > 32767) return PBGDN_ERR_UNSUPPORTED;
+  if (static_cast<long>(V / 16) * Hv * 2 * B > 0x7fffffffL) return PBGDN_ERR_UNSUPPORTED;  // the scans' 1-D grid
   if (!workspace || workspace_bytes < pbgdn_chunk_bwd_workspace_size(B, T, Hk, Hv, K, V) ||
       reinterpret_cast<uintptr_t>(workspace) % 16 != 0) {
     return PBGDN_ERR_INVALID_ARGUMENT;

@@ -296,6 +296,8 @@ def chunk_bwd_call(**over):
     (dict(ws_bytes=1024), _lib.ERR_INVALID_ARGUMENT),    # smaller than the workspace size
     (dict(ws=FAKE + 4), _lib.ERR_INVALID_ARGUMENT),      # 16-byte alignment
     (dict(T=64 * 65536), _lib.ERR_UNSUPPORTED),          # more chunks than a grid axis holds
+    (dict(B=32768), _lib.ERR_UNSUPPORTED),               # twice B rows of the scans' grid
+    (dict(B=30000, Hk=65535, Hv=65535, T=64), _lib.ERR_UNSUPPORTED),  # the scans' 1-D grid past 2^31
 ])
 def test_chunk_bwd_rejects_bad_arguments(over, code):
     assert chunk_bwd_call(**over) == code
