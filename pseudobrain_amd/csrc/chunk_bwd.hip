@@ -15,7 +15,7 @@
 // and each chunk's gradients follow from its start state S, its end adjoint
 // dS' and its own inputs. Four launches on the caller's stream:
 //
-//   bwd_local_kernel     per (chunk, value head): T = (I + A)^-1 by forward
+//   bwd_local_kernel     per (chunk, value head): T = (I + A)^-1 by block
 //                        substitution, dU0 = M^T dO, J = scale (Gamma Q)^T dO
 //   bwd_scans_kernel     per (value head, 16 value columns), serial over the
 //                        chunks, two independent roles in one launch: the
@@ -199,19 +199,63 @@ __device__ __forceinline__ void form_a_m(const BwdParams &p, const float *sq, co
 // ---------------------------------------------------------------------------
 // Per (chunk, value head): T, dU0 = M^T dO, J = scale (Gamma Q)^T dO, c.
 // ---------------------------------------------------------------------------
+// Element idx of an LDS array of TIn, as float.
+template <typename TIn>
+__device__ __forceinline__ float ld_el(const TIn *m, int idx) {
+  if constexpr (sizeof(TIn) == 4) {
+    return m[idx];
+  } else if constexpr (dtype_of_bwd<TIn>() == PBGDN_BF16) {
+    return __uint_as_float(static_cast<uint32_t>(m[idx]) << 16);
+  } else {
+    return static_cast<float>(m[idx]);
+  }
+}
+
+// Rows t0 .. t0+63 of a [B,T,H,W] tensor of TIn (head hd, columns 0 ..
+// COLS-1) into LDS as they are (16-byte pieces; rows of ld elements, ld a
+// multiple of 16 bytes), zero past T.
+template <typename TIn, int COLS>
+__device__ __forceinline__ void load_rows_raw(TIn *dst, int ld, const void *src, const BwdParams &p, int b, int t0,
+                                              int heads, int hd, int width) {
+  constexpr int EPP = 16 / sizeof(TIn), PPR = COLS / EPP, TOTAL = BC * PPR, PER = (TOTAL + BNT - 1) / BNT;
+  const unsigned char *base = static_cast<const unsigned char *>(src);
+  uint4 raw[PER];
+#pragma unroll
+  for (int m = 0; m < PER; ++m) {
+    const int e = threadIdx.x + BNT * m, row = e / PPR, part = e % PPR, t = t0 + row;
+    const long off = ((static_cast<long>(b) * p.T + t) * heads + hd) * width * static_cast<long>(sizeof(TIn));
+    raw[m] = e < TOTAL && t < p.T ? *reinterpret_cast<const uint4 *>(base + off + part * 16) : uint4{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int m = 0; m < PER; ++m) {
+    const int e = threadIdx.x + BNT * m, row = e / PPR, part = e % PPR;
+    if (e < TOTAL) *reinterpret_cast<uint4 *>(&dst[row * ld + part * EPP]) = raw[m];
+  }
+}
+
+// q, k and dO stay in LDS in the input dtype (converted on read), and M is
+// formed in A's place once T has been written out: 72 KiB for 16-bit inputs at
+// K = V = 128, so two workgroups share a CU.
+template <int K, int V, typename TIn>
+constexpr size_t local_lds() {
+  return sizeof(TIn) * BC * (2 * (K + 16 / sizeof(TIn)) + V + 16 / sizeof(TIn)) +
+         sizeof(float) * (BC * LC + 3 * BC + 3 * 256);
+}
+
 template <int K, int V, typename TIn>
 __global__ __launch_bounds__(BNT) void bwd_local_kernel(BwdParams p) {
-  constexpr int LK = K + 4, LV = V + 4;
+  constexpr int PADE = 16 / sizeof(TIn), LK = K + PADE, LV = V + PADE;
   extern __shared__ __align__(16) float lds[];
-  float *sq = lds, *sk = sq + BC * LK, *sdo = sk + BC * LK, *sa = sdo + BC * LV, *sm = sa + BC * LC;
-  float *sc = sm + BC * LC, *sgam = sc + BC, *sbeta = sgam + BC, *sr = sbeta + BC;
+  TIn *sq = reinterpret_cast<TIn *>(lds), *sk = sq + BC * LK, *sdo = sk + BC * LK;
+  float *sa = reinterpret_cast<float *>(sdo + BC * LV);
+  float *sc = sa + BC * LC, *sgam = sc + BC, *sbeta = sgam + BC, *sr = sbeta + BC;
   const int i = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 15, g4 = lane >> 4;
   const int hk = h / (p.Hv / p.Hk);
   const int t0 = i * BC;
-  load_rows_vec<TIn, K>(sq, LK, p.q, p, b, t0, p.Hk, hk, K, 0);
-  load_rows_vec<TIn, K>(sk, LK, p.k, p, b, t0, p.Hk, hk, K, 0);
-  load_rows_vec<TIn, V>(sdo, LV, p.dout, p, b, t0, p.Hv, h, V, 0);
+  load_rows_raw<TIn, K>(sq, LK, p.q, p, b, t0, p.Hk, hk, K);
+  load_rows_raw<TIn, K>(sk, LK, p.k, p, b, t0, p.Hk, hk, K);
+  load_rows_raw<TIn, V>(sdo, LV, p.dout, p, b, t0, p.Hv, h, V);
   if (wave == 0) {  // inclusive cumulative sum of g over the chunk (zero past T)
     const int t = t0 + lane;
     float x = t < p.T ? p.g[(static_cast<long>(b) * p.T + t) * p.Hv + h] : 0.f;
@@ -226,7 +270,17 @@ __global__ __launch_bounds__(BNT) void bwd_local_kernel(BwdParams p) {
     p.ws_c[rec(p, b, h, i) * BC + lane] = x;
   }
   __syncthreads();
-  form_a_m<K, true>(p, sq, sk, sc, sbeta, sa, sm);
+  auto krow = [&](int kk, int j, int tc) { return ld_el(sk, (16 * tc + j) * LK + kk); };
+  // A = strict_lower(beta_t (K K^T) o D), rows 16w .. of this wave
+  for (int tc = 0; tc < 4; ++tc) {
+    const float4_t kk_acc = tile_mm<K>(zero4(), [&](int r, int kk) { return ld_el(sk, (16 * wave + r) * LK + kk); },
+                                       [&](int kk, int j) { return krow(kk, j, tc); });
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = 16 * wave + 4 * g4 + r, s2 = 16 * tc + c;
+      sa[t * LC + s2] = t > s2 ? sbeta[t] * kk_acc[r] * expf(sc[t] - sc[s2]) : 0.f;
+    }
+  }
   __syncthreads();
   // T = (I + A)^-1 (unit lower triangular) in place over A, by 16 x 16
   // blocks. Wave w inverts diagonal block w by forward substitution: lane
@@ -268,12 +322,23 @@ __global__ __launch_bounds__(BNT) void bwd_local_kernel(BwdParams p) {
   }
   float *wt = p.ws_T + rec(p, b, h, i) * BC * BC;
   for (int e = tid; e < BC * BC; e += BNT) wt[e] = sa[(e / BC) * LC + e % BC];
+  __syncthreads();  // T is out: M = scale (Q K^T) o D takes its place
+  for (int tc = 0; tc < 4; ++tc) {
+    const float4_t qk_acc = tile_mm<K>(zero4(), [&](int r, int kk) { return ld_el(sq, (16 * wave + r) * LK + kk); },
+                                       [&](int kk, int j) { return krow(kk, j, tc); });
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = 16 * wave + 4 * g4 + r, s2 = 16 * tc + c;
+      sa[t * LC + s2] = t >= s2 ? p.scale * qk_acc[r] * expf(sc[t] - sc[s2]) : 0.f;
+    }
+  }
+  __syncthreads();
   // dU0 = M^T dO: tiles (row tile, 16-column tile)
   float *wu = p.ws_dU0 + rec(p, b, h, i) * BC * V;
   for (int tile = wave; tile < 4 * (V / 16); tile += 4) {
     const int tr = tile & 3, tv = tile >> 2;
-    const float4_t acc = tile_mm<BC>(zero4(), [&](int r, int s) { return sm[s * LC + 16 * tr + r]; },
-                                     [&](int s, int col) { return sdo[s * LV + 16 * tv + col]; });
+    const float4_t acc = tile_mm<BC>(zero4(), [&](int r, int s2) { return sa[s2 * LC + 16 * tr + r]; },
+                                     [&](int s2, int col) { return ld_el(sdo, s2 * LV + 16 * tv + col); });
 #pragma unroll
     for (int r = 0; r < 4; ++r) wu[(16 * tr + 4 * g4 + r) * V + 16 * tv + c] = acc[r];
   }
@@ -281,8 +346,8 @@ __global__ __launch_bounds__(BNT) void bwd_local_kernel(BwdParams p) {
   float *wj = p.ws_J + rec(p, b, h, i) * static_cast<long>(K) * V;
   for (int tile = wave; tile < (K / 16) * (V / 16); tile += 4) {
     const int tk = tile % (K / 16), tv = tile / (K / 16);
-    const float4_t acc = tile_mm<BC>(zero4(), [&](int r, int t) { return sq[t * LK + 16 * tk + r] * sgam[t]; },
-                                     [&](int t, int col) { return sdo[t * LV + 16 * tv + col]; });
+    const float4_t acc = tile_mm<BC>(zero4(), [&](int r, int t) { return ld_el(sq, t * LK + 16 * tk + r) * sgam[t]; },
+                                     [&](int t, int col) { return ld_el(sdo, t * LV + 16 * tv + col); });
 #pragma unroll
     for (int r = 0; r < 4; ++r) wj[(16 * tk + 4 * g4 + r) * V + 16 * tv + c] = p.scale * acc[r];
   }
@@ -882,10 +947,6 @@ __global__ __launch_bounds__(BNT) void bwd_gqa_reduce_kernel(BwdParams p) {
 }
 
 // LDS bytes of each kernel.
-template <int K, int V>
-constexpr size_t local_lds() {
-  return sizeof(float) * (2 * BC * (K + 4) + BC * (V + 4) + 2 * BC * LC + 3 * BC + 3 * 256);
-}
 template <int K>
 constexpr size_t scan_lds() { return sizeof(float) * (BC * (K + 4) + BC * LC + K * LT + 2 * BC * LT + 4 * BC); }
 template <int K>
@@ -907,14 +968,14 @@ int launch(Kern kernel, dim3 grid, size_t lds, hipStream_t st, const BwdParams &
 
 template <int K, int V>
 int run_backward(const BwdParams &p, hipStream_t st) {
-  static_assert(grad_lds<K>() <= 160 * 1024 && local_lds<K, V>() <= 160 * 1024, "LDS budget");
+  static_assert(grad_lds<K>() <= 160 * 1024 && local_lds<K, V, float>() <= 160 * 1024, "LDS budget");
   const dim3 per_chunk(p.n, p.Hv, p.B), per_tile2((V / 16) * p.Hv * 2 * p.B);
   int rc = PBGDN_OK;
   if (p.n > 0) {
     switch (p.in_dtype) {
-      case PBGDN_F32: rc = launch(bwd_local_kernel<K, V, float>, per_chunk, local_lds<K, V>(), st, p); break;
-      case PBGDN_BF16: rc = launch(bwd_local_kernel<K, V, u16>, per_chunk, local_lds<K, V>(), st, p); break;
-      default: rc = launch(bwd_local_kernel<K, V, half_t>, per_chunk, local_lds<K, V>(), st, p); break;
+      case PBGDN_F32: rc = launch(bwd_local_kernel<K, V, float>, per_chunk, local_lds<K, V, float>(), st, p); break;
+      case PBGDN_BF16: rc = launch(bwd_local_kernel<K, V, u16>, per_chunk, local_lds<K, V, u16>(), st, p); break;
+      default: rc = launch(bwd_local_kernel<K, V, half_t>, per_chunk, local_lds<K, V, half_t>(), st, p); break;
     }
   }
   if (rc == PBGDN_OK) {  // both scans in one launch (with T = 0 only the reverse one writes: dh0 = dht)
