@@ -113,3 +113,30 @@ def test_zero_length_gives_the_final_gradient_as_dh0():
     torch.cuda.synchronize()
     assert torch.equal(got[5].cpu(), dht)
     assert got[0].numel() == 0 and got[3].numel() == 0
+
+
+def test_full_size_gradients_are_linear_in_the_output_gradients():
+    """At the prefill shape (B=1, T=32768, Hk=16, Hv=32, K=V=128, bf16), too
+    large for the oracle: every gradient is linear in (dO, dht), so the
+    gradients for (dO1 + dO2, dht1 + dht2) equal the sum of the two calls'.
+    dO1 and dO2 live on the even and the odd tokens, so their sum is exact in
+    bf16. Float32 results within 1e-4 of the largest magnitude, bf16 results
+    within their rounding (1e-2)."""
+    from pseudobrain_amd.workloads import workload
+    q, k, v, g, beta, h0 = (x.to(DEV) for x in workload("prefill_qwen3next", seed=0))
+    gen = torch.Generator().manual_seed(21)
+    length = q.shape[1]
+    do = (torch.randn(1, length, v.shape[2], v.shape[3], generator=gen) * 0.05).to(torch.bfloat16)
+    even = (torch.arange(length) % 2 == 0).view(1, length, 1, 1)
+    do1, do2 = (do * even).to(DEV), (do * ~even).to(DEV)
+    d1, d2 = [(torch.randn(h0.shape, generator=gen) * 0.05).to(DEV) for _ in range(2)]
+    scale = q.shape[-1] ** -0.5
+    ga = [x.float().cpu() for x in gd.chunk_bwd(q, k, v, g, beta, scale, h0, do1, d1)]
+    gb = [x.float().cpu() for x in gd.chunk_bwd(q, k, v, g, beta, scale, h0, do2, d2)]
+    gs = gd.chunk_bwd(q, k, v, g, beta, scale, h0, do.to(DEV), d1 + d2)
+    torch.cuda.synchronize()
+    for name, a, b2, s in zip(NAMES, ga, gb, gs):
+        err = rel_err(s, to_numpy(a + b2))
+        tol = BF16_TOL if s.dtype == torch.bfloat16 else 1e-4
+        print(f"[full-size linearity] {name} rel_inf={err:.2e}", flush=True)
+        assert err <= tol, f"{name}: {err:.3e}"
