@@ -140,3 +140,32 @@ def test_full_size_gradients_are_linear_in_the_output_gradients():
         tol = BF16_TOL if s.dtype == torch.bfloat16 else 1e-4
         print(f"[full-size linearity] {name} rel_inf={err:.2e}", flush=True)
         assert err <= tol, f"{name}: {err:.3e}"
+
+
+@pytest.mark.parametrize("case", range(8))
+def test_random_backward(case):
+    """Randomised shapes against the oracle: head widths, GQA ratio, batch,
+    length (padding), input dtype, beta in float32 or q's dtype, h0 and dht
+    present or absent; drawn from a fixed seed."""
+    rng = np.random.default_rng(3000 + case)
+    pick = lambda xs: xs[int(rng.integers(len(xs)))]  # noqa: E731
+    dk, dv = pick([64, 128]), pick([64, 128])
+    hk = pick([1, 2])
+    hv = hk * pick([1, 2, 4])
+    dtype = pick([torch.float32, torch.bfloat16, torch.float16])
+    batch, length = int(rng.integers(1, 3)), int(rng.integers(1, 300))
+    with_h0, with_dht = bool(rng.integers(2)), bool(rng.integers(2))
+    q, k, v, g, beta, h0, do, dht = make(batch, length, hk, hv, dk, dv, dtype, seed=40 + case, h0=with_h0,
+                                         dht=with_dht)
+    if dtype != torch.float32 and bool(rng.integers(2)):
+        beta = beta.to(dtype)
+    name = (f"random bwd {case}: B={batch} T={length} {hk}->{hv} K={dk} V={dv} {dtype} beta {beta.dtype} "
+            f"h0={with_h0} dht={with_dht}")
+    print(f"[{name}]", flush=True)
+    scale = dk ** -0.5
+    got = gd.chunk_bwd(*[x.to(DEV) for x in (q, k, v, g, beta)], scale, None if h0 is None else h0.to(DEV),
+                       do.to(DEV), None if dht is None else dht.to(DEV))
+    torch.cuda.synchronize()
+    ref = oracle_grads(q, k, v, g, beta, scale, h0, do, dht)
+    check(name, got, ref, dict(dq=dtype, dk=dtype, dv=dtype, dg=torch.float32, dbeta=beta.dtype,
+                               dh0=torch.float32))
