@@ -97,13 +97,18 @@ struct ChunkParams {
 
 // Sequence s (wave-uniform): first token and end. cu_seqlens is read through
 // the constant address space (it is not written during a call), so these are
-// scalar loads.
+// scalar loads. Whatever cu_seqlens holds, the bounds are clamped to
+// 0 <= bos <= eos <= T (B == 1 with cu_seqlens), so every token, record and
+// output row a sequence touches lies inside the call's buffers; a decreasing
+// cu_seqlens gives meaningless results, never an access out of bounds.
 typedef const __attribute__((address_space(4))) int32_t const_i32;
 __device__ __forceinline__ void seq_bounds(const ChunkParams &p, int s, long &bos, long &eos) {
   if (p.cu_seqlens) {
     const_i32 *cu = (const_i32 *)p.cu_seqlens;  // C-style: an address-space cast
-    bos = cu[s];
-    eos = cu[s + 1];
+    const long total = p.T;
+    const long b = cu[s], e = cu[s + 1];
+    bos = b < 0 ? 0 : (b > total ? total : b);
+    eos = e < bos ? bos : (e > total ? total : e);
   } else {
     bos = static_cast<long>(s) * p.T;
     eos = bos + p.T;

@@ -13,14 +13,28 @@ repeat_interleave mapping of gated_deltanet.py:422-424).
 Kernels (all run on the GPU; there is no CPU path in this package):
   * "hip"         chunkwise prefill kernel (pbgdn_chunk_fwd), the replacement of
                   fla's chunk kernels (delta_rule_fla, :280-285)
-  * "chunked"     the same chunk kernel: the device counterpart of the
-                  reference's PyTorch delta_rule_chunked (:110-165)
+  * "chunked"     the same device path: the counterpart of the reference's
+                  PyTorch delta_rule_chunked (:110-165) for device tensors
   * "sequential"  fused recurrent kernel (pbgdn_recurrent_fwd), the device
                   counterpart of delta_rule_sequential (:93-107), used for decode
                   and T <= SEQUENTIAL_MAX as select_kernel does (:291-297)
 Every entry returns (o float32 [B,T,Hv,V], final state float32 [B,Hv,K,V]) like
 the reference. cu_seqlens (int32 [N+1], B == 1) packs N independent sequences
 with h0 / final states [N,Hv,K,V].
+
+Head widths. Every device call with K, V <= 256 (fla_usable's bound, :189-197)
+runs: widths between the kernels' instantiations are zero-padded, which leaves
+the recurrence exact (a zero key or query dimension never enters a product, and
+zero value columns start and stay zero); K above 128, which the chunk kernel is
+not built for, runs the prefill through the recurrent kernel.
+
+Gradients. gated_delta_rule's device paths are differentiable through the chunk
+operator's backward (pbgdn::gated_delta_chunk, for K, V <= 128 and [B,T]
+batches); a training call through "sequential" (T <= SEQUENTIAL_MAX) takes the
+same operator. The lower-level entry points (chunk_fwd, chunk_fwd_slots,
+recurrent_fwd, the decode and slot ops, the layer kernels in
+pseudobrain_amd.layer) have no backward: with grad mode on and an input that
+requires grad they raise instead of returning tensors cut from the graph.
 """
 from __future__ import annotations
 
@@ -33,6 +47,8 @@ SEQUENTIAL_MAX = 4    # gated_deltanet.py:54
 KERNELS = ("sequential", "chunked", "hip")
 CHUNK_HEAD_DIMS = (64, 128)               # key widths the chunk kernel is built for
 RECURRENT_HEAD_DIMS = (32, 64, 128, 256)  # key and value widths of the recurrent kernel
+BACKWARD_HEAD_DIMS = (64, 128)            # key and value widths of the chunk backward
+MAX_HEAD_DIM = 256                        # widest head a device path takes (fla_usable, :189-197)
 
 
 # ----------------------------------------------------------------------------
@@ -83,6 +99,51 @@ def _aligned(x: torch.Tensor, nbytes: int) -> torch.Tensor:
     return x if x.data_ptr() % nbytes == 0 else x.clone()
 
 
+def grad_needed(*tensors) -> bool:
+    """Autograd would want gradients of a result computed from these tensors."""
+    return torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in tensors)
+
+
+def require_no_grad(where: str, *tensors) -> None:
+    """Raise when `where`, which has no backward, is called with grad mode on and
+    an input that requires grad: its results would silently leave the graph."""
+    if grad_needed(*tensors):
+        raise RuntimeError(
+            f"{where} has no backward: call it under torch.no_grad() (inference), or use "
+            "gated_delta_rule(..., kernel='hip'), whose chunk operator has one")
+
+
+def _head_bound(dk: int, dv: int) -> None:
+    if dk > MAX_HEAD_DIM or dv > MAX_HEAD_DIM:
+        raise ValueError(f"no device kernel for head widths above {MAX_HEAD_DIM} (got K={dk}, V={dv}); "
+                         "fla_usable has the same bound and the reference runs such heads on delta_rule_chunked")
+
+
+def _width_at_least(d: int, widths) -> int:
+    return next(w for w in widths if w >= d)
+
+
+def _pad_last(x: torch.Tensor | None, width: int) -> torch.Tensor | None:
+    if x is None or x.shape[-1] == width:
+        return x
+    return torch.nn.functional.pad(x, (0, width - x.shape[-1]))
+
+
+def _pad_state(h: torch.Tensor | None, dk: int, dv: int) -> torch.Tensor | None:
+    if h is None or h.shape[-2:] == (dk, dv):
+        return h
+    return torch.nn.functional.pad(h, (0, dv - h.shape[-1], 0, dk - h.shape[-2]))
+
+
+def _chunk_widths(dk: int, dv: int, grad: bool) -> tuple[int, int]:
+    """(K, V) a chunk-kernel call of these head widths runs at: K in
+    CHUNK_HEAD_DIMS, V a multiple of 16 (in BACKWARD_HEAD_DIMS when a backward
+    may follow)."""
+    if grad:
+        return _width_at_least(dk, BACKWARD_HEAD_DIMS), _width_at_least(dv, BACKWARD_HEAD_DIMS)
+    return _width_at_least(dk, CHUNK_HEAD_DIMS), -(-dv // 16) * 16
+
+
 # ----------------------------------------------------------------------------
 # Chunk kernel.
 # ----------------------------------------------------------------------------
@@ -90,7 +151,16 @@ def chunk_fwd(q, k, v, g, beta, scale: float, h0=None, cu_seqlens=None, *,
               out_dtype: torch.dtype | None = None, output_final_state: bool = True,
               out: torch.Tensor | None = None):
     """Launch pbgdn_chunk_fwd. Returns (o [B,T,Hv,V] in out_dtype (default q's dtype),
-    final [N,Hv,K,V] fp32 or None). `out` may supply the output buffer."""
+    final [N,Hv,K,V] fp32 or None). `out` may supply the output buffer.
+    Inference only (no backward; see gated_delta_chunk for the differentiable op)."""
+    require_no_grad("chunk_fwd", q, k, v, g, beta, h0)
+    return _chunk_fwd(q, k, v, g, beta, scale, h0, cu_seqlens, out_dtype=out_dtype,
+                      output_final_state=output_final_state, out=out)
+
+
+def _chunk_fwd(q, k, v, g, beta, scale: float, h0=None, cu_seqlens=None, *,
+               out_dtype: torch.dtype | None = None, output_final_state: bool = True,
+               out: torch.Tensor | None = None):
     batch, length, hk, hv, dk, dv = _shapes(q, k, v, g, beta)
     if out_dtype is not None and out_dtype not in (torch.float32, q.dtype):
         raise ValueError(f"chunk kernel writes o as float32 or q's dtype ({q.dtype}), not {out_dtype}")
@@ -145,7 +215,9 @@ def chunk_fwd_slots(q, k, v, g, beta, scale: float, states, state_idx, cu_seqlen
     is False, or where the slot is outside the pool) and its final state is
     written back to that slot, in the pool's dtype (float32, bfloat16 or
     float16; the arithmetic is float32). Slots must be distinct. One call of
-    pbgdn_chunk_fwd; no gather or scatter copies. Returns o [B,T,Hv,V]."""
+    pbgdn_chunk_fwd; no gather or scatter copies. Returns o [B,T,Hv,V].
+    Inference only (no backward)."""
+    require_no_grad("chunk_fwd_slots", q, k, v, g, beta, states)
     batch, length, hk, hv, dk, dv = _shapes(q, k, v, g, beta)
     if out_dtype is not None and out_dtype not in (torch.float32, q.dtype):
         raise ValueError(f"chunk kernel writes o as float32 or q's dtype ({q.dtype}), not {out_dtype}")
@@ -203,7 +275,17 @@ def recurrent_fwd(q, k, v, g, beta, scale: float, state_in, state_out=None, stat
     (pbgdn_recurrent_verify_fwd): sequence b starts from slot state_idx[b] and
     the state after its token t is written to slot token_state_idx[b, t] of
     state_out (skipped when outside the state tensor); nothing else is
-    written."""
+    written. With state_out None the new tensor starts as a copy of state_in,
+    so the slots a call does not write keep their values there.
+    Inference only (no backward)."""
+    require_no_grad("recurrent_fwd", q, k, v, g, beta, state_in)
+    return _recurrent_fwd(q, k, v, g, beta, scale, state_in, state_out, state_idx, out_dtype=out_dtype, out=out,
+                          token_state_idx=token_state_idx)
+
+
+def _recurrent_fwd(q, k, v, g, beta, scale: float, state_in, state_out=None, state_idx=None, *,
+                   out_dtype: torch.dtype = torch.float32, out: torch.Tensor | None = None,
+                   token_state_idx: torch.Tensor | None = None):
     batch, length, hk, hv, dk, dv = _shapes(q, k, v, g, beta)
     dev = _require_device(q, k, v, g, beta, state_in, state_out, state_idx)
     if dk not in RECURRENT_HEAD_DIMS or dv not in RECURRENT_HEAD_DIMS:
@@ -218,11 +300,18 @@ def recurrent_fwd(q, k, v, g, beta, scale: float, state_in, state_out=None, stat
             raise ValueError("state_idx must be [B]")
         state_idx = state_idx.to(torch.int32).contiguous()
     if state_out is None:
-        state_out = torch.empty_like(state_in)
+        # every slot the kernel leaves alone (unnamed, out-of-pool, and in verify
+        # mode all but the token slots) keeps state_in's value
+        partial = state_idx is not None or token_state_idx is not None or state_in.shape[0] != batch
+        state_out = state_in.clone() if partial else torch.empty_like(state_in)
     elif state_out.shape != state_in.shape or state_out.dtype != state_in.dtype or not state_out.is_contiguous():
         raise ValueError("state_out must match state_in")
     if out is None:
         out = torch.empty(batch, length, hv, dv, dtype=out_dtype, device=dev)
+    elif (out.shape != (batch, length, hv, dv) or out.dtype not in _lib.DTYPE_CODES or not out.is_contiguous()
+          or out.device != dev):
+        raise ValueError(f"out must be a contiguous [B,T,Hv,V] = {(batch, length, hv, dv)} float32, bfloat16 or "
+                         "float16 tensor on the inputs' device")
     codes = _lib.DTYPE_CODES
     if token_state_idx is not None:
         if token_state_idx.shape != (batch, length):
@@ -243,8 +332,6 @@ def recurrent_fwd(q, k, v, g, beta, scale: float, state_in, state_out=None, stat
     _lib.check(status, "pbgdn_recurrent_fwd")
     return out, state_out
 
-
-BACKWARD_HEAD_DIMS = (64, 128)
 
 
 def chunk_bwd(q, k, v, g, beta, scale: float, h0, do, dht=None):
@@ -298,7 +385,7 @@ def chunk_bwd(q, k, v, g, beta, scale: float, h0, do, dht=None):
                                 "Tensor? cu_seqlens, float scale) -> (Tensor, Tensor)")
 def gated_delta_chunk(q, k, v, g, beta, h0, cu_seqlens, scale):
     """(o [B,T,Hv,V] in q's dtype, final state fp32 [N,Hv,K,V])."""
-    return chunk_fwd(q, k, v, g, beta, scale, h0, cu_seqlens)
+    return _chunk_fwd(q, k, v, g, beta, scale, h0, cu_seqlens)
 
 
 @gated_delta_chunk.register_fake
@@ -358,7 +445,7 @@ gated_delta_chunk.register_autograd(_chunk_grad, setup_context=_chunk_setup)
                                 "Tensor? state_idx, float scale) -> Tensor")
 def recurrent_step_(q, k, v, g, beta, state, state_idx, scale):
     """Decode step(s) updating `state` [S,Hv,K,V] in place; o in q's dtype."""
-    out, _ = recurrent_fwd(q, k, v, g, beta, scale, state, state, state_idx, out_dtype=q.dtype)
+    out, _ = _recurrent_fwd(q, k, v, g, beta, scale, state, state, state_idx, out_dtype=q.dtype)
     return out
 
 
@@ -385,32 +472,103 @@ def _(q, k, v, g, beta, states, state_idx, cu_seqlens, has_initial_state, scale)
 # The reference's kernel-level API.
 # ----------------------------------------------------------------------------
 def delta_rule_hip(q, k, v, g, beta, scale, h0, cu_seqlens=None):
-    """Chunk kernel with the fla path's conventions (gated_deltanet.py:280-285):
-    q/k/v at their own precision, fp32 state and decay; returns (o.float(), final)."""
-    o, final = gated_delta_chunk(q, k, v, g, beta, h0, cu_seqlens, float(scale))
+    """The device prefill with the fla path's conventions (gated_deltanet.py:280-285):
+    q/k/v at their own precision, fp32 state and decay; returns (o.float(), final).
+
+    K <= 128: the chunk kernel through pbgdn::gated_delta_chunk (differentiable
+    for [B,T] batches with K, V <= 128), the head widths zero-padded to the
+    kernel's. 128 < K <= 256: the recurrent kernel over every token (no backward)."""
+    batch, length, hk, hv, dk, dv = _shapes(q, k, v, g, beta)
+    _require_device(q, k, v, g, beta, h0, cu_seqlens)
+    _head_bound(dk, dv)
+    grad = grad_needed(q, k, v, g, beta, h0)
+    if grad:
+        if cu_seqlens is not None:
+            raise RuntimeError("the chunk backward takes [B,T] batches: packed sequences (cu_seqlens) have no "
+                               "backward; call under torch.no_grad() or pass a batch")
+        if dk > BACKWARD_HEAD_DIMS[-1] or dv > BACKWARD_HEAD_DIMS[-1]:
+            raise RuntimeError(f"the chunk backward is built for K, V <= {BACKWARD_HEAD_DIMS[-1]} "
+                               f"(got K={dk}, V={dv}); call under torch.no_grad()")
+    if dk > CHUNK_HEAD_DIMS[-1]:
+        return _recurrent_prefill(q, k, v, g, beta, scale, h0, cu_seqlens)
+    kp, vp = _chunk_widths(dk, dv, grad)
+    o, final = gated_delta_chunk(_pad_last(q, kp), _pad_last(k, kp), _pad_last(v, vp), g, beta,
+                                 _pad_state(h0, kp, vp), cu_seqlens, float(scale))
+    if (kp, vp) != (dk, dv):
+        o, final = o[..., :dv], final[..., :dk, :dv].contiguous()
     return o.float(), final
+
+
+def _recurrent_prefill(q, k, v, g, beta, scale, h0, cu_seqlens):
+    """Prefill of key widths above the chunk kernel's (up to 256) through the
+    recurrent kernel, every token in order (one workgroup per sequence and value
+    head holds the state in registers for the whole sequence). Packed sequences
+    run one call each."""
+    batch, length, hk, hv, dk, dv = _shapes(q, k, v, g, beta)
+    kp, vp = _width_at_least(dk, RECURRENT_HEAD_DIMS), _width_at_least(dv, RECURRENT_HEAD_DIMS)
+    qp, kq, vq = _pad_last(q, kp), _pad_last(k, kp), _pad_last(v, vp)
+    nseq = batch if cu_seqlens is None else cu_seqlens.numel() - 1
+    if h0 is None:
+        state = torch.zeros(nseq, hv, kp, vp, dtype=torch.float32, device=q.device)
+    else:
+        if h0.shape != (nseq, hv, dk, dv):
+            raise ValueError(f"initial state must be [N,Hv,K,V] = {(nseq, hv, dk, dv)}")
+        state = _pad_state(h0.to(torch.float32), kp, vp).contiguous().clone()
+    o = torch.empty(batch, length, hv, vp, dtype=torch.float32, device=q.device)
+    if cu_seqlens is None:
+        _recurrent_fwd(qp, kq, vq, g, beta, scale, state, state, out=o)
+    else:
+        if batch != 1:
+            raise ValueError("cu_seqlens needs B == 1 (sequences packed along T)")
+        bounds = [min(max(int(x), 0), length) for x in cu_seqlens.tolist()]
+        for n in range(nseq):
+            lo, hi = bounds[n], max(bounds[n], bounds[n + 1])
+            if hi == lo:
+                continue
+            sl = slice(lo, hi)
+            idx = torch.full((1,), n, dtype=torch.int32, device=q.device)
+            _recurrent_fwd(qp[:, sl], kq[:, sl], vq[:, sl], g[:, sl], beta[:, sl], scale, state, state, idx,
+                           out=o[:, sl])
+    return o[..., :dv].contiguous() if vp != dv else o, state[..., :dk, :dv].contiguous()
 
 
 def delta_rule_sequential(q, k, v, g, beta, scale, h0):
     """Per-step recurrence on the device (gated_deltanet.py:93-107); the state is
-    returned, not mutated. o is float32."""
-    batch = q.shape[0]
-    hv, dk, dv = v.shape[2], q.shape[3], v.shape[3]
+    returned, not mutated. o is float32. With grad mode on and an input that
+    requires grad the call goes through the chunk operator, which computes the
+    same recurrence for any T and has a backward (K, V <= 128)."""
+    batch, length, hk, hv, dk, dv = _shapes(q, k, v, g, beta)
     if h0.shape != (batch, hv, dk, dv):
         raise ValueError(f"initial state must be [B,Hv,K,V] = {(batch, hv, dk, dv)}")
-    state = h0.to(torch.float32).contiguous()
-    return recurrent_fwd(q, k, v, g, beta, scale, state, None, out_dtype=torch.float32)
+    _require_device(q, k, v, g, beta, h0)
+    _head_bound(dk, dv)
+    if grad_needed(q, k, v, g, beta, h0):
+        return delta_rule_hip(q, k, v, g, beta, scale, h0)
+    kp, vp = _width_at_least(dk, RECURRENT_HEAD_DIMS), _width_at_least(dv, RECURRENT_HEAD_DIMS)
+    state = _pad_state(h0.to(torch.float32), kp, vp).contiguous()
+    o, final = _recurrent_fwd(_pad_last(q, kp), _pad_last(k, kp), _pad_last(v, vp), g, beta, scale, state, None,
+                              out_dtype=torch.float32)
+    if (kp, vp) != (dk, dv):
+        o, final = o[..., :dv].contiguous(), final[..., :dk, :dv].contiguous()
+    return o, final
 
 
 def hip_usable(*tensors: torch.Tensor) -> bool:
-    """The chunk kernel applies (the fla_usable gate, gated_deltanet.py:189-197):
-    device tensors and head widths this library has kernels for. tensors[0] is the
-    matrix state [..., K, V]. Raises if the tensors are on a GPU but the library
-    is missing: a GPU caller never silently loses the kernel."""
+    """The device kernels apply (the fla_usable gate, gated_deltanet.py:189-197):
+    every tensor on the device, a dtype the kernels read (float32, bfloat16,
+    float16), and head widths K, V <= 256; when a gradient will be wanted, K,
+    V <= 128 (the chunk backward's widths), so that a training call the device
+    cannot differentiate stays on the reference's PyTorch path. tensors[0] is
+    the matrix state [..., K, V]. Raises if the tensors are on a GPU but the
+    library is missing: a GPU caller never silently loses the kernel."""
     if not tensors or not all(t.is_cuda for t in tensors):
         return False
+    if not all(t.dtype in _lib.DTYPE_CODES for t in tensors if t.is_floating_point()):
+        return False
     state = tensors[0]
-    if state.ndim < 2 or state.shape[-2] not in CHUNK_HEAD_DIMS or state.shape[-1] % 16:
+    widths = [state.shape[-1]] + ([state.shape[-2]] if state.ndim >= 2 else [])
+    bound = BACKWARD_HEAD_DIMS[-1] if grad_needed(*tensors) else MAX_HEAD_DIM
+    if max(widths) > bound:
         return False
     _lib.lib()
     return True
@@ -418,8 +576,10 @@ def hip_usable(*tensors: torch.Tensor) -> bool:
 
 def select_kernel(backend: str, serial: bool, length: int, *tensors: torch.Tensor) -> str:
     """Kernel for one call (gated_deltanet.py:291-297), with "hip" in fla's place:
-    sequential for serial calls and T <= SEQUENTIAL_MAX, the chunk kernel for the
-    'fused' backend when usable, else "chunked"."""
+    sequential for serial calls and T <= SEQUENTIAL_MAX, the device prefill for
+    the 'fused' backend when usable, else "chunked". On device tensors every
+    name it returns runs here; "chunked" on CPU tensors is the reference's own
+    PyTorch path (this package has none)."""
     if serial or length <= SEQUENTIAL_MAX:
         return "sequential"
     if backend == "fused" and hip_usable(*tensors):

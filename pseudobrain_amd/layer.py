@@ -17,13 +17,18 @@ updated in place, the way a serving cache holds them.
 
 q and k come out [B,T,Hk,K] without the GQA repeat (:422-424): the operator
 maps value head h to key head h // (Hv // Hk) itself. Both kernels run on the
-GPU only; a missing library or a CPU tensor raises.
+GPU only; a missing library or a CPU tensor raises. They are inference
+kernels: none has a backward, so each raises when grad mode is on and an input
+(the projection, the tails, conv_weight, A_log, dt_bias, o_norm, the state)
+requires grad, rather than returning results cut from the graph; training
+keeps the reference's differentiable PyTorch layer around the operator.
 """
 from __future__ import annotations
 
 import torch
 
 from . import _lib
+from .gated_deltanet import require_no_grad
 
 NORM_EPS = 1e-5           # gated_deltanet.py:72
 L2_MODES = ("max", "hf")  # gated_deltanet.py:57
@@ -59,6 +64,7 @@ def layer_prologue(z: torch.Tensor, tail: torch.Tensor | None, conv_weight: torc
     the epilogue takes), new tail [B,conv-1,channels] in the tail's dtype,
     written to tail_out when given: a contiguous tensor of the tail's shape
     and dtype, which may be the tail itself)."""
+    require_no_grad("layer_prologue", z, tail, conv_weight, A_log, dt_bias)
     if l2norm not in L2_MODES:
         raise ValueError(f"l2 normalization mode must be one of {L2_MODES}")
     if heads < 1 or value_heads % heads:
@@ -137,6 +143,7 @@ def layer_prologue_varlen(z: torch.Tensor, cu_seqlens: torch.Tensor, tail_pool: 
     tails go to tail_out (default: the pool itself, updated in place).
     Returns (q [1,T,heads,key_dim], k, v [1,T,value_heads,value_dim] in
     out_dtype, g, beta [1,T,value_heads] float32, gate view of z)."""
+    require_no_grad("layer_prologue_varlen", z, tail_pool, conv_weight, A_log, dt_bias)
     if l2norm not in L2_MODES:
         raise ValueError(f"l2 normalization mode must be one of {L2_MODES}")
     if heads < 1 or value_heads % heads:
@@ -224,6 +231,7 @@ def layer_epilogue(o: torch.Tensor, gate: torch.Tensor, o_norm: torch.Tensor, ep
     gated_deltanet.py:439-441 computes it, in one kernel. o [B,T,Hv,V] (the
     operator's output, any float dtype); gate [B,T,Hv*V] (the projection's
     gate columns, e.g. the view layer_prologue returns); o_norm [V]."""
+    require_no_grad("layer_epilogue", o, gate, o_norm)
     if o.ndim != 4:
         raise ValueError("o must be [B,T,Hv,V]")
     batch, length, hv, dv = o.shape
@@ -274,6 +282,7 @@ def decode_layer_step(z: torch.Tensor, conv_state: torch.Tensor | None, conv_wei
     state_idx[b] (int32 [B], or None for slot b; a slot outside the pools
     touches nothing and gives zeros). Returns hs [B, value_heads*value_dim] in
     out_dtype."""
+    require_no_grad("decode_layer_step", z, conv_state, conv_weight, A_log, dt_bias, state, o_norm)
     if l2norm not in L2_MODES:
         raise ValueError(f"l2 normalization mode must be one of {L2_MODES}")
     if heads < 1 or value_heads % heads:

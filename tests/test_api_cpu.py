@@ -74,3 +74,53 @@ def test_custom_ops_are_registered_with_shape_inference():
         o3 = torch.ops.pbgdn.chunk_slots_(q, k, v, g, beta, pool, torch.zeros(1, dtype=torch.int32), None, None,
                                           0.1)
         assert o3.shape == (1, 300, 4, 64) and o3.dtype == torch.bfloat16
+
+
+def test_entry_points_without_backward_refuse_grad_before_anything_runs():
+    """With grad mode on, a grad-requiring input to an entry point that has no
+    backward raises (before any device work) instead of silently detaching."""
+    from pseudobrain_amd import layer
+    q, k, v, g, beta, h0 = inputs()
+    v.requires_grad_(True)
+    for fn in (lambda: gd.chunk_fwd(q, k, v, g, beta, 0.1, h0),
+               lambda: gd.recurrent_fwd(q, k, v, g, beta, 0.1, h0),
+               lambda: gd.chunk_fwd_slots(q, k, v, g, beta, 0.1, h0, torch.zeros(1, dtype=torch.int32))):
+        with pytest.raises(RuntimeError, match="no backward"):
+            fn()
+    z = torch.randn(1, 4, 2 * 2 * 64 + 2 * 4 * 64 + 8, requires_grad=True)
+    with pytest.raises(RuntimeError, match="layer_prologue has no backward"):
+        layer.layer_prologue(z, None, None, torch.zeros(4), torch.zeros(4), 2, 64, 4, 64)
+    weight = torch.randn(2 * 2 * 64 + 4 * 64, 4, requires_grad=True)
+    with pytest.raises(RuntimeError, match="no backward"):
+        layer.layer_prologue(z.detach(), torch.zeros(1, 3, weight.shape[0]), weight, torch.zeros(4),
+                             torch.zeros(4), 2, 64, 4, 64)
+    o = torch.randn(1, 4, 4, 64, requires_grad=True)
+    with pytest.raises(RuntimeError, match="layer_epilogue has no backward"):
+        layer.layer_epilogue(o, torch.randn(1, 4, 256), torch.ones(64))
+    with pytest.raises(RuntimeError, match="decode_layer_step has no backward"):
+        layer.decode_layer_step(z[:, 0], None, None, torch.zeros(4), torch.zeros(4),
+                                torch.zeros(1, 4, 64, 64), torch.ones(64, requires_grad=True), 2, 64, 4, 64)
+    # under no_grad the guard is silent (and the CPU tensors are then refused)
+    with torch.no_grad(), pytest.raises(RuntimeError, match="ROCm devices only"):
+        gd.chunk_fwd(q, k, v, g, beta, 0.1, h0)
+
+
+def test_head_widths_route_to_kernels_that_run():
+    """The widths a call runs at: the chunk kernel's K in {64, 128} and V a
+    multiple of 16 (the backward's {64, 128} when grad is wanted); wider keys
+    (up to 256) go to the recurrent kernel; above 256 there is no device path."""
+    assert gd._chunk_widths(128, 128, False) == (128, 128)
+    assert gd._chunk_widths(96, 40, False) == (128, 48)
+    assert gd._chunk_widths(32, 16, False) == (64, 16)
+    assert gd._chunk_widths(96, 40, True) == (128, 64)
+    assert gd._chunk_widths(64, 100, True) == (64, 128)
+    assert gd._width_at_least(200, gd.RECURRENT_HEAD_DIMS) == 256
+    with pytest.raises(ValueError, match="above 256"):
+        gd._head_bound(300, 64)
+    # zero padding of the state: the original block is kept, the rest is zero
+    h = torch.randn(2, 3, 5, 7)
+    p = gd._pad_state(h, 8, 16)
+    assert p.shape == (2, 3, 8, 16) and torch.equal(p[..., :5, :7], h)
+    assert torch.count_nonzero(p[..., 5:, :]) == 0 and torch.count_nonzero(p[..., :, 7:]) == 0
+    # float64 (the reference's check precision) is not a device dtype: the gate says so
+    assert not gd.hip_usable(torch.zeros(1, 2, 64, 64, dtype=torch.float64))
