@@ -58,7 +58,7 @@
 extern "C" {
 #endif
 
-#define PBGDN_ABI_VERSION 7
+#define PBGDN_ABI_VERSION 8
 
 /* element types */
 #define PBGDN_F32 0
@@ -70,6 +70,7 @@ extern "C" {
 #define PBGDN_ERR_INVALID_ARGUMENT 1 /* a null pointer, a bad size or dtype code */
 #define PBGDN_ERR_UNSUPPORTED 2      /* valid, but a head width / chunk this library has no kernel for */
 #define PBGDN_ERR_LAUNCH 3           /* the HIP launch failed (hipGetLastError) */
+#define PBGDN_ERR_SCRATCH 4          /* more workspace than pbgdn_chunk_fwd_noalloc's scratch holds */
 
 /* Version of this ABI (PBGDN_ABI_VERSION). */
 int pbgdn_abi_version(void);
@@ -137,6 +138,36 @@ int pbgdn_chunk_fwd(const void *q, const void *k, const void *v, int in_dtype,
  * (gated_deltanet.py:143-157) with torch allocations.
  */
 size_t pbgdn_chunk_workspace_size(int B, int T, int Hv, int num_seqs);
+
+/* Bytes of device scratch each GPU holds for pbgdn_chunk_fwd_noalloc (64 MiB). */
+#define PBGDN_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+/*
+ * pbgdn_chunk_fwd without a workspace argument and without any allocation:
+ * the prefill's workspace records live in a device array of
+ * PBGDN_NOALLOC_SCRATCH_BYTES that the library holds on each GPU it runs on
+ * until the process ends. No counterpart in the reference: it is for callers
+ * that cannot allocate (code under HIP graph capture, allocation-free serving
+ * loops, harnesses that forbid hipMalloc).
+ *
+ * Arguments, results and kernels are those of pbgdn_chunk_fwd; `stream` must
+ * belong to the current device (PBGDN_ERR_INVALID_ARGUMENT otherwise). A call
+ * whose pbgdn_chunk_workspace_size(B, T, Hv, num_seqs) exceeds
+ * PBGDN_NOALLOC_SCRATCH_BYTES returns PBGDN_ERR_SCRATCH and launches nothing
+ * (e.g. at Hv = 32 about 9,900 tokens in one sequence; at Hv = 16 twice that).
+ * Every call on one GPU shares that GPU's array: calls whose work overlaps on
+ * one GPU (other streams, other threads) race and must be serialised by the
+ * caller. The array keeps the last call's contents; nothing in it needs
+ * clearing (each call writes every record it reads).
+ */
+int pbgdn_chunk_fwd_noalloc(const void *q, const void *k, const void *v,
+                            int in_dtype, const float *g, const void *beta,
+                            int beta_dtype, const void *h0, void *ht,
+                            int state_dtype, const int32_t *state_idx,
+                            const uint8_t *has_initial_state, int num_states,
+                            const int32_t *cu_seqlens, int num_seqs, void *o,
+                            int out_dtype, int B, int T, int Hk, int Hv, int K,
+                            int V, float scale, int chunk, void *stream);
 
 /*
  * Fused recurrent steps: for each token, in one pass over the state,

@@ -13,10 +13,11 @@ import threading
 import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpbgdn.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 F32, BF16, F16 = 0, 1, 2
-OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3
+OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED, ERR_LAUNCH, ERR_SCRATCH = 0, 1, 2, 3, 4
+NOALLOC_SCRATCH_BYTES = 64 << 20  # PBGDN_NOALLOC_SCRATCH_BYTES
 
 DTYPE_CODES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
 
@@ -28,6 +29,8 @@ SIGNATURES = {
     "pbgdn_chunk_fwd": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _i, _vp, _i,
                          _i, _i, _i, _i, _i, _i, _f, _i, _vp, ctypes.c_size_t, _vp], _i),
     "pbgdn_chunk_workspace_size": ([_i, _i, _i, _i], ctypes.c_size_t),
+    "pbgdn_chunk_fwd_noalloc": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _i, _vp, _i,
+                                 _i, _i, _i, _i, _i, _i, _f, _i, _vp], _i),
     "pbgdn_recurrent_fwd": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _i, _vp, _i,
                              _i, _i, _i, _i, _i, _i, _f, _vp], _i),
     "pbgdn_recurrent_verify_fwd": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _i,

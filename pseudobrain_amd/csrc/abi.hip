@@ -9,6 +9,9 @@ extern "C" const char *pbgdn_status_string(int status) {
     case PBGDN_ERR_INVALID_ARGUMENT: return "invalid argument (null pointer, size or dtype code)";
     case PBGDN_ERR_UNSUPPORTED: return "unsupported shape (head width, chunk or grid size)";
     case PBGDN_ERR_LAUNCH: return "HIP kernel launch failed";
+    case PBGDN_ERR_SCRATCH:
+      return "the call needs more workspace than the no-allocation entry point's scratch "
+             "(PBGDN_NOALLOC_SCRATCH_BYTES) holds";
     default: return "unknown pbgdn status";
   }
 }

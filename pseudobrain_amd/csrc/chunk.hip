@@ -5,8 +5,17 @@
 // records to the scan kernel; see chunk.hpp for the algorithm and the record
 // format.
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 
 #include "chunk.hpp"
+
+// Scratch of pbgdn_chunk_fwd_noalloc: the prep kernel's workspace records for
+// callers that cannot allocate. Each GPU the library runs on holds its own copy
+// until the process ends. In host code `scratch` names a host-side stand-in,
+// not a device address: kernels and copies take the address that
+// hipGetSymbolAddress returns for the current device (scratch_for_stream).
+static __device__ __align__(256) unsigned char scratch[PBGDN_NOALLOC_SCRATCH_BYTES];
 
 namespace pbgdn {
 namespace {
@@ -32,6 +41,37 @@ int dispatch_in(const ChunkParams &p, long records, int in_dtype, int out_dtype,
 bool valid_dtype(int d) { return d == PBGDN_F32 || d == PBGDN_BF16 || d == PBGDN_F16; }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Device address of `scratch` per device ordinal, resolved once per device
+// (with that device current) on the first no-allocation call there.
+constexpr int MAX_DEVICES = 64;
+std::atomic<unsigned char *> scratch_ptr[MAX_DEVICES];
+std::mutex scratch_mu;
+
+// This call's scratch: the copy on the current device, which must be the
+// device of `stream` (the kernels run on the stream's device).
+int scratch_for_stream(hipStream_t stream, unsigned char **out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return PBGDN_ERR_LAUNCH;
+  if (dev >= MAX_DEVICES) return PBGDN_ERR_UNSUPPORTED;
+  if (stream) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(stream, &sdev) != hipSuccess || sdev != dev) return PBGDN_ERR_INVALID_ARGUMENT;
+  }
+  unsigned char *ptr = scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!ptr) {
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    ptr = scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!ptr) {
+      void *addr = nullptr;
+      if (hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)) != hipSuccess || !addr) return PBGDN_ERR_LAUNCH;
+      ptr = static_cast<unsigned char *>(addr);
+      scratch_ptr[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return PBGDN_OK;
+}
 
 }  // namespace
 }  // namespace pbgdn
@@ -96,4 +136,26 @@ extern "C" int pbgdn_chunk_fwd(const void *q, const void *k, const void *v, int 
     case 128: return pbgdn::dispatch_in<128>(p, records, in_dtype, out_dtype, s);
     default: return PBGDN_ERR_UNSUPPORTED;
   }
+}
+
+// The prefill of pbgdn_chunk_fwd with the workspace taken from this device's
+// `scratch` array: nothing is allocated (no hipMalloc, hipFree or allocating
+// library call), so callers under graph capture or in allocation-free loops
+// can use it. Calls on one GPU share its array; calls whose work overlaps on
+// one GPU (two streams, or two threads) race on it.
+extern "C" int pbgdn_chunk_fwd_noalloc(const void *q, const void *k, const void *v, int in_dtype, const float *g,
+                                       const void *beta, int beta_dtype, const void *h0, void *ht,
+                                       int state_dtype, const int32_t *state_idx,
+                                       const uint8_t *has_initial_state, int num_states,
+                                       const int32_t *cu_seqlens, int num_seqs, void *o, int out_dtype, int B,
+                                       int T, int Hk, int Hv, int K, int V, float scale, int chunk,
+                                       void *stream) {
+  if (pbgdn_chunk_workspace_size(B, T, Hv, num_seqs) > PBGDN_NOALLOC_SCRATCH_BYTES) return PBGDN_ERR_SCRATCH;
+  unsigned char *ws = nullptr;
+  const int st = pbgdn::scratch_for_stream(static_cast<hipStream_t>(stream), &ws);
+  if (st != PBGDN_OK) return st;
+  // the records need no initialisation: the prep kernel writes every record the scan reads
+  return pbgdn_chunk_fwd(q, k, v, in_dtype, g, beta, beta_dtype, h0, ht, state_dtype, state_idx,
+                         has_initial_state, num_states, cu_seqlens, num_seqs, o, out_dtype, B, T, Hk, Hv, K, V,
+                         scale, chunk, ws, PBGDN_NOALLOC_SCRATCH_BYTES, stream);
 }

@@ -28,11 +28,11 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version_and_status_strings():
-    assert _lib.lib().pbgdn_abi_version() == _lib.ABI_VERSION == 7
+    assert _lib.lib().pbgdn_abi_version() == _lib.ABI_VERSION == 8
     header = open(HEADER).read()
     assert re.search(r"#define PBGDN_ABI_VERSION (\d+)", header).group(1) == str(_lib.ABI_VERSION)
     assert _lib.status_string(0) == "ok"
-    for code in (1, 2, 3, 99):
+    for code in (1, 2, 3, 4, 99):
         assert _lib.status_string(code)
     with pytest.raises(_lib.PbgdnError, match="status 2"):
         _lib.check(2, "x")
@@ -47,6 +47,20 @@ def chunk_call(**over):
                 V=128, scale=0.1, chunk=64, ws=FAKE, ws_bytes=1 << 40, stream=None)
     args.update(over)
     return _lib.lib().pbgdn_chunk_fwd(*args.values())
+
+
+def test_chunk_fwd_noalloc_rejects_calls_beyond_its_scratch():
+    """The no-allocation prefill refuses, before touching any device, a call
+    whose workspace would not fit its fixed scratch."""
+    header = open(HEADER).read()
+    assert re.search(r"#define PBGDN_NOALLOC_SCRATCH_BYTES \(64u << 20\)", header)
+    lib = _lib.lib()
+    assert lib.pbgdn_chunk_workspace_size(1, 32768, 32, 1) > _lib.NOALLOC_SCRATCH_BYTES
+    args = dict(q=FAKE, k=FAKE, v=FAKE, in_dtype=1, g=FAKE, beta=FAKE, beta_dtype=0, h0=None, ht=None, sdt=0,
+                sidx=None, has_init=None, nstates=0, cu=None, nseq=1, o=FAKE, out_dtype=1, B=1, T=32768, Hk=16,
+                Hv=32, K=128, V=128, scale=0.1, chunk=64, stream=None)
+    assert lib.pbgdn_chunk_fwd_noalloc(*args.values()) == _lib.ERR_SCRATCH
+    assert "scratch" in _lib.status_string(_lib.ERR_SCRATCH)
 
 
 def recurrent_call(**over):
