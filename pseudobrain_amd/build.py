@@ -19,7 +19,8 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(PKG, "libpbgdn.so")
-SOURCES = ("abi.hip", "recurrent.hip", "chunk.hip", "chunk_prep.hip", "chunk_scan.hip", "chunk_bwd.hip",
+SOURCES = ("abi.hip", "recurrent.hip", "chunk.hip", "chunk_prep.hip", "chunk_scan.hip", "chunk_wide.hip",
+           "chunk_bwd.hip",
            "layer.hip", "decode_layer.hip")
 ARCH = "gfx950"
 

@@ -6,6 +6,8 @@
 // format.
 #include <algorithm>
 #include <atomic>
+#include <cstdlib>
+#include <cstring>
 #include <mutex>
 
 #include "chunk.hpp"
@@ -20,10 +22,41 @@ static __device__ __align__(256) unsigned char scratch[PBGDN_NOALLOC_SCRATCH_BYT
 namespace pbgdn {
 namespace {
 
+// The scan kernel of a call. The wide scan (chunk_wide.hip: 64 columns of a
+// (sequence, value head) per workgroup, one wave per 16-column tile) takes
+// 16-bit inputs and outputs at K = 128 with V a multiple of 64. It stages each
+// chunk once for four tiles, so it wins whenever its workgroups number at
+// least half the CUs (measured at the Qwen3-Next head shape, 32,768 tokens:
+// 8 x 4,096 0.52 vs 0.82 ms, 1024 x 32 2.41 vs 2.67 ms); one sequence of that
+// shape has 64 of them and runs faster on the narrow scan, which spreads each
+// head over 8 workgroups (0.74 vs 1.12 ms). PBGDN_SCAN=narrow|wide in the
+// environment forces a choice (for measurements).
+inline int scan_choice() {
+  static const int choice = [] {
+    const char *e = getenv("PBGDN_SCAN");
+    if (!e) return 0;
+    return strcmp(e, "narrow") == 0 ? 1 : strcmp(e, "wide") == 0 ? 2 : 0;
+  }();
+  return choice;
+}
+
+template <int K, typename TIn>
+bool wide_eligible(const ChunkParams &p) {
+  if constexpr (K != 128 || sizeof(TIn) != 2) {
+    return false;
+  } else {
+    if (p.V % 64 != 0 || scan_choice() == 1) return false;
+    return scan_choice() == 2 || static_cast<long>(p.num_seqs) * p.Hv * (p.V / 64) >= SCAN_CUS / 2;
+  }
+}
+
 template <int K, typename TIn>
 int run_chunk(const ChunkParams &p, long records, int out_dtype, hipStream_t s) {
   const int st = launch_prep<K, TIn>(p, records, s);
   if (st != PBGDN_OK) return st;
+  if constexpr (K == 128 && sizeof(TIn) == 2) {
+    if (out_dtype != PBGDN_F32 && wide_eligible<K, TIn>(p)) return launch_wide<K, TIn, TIn>(p, s);
+  }
   if (out_dtype == PBGDN_F32) return launch_scan<K, TIn, float>(p, s);
   return launch_scan<K, TIn, TIn>(p, s);  // out_dtype == in_dtype, checked by the caller
 }

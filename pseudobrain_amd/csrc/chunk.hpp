@@ -342,5 +342,7 @@ template <int K, typename TIn>
 int launch_prep(const ChunkParams &p, long records, hipStream_t stream);
 template <int K, typename TIn, typename TOut>
 int launch_scan(const ChunkParams &p, hipStream_t stream);
+template <int K, typename TIn, typename TOut>
+int launch_wide(const ChunkParams &p, hipStream_t stream);
 
 }  // namespace pbgdn

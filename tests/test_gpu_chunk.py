@@ -23,6 +23,10 @@ def to_dev(*xs):
     return [x.to(DEV) for x in xs]
 
 
+def to_np(t):
+    return t.float().cpu().numpy()
+
+
 def run(q, k, v, g, beta, scale, h0, cu=None):
     o, s = gd.chunk_fwd(*to_dev(q, k, v, g, beta), scale, None if h0 is None else h0.to(DEV),
                         None if cu is None else cu.to(DEV))
@@ -157,8 +161,10 @@ def test_many_short_sequences(nseq, hk, hv, dv):
 
 
 def test_varlen_full_size_packing_equals_separate_calls():
-    """262,144 packed tokens in 8 sequences: the packed call equals one call per
-    sequence bit for bit, and the shortest sequence matches the oracle."""
+    """262,144 packed tokens in 8 sequences: the packed call (the wide scan: 512
+    of its workgroups) agrees with one call per sequence (the narrow scan, 64
+    wide workgroups each being too few) within the tolerances, at full length,
+    and the shortest sequence matches the oracle."""
     q, k, v, g, beta, h0, cu = varlen_workload(seed=0)
     o, s = run(q, k, v, g, beta, SCALE, h0, cu)
     bounds = cu.tolist()
@@ -167,8 +173,8 @@ def test_varlen_full_size_packing_equals_separate_calls():
         lo, hi = bounds[n], bounds[n + 1]
         o_n, s_n = gd.chunk_fwd(dq[:, lo:hi], dk[:, lo:hi], dv[:, lo:hi], dg[:, lo:hi], db[:, lo:hi],
                                 SCALE, dh[n:n + 1])
-        assert torch.equal(o[:, lo:hi], o_n), f"sequence {n}"
-        assert torch.equal(s[n:n + 1], s_n), f"sequence {n}"
+        assert_parity(f"packed vs separate, sequence {n} (T={hi - lo})", o[:, lo:hi], to_np(o_n),
+                      s[n:n + 1], to_np(s_n))
     n = int(np.argmin(np.diff(bounds)))
     lo, hi = bounds[n], bounds[n + 1]
     o_ref, s_ref = oracle(q[:, lo:hi], k[:, lo:hi], v[:, lo:hi], g[:, lo:hi], beta[:, lo:hi], SCALE,
