@@ -22,14 +22,15 @@ static __device__ __align__(256) unsigned char scratch[PBGDN_NOALLOC_SCRATCH_BYT
 namespace pbgdn {
 namespace {
 
-// The scan kernel of a call. The wide scan (chunk_wide.hip: 64 columns of a
-// (sequence, value head) per workgroup, one wave per 16-column tile) takes
-// 16-bit inputs and outputs at K = 128 with V a multiple of 64. It stages each
-// chunk once for four tiles, so it wins whenever its workgroups number at
-// least half the CUs (measured at the Qwen3-Next head shape, 32,768 tokens:
-// 8 x 4,096 0.52 vs 0.82 ms, 1024 x 32 2.41 vs 2.67 ms); one sequence of that
-// shape has 64 of them and runs faster on the narrow scan, which spreads each
-// head over 8 workgroups (0.74 vs 1.12 ms). PBGDN_SCAN=narrow|wide in the
+// The scan kernel of a call. The wide scan (chunk_wide.hip: all 128 columns
+// of a (sequence, value head) per workgroup, one wave per 16-column tile)
+// takes 16-bit inputs and outputs at K = 128 with V a multiple of 128. It
+// stages each chunk once for eight tiles, so it wins whenever its workgroups
+// number at least half the CUs (measured at the Qwen3-Next head shape, 32,768
+// tokens: 4 x 8,192 0.53 vs 0.72 ms, 8 x 4,096 0.39 vs 0.73 ms, 1024 x 32
+// 1.76 vs 2.68 ms); one or two sequences of that shape have 32 or 64 of them
+// and run faster on the narrow scan, which spreads each head over 8
+// workgroups (1 x 32,768: 0.78 vs 1.69 ms). PBGDN_SCAN=narrow|wide in the
 // environment forces a choice (for measurements).
 inline int scan_choice() {
   static const int choice = [] {
@@ -45,8 +46,8 @@ bool wide_eligible(const ChunkParams &p) {
   if constexpr (K != 128 || sizeof(TIn) != 2) {
     return false;
   } else {
-    if (p.V % 64 != 0 || scan_choice() == 1) return false;
-    return scan_choice() == 2 || static_cast<long>(p.num_seqs) * p.Hv * (p.V / 64) >= SCAN_CUS / 2;
+    if (p.V % 128 != 0 || scan_choice() == 1) return false;
+    return scan_choice() == 2 || static_cast<long>(p.num_seqs) * p.Hv * (p.V / 128) >= SCAN_CUS / 2;
   }
 }
 

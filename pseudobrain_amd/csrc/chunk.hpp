@@ -120,23 +120,33 @@ template <typename TIn>
 struct OpOf {
   using T4 = half4_t;
   using T8 = half8_t;
-  __device__ static T4 from(float4_t x) { return to_half4(x); }
-  __device__ static float4_t to(T4 x) { return to_float4(x); }
-  __device__ static float4_t bits_to_float(i16x4_t x) { return to_float4(__builtin_bit_cast(half4_t, x)); }
+  __device__ static T4 from(float4_t x) { return __builtin_convertvector(x, half4_t); }
+  __device__ static float4_t to(T4 x) { return __builtin_convertvector(x, float4_t); }
+  __device__ static float4_t bits_to_float(i16x4_t x) { return to(__builtin_bit_cast(half4_t, x)); }
+  // x = hi + lo, each rounded to the operand type in turn (packed conversions)
+  __device__ static void split(float4_t x, T4 &hi, T4 &lo) {
+    hi = from(x);
+    lo = from(x - to(hi));
+  }
 };
 template <>
 struct OpOf<u16> {
   using T4 = bf16x4_t;
   using T8 = bf16x8_t;
-  __device__ static T4 from(float4_t x) {
-    return T4{static_cast<bf16_t>(x[0]), static_cast<bf16_t>(x[1]), static_cast<bf16_t>(x[2]),
-              static_cast<bf16_t>(x[3])};
-  }
+  // round to nearest even, two values per conversion
+  __device__ static T4 from(float4_t x) { return __builtin_convertvector(x, bf16x4_t); }
+  // widening is exact: the bf16 bits are the high half of the float
   __device__ static float4_t to(T4 x) {
-    return float4_t{static_cast<float>(x[0]), static_cast<float>(x[1]), static_cast<float>(x[2]),
-                    static_cast<float>(x[3])};
+    const v2u32_t w = __builtin_bit_cast(v2u32_t, x);
+    return float4_t{__uint_as_float(w[0] << 16), __uint_as_float(w[0] & 0xffff0000u), __uint_as_float(w[1] << 16),
+                    __uint_as_float(w[1] & 0xffff0000u)};
   }
   __device__ static float4_t bits_to_float(i16x4_t x) { return to(__builtin_bit_cast(bf16x4_t, x)); }
+  // x = hi + lo, each rounded to bf16 in turn (packed conversions)
+  __device__ static void split(float4_t x, T4 &hi, T4 &lo) {
+    hi = from(x);
+    lo = from(x - to(hi));
+  }
 };
 
 __device__ __forceinline__ float4_t mma(half8_t a, half8_t b, float4_t c) {

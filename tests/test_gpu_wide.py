@@ -1,7 +1,7 @@
-"""Parity of the wide prefill scan (chunk_wide.hip: 64 value columns of a
+"""Parity of the wide prefill scan (chunk_wide.hip: 128 value columns of a
 (sequence, value head) per workgroup) with the fp32 oracle, at shapes that
-select it: 16-bit inputs and outputs, K = 128, V a multiple of 64, and at
-least 128 of its workgroups (sequences x value heads x V/64).
+select it: 16-bit inputs and outputs, K = 128, V a multiple of 128, and at
+least 128 of its workgroups (sequences x value heads x V/128).
 
 Tolerances as tests/test_gpu_chunk.py: outputs 2e-2, final states 1e-3
 (infinity-norm relative error against the fp32 oracle on the same inputs)."""
@@ -22,13 +22,13 @@ def to_dev(*xs):
 
 @pytest.mark.parametrize("batch,length,hk,hv,dtype", [
     (4, 300, 16, 32, torch.bfloat16),   # Qwen3-Next heads, a padded last chunk
-    (2, 130, 32, 32, torch.float16),    # no GQA, fp16
+    (4, 130, 32, 32, torch.float16),    # no GQA, fp16
     (4, 64, 8, 32, torch.bfloat16),     # 4 value heads per key head, exactly one chunk
     (8, 1, 16, 32, torch.bfloat16),     # one token
 ])
 def test_wide_batch(batch, length, hk, hv, dtype):
     q, k, v, g, beta, h0 = generate(batch, length, hk, hv, 128, 128, dtype, 0.02, seed=length + hk)
-    assert batch * hv * 2 >= 128  # the wide scan's workgroups
+    assert batch * hv >= 128  # the wide scan's workgroups
     with torch.no_grad():
         o, s = gd.chunk_fwd(*to_dev(q, k, v, g, beta), 128 ** -0.5, h0.to(DEV))
     torch.cuda.synchronize()
@@ -74,17 +74,17 @@ def test_wide_state_slots(state_dtype):
     assert torch.equal(dpool.cpu()[untouched], pool[untouched])
 
 
-def test_wide_matches_the_narrow_scan_on_one_long_sequence_pair():
-    """Two sequences of 4,096 tokens (128 wide workgroups): against the oracle,
-    and the same call split into two one-sequence calls (narrow scan) agrees
-    within the tolerance."""
-    q, k, v, g, beta, h0 = generate(2, 4096, 16, 32, 128, 128, torch.bfloat16, 0.02, seed=11)
+def test_wide_matches_the_narrow_scan_on_long_sequences():
+    """Four sequences of 2,048 tokens (128 wide workgroups): against the
+    oracle, and the same call split into one-sequence calls (narrow scan)
+    agrees within the tolerance."""
+    q, k, v, g, beta, h0 = generate(4, 2048, 16, 32, 128, 128, torch.bfloat16, 0.02, seed=11)
     with torch.no_grad():
         o, s = gd.chunk_fwd(*to_dev(q, k, v, g, beta), 128 ** -0.5, h0.to(DEV))
         parts = [gd.chunk_fwd(*to_dev(q[b:b + 1], k[b:b + 1], v[b:b + 1], g[b:b + 1], beta[b:b + 1]), 128 ** -0.5,
-                              h0[b:b + 1].to(DEV)) for b in range(2)]
+                              h0[b:b + 1].to(DEV)) for b in range(4)]
     torch.cuda.synchronize()
     o_ref, s_ref = oracle(q, k, v, g, beta, 128 ** -0.5, h0)
-    assert_parity("wide 2x4096", o, o_ref, s, s_ref)
-    assert_parity("narrow 1x4096 pair", torch.cat([p[0] for p in parts]), o_ref, torch.cat([p[1] for p in parts]),
+    assert_parity("wide 4x2048", o, o_ref, s, s_ref)
+    assert_parity("narrow 1x2048 each", torch.cat([p[0] for p in parts]), o_ref, torch.cat([p[1] for p in parts]),
                   s_ref)
