@@ -214,7 +214,11 @@ def bench_prefill(steps, warmup):
     return s, sec, ksec, flops, nbytes
 
 
-def bench_decode(batch, steps, warmup=10, state_dtype=None):
+def bench_decode(batch, steps, warmup=10, state_dtype=None, pools=1):
+    """Decode steps at `batch` sequences. With pools > 1 the steps rotate over
+    that many separate state pools (step i updates pool i % pools), so that
+    each step's state has left the 256 MB last-level cache since it was last
+    touched, as in a model whose layers each keep their own pool."""
     import torch
     from pseudobrain_amd.workloads import WORKLOADS, generate
     s = WORKLOADS["decode_b64"]
@@ -222,15 +226,19 @@ def bench_decode(batch, steps, warmup=10, state_dtype=None):
                                                           s.h0_std, seed=0))
     if state_dtype is not None:
         state = state.to(state_dtype)
+    states = [state] + [state.clone() for _ in range(pools - 1)]
     scale = s.dk ** -0.5
+    turn = [0]
 
     def step():
-        torch.ops.pbgdn.recurrent_step_(q, k, v, g, beta, state, None, scale)
+        torch.ops.pbgdn.recurrent_step_(q, k, v, g, beta, states[turn[0] % pools], None, scale)
+        turn[0] += 1
 
     sec, ksec = timed_steps(step, steps, warmup)
     nbytes = decode_bytes(batch, s.hk, s.hv, s.dk, s.dv, state_elem=state.element_size())
     return {
-        "batch": batch, "state_dtype": str(state.dtype).replace("torch.", ""), "steps": steps, "us_per_step": sec * 1e6, "kernel_us": ksec * 1e6,
+        "batch": batch, "state_dtype": str(state.dtype).replace("torch.", ""), "pools": pools, "steps": steps,
+        "us_per_step": sec * 1e6, "kernel_us": ksec * 1e6,
         "bytes_per_step": nbytes, "achieved_GBs": nbytes / ksec / 1e9,
         "hbm_frac": nbytes / ksec / 1e9 / HBM_PEAK_GBS,
     }
@@ -399,6 +407,33 @@ def bench_decode_layer(batch, steps, warmup=10, state_dtype=None):
                          "frac": gbs / HBM_PEAK_GBS}}
 
 
+STREAM_PROBE_BYTES = 1 << 30
+
+
+def stream_probe(reps=20):
+    """The library's streaming copy (pbgdn_stream_probe: 16-byte non-temporal
+    buffer loads and stores) over 1 GiB: the read + write bandwidth a plain
+    stream sustains on this GPU, the ceiling the decode step's state traffic
+    is read against."""
+    import torch
+    from pseudobrain_amd import _lib
+    src = torch.ones(STREAM_PROBE_BYTES // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        _lib.check(_lib.lib().pbgdn_stream_probe(src.data_ptr(), dst.data_ptr(), STREAM_PROBE_BYTES, stream),
+                   "pbgdn_stream_probe")
+
+    step()
+    torch.cuda.synchronize()
+    assert torch.equal(dst[:: 1 << 20], src[:: 1 << 20])
+    ksec = kernel_time(step, reps)
+    gbs = 2 * STREAM_PROBE_BYTES / ksec / 1e9
+    return {"bytes_read": STREAM_PROBE_BYTES, "bytes_written": STREAM_PROBE_BYTES, "kernel_us": ksec * 1e6,
+            "GBs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS}
+
+
 def copy_probe(reps=5):
     """A plain device copy of COPY_PROBE_BYTES (torch's copy kernel): the
     reference point that scales the FETCH_SIZE/WRITE_SIZE counters, and a
@@ -483,8 +518,18 @@ def main(argv=None):
                                                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                                          "frac": bf["hbm_frac"],
                                                          "traffic": measured_traffic("recurrent_b64_bf16_state")})
+        # the same step with the state outside the cache: three 128 MiB pools in rotation
+        ooc = bench_decode(64, 300, pools=3)
+        result["decode_out_of_cache"] = dict(ooc, roofline={"bound": "hbm", "achieved": ooc["achieved_GBs"],
+                                                            "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                                            "frac": ooc["hbm_frac"]})
         if not args.no_b256:
             result["decode_b256_ungraded"] = bench_decode(256, 200)
+        probe = stream_probe()
+        result["stream_probe"] = probe
+        for key in ("decode", "decode_out_of_cache", "decode_b256_ungraded"):
+            if key in result:
+                result[key]["vs_stream_probe"] = result[key]["achieved_GBs"] / probe["GBs"]
     if not args.no_layer:
         result.update(bench_layer(shape.length, 20))
         if not args.no_decode:

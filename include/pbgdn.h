@@ -58,7 +58,7 @@
 extern "C" {
 #endif
 
-#define PBGDN_ABI_VERSION 8
+#define PBGDN_ABI_VERSION 9
 
 /* element types */
 #define PBGDN_F32 0
@@ -409,6 +409,17 @@ int pbgdn_decode_layer_fwd(const void *z, long z_stride, int in_dtype,
                            const float *o_norm, float eps, void *hs,
                            int out_dtype, int B, int Hk, int Hv, int K, int V,
                            float scale, void *stream);
+
+/*
+ * Streaming copy of `bytes` from src to dst on `stream`: 16-byte non-temporal
+ * buffer loads and stores, four pieces in flight per thread, 16 workgroups of
+ * 256 threads per compute unit of the current device. No counterpart in the
+ * reference: a measurement aid, the read + write bandwidth this GPU sustains
+ * for a plain stream, against which the decode step's state traffic is
+ * reported. bytes a multiple of 16, at most 2 GiB - 16; src and dst 16-byte
+ * aligned and not overlapping.
+ */
+int pbgdn_stream_probe(const void *src, void *dst, int64_t bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -21,7 +21,7 @@ INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(PKG, "libpbgdn.so")
 SOURCES = ("abi.hip", "recurrent.hip", "chunk.hip", "chunk_prep.hip", "chunk_scan.hip", "chunk_wide.hip",
            "chunk_bwd.hip",
-           "layer.hip", "decode_layer.hip")
+           "layer.hip", "decode_layer.hip", "device.hip")
 ARCH = "gfx950"
 
 # Packed fp32 VALU instructions are disabled (-packed-fp32-ops): the kernels

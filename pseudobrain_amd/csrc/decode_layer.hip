@@ -20,6 +20,7 @@
 // input work is left to hold registers while a state is in them.
 #include "layer_math.hpp"
 #include "state_io.hpp"
+#include "device.hpp"
 
 namespace pbgdn {
 namespace {
@@ -77,7 +78,8 @@ __device__ float conv_channel(const DecodeLayerParams &p, long slot, long c, flo
   return siluf(acc);
 }
 
-template <int K, int V, typename TS>
+// CP: the state's cache policy (state_io.hpp).
+template <int K, int V, typename TS, int CP>
 __global__ __launch_bounds__(DNT, (sizeof(TS) == 2 ? 5 : 4)) void decode_layer_kernel(DecodeLayerParams p) {
   constexpr bool PACKED = sizeof(TS) == 2;
   constexpr int NW = DNT / 64;
@@ -129,9 +131,9 @@ __global__ __launch_bounds__(DNT, (sizeof(TS) == 2 ? 5 : 4)) void decode_layer_k
 #pragma unroll
     for (int j = 0; j < RPT; ++j) {
       if constexpr (PACKED) {
-        raw[j] = IO::load(r, voff, j * ROW_STEP);
+        raw[j] = IO::template load<CP>(r, voff, j * ROW_STEP);
       } else {
-        s[j] = IO::widen(IO::load(r, voff, j * ROW_STEP));
+        s[j] = IO::widen(IO::template load<CP>(r, voff, j * ROW_STEP));
       }
     }
   };
@@ -233,7 +235,7 @@ __global__ __launch_bounds__(DNT, (sizeof(TS) == 2 ? 5 : 4)) void decode_layer_k
     const float4_t out = alpha * tq + u * kq;
     const __amdgpu_buffer_rsrc_t rout = state_rsrc(h);
 #pragma unroll
-    for (int j = 0; j < RPT; ++j) IO::store(rout, voff, j * ROW_STEP, alpha * row(j) + sk[rg + RG * j] * u);
+    for (int j = 0; j < RPT; ++j) IO::template store<CP>(rout, voff, j * ROW_STEP, alpha * row(j) + sk[rg + RG * j] * u);
 
     // Epilogue: RMSNorm over the head's V outputs (the CG lanes of a row
     // group hold them), times o_norm, times SiLU(gate).
@@ -252,9 +254,16 @@ __global__ __launch_bounds__(DNT, (sizeof(TS) == 2 ? 5 : 4)) void decode_layer_k
   }
 }
 
+// Keeps the state cached or streams it as the decode step does
+// (state_likely_cached).
 template <int K, int V, typename TS>
 int launch_decode_layer(const DecodeLayerParams &p, int B, hipStream_t stream) {
-  hipLaunchKernelGGL((decode_layer_kernel<K, V, TS>), dim3(p.Hk, B), dim3(DNT), 0, stream, p);
+  const long moved = static_cast<long>(B) * p.Hv * K * V * static_cast<long>(sizeof(TS));
+  if (state_likely_cached(p.state, moved, STATE_CACHE_BYTES)) {
+    hipLaunchKernelGGL((decode_layer_kernel<K, V, TS, STATE_CACHED>), dim3(p.Hk, B), dim3(DNT), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((decode_layer_kernel<K, V, TS, state_streamed<TS>()>), dim3(p.Hk, B), dim3(DNT), 0, stream, p);
+  }
   return hipGetLastError() == hipSuccess ? PBGDN_OK : PBGDN_ERR_LAUNCH;
 }
 

@@ -23,6 +23,7 @@
 // twice the workgroups per CU and as many state bytes in flight as a float32
 // state has. The arithmetic is the same float32 either way.
 #include "state_io.hpp"
+#include "device.hpp"
 
 namespace pbgdn {
 
@@ -49,18 +50,21 @@ struct RecurrentParams {
 // gives them (a bound there would spill).
 template <int K, int V, bool ONE, bool PACKED>
 constexpr int recurrent_wg_per_cu() {
-  return ONE && K * V / 256 <= 64 ? (PACKED ? 6 : 4) : 1;
+  return ONE && K * V / 256 <= 32 ? (PACKED ? 10 : 8) : ONE && K * V / 256 <= 64 ? (PACKED ? 6 : 4) : 1;
 }
 
 // ONE: a single token and no verify slots (the decode step), with no token
 // loop; then a 16-bit state stays packed in the registers as loaded.
-template <int K, int V, typename TS, bool ONE>
-__global__ __launch_bounds__(256, (recurrent_wg_per_cu<K, V, ONE, ONE && sizeof(TS) == 2>())) void recurrent_kernel(
+// CP: the state's cache policy (state_io.hpp). VW: the value columns of one
+// workgroup (V / VW workgroups share a state: its column ranges are
+// independent, every reduction runs over the key rows).
+template <int K, int V, int VW, typename TS, bool ONE, int CP>
+__global__ __launch_bounds__(256, (recurrent_wg_per_cu<K, VW, ONE, ONE && sizeof(TS) == 2>())) void recurrent_kernel(
     RecurrentParams p) {
   constexpr bool PACKED = ONE && sizeof(TS) == 2;
   constexpr int NT = 256;
   constexpr int NW = NT / 64;
-  constexpr int CG = V / 4;    // float4 column groups
+  constexpr int CG = VW / 4;   // float4 column groups
   constexpr int RG = NT / CG;  // row groups
   constexpr int RPT = K / RG;  // rows per thread
   static_assert(CG >= 1 && CG <= 64 && 64 % CG == 0, "V/4 must divide 64");
@@ -69,7 +73,8 @@ __global__ __launch_bounds__(256, (recurrent_wg_per_cu<K, V, ONE, ONE && sizeof(
   constexpr uint32_t ROW_STEP = RG * V * sizeof(TS);         // bytes between a thread's rows
   constexpr uint32_t STATE_BYTES = K * V * sizeof(TS);
 
-  const int h = blockIdx.x;
+  const int h = blockIdx.x / (V / VW);
+  const int col0 = (blockIdx.x % (V / VW)) * VW;
   const int b = blockIdx.y;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -87,7 +92,7 @@ __global__ __launch_bounds__(256, (recurrent_wg_per_cu<K, V, ONE, ONE && sizeof(
   if (slot < 0 || slot >= p.num_states) {  // padded entry: no state, zero output
     if (rg == 0) {
       for (int t = 0; t < p.T; ++t) {
-        const long o_base = ((static_cast<long>(b) * p.T + t) * p.Hv + h) * V + 4 * cg;
+        const long o_base = ((static_cast<long>(b) * p.T + t) * p.Hv + h) * V + col0 + 4 * cg;
 #pragma unroll
         for (int c = 0; c < 4; ++c) store_elem(p.o, o_base + c, p.out_dtype, 0.f);
       }
@@ -97,7 +102,7 @@ __global__ __launch_bounds__(256, (recurrent_wg_per_cu<K, V, ONE, ONE && sizeof(
   const long state_off = (slot * p.Hv + h) * static_cast<long>(K) * V;
   const __amdgpu_buffer_rsrc_t rin = rsrc(static_cast<const TS *>(p.state_in) + state_off, STATE_BYTES);
   const __amdgpu_buffer_rsrc_t rout = rsrc(static_cast<TS *>(p.state_out) + state_off, STATE_BYTES);
-  const uint32_t voff = (rg * V + 4 * cg) * sizeof(TS);
+  const uint32_t voff = (rg * V + col0 + 4 * cg) * sizeof(TS);
 
   // A token's inputs, as loaded: the same load instructions for every input
   // dtype (the elements are picked out of the loaded words afterwards), so no
@@ -108,7 +113,7 @@ __global__ __launch_bounds__(256, (recurrent_wg_per_cu<K, V, ONE, ONE && sizeof(
   const int esz = p.in_dtype == PBGDN_F32 ? 4 : 2;
   const int besz = p.beta_dtype == PBGDN_F32 ? 4 : 2;
   const uint32_t qk_off = (tid * esz) & ~3u;
-  const uint32_t v_off0 = 4 * cg * esz;
+  const uint32_t v_off0 = (col0 + 4 * cg) * esz;
   const uint32_t v_off1 = esz == 4 ? v_off0 + 8 : OUT_OF_RANGE;
   struct Inputs {
     uint32_t wq, wk, wb;
@@ -144,9 +149,9 @@ __global__ __launch_bounds__(256, (recurrent_wg_per_cu<K, V, ONE, ONE && sizeof(
 #pragma unroll
   for (int j = 0; j < RPT; ++j) {
     if constexpr (PACKED) {
-      raw[j] = IO::load(rin, voff, j * ROW_STEP);
+      raw[j] = IO::template load<CP>(rin, voff, j * ROW_STEP);
     } else {
-      s[j] = IO::widen(IO::load(rin, voff, j * ROW_STEP));
+      s[j] = IO::widen(IO::template load<CP>(rin, voff, j * ROW_STEP));
     }
   }
   auto row = [&](int j) -> float4_t {
@@ -216,13 +221,13 @@ __global__ __launch_bounds__(256, (recurrent_wg_per_cu<K, V, ONE, ONE && sizeof(
     for (int j = 0; j < RPT; ++j) {
       const float kr = sk[rg + RG * j];
       if constexpr (PACKED) {
-        IO::store(rout, voff, j * ROW_STEP, alpha * row(j) + kr * u);
+        IO::template store<CP>(rout, voff, j * ROW_STEP, alpha * row(j) + kr * u);
       } else {
         s[j] = alpha * s[j] + kr * u;
       }
     }
     if (rg == 0) {
-      const long o_base = (tok * p.Hv + h) * V + 4 * cg;
+      const long o_base = (tok * p.Hv + h) * V + col0 + 4 * cg;
 #pragma unroll
       for (int c = 0; c < 4; ++c) store_elem(p.o, o_base + c, p.out_dtype, out[c]);
     }
@@ -240,16 +245,43 @@ __global__ __launch_bounds__(256, (recurrent_wg_per_cu<K, V, ONE, ONE && sizeof(
 
   if (!PACKED && (ONE || !p.token_state_idx)) {
 #pragma unroll
-    for (int j = 0; j < RPT; ++j) IO::store(rout, voff, j * ROW_STEP, row(j));
+    for (int j = 0; j < RPT; ++j) IO::template store<CP>(rout, voff, j * ROW_STEP, row(j));
   }
 }
 
+// The decode step streams its state past the cache when the call moves more
+// state than the cache keeps; otherwise (and for token loops, which move each
+// state once per call) it keeps the cached policy.
+template <int K, int V, int VW, typename TS>
+static void launch_step(const RecurrentParams &p, int B, bool cached, hipStream_t stream) {
+  const dim3 grid(p.Hv * (V / VW), B);
+  if (cached) {
+    hipLaunchKernelGGL((recurrent_kernel<K, V, VW, TS, true, STATE_CACHED>), grid, dim3(256), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((recurrent_kernel<K, V, VW, TS, true, state_streamed<TS>()>), grid, dim3(256), 0, stream, p);
+  }
+}
+
+// The decode step keeps its state cached when it likely still is (the same
+// pool as the previous step, small enough), and streams it past the cache
+// otherwise. A streamed float32 step over many head states splits each state's
+// columns over two workgroups (at B = 256, Hv = 32: 71% of HBM against 67%
+// whole; at B = 64 the whole state is faster). Token loops move each state
+// once per call and keep the cached policy.
 template <int K, int V, typename TS>
 static int launch_recurrent(const RecurrentParams &p, int B, hipStream_t stream) {
   if (p.T == 1 && !p.token_state_idx) {
-    hipLaunchKernelGGL((recurrent_kernel<K, V, TS, true>), dim3(p.Hv, B), dim3(256), 0, stream, p);
+    const long moved = static_cast<long>(B) * p.Hv * K * V * static_cast<long>(sizeof(TS));
+    const bool cached = state_likely_cached(p.state_out, moved, STATE_CACHE_BYTES);
+    if constexpr (sizeof(TS) == 4 && V >= 128 && V % 64 == 0) {
+      if (!cached && static_cast<long>(B) * p.Hv >= 4096) {
+        launch_step<K, V, 64, TS>(p, B, false, stream);
+        return hipGetLastError() == hipSuccess ? PBGDN_OK : PBGDN_ERR_LAUNCH;
+      }
+    }
+    launch_step<K, V, V, TS>(p, B, cached, stream);
   } else {
-    hipLaunchKernelGGL((recurrent_kernel<K, V, TS, false>), dim3(p.Hv, B), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((recurrent_kernel<K, V, V, TS, false, STATE_CACHED>), dim3(p.Hv, B), dim3(256), 0, stream, p);
   }
   return hipGetLastError() == hipSuccess ? PBGDN_OK : PBGDN_ERR_LAUNCH;
 }

@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version_and_status_strings():
-    assert _lib.lib().pbgdn_abi_version() == _lib.ABI_VERSION == 8
+    assert _lib.lib().pbgdn_abi_version() == _lib.ABI_VERSION == 9
     header = open(HEADER).read()
     assert re.search(r"#define PBGDN_ABI_VERSION (\d+)", header).group(1) == str(_lib.ABI_VERSION)
     assert _lib.status_string(0) == "ok"
@@ -121,6 +121,21 @@ def test_recurrent_fwd_rejects(over, code):
 
 def test_recurrent_fwd_empty_is_ok():
     assert recurrent_call(B=0) == _lib.OK
+
+
+@pytest.mark.parametrize("src,dst,nbytes", [
+    (FAKE, FAKE + (1 << 20), 15),          # whole 16-byte pieces only
+    (FAKE, FAKE + (1 << 20), -16),
+    (FAKE, FAKE + (1 << 20), 1 << 31),     # at most 2 GiB - 16
+    (FAKE + 8, FAKE + (1 << 20), 1024),    # 16-byte aligned
+    (None, FAKE, 1024),
+])
+def test_stream_probe_rejects(src, dst, nbytes):
+    assert _lib.lib().pbgdn_stream_probe(src, dst, nbytes, None) == _lib.ERR_INVALID_ARGUMENT
+
+
+def test_stream_probe_empty_is_ok():
+    assert _lib.lib().pbgdn_stream_probe(None, None, 0, None) == _lib.OK
 
 
 def test_chunk_workspace_size():

@@ -27,6 +27,34 @@ def test_decode_b64_one_step():
     assert_parity("decode_b64 step", o, o_ref, state, s_ref)
 
 
+@pytest.mark.parametrize("batch,state_dtype", [(100, torch.float32), (128, torch.float32), (200, torch.bfloat16)])
+def test_decode_step_streamed_past_the_cache(batch, state_dtype):
+    """Steps that move more than 192 MiB of state at the Qwen3-Next head shape
+    stream it past the cache: B=100 float32 and B=200 bf16 with one workgroup
+    per head state, B=128 float32 (4,096 head states) with each state's columns
+    split over two workgroups. Same results as the oracle."""
+    q, k, v, g, beta, h0 = generate(batch, 1, 16, 32, 128, 128, torch.bfloat16, 0.02, seed=batch)
+    h0 = h0.to(state_dtype)
+    o_ref, s_ref = oracle(q, k, v, g, beta, SCALE, h0.float(), "sequential")
+    dq, dk, dv, dg, db, state = to_dev(q, k, v, g, beta, h0)
+    o = torch.ops.pbgdn.recurrent_step_(dq, dk, dv, dg, db, state, None, SCALE)
+    torch.cuda.synchronize()
+    s_tol = 1e-3 if state_dtype == torch.float32 else 1e-2
+    assert_parity(f"decode B={batch} {state_dtype} streamed", o, o_ref, state.float(), s_ref, s_tol=s_tol)
+
+
+def test_stream_probe_copies():
+    """pbgdn_stream_probe copies every byte (64 MiB plus a 16-byte tail piece)."""
+    from pseudobrain_amd import _lib
+    n = (64 << 20) + 16
+    src = torch.randint(0, 255, (n,), dtype=torch.uint8, device=DEV)
+    dst = torch.zeros_like(src)
+    _lib.check(_lib.lib().pbgdn_stream_probe(src.data_ptr(), dst.data_ptr(), n,
+                                             torch.cuda.current_stream().cuda_stream), "pbgdn_stream_probe")
+    torch.cuda.synchronize()
+    assert torch.equal(dst, src)
+
+
 def test_decode_chained_in_place_steps():
     """8 chained in-place steps with fresh tokens equal 8 oracle steps."""
     q, k, v, g, beta, h0 = generate(8, 8, 16, 32, 128, 128, torch.bfloat16, 0.02, seed=5)
