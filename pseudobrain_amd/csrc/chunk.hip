@@ -47,7 +47,7 @@ bool wide_eligible(const ChunkParams &p) {
     return false;
   } else {
     if (p.V % 128 != 0 || scan_choice() == 1) return false;
-    return scan_choice() == 2 || static_cast<long>(p.num_seqs) * p.Hv * (p.V / 128) >= SCAN_CUS / 2;
+    return scan_choice() == 2 || static_cast<long>(p.num_seqs) * p.Hv * (p.V / 128) >= p.cus / 2;
   }
 }
 
@@ -151,19 +151,16 @@ extern "C" int pbgdn_chunk_fwd(const void *q, const void *k, const void *v, int 
   const long total = static_cast<long>(V / pbgdn::VT) * Hv * num_seqs;
   if (total > 0x7fffffffL) return PBGDN_ERR_UNSUPPORTED;
   const long records = pbgdn::chunk_records(static_cast<long>(B) * T, num_seqs);
-  // The scan's sequence groups. Sequences of 2,048 tokens or more on average
-  // get a workgroup each (the unchained kernel: its step is ~10% shorter,
-  // and a sequence's pipeline fill is small next to its length). Shorter
-  // ones run back to back in groups (a chained workgroup pays ~1 µs per
-  // sequence boundary instead of a fill and drain): one group when the
-  // (value head, column tile) pairs fill the CUs, else enough groups to.
+  // The scan's sequence groups (scan_groups): a chained workgroup pays
+  // ~1 µs per sequence boundary instead of a pipeline fill and drain, and the
+  // unchained kernel's step is ~10% shorter.
+  pbgdn::DeviceShape shape;
+  if (!pbgdn::device_shape(shape)) return PBGDN_ERR_LAUNCH;
   const int pairs = (V / pbgdn::VT) * Hv;
-  const long tokens = static_cast<long>(B) * T;
-  const int groups = tokens >= 2048L * num_seqs ? num_seqs
-                                                : std::max(1, std::min(num_seqs, pbgdn::SCAN_CUS / pairs));
+  const int groups = pbgdn::scan_groups(static_cast<long>(B) * T, num_seqs, pairs, shape.cus);
   pbgdn::ChunkParams p{q, k, v, g, beta, beta_dtype, h0, ht, state_dtype, state_idx, has_initial_state,
                        num_states, cu_seqlens, o, static_cast<unsigned char *>(workspace), T, Hk, Hv, V,
-                       num_seqs, groups, scale};
+                       num_seqs, groups, scale, shape.cus, shape.xcds};
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (K) {
     case 64: return pbgdn::dispatch_in<64>(p, records, in_dtype, out_dtype, s);

@@ -35,6 +35,8 @@
 #pragma once
 
 #include "common.hpp"
+#include "device.hpp"
+#include "schedule.hpp"
 
 namespace pbgdn {
 
@@ -44,7 +46,6 @@ typedef short i16x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int CH = 64;                  // chunk length (CHUNK, gated_deltanet.py:49)
 constexpr int VT = 16;                  // value columns per scan workgroup
-constexpr int SCAN_CUS = 256;            // CUs of an MI355X: the scan runs one workgroup per CU
 
 // Workspace record of one (chunk, value head), REC_BYTES bytes:
 //   REC_SC   fp32 [64] gamma_t, [64] scale gamma_t, [64] exp(c_63 - c_t),
@@ -93,6 +94,7 @@ struct ChunkParams {
   int T, Hk, Hv, V, num_seqs;
   int seq_groups;  // the scan's sequence groups (a workgroup runs one group's sequences back to back)
   float scale;
+  int cus, xcds;   // the device's compute units and XCDs (device.hpp)
 };
 
 // Sequence s (wave-uniform): first token and end. cu_seqlens is read through

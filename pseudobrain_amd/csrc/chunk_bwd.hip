@@ -32,6 +32,8 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "device.hpp"
+#include "schedule.hpp"
 
 namespace pbgdn {
 namespace {
@@ -56,6 +58,7 @@ struct BwdParams {
   int in_dtype, beta_dtype;
   int B, T, Hk, Hv, K, V, n;
   float scale;
+  int xcds;  // the device's XCDs (device.hpp)
 };
 
 // fp32 MFMA: acc (16x16) += A (16x4) B (4x16). Lane l, c = l & 15, g = l >> 4:
@@ -604,24 +607,17 @@ __device__ __forceinline__ void adjoint_pass(const BwdParams &p, float *lds, int
 // and dht, not the states), so one launch runs both: pair z = (role, batch
 // row, value head), role 0 the forward pass, 1 the reverse pass. Two
 // workgroups fit a CU, so each CU overlaps a forward and a reverse scan.
-// Workgroups go to the 8 XCDs round-robin by linear index; the V/16 tiles of
+// Workgroups go to the XCDs round-robin by linear index; the V/16 tiles of
 // one pair read the same K rows and T records every step, so when the pairs
-// fill the XCDs evenly all tiles of a pair are given indices on one XCD and
-// those reads come from its L2 after the first.
+// fill the XCDs evenly all tiles of a pair are given indices on one XCD
+// (xcd_group) and those reads come from its L2 after the first.
 template <int K, typename TIn>
 __global__ __launch_bounds__(BNT) void bwd_scans_kernel(BwdParams p) {
   extern __shared__ __align__(16) float lds[];
   const int tiles = p.V / 16, pairs = 2 * p.B * p.Hv;
   const int l = blockIdx.x;
   int pair, tile;
-  if (pairs % 8 == 0) {
-    const int rest = l >> 3;
-    tile = rest % tiles;
-    pair = (rest / tiles) * 8 + (l & 7);
-  } else {
-    tile = l % tiles;
-    pair = l / tiles;
-  }
+  xcd_group(l, pairs, tiles, p.xcds, pair, tile);
   const int role_b = pair / p.Hv, h = pair % p.Hv;
   if (role_b < p.B) {
     state_pass<K, TIn>(p, lds, role_b, h, 16 * tile);
@@ -1045,6 +1041,9 @@ extern "C" int pbgdn_chunk_bwd(const void *q, const void *k, const void *v, int 
   float *ws = static_cast<float *>(workspace);
   const long recs = static_cast<long>(B) * Hv * n;
   BwdParams p{};
+  DeviceShape shape;
+  if (!device_shape(shape)) return PBGDN_ERR_LAUNCH;
+  p.xcds = shape.xcds;
   p.q = q;
   p.k = k;
   p.v = v;

@@ -37,7 +37,6 @@ namespace pbgdn {
 namespace {
 
 constexpr int PNT = 256;          // threads per prep workgroup
-constexpr int NUM_CU = 256;
 // Resident workgroups per CU: three when the registers allow it (16-bit
 // inputs); fp32 inputs hold more registers and keep two.
 template <typename TIn>
@@ -348,31 +347,12 @@ struct PrepBlock {
     st(base + 16 * r * L::SPB + 32 * (r + 1) + sp_tile, half4_t{});
   }
 
-  // Items of this workgroup: the grid is resident from the start with
-  // tiers = grid / NUM_CU workgroups per CU, and the k-th workgroup dispatched
-  // to a CU (block index / NUM_CU) runs slower than the ones before it (the
-  // oldest waves win issue arbitration): at T = 32K the second and third go
-  // at about 0.85 and 0.74 of the first one's pace. The items are split into one
-  // contiguous segment per tier in proportion to these paces; within a
-  // segment the tier's workgroups take every `stride`-th item from `first`.
+  // Items of this workgroup (prep_share, schedule.hpp).
   __device__ void share(int items, int &first, int &stride, int &end) const {
-    constexpr int PACE[3] = {100, 85, 74};
-    const int grid = gridDim.x;
-    const int tiers = (grid % NUM_CU == 0 && grid / NUM_CU <= 3) ? grid / NUM_CU : 1;
-    stride = grid / tiers;
-    const int tier = static_cast<int>(blockIdx.x) / stride;
-    const int j = static_cast<int>(blockIdx.x) % stride;
-    int total = 0, before = 0;
-    for (int t = 0; t < tiers; ++t) {
-      total += PACE[t];
-      if (t < tier) before += PACE[t];
-    }
-    const int begin = static_cast<int>(static_cast<long>(items) * before / total);
-    end = static_cast<int>(static_cast<long>(items) * (before + PACE[tier]) / total);
-    // Workgroups are dispatched round-robin over the 8 XCDs: number the
-    // items so that consecutive ones (the value heads of one key head) share
-    // an XCD.
-    first = begin + ((stride % 8 == 0) ? (j & 7) * (stride / 8) + (j >> 3) : j);
+    const PrepShare sh = prep_share(items, static_cast<int>(gridDim.x), static_cast<int>(blockIdx.x), p.cus, p.xcds);
+    first = sh.first;
+    stride = sh.stride;
+    end = sh.end;
   }
 
   __device__ void run(int items) {
@@ -429,21 +409,14 @@ __global__ __launch_bounds__(PNT, prep_wg_per_cu<TIn>()) void prep_kernel(ChunkP
 
 template <int K, typename TIn>
 int launch_prep(const ChunkParams &p, long records, hipStream_t stream) {
-  static bool configured = false;  // benign race: the attribute call is idempotent
+  static std::atomic<bool> configured[MAX_DEVICES];  // the attribute is set per device
   const size_t smem = PrepLayout<K>::BYTES;
   auto kernel = prep_kernel<K, TIn>;
-  if (!configured) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            static_cast<int>(smem)) != hipSuccess) {
-      return PBGDN_ERR_LAUNCH;
-    }
-    configured = true;
-  }
+  if (!smem_configured(reinterpret_cast<const void *>(kernel), smem, configured)) return PBGDN_ERR_LAUNCH;
   const int hpi = ((p.Hv / p.Hk) % 2 == 0) ? 2 : 1;  // value heads per item (PrepBlock::hpi)
   const long items = records * (p.Hv / hpi);
   if (items > 0x3fffffffL) return PBGDN_ERR_UNSUPPORTED;  // item numbers are 32-bit
-  long grid = static_cast<long>(NUM_CU) * prep_wg_per_cu<TIn>();
-  if (items < grid) grid = (items + 7) / 8 * 8;
+  const long grid = prep_grid(items, p.cus, prep_wg_per_cu<TIn>(), p.xcds);
   hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(PNT), smem, stream, p, static_cast<int>(items));
   return hipGetLastError() == hipSuccess ? PBGDN_OK : PBGDN_ERR_LAUNCH;
 }

@@ -223,23 +223,13 @@ struct ScanStage {
 
 // Block index -> (sequence, value head, column tile). All column tiles of the
 // value heads that share one query/key head of one sequence form a group; a
-// group is kept on one XCD (workgroups are dispatched round-robin over the 8
-// XCDs) so that its q/k chunks and Tb/QKD records are fetched into that XCD's
-// L2 once.
-__device__ __forceinline__ void decode_block(int L, int total, int nv, int group_heads, int Hk, int &grp_seq, int &h,
-                                             int &vtile, int &member) {
+// group is kept on one XCD (xcd_group) so that its q/k chunks and Tb/QKD
+// records are fetched into that XCD's L2 once.
+__device__ __forceinline__ void decode_block(int L, int total, int nv, int group_heads, int Hk, int xcds, int &grp_seq,
+                                             int &h, int &vtile, int &member) {
   const int gsize = nv * group_heads;
-  const int ngroups = total / gsize;
   int grp, in;
-  if (ngroups % 8 == 0) {
-    const int xcd = L & 7;
-    const int slot = L >> 3;
-    grp = (slot / gsize) * 8 + xcd;
-    in = slot % gsize;
-  } else {
-    grp = L / gsize;
-    in = L % gsize;
-  }
+  xcd_group(L, total / gsize, gsize, xcds, grp, in);
   const int hk = grp % Hk;
   grp_seq = grp / Hk;
   h = hk * group_heads + in / nv;
@@ -306,7 +296,7 @@ struct ScanBlock {
     lt = tid - NCW * 64;
     const int group_heads = p.Hv / p.Hk;
     int vtile, member, grp;
-    decode_block(blockIdx.x, gridDim.x, p.V / VT, group_heads, p.Hk, grp, h, vtile, member);
+    decode_block(blockIdx.x, gridDim.x, p.V / VT, group_heads, p.Hk, p.xcds, grp, h, vtile, member);
     hk = h / group_heads;
     v0 = vtile * VT;
     s_begin = static_cast<int>(static_cast<long>(grp) * p.num_seqs / p.seq_groups);
@@ -835,16 +825,10 @@ __global__ __launch_bounds__(NT) void scan_kernel(ChunkParams p) {
 
 template <int K, typename TIn, typename TOut, bool CHAIN>
 int launch_scan_kernel(const ChunkParams &p, hipStream_t stream) {
-  static bool configured = false;  // benign race: the attribute call is idempotent
+  static std::atomic<bool> configured[MAX_DEVICES];  // the attribute is set per device
   const size_t smem = CHAIN ? ScanLayout<K>::CHAIN_BYTES : ScanLayout<K>::BYTES;
   auto kernel = scan_kernel<K, TIn, TOut, CHAIN>;
-  if (!configured) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            static_cast<int>(smem)) != hipSuccess) {
-      return PBGDN_ERR_LAUNCH;
-    }
-    configured = true;
-  }
+  if (!smem_configured(reinterpret_cast<const void *>(kernel), smem, configured)) return PBGDN_ERR_LAUNCH;
   const int total = (p.V / VT) * p.Hv * p.seq_groups;
   hipLaunchKernelGGL(kernel, dim3(total), dim3(NT), smem, stream, p);
   return hipGetLastError() == hipSuccess ? PBGDN_OK : PBGDN_ERR_LAUNCH;

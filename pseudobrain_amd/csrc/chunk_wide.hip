@@ -133,19 +133,12 @@ struct WideBlock {
     g4 = lane >> 4;
     // Block -> (sequence, value head, column group): the column groups and the
     // value heads of one key head of one sequence share their K/Q rows; keep
-    // them on one XCD (blocks go round-robin over the 8 XCDs).
+    // them on one XCD (xcd_group).
     const int groups = p.V / WCOLS;
     const int per_key = groups * (p.Hv / p.Hk);
     const int total = static_cast<int>(gridDim.x);
-    const int L_ = static_cast<int>(blockIdx.x);
     int kgrp, member;
-    if ((total / per_key) % 8 == 0) {
-      kgrp = ((L_ >> 3) / per_key) * 8 + (L_ & 7);
-      member = (L_ >> 3) % per_key;
-    } else {
-      kgrp = L_ / per_key;
-      member = L_ % per_key;
-    }
+    xcd_group(static_cast<int>(blockIdx.x), total / per_key, per_key, p.xcds, kgrp, member);
     seq = kgrp / p.Hk;
     hk = kgrp % p.Hk;
     h = hk * (p.Hv / p.Hk) + member / groups;
@@ -528,16 +521,10 @@ __global__ __launch_bounds__(WNT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
 template <int K, typename TIn, typename TOut>
 int launch_wide(const ChunkParams &p, hipStream_t stream) {
-  static bool configured = false;  // benign race: the attribute call is idempotent
+  static std::atomic<bool> configured[MAX_DEVICES];  // the attribute is set per device
   const size_t smem = WideLayout<K>::BYTES;
   auto kernel = wide_kernel<K, TIn, TOut>;
-  if (!configured) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            static_cast<int>(smem)) != hipSuccess) {
-      return PBGDN_ERR_LAUNCH;
-    }
-    configured = true;
-  }
+  if (!smem_configured(reinterpret_cast<const void *>(kernel), smem, configured)) return PBGDN_ERR_LAUNCH;
   const long total = static_cast<long>(p.V / WCOLS) * p.Hv * p.num_seqs;
   if (total > 0x7fffffffL) return PBGDN_ERR_UNSUPPORTED;
   hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(total)), dim3(WNT), smem, stream, p);

@@ -43,6 +43,18 @@ bool state_likely_cached(const void *state, long moved, long cache_bytes) {
   return prev == reinterpret_cast<uintptr_t>(state) && moved <= cache_bytes;
 }
 
+bool smem_configured(const void *kernel, size_t bytes, std::atomic<bool> *flags) {
+  const int dev = current_device();
+  if (dev < 0) return false;
+  if (flags[dev].load(std::memory_order_acquire)) return true;
+  // racing first calls set the same attribute: idempotent
+  if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)) != hipSuccess) {
+    return false;
+  }
+  flags[dev].store(true, std::memory_order_release);
+  return true;
+}
+
 namespace {
 
 // Streaming copy: 16-byte buffer loads then stores, UNITS pieces of 16 bytes

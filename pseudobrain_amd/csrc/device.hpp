@@ -5,6 +5,9 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+#include <cstddef>
+
 namespace pbgdn {
 
 struct DeviceShape {
@@ -29,5 +32,10 @@ bool device_shape(DeviceShape &out);
 // pools and stream; a loop stepping one pool keeps it cached. Records `state`
 // for the next call.
 bool state_likely_cached(const void *state, long moved, long cache_bytes);
+
+// Raises `kernel`'s dynamic LDS limit to `bytes` on the current device, once
+// per device (`flags`: MAX_DEVICES entries kept by the caller); false when the
+// runtime refuses.
+bool smem_configured(const void *kernel, size_t bytes, std::atomic<bool> *flags);
 
 }  // namespace pbgdn
