@@ -151,6 +151,24 @@ struct OpOf<u16> {
   }
 };
 
+// Range of the fp16 operands X (and through Tb X, U). A tile of X whose largest
+// magnitude m exceeds X_LIMIT is scaled by 2^-e, e = the least power that
+// brings it to at most X_LIMIT (exact: a power of two), so that U' = Tb X'
+// (at most 64 |Tb| X_LIMIT) stays inside fp16; U = U' 2^e is restored in fp32.
+constexpr float X_LIMIT = 256.f;
+// 2^-e for a tile maximum m > X_LIMIT (m finite): scales m to at most X_LIMIT.
+__device__ __forceinline__ float range_scale(float m) {
+  int e;
+  frexpf(m / X_LIMIT, &e);  // m / X_LIMIT = f 2^e, f in [0.5, 1)
+  return ldexpf(1.f, -e);
+}
+__device__ __forceinline__ float tile_max(const float4_t (&x)[4]) {
+  float m = 0.f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) m = fmaxf(m, fmaxf(fmaxf(fabsf(x[r][0]), fabsf(x[r][1])), fmaxf(fabsf(x[r][2]), fabsf(x[r][3]))));
+  return m;
+}
+
 __device__ __forceinline__ float4_t mma(half8_t a, half8_t b, float4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }

@@ -42,11 +42,16 @@
 //
 // Arithmetic (fp32 accumulation throughout):
 //   * K, Q enter MFMA in the input's 16-bit type (bf16 unconverted; fp32
-//     inputs staged as fp16); V as staged.
+//     inputs staged as fp16); V as staged (fp32 inputs as a bf16 high + low
+//     pair, fp32 range).
 //   * S enters K S as a high + low pair of that type (two MFMAs), so X sees
 //     the fp32 state to ~16 bits; Q S, which only reaches the output, uses the
 //     high part. The state update K^T (dec U) uses dec U as a pair.
-//   * Tb, X, U and QKD are fp16 (11-bit significand) on the fp16 MFMA.
+//   * Tb, X, U and QKD are fp16 (11-bit significand) on the fp16 MFMA. A
+//     chunk whose X exceeds X_LIMIT somewhere is scaled by a power of two
+//     (chunk.hpp) before it becomes fp16: each X wave publishes its tile's
+//     scale, the U waves bring the tiles to the chunk's smallest one through
+//     the lanes of their Tb fragments, and U, O are restored in fp32.
 //
 // LDS costs that shape the code (MI355X, CU cycles per wave64 instruction):
 // 16-byte fragment reads and transposing reads 4, 8-byte tile writes 6.7 in
@@ -70,7 +75,8 @@ struct ScanLayout {
   static constexpr int SPB = 2 * CH + 32;
   static constexpr int KQ_MAT = CH * KPB;
   static constexpr int V16_OFF = 2 * KQ_MAT;
-  static constexpr int REC_OFF = V16_OFF + CH * 32;
+  static constexpr int V16LO_OFF = V16_OFF + CH * 32;  // fp32 inputs: the low bf16 part of V
+  static constexpr int REC_OFF = V16LO_OFF + CH * 32;
   static constexpr int BUF = REC_OFF + REC_BYTES;
   static constexpr int XT = 2 * BUF;                  // [16 col][64 t] fp16 X^T (swz)
   static constexpr int UT = XT + VT * SPB;            // [2] U^T fp16 (swz), by chunk parity
@@ -80,7 +86,8 @@ struct ScanLayout {
   static constexpr int SL = SH + VT * KPB;            // S^T low (swz)
   static constexpr int OT = SL + VT * KPB;            // [2][64 t][16] output type
   static constexpr int OT_BUF = CH * VT * 4;
-  static constexpr int BYTES = OT + 2 * OT_BUF;
+  static constexpr int RS = OT + 2 * OT_BUF;          // fp32 range scales: [4] X tiles, [2] chunk by parity
+  static constexpr int BYTES = RS + 32;
   // Chained streams only: the initial state of the sequence whose first
   // chunk is in chunk buffer b ([K rows][16 columns] as stored), staged by the
   // loader waves with that chunk.
@@ -89,6 +96,7 @@ struct ScanLayout {
   __device__ static constexpr int h0(int b) { return BYTES + b * H0_BYTES; }
   __device__ static constexpr int kq(int b) { return b * BUF; }
   __device__ static constexpr int v16(int b) { return b * BUF + V16_OFF; }
+  __device__ static constexpr int v16lo(int b) { return b * BUF + V16LO_OFF; }
   __device__ static constexpr int rec(int b) { return b * BUF + REC_OFF; }
   __device__ static constexpr int ot(int b) { return OT + b * OT_BUF; }
   __device__ static constexpr int ut(int b) { return UT + b * VT * SPB; }
@@ -202,7 +210,14 @@ struct ScanStage {
   __device__ __forceinline__ void store_unit(unsigned char *buf, const Regs &r, int l, int i) const {
     if (l + NLT * i >= UNITS) return;
     unsigned char *d = buf + dst[i];
-    if (EPU == 4 && (i < SLOT_V || (i == SLOT_V && v_wave))) {
+    if (EPU == 4 && i == SLOT_V && v_wave) {  // fp32 V: bf16 high and low parts (fp32 range)
+      const uint4 x = r.u[i];
+      bf16x4_t hi, lo;
+      OpOf<u16>::split(float4_t{__uint_as_float(x.x), __uint_as_float(x.y), __uint_as_float(x.z),
+                                __uint_as_float(x.w)}, hi, lo);
+      *reinterpret_cast<bf16x4_t *>(d) = hi;
+      *reinterpret_cast<bf16x4_t *>(d + (L::V16LO_OFF - L::V16_OFF)) = lo;
+    } else if (EPU == 4 && i < SLOT_V) {
       const uint4 x = r.u[i];
       *reinterpret_cast<half4_t *>(d) = to_half4(float4_t{__uint_as_float(x.x), __uint_as_float(x.y),
                                                           __uint_as_float(x.z), __uint_as_float(x.w)});
@@ -506,6 +521,16 @@ struct ScanBlock {
   // ------------------------------------------------------------ compute waves
   // Row float4 of a record vector (SC_GAM, SC_GSC, SC_DEC) for this lane's
   // accumulator rows 16 r + 4 g.. of the chunk in buffer b.
+  // V rows 16r + 4g.. of column c of chunk buffer b (fp32 inputs: high + low parts)
+  __device__ __forceinline__ float4_t v_rows(int b, int r) const {
+    if constexpr (sizeof(TIn) == 4) {
+      return OpOf<u16>::bits_to_float(ld_tr(L::v16(b) + 16 * r * 32 + tr_v)) +
+             OpOf<u16>::bits_to_float(ld_tr(L::v16lo(b) + 16 * r * 32 + tr_v));
+    } else {
+      return Op::bits_to_float(ld_tr(L::v16(b) + 16 * r * 32 + tr_v));
+    }
+  }
+
   __device__ __forceinline__ float4_t rec_rows(int b, int vec, int r) const {
     return ld<float4_t>(L::rec(b) + REC_SC + vec + (16 * r + 4 * g4) * 4);
   }
@@ -596,17 +621,39 @@ struct ScanBlock {
         acc = mma(mf[kk], shi[kk], acc);
         acl = mma(mf[kk], slo[kk], acl);
       }
-      st(L::XT + sp_tile + 32 * r, to_half4(vv - gg * (acc + acl)));
+      // X of token rows 16r..: scaled into range if it leaves it (a wave vote),
+      // its scale published for the U waves
+      float4_t x = vv - gg * (acc + acl);
+      const float xm = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+      float down = 1.f;
+      if (__builtin_amdgcn_ballot_w64(xm > X_LIMIT) != 0) {
+        down = range_scale(wave_max(xm));
+        x *= down;
+      }
+      st(L::XT + sp_tile + 32 * r, to_half4(x));
+      if (lane == 0) st(L::RS + 4 * r, down);
     }
     block_sync();
     {
       const half8_t x0 = ld<half8_t>(L::XT + sp_frag);
       const half8_t x1 = ld<half8_t>(L::XT + sp_frag + 64);
+      const float4_t downs = ld<float4_t>(L::RS);
       fetch_kt(b, kt);
+      // the chunk's scale: the smallest of its tiles'; the Tb lanes that
+      // multiply tile t (tokens 8g.. of step kk: tile 2 kk + g/2) take
+      // d / downs[t] (a power of two, at most 1)
+      const float d = fminf(fminf(downs[0], downs[1]), fminf(downs[2], downs[3]));
+      if (d < 1.f) {
+        const int t = g4 >> 1;
+        f0 *= static_cast<half_t>(d / downs[t]);
+        f1 *= static_cast<half_t>(d / downs[2 + t]);
+      }
       float4_t u = mfma32(f0, x0, float4_t{0.f, 0.f, 0.f, 0.f});
       if (r >= 2) u = mfma32(f1, x1, u);
       const uint32_t o = sp_tile + 32 * r;
-      st(L::ut(b) + o, to_half4(u));
+      st(L::ut(b) + o, to_half4(u));  // U' = U d, for O of this chunk
+      if (wave == 0 && lane == 0) st(L::RS + 16 + 4 * b, d);
+      if (d < 1.f) u *= 1.f / d;
       const float4_t du = u * dd;
       const O4 hi = Op::from(du);
       st(L::UH + o, hi);
@@ -616,7 +663,7 @@ struct ScanBlock {
     {
       O8 nmf[KS];
       fetch_rows(b ^ 1, 0, nmf);
-      const float4_t nvv = Op::bits_to_float(ld_tr(L::v16(b ^ 1) + 16 * r * 32 + tr_v));
+      const float4_t nvv = v_rows(b ^ 1, r);
       const float4_t ngg = rec_rows(b ^ 1, SC_GAM, r);
       update_state(b, kt);
       next_chunk(wave, b ^ 1);
@@ -634,9 +681,13 @@ struct ScanBlock {
   __device__ __forceinline__ void out_tile(int ob, const float4_t &qs, const float4_t &gs, const half8_t &f0,
                                            const half8_t &f1) {
     const int r = wave & 3;
+    // U^T of the chunk holds U d (d its range scale, usually 1): O = (scale gamma Q S d + QKD U d) / d
+    const float d = ld<float>(L::RS + 16 + 4 * ob);
     float4_t o = qs * gs;
+    if (d < 1.f) o *= d;
     o = mfma32(f0, ld<half8_t>(L::ut(ob) + sp_frag), o);
     if (r >= 2) o = mfma32(f1, ld<half8_t>(L::ut(ob) + sp_frag + 64), o);
+    if (d < 1.f) o *= 1.f / d;
 #pragma unroll
     for (int i = 0; i < 4; ++i) st(L::ot(ob) + ((16 * r + 4 * g4 + i) * VT + c16) * sizeof(TOut), out_elem<TOut>(o[i]));
   }
@@ -788,7 +839,7 @@ struct ScanBlock {
     if (wave < 4) {
       O8 mf[KS];
       fetch_rows(0, 0, mf);
-      float4_t vv = Op::bits_to_float(ld_tr(L::v16(0) + 16 * wave * 32 + tr_v));
+      float4_t vv = v_rows(0, wave);
       float4_t gg = rec_rows(0, SC_GAM, wave);
       long n = 0;
       for (; n + 1 < nchunks; n += 2) {

@@ -405,6 +405,15 @@ struct WideBlock {
       float4_t x[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) x[r] = Op::bits_to_float(vraw[r]) - gam[r] * ah[r];
+      // X beyond X_LIMIT anywhere in the tile (a wave vote): scale it into range
+      // (range_scale); U, its products and O are restored in fp32 below.
+      const bool big = __builtin_amdgcn_ballot_w64(tile_max(x) > X_LIMIT) != 0;
+      float down = 1.f;
+      if (big) {
+        down = range_scale(wave_max(tile_max(x)));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x[r] *= down;
+      }
       // The state update's reads of chunk n (K^T for tokens 0..31, dec, gamma_63)
       // go out before U and the barrier: chunk n has been in LDS since barrier n-1.
       O8 tf[2][NKT];
@@ -424,6 +433,15 @@ struct WideBlock {
       for (int r = 0; r < 4; ++r) u[r] = mfma32(tbf[frag_index(r, 0)], xb0, float4_t{0.f, 0.f, 0.f, 0.f});
       u[2] = mfma32(tbf[frag_index(2, 1)], xb1, u[2]);
       u[3] = mfma32(tbf[frag_index(3, 1)], xb1, u[3]);
+      // ub (U' for O) is taken from the scaled U; the state update uses U itself
+      half8_t ub[2];
+      ub[0] = pairh(to_half4(u[0]), to_half4(u[1]));
+      ub[1] = pairh(to_half4(u[2]), to_half4(u[3]));
+      if (big) {
+        const float up = 1.f / down;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) u[r] *= up;
+      }
       // barrier n: chunk n+1 is in LDS (each wave waited for its loads; the
       // O stores of chunk n-1, issued after them, may still be in flight),
       // every wave is past chunk n-1
@@ -435,7 +453,6 @@ struct WideBlock {
 #pragma unroll
       for (int t = 0; t < NKT; ++t) tf[1][t] = kt_frag(tb[t >> 1], t & 1, 1);
       O8 dhi[2], dlo[2];
-      half8_t ub[2];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         O4 h0, h1, l0, l1;
@@ -443,7 +460,6 @@ struct WideBlock {
         Op::split(u[2 * ks + 1] * dec[2 * ks + 1], h1, l1);
         dhi[ks] = pair(h0, h1);
         dlo[ks] = pair(l0, l1);
-        ub[ks] = pairh(to_half4(u[2 * ks]), to_half4(u[2 * ks + 1]));
       }
 #pragma unroll
       for (int t = 0; t < NKT; ++t) s[t] *= g63;
@@ -486,14 +502,20 @@ struct WideBlock {
       }
       // ---- O^T = (Q S)^T diag(scale gamma) + U^T QKD^T: lane (g, c) holds
       // O[16 r + c][v0 + 4 g .. + 3], stored as one 8-byte piece
+      // (with a scaled tile: O = (scale gamma Q S down + U' QKD^T) / down)
       float4_t o[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        o[r] = aq[r] * gsc[r];
+        o[r] = aq[r] * (big ? gsc[r] * down : gsc[r]);
         o[r] = mfma32(ub[0], qkf[frag_index(r, 0)], o[r]);
       }
       o[2] = mfma32(ub[1], qkf[frag_index(2, 1)], o[2]);
       o[3] = mfma32(ub[1], qkf[frag_index(3, 1)], o[3]);
+      if (big) {
+        const float up = 1.f / down;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] *= up;
+      }
       const long rows = oleft < CH ? oleft : CH;  // >= 1: chunk n holds tokens
       const __amdgpu_buffer_rsrc_t ro = rsrc(op, (rows - 1) * ostride + p.V * static_cast<long>(sizeof(TOut)));
 #pragma unroll

@@ -1,0 +1,116 @@
+"""Precision envelope of the chunkwise prefill against the fp32 oracle
+(delta_rule_chunked, gated_deltanet.py:110-165): inputs of large magnitude,
+fp32 inputs beyond the fp16 range, and slow or no decay over a full 32K
+sequence and over a streamed sequence, where rounding errors in the state
+accumulate instead of being forgotten. Tolerances as the other parity tests:
+outputs 2e-2, final states 1e-3 (infinity-norm relative error); the errors
+are printed per case (and per segment for the streamed run)."""
+import pytest
+import torch
+
+from pseudobrain_amd import gated_deltanet as gd
+from pseudobrain_amd.workloads import generate
+from tests.gpu_util import assert_parity, oracle, rel_err
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def run(q, k, v, g, beta, scale, h0):
+    with torch.no_grad():
+        o, s = gd.chunk_fwd(*(x.to(DEV) for x in (q, k, v, g, beta)), scale, h0.to(DEV))
+    torch.cuda.synchronize()
+    return o, s
+
+
+@pytest.mark.parametrize("v_scale", [1e3, 1e5])
+def test_large_values_bf16(v_scale):
+    """v (and h0 with it) x 1e3 and x 1e5 in bf16: |v| reaches ~4e5, beyond
+    the fp16 range of intermediate operands."""
+    q, k, v, g, beta, h0 = generate(1, 2048, 2, 4, 128, 128, torch.bfloat16, 0.02, seed=31)
+    v = (v.float() * v_scale).to(torch.bfloat16)
+    h0 = h0 * v_scale
+    o, s = run(q, k, v, g, beta, 128 ** -0.5, h0)
+    o_ref, s_ref = oracle(q, k, v, g, beta, 128 ** -0.5, h0)
+    assert_parity(f"v x {v_scale:g}", o, o_ref, s, s_ref)
+
+
+@pytest.mark.parametrize("v_scale", [1e3, 1e5])
+def test_large_values_bf16_wide_scan(v_scale):
+    """The same at a shape that runs the wide scan (4 sequences x 32 value heads)."""
+    q, k, v, g, beta, h0 = generate(4, 256, 16, 32, 128, 128, torch.bfloat16, 0.02, seed=36)
+    v = (v.float() * v_scale).to(torch.bfloat16)
+    h0 = h0 * v_scale
+    o, s = run(q, k, v, g, beta, 128 ** -0.5, h0)
+    o_ref, s_ref = oracle(q, k, v, g, beta, 128 ** -0.5, h0)
+    assert_parity(f"wide v x {v_scale:g}", o, o_ref, s, s_ref)
+
+
+def test_large_initial_state():
+    """h0 x 100 (N(0, 2)) with unit-scale v."""
+    q, k, v, g, beta, h0 = generate(1, 1024, 2, 4, 128, 128, torch.bfloat16, 2.0, seed=32)
+    o, s = run(q, k, v, g, beta, 128 ** -0.5, h0)
+    o_ref, s_ref = oracle(q, k, v, g, beta, 128 ** -0.5, h0)
+    assert_parity("h0 x 100", o, o_ref, s, s_ref)
+
+
+@pytest.mark.parametrize("dk", [64, 128])
+def test_fp32_inputs_beyond_fp16_range(dk):
+    """fp32 q, k, v (the reference CPU path's dtype) with |v| up to ~4e5."""
+    q, k, v, g, beta, h0 = generate(1, 2048, 4, 4, dk, dk, torch.float32, 0.0, seed=33)
+    v = v * 1e5
+    o, s = run(q, k, v, g, beta, dk ** -0.5, h0)
+    o_ref, s_ref = oracle(q, k, v, g, beta, dk ** -0.5, h0)
+    assert_parity(f"fp32 |v|~1e5 K={dk}", o, o_ref, s, s_ref)
+
+
+def test_fp32_inputs_beyond_fp16_range_state_slots():
+    """The same through a slot pool (chunk_fwd_slots): slots gathered, the
+    prefill kept in range, final states written back; other slots untouched."""
+    lengths = [300, 0, 129]
+    q, k, v, g, beta, _ = generate(1, sum(lengths), 2, 4, 64, 64, torch.float32, 0.0, seed=37)
+    v = v * 1e5
+    pool = torch.randn(6, 4, 64, 64) * 1e4
+    slots = torch.tensor([4, 1, -1], dtype=torch.int32)
+    has_init = torch.tensor([1, 1, 0], dtype=torch.uint8)
+    cu = torch.tensor([0, 300, 300, 429], dtype=torch.int32)
+    dpool = pool.to(DEV)
+    with torch.no_grad():
+        o = gd.chunk_fwd_slots(*(x.to(DEV) for x in (q, k, v, g, beta)), 0.125, dpool, slots.to(DEV), cu.to(DEV),
+                               has_init.to(DEV))
+    torch.cuda.synchronize()
+    init = torch.stack([pool[4], pool[1], torch.zeros(4, 64, 64)])
+    o_ref, s_ref = oracle(q, k, v, g, beta, 0.125, init, cu_seqlens=cu)
+    assert_parity("fp32 |v|~1e5 slots", o, o_ref, dpool.cpu()[[4, 1]], s_ref[:2])
+    assert torch.equal(dpool.cpu()[[0, 2, 3, 5]], pool[[0, 2, 3, 5]])
+
+
+@pytest.mark.parametrize("g_scale", [0.01, 0.0])
+def test_low_decay_full_length(g_scale):
+    """g x 0.01 and g = 0 over 32,768 tokens (Qwen3-Next head width): the
+    state keeps what it learns, so its rounding errors accumulate over all
+    512 chunks."""
+    q, k, v, g, beta, h0 = generate(1, 32768, 1, 2, 128, 128, torch.bfloat16, 0.02, seed=34, g_scale=g_scale)
+    o, s = run(q, k, v, g, beta, 128 ** -0.5, h0)
+    o_ref, s_ref = oracle(q, k, v, g, beta, 128 ** -0.5, h0)
+    assert_parity(f"low decay g x {g_scale:g} T=32768", o, o_ref, s, s_ref)
+
+
+def test_streamed_low_decay_segments():
+    """16 segments of 4,096 tokens with g x 0.01, each segment's final state
+    the next one's initial state (the million-token workload's scheme at a
+    checkable size), compared with the oracle after every segment."""
+    q, k, v, g, beta, h0 = generate(1, 16 * 4096, 1, 2, 128, 128, torch.bfloat16, 0.02, seed=35, g_scale=0.01)
+    state, ref_state = h0.clone(), h0.clone()
+    errs = []
+    for seg in range(16):
+        sl = slice(seg * 4096, (seg + 1) * 4096)
+        o, state = run(q[:, sl], k[:, sl], v[:, sl], g[:, sl], beta[:, sl], 128 ** -0.5, state)
+        o_ref, ref_state = oracle(q[:, sl], k[:, sl], v[:, sl], g[:, sl], beta[:, sl], 128 ** -0.5, ref_state)
+        ref_state = torch.from_numpy(ref_state)
+        errs.append((rel_err(o, o_ref), rel_err(state, ref_state.numpy())))
+        state = state.cpu()
+    print("[streamed low decay] segment errors (o, S): " + ", ".join(f"{eo:.2e}/{es:.2e}" for eo, es in errs),
+          flush=True)
+    for seg, (eo, es) in enumerate(errs):
+        assert eo <= 2e-2 and es <= 1e-3, f"segment {seg}: o {eo:.3e}, S {es:.3e}"
