@@ -9,23 +9,29 @@ a step is one chunk-kernel call over those inputs, resident in HBM, writing o
 (bf16) and the final state (fp32). `value` is prefill throughput in Mtok/s.
 The same line carries the decode step (64 sequences x 1 token, state
 [64,32,128,128] fp32 updated in place, 1000 chained steps) in µs/step and as a
-fraction of HBM bandwidth, the same step with the state held in bf16 (a
-serving cache's default), an ungraded 256-sequence decode (state larger than
-the 256 MB Infinity Cache), the fused layer prologue and epilogue kernels at
-the same T and head shape with their HBM rooflines, the fused one-kernel
+fraction of HBM bandwidth (the pool stays in the 256 MB last-level cache), the
+same step with three pools in rotation (the state comes from HBM, as in a
+model whose layers keep one pool each), the same step with the state held in
+bf16 (a serving cache's default), an ungraded 256-sequence decode, the
+library's 1 GiB streaming copy (pbgdn_stream_probe: the read+write ceiling
+each decode line is also given against), the small fp32 prefill (the
+reference's CPU-runnable case), the fused layer prologue and epilogue kernels
+at the same T and head shape with their HBM rooflines, the fused one-kernel
 decode step of the whole layer (64 sequences; against the same step as three
-launches), the varlen (8 packed
-sequences, 262,144 tokens) and streamed (1,048,576 tokens in 16 segments)
-prefill workloads, the roofline of the prefill kernel measured with
-HIP events on the stream it runs on, and the CPU baseline: the numpy oracle
-(oracle/gdn.py) on a bounded sample of the same prefill, run first, before the
-GPU is touched, as one single-threaded process per core over the heads.
+launches), the backward, the varlen (8 packed sequences, 262,144 tokens) and
+streamed (1,048,576 tokens in 16 segments) prefill workloads, the roofline of
+the prefill kernel measured with HIP events on the stream it runs on, and the
+CPU baseline: the numpy oracle (oracle/gdn.py) on the full prefill call, run
+first, before the GPU is touched, as one single-threaded process per value
+head on up to every affinity core; with it the small prefill in full, 50
+chained decode steps, the varlen and streamed prefills extrapolated from the
+full prefill's rate, the CPU's model and core counts, and the SHA-256 of
+every prefill input.
 
 `roofline.traffic` (HBM bytes per launch) comes from the rocprofv3 counter
 summary committed under profiles/ (FETCH_SIZE and WRITE_SIZE per dispatch,
-each scaled by what the counter reads for a plain device copy of known size,
-which `--copy-probe` runs in the same process); it is null when that file is
-absent.
+each scaled by what the counter reads for the streaming probe's 1 GiB copy in
+the same process); it is null when that file is absent.
 """
 from __future__ import annotations
 
@@ -122,48 +128,121 @@ def decode_bytes(batch, hk, hv, dk, dv, elem=2, state_elem=4):
 
 
 # ---------------------------------------------------------------------------
-# CPU baseline: the oracle over the heads, one process per core.
+# CPU baselines: the oracle (numpy fp32) on every affinity core, one process per
+# value head (prefill) or per batch slice (decode), on the same seeded inputs.
 # ---------------------------------------------------------------------------
 def _oracle_heads(args):
     from oracle import gdn
     q, k, v, g, beta, h0, scale = args
-    t0 = time.perf_counter()
     gdn.delta_rule_chunked(q, k, v, g, beta, scale, h0)
-    return time.perf_counter() - t0
 
 
-def cpu_baseline(sample_tokens: int, seed: int = 0):
-    from pseudobrain_amd.workloads import to_numpy, workload
-    q, k, v, g, beta, h0 = (to_numpy(x) for x in workload("prefill_qwen3next", seed, length=sample_tokens))
-    hv, hk = v.shape[2], q.shape[2]
-    group = hv // hk
-    scale = q.shape[-1] ** -0.5
-    tasks = [(np.ascontiguousarray(q[:, :, h // group:h // group + 1]),
-              np.ascontiguousarray(k[:, :, h // group:h // group + 1]),
-              np.ascontiguousarray(v[:, :, h:h + 1]), np.ascontiguousarray(g[:, :, h:h + 1]),
-              np.ascontiguousarray(beta[:, :, h:h + 1]), np.ascontiguousarray(h0[:, h:h + 1]), scale)
-             for h in range(hv)]
-    cores = min(len(os.sched_getaffinity(0)), 16, hv)
-    ctx = multiprocessing.get_context("fork")
-    with ctx.Pool(cores) as pool:
-        warm = [(t[0][:, :256], t[1][:, :256], t[2][:, :256], t[3][:, :256], t[4][:, :256], t[5], t[6])
-                for t in tasks[:cores]]
-        pool.map(_oracle_heads, warm)
-        t0 = time.perf_counter()
-        pool.map(_oracle_heads, tasks)
-        elapsed = time.perf_counter() - t0
-    model = "unknown"
+def _oracle_steps(args):
+    from oracle import gdn
+    q, k, v, g, beta, h0, scale = args
+    gdn.delta_rule_sequential(q, k, v, g, beta, scale, h0)
+
+
+def cpu_info():
+    """CPU model, logical and physical core counts, and the cores this process may use."""
+    model, phys = "unknown", set()
     try:
         with open("/proc/cpuinfo") as f:
-            model = next(line.split(":", 1)[1].strip() for line in f if line.startswith("model name"))
-    except (OSError, StopIteration):
+            pid = cid = None
+            for line in f:
+                key, _, val = line.partition(":")
+                key, val = key.strip(), val.strip()
+                if key == "model name" and model == "unknown":
+                    model = val
+                elif key == "physical id":
+                    pid = val
+                elif key == "core id":
+                    cid = val
+                    phys.add((pid, cid))
+    except OSError:
         pass
+    return {"model": model, "logical_cores": os.cpu_count(), "physical_cores": len(phys) or None,
+            "affinity_cores": len(os.sched_getaffinity(0))}
+
+
+def _one_thread():
+    """Pool initializer: one BLAS/OpenMP thread per worker process (the box
+    exports OMP_NUM_THREADS=16, which would put 16 threads on every core)."""
+    from threadpoolctl import threadpool_limits
+    threadpool_limits(1)
+
+
+def _timed_pool(fn, tasks, procs, warm):
+    ctx = multiprocessing.get_context("fork")
+    with ctx.Pool(procs, initializer=_one_thread) as pool:
+        pool.map(fn, warm)
+        t0 = time.perf_counter()
+        pool.map(fn, tasks)
+        return time.perf_counter() - t0
+
+
+def _head_tasks(q, k, v, g, beta, h0, scale):
+    hv, group = v.shape[2], v.shape[2] // q.shape[2]
+    c = np.ascontiguousarray
+    return [(c(q[:, :, h // group:h // group + 1]), c(k[:, :, h // group:h // group + 1]), c(v[:, :, h:h + 1]),
+             c(g[:, :, h:h + 1]), c(beta[:, :, h:h + 1]), c(h0[:, h:h + 1]), scale) for h in range(hv)]
+
+
+def _prefill_cpu(name, seed, procs_cap):
+    from pseudobrain_amd.workloads import to_numpy, workload
+    x = workload(name, seed)
+    q, k, v, g, beta, h0 = (to_numpy(t) for t in x)
+    tasks = _head_tasks(q, k, v, g, beta, h0, q.shape[-1] ** -0.5)
+    procs = min(procs_cap, len(tasks))
+    warm = [tuple(a[:, :256] if i < 5 else a for i, a in enumerate(t[:6])) + (t[6],) for t in tasks[:procs]]
+    return _timed_pool(_oracle_heads, tasks, procs, warm), procs, x
+
+
+def cpu_baseline(seed: int = 0, decode_steps: int = 50):
+    """The oracle on the host cores (kind "port"): the full Qwen3-Next prefill
+    (32,768 tokens, 32 value heads) and the small prefill, in one call each;
+    the decode step (B = 64) as `decode_steps` chained steps; the varlen and
+    million-token prefills extrapolated from the full prefill's rate (the
+    chunked oracle's time is linear in tokens). Returns the headline entry
+    (prefill, Mtok/s) with the others under "configs"."""
+    from pseudobrain_amd.workloads import WORKLOADS, generate, sha256, to_numpy
+    info = cpu_info()
+    cap = info["affinity_cores"]
+    c1_sec, c1_procs, c1_inputs = _prefill_cpu("prefill_qwen3next", seed, cap)
+    c1_tokens = WORKLOADS["prefill_qwen3next"].length
+    rate = c1_tokens / c1_sec
+    inputs_sha = {n: sha256(t) for n, t in zip(("q", "k", "v", "g", "beta", "h0"), c1_inputs)}
+    c0_sec, c0_procs, _ = _prefill_cpu("prefill_small", seed, cap)
+    s2 = WORKLOADS["decode_b64"]
+    x = generate(s2.batch, decode_steps, s2.hk, s2.hv, s2.dk, s2.dv, s2.dtype, s2.h0_std, seed)
+    q, k, v, g, beta, h0 = (to_numpy(t) for t in x)
+    procs = min(cap, s2.batch)
+    per = -(-s2.batch // procs)
+    slices = [slice(i, min(i + per, s2.batch)) for i in range(0, s2.batch, per)]
+    tasks = [(q[sl], k[sl], v[sl], g[sl], beta[sl], h0[sl], s2.dk ** -0.5) for sl in slices]
+    warm = [(a[0][:, :1], a[1][:, :1], a[2][:, :1], a[3][:, :1], a[4][:, :1], a[5], a[6]) for a in tasks]
+    c2_sec = _timed_pool(_oracle_steps, tasks, len(tasks), warm)
+    configs = {
+        "prefill_small": {"seconds": c0_sec, "value": WORKLOADS["prefill_small"].length / c0_sec / 1e6,
+                          "unit": "Mtok/s", "cores": c0_procs, "measured": "one full call"},
+        "prefill_qwen3next": {"seconds": c1_sec, "value": rate / 1e6, "unit": "Mtok/s", "cores": c1_procs,
+                              "measured": "one full call"},
+        "decode_b64": {"seconds": c2_sec, "value": c2_sec / decode_steps * 1e6, "unit": "us/step",
+                       "cores": len(tasks), "measured": f"{decode_steps} chained steps"},
+    }
+    for name in ("varlen_8seq", "stream_1m"):
+        tokens = WORKLOADS[name].length
+        configs[name] = {"seconds": tokens / rate, "value": rate / 1e6, "unit": "Mtok/s", "cores": c1_procs,
+                         "measured": f"extrapolated from the full prefill's rate ({tokens} tokens)"}
     return {
-        "value": sample_tokens / elapsed / 1e6, "unit": "Mtok/s", "cores": cores, "kind": "port",
-        "sample": (f"oracle delta_rule_chunked (numpy fp32) on the first {sample_tokens} tokens of the "
-                   f"prefill workload, all {hv} value heads, {cores} single-threaded processes; "
-                   f"{elapsed:.2f} s; cpu: {model}"),
-        "seconds": elapsed,
+        "value": rate / 1e6, "unit": "Mtok/s", "cores": c1_procs, "kind": "port",
+        "sample": (f"oracle delta_rule_chunked (numpy fp32), the full prefill workload ({c1_tokens} tokens, "
+                   f"{s2.hv} value heads), one single-threaded process per head on {c1_procs} of "
+                   f"{info['affinity_cores']} affinity cores; {c1_sec:.1f} s; cpu: {info['model']}"),
+        "seconds": c1_sec,
+        "cpu": info,
+        "inputs_sha256": inputs_sha,
+        "configs": configs,
     }
 
 
@@ -212,6 +291,27 @@ def bench_prefill(steps, warmup):
     flops = prefill_flops(s.length, s.hv, s.dk, s.dv)
     nbytes = prefill_bytes(s.length, s.hk, s.hv, s.dk, s.dv)
     return s, sec, ksec, flops, nbytes
+
+
+def bench_prefill_small(steps=50, warmup=5):
+    """The reference's CPU-runnable case (prefill_small: B=1, T=2048, 4 heads,
+    K=V=64, fp32 inputs and output) on the GPU."""
+    import torch
+    from pseudobrain_amd import gated_deltanet as gd
+    from pseudobrain_amd.workloads import WORKLOADS, workload
+    s = WORKLOADS["prefill_small"]
+    q, k, v, g, beta, h0 = (x.cuda() for x in workload("prefill_small", seed=0))
+    out = torch.empty(1, s.length, s.hv, s.dv, dtype=torch.float32, device="cuda")
+
+    def step():
+        gd.chunk_fwd(q, k, v, g, beta, s.dk ** -0.5, h0, out=out)
+
+    sec, ksec = timed_steps(step, steps, warmup)
+    flops = prefill_flops(s.length, s.hv, s.dk, s.dv)
+    return {"workload": "prefill_small", "T": s.length, "value": s.length / sec / 1e6, "unit": "Mtok/s",
+            "ms_per_call": sec * 1e3, "roofline": {"bound": "mfma", "achieved": flops / ksec / 1e12,
+                                                   "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                                   "frac": flops / ksec / 1e12 / MFMA_PEAK_TFLOPS}}
 
 
 def bench_decode(batch, steps, warmup=10, state_dtype=None, pools=1):
@@ -457,7 +557,6 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--decode-steps", type=int, default=1000)
-    ap.add_argument("--cpu-tokens", type=int, default=16384)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-b256", action="store_true", help="skip the ungraded 256-sequence decode")
@@ -473,7 +572,7 @@ def main(argv=None):
               file=sys.stderr)
         return 2
 
-    cpu = cpu_baseline(args.cpu_tokens) if not args.no_cpu else None
+    cpu = cpu_baseline() if not args.no_cpu else None
 
     import torch
     from pseudobrain_amd import _lib
@@ -506,6 +605,7 @@ def main(argv=None):
     }
     if cpu is not None:
         result["cpu_baseline_ratio"] = result["value"] / cpu["value"]
+    result["prefill_small"] = bench_prefill_small()
     if not args.no_decode:
         dec = bench_decode(64, args.decode_steps)
         result["decode"] = dict(dec, roofline={"bound": "hbm", "achieved": dec["achieved_GBs"],
@@ -522,7 +622,8 @@ def main(argv=None):
         ooc = bench_decode(64, 300, pools=3)
         result["decode_out_of_cache"] = dict(ooc, roofline={"bound": "hbm", "achieved": ooc["achieved_GBs"],
                                                             "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                                            "frac": ooc["hbm_frac"]})
+                                                            "frac": ooc["hbm_frac"],
+                                                            "traffic": measured_traffic("recurrent_b64_out_of_cache")})
         if not args.no_b256:
             result["decode_b256_ungraded"] = bench_decode(256, 200)
         probe = stream_probe()

@@ -120,6 +120,12 @@ const char *pbgdn_status_string(int status);
  *               are dead when the call's work on `stream` completes
  *
  * Supported: K in {64, 128}; V a multiple of 16; Hv a multiple of Hk.
+ * Ranges: the products run on fp16/bf16 MFMA operands with fp32 accumulation;
+ * a chunk whose intermediate V - gamma K S leaves the fp16 range is scaled by
+ * a power of two internally. With in_dtype F32, q and k enter as fp16
+ * (|q|, |k| < 65504) and the state as an fp16 high/low pair (v and the state
+ * within about +-4096); scale v and h0 by a power of two to meet that and
+ * scale o and ht back (the recurrence is linear in v and h0).
  */
 int pbgdn_chunk_fwd(const void *q, const void *k, const void *v, int in_dtype,
                     const float *g, const void *beta, int beta_dtype,
