@@ -464,6 +464,46 @@ def bench_layer(length, steps, warmup=3):
     return out
 
 
+def bench_layer_core(steps, warmup=3, rounds=3):
+    """The prefill layer core (the operator, then RMSNorm x o_norm x SiLU(gate))
+    over 32,768 tokens of the Qwen3-Next head shape, bf16 in, fp32 hs out: one
+    call (chunk_layer_fwd) against the operator (chunk_fwd) followed by the
+    epilogue kernel (layer_epilogue). At 8 x 4,096 the wide scan applies the
+    epilogue itself; at 1 x 32,768 (the narrow scan) both forms are two passes.
+    The forms alternate for `rounds` rounds; each figure is its median."""
+    import torch
+    from pseudobrain_amd import gated_deltanet as gd
+    from pseudobrain_amd.layer import chunk_layer_fwd, layer_epilogue
+    from pseudobrain_amd.workloads import cu_seqlens_of, generate
+    out = {}
+    gen = torch.Generator().manual_seed(3)
+    z = torch.randn(1, 32768, 2 * 32 * 128, generator=gen).to(torch.bfloat16).cuda()
+    gate = z[..., 32 * 128:]
+    o_norm = (torch.rand(128, generator=gen) + 0.5).cuda()
+    scale = 128 ** -0.5
+    for nseq in (8, 1):
+        q, k, v, g, beta, h0 = generate(1, 32768, 16, 32, 128, 128, torch.bfloat16, 0.02, seed=0, nstates=nseq,
+                                        device="cuda")
+        cu = cu_seqlens_of([32768 // nseq] * nseq).to("cuda")
+
+        def fused():
+            chunk_layer_fwd(q, k, v, g, beta, scale, h0, gate, o_norm, 1e-5, cu)
+
+        def two_pass():
+            o, _ = gd.chunk_fwd(q, k, v, g, beta, scale, h0, cu)
+            layer_epilogue(o, gate, o_norm, 1e-5)
+
+        kf, kt = [], []
+        with torch.no_grad():
+            for _ in range(rounds):
+                kf.append(timed_steps(fused, steps, warmup)[1])
+                kt.append(timed_steps(two_pass, steps, warmup)[1])
+        kf, kt = statistics.median(kf), statistics.median(kt)
+        out[f"{nseq}x{32768 // nseq}"] = {"one_call_ms": kf * 1e3, "operator_then_epilogue_ms": kt * 1e3,
+                                          "Mtok_s_one_call": 32768 / kf / 1e6}
+    return {"layer_core_ungraded": out}
+
+
 def bench_decode_layer(batch, steps, warmup=10, state_dtype=None):
     """The fused decode step of the whole layer (pbgdn_decode_layer_fwd) at the
     Qwen3-Next layer shape for `batch` sequences of one token, state and conv
@@ -633,6 +673,7 @@ def main(argv=None):
                 result[key]["vs_stream_probe"] = result[key]["achieved_GBs"] / probe["GBs"]
     if not args.no_layer:
         result.update(bench_layer(shape.length, 20))
+        result.update(bench_layer_core(10))
         if not args.no_decode:
             result["decode_layer_b64"] = bench_decode_layer(64, 200)
             result["decode_layer_b64"]["roofline"]["traffic"] = measured_traffic("decode_layer_b64")

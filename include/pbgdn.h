@@ -58,7 +58,7 @@
 extern "C" {
 #endif
 
-#define PBGDN_ABI_VERSION 9
+#define PBGDN_ABI_VERSION 10
 
 /* element types */
 #define PBGDN_F32 0
@@ -135,6 +135,42 @@ int pbgdn_chunk_fwd(const void *q, const void *k, const void *v, int in_dtype,
                     void *o, int out_dtype, int B, int T, int Hk, int Hv,
                     int K, int V, float scale, int chunk, void *workspace,
                     size_t workspace_bytes, void *stream);
+
+/*
+ * The layer core of a prefill: pbgdn_chunk_fwd followed by the epilogue of
+ * pbgdn_epilogue_fwd, hs = o rsqrt(mean(o^2) + eps) o_norm SiLU(gate) per
+ * (token, value head). Reference: GatedDeltaNetLayer.forward,
+ * gated_deltanet.py:437-441 (gated_delta_rule, then the norm and gate).
+ *
+ *   q .. num_seqs, B .. stream   as pbgdn_chunk_fwd
+ *   gate        [B, T, gate_stride] rows, value head h at columns h V .. h V + V - 1
+ *               (a column slice of the projection), dtype gate_dtype;
+ *               gate_stride >= Hv V, a multiple of 8
+ *   o_norm      [V] float32; eps >= 0
+ *   hs          [B, T, Hv V] dtype hs_dtype, written
+ *   o           [B, T, Hv, V] in in_dtype: the operator's output when the
+ *               epilogue runs as a pass of its own (written then), else unused
+ *
+ * When the wide scan takes the call (in_dtype BF16 or F16, K = V = 128, N x
+ * Hv at least half the device's CUs, gate_dtype == in_dtype, hs_dtype F32 or
+ * in_dtype), the scan applies the epilogue to each chunk's output in
+ * registers (fp32, before any rounding) and writes hs: o is not touched and
+ * the epilogue pass, with its read of o, is saved. Otherwise o is written in
+ * in_dtype and the epilogue runs after it on the same stream. V must be 64 or
+ * 128 (the epilogue's widths).
+ */
+int pbgdn_chunk_layer_fwd(const void *q, const void *k, const void *v,
+                          int in_dtype, const float *g, const void *beta,
+                          int beta_dtype, const void *h0, void *ht,
+                          int state_dtype, const int32_t *state_idx,
+                          const uint8_t *has_initial_state, int num_states,
+                          const int32_t *cu_seqlens, int num_seqs,
+                          const void *gate, long gate_stride, int gate_dtype,
+                          const float *o_norm, float eps, void *hs,
+                          int hs_dtype, void *o, int B, int T, int Hk, int Hv,
+                          int K, int V, float scale, int chunk,
+                          void *workspace, size_t workspace_bytes,
+                          void *stream);
 
 /*
  * Bytes of workspace pbgdn_chunk_fwd needs for a call with these sizes

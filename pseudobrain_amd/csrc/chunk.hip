@@ -56,7 +56,7 @@ int run_chunk(const ChunkParams &p, long records, int out_dtype, hipStream_t s) 
   const int st = launch_prep<K, TIn>(p, records, s);
   if (st != PBGDN_OK) return st;
   if constexpr (K == 128 && sizeof(TIn) == 2) {
-    if (out_dtype != PBGDN_F32 && wide_eligible<K, TIn>(p)) return launch_wide<K, TIn, TIn>(p, s);
+    if (out_dtype != PBGDN_F32 && wide_eligible<K, TIn>(p)) return launch_wide<K, TIn, TIn, false>(p, s);
   }
   if (out_dtype == PBGDN_F32) return launch_scan<K, TIn, float>(p, s);
   return launch_scan<K, TIn, TIn>(p, s);  // out_dtype == in_dtype, checked by the caller
@@ -70,6 +70,15 @@ int dispatch_in(const ChunkParams &p, long records, int in_dtype, int out_dtype,
     case PBGDN_F32: return run_chunk<K, float>(p, records, out_dtype, s);
     default: return PBGDN_ERR_INVALID_ARGUMENT;
   }
+}
+
+// The prefill with the layer epilogue in the wide scan (p.o is hs).
+template <typename TIn>
+int run_chunk_epilogue(const ChunkParams &p, long records, int hs_dtype, hipStream_t s) {
+  const int st = launch_prep<128, TIn>(p, records, s);
+  if (st != PBGDN_OK) return st;
+  if (hs_dtype == PBGDN_F32) return launch_wide<128, TIn, float, true>(p, s);
+  return launch_wide<128, TIn, TIn, true>(p, s);  // hs_dtype == in_dtype, checked by the caller
 }
 
 bool valid_dtype(int d) { return d == PBGDN_F32 || d == PBGDN_BF16 || d == PBGDN_F16; }
@@ -116,14 +125,17 @@ extern "C" size_t pbgdn_chunk_workspace_size(int B, int T, int Hv, int num_seqs)
   return static_cast<size_t>(records) * Hv * pbgdn::REC_BYTES;
 }
 
-extern "C" int pbgdn_chunk_fwd(const void *q, const void *k, const void *v, int in_dtype, const float *g,
-                               const void *beta, int beta_dtype, const void *h0, void *ht, int state_dtype,
-                               const int32_t *state_idx, const uint8_t *has_initial_state, int num_states,
-                               const int32_t *cu_seqlens, int num_seqs, void *o, int out_dtype, int B, int T,
-                               int Hk, int Hv, int K, int V, float scale, int chunk, void *workspace,
-                               size_t workspace_bytes, void *stream) {
-  using pbgdn::aligned16;
-  using pbgdn::valid_dtype;
+namespace pbgdn {
+namespace {
+
+// Argument checks of pbgdn_chunk_fwd and its launch parameters: PBGDN_OK with
+// *empty set when there is nothing to launch.
+int chunk_setup(const void *q, const void *k, const void *v, int in_dtype, const float *g, const void *beta,
+                int beta_dtype, const void *h0, void *ht, int state_dtype, const int32_t *state_idx,
+                const uint8_t *has_initial_state, int num_states, const int32_t *cu_seqlens, int num_seqs, void *o,
+                int out_dtype, int B, int T, int Hk, int Hv, int K, int V, float scale, int chunk, void *workspace,
+                size_t workspace_bytes, ChunkParams &p, long &records, bool &empty) {
+  empty = false;
   if (B < 0 || T < 0 || Hk <= 0 || Hv <= 0 || K <= 0 || V <= 0 || Hv % Hk != 0 || num_seqs < 0) {
     return PBGDN_ERR_INVALID_ARGUMENT;
   }
@@ -141,7 +153,10 @@ extern "C" int pbgdn_chunk_fwd(const void *q, const void *k, const void *v, int 
       static_cast<long>(pbgdn::CH) * Hk * K * 4 > 0x7fffffffL) {
     return PBGDN_ERR_UNSUPPORTED;
   }
-  if (num_seqs == 0) return PBGDN_OK;
+  if (num_seqs == 0) {
+    empty = true;
+    return PBGDN_OK;
+  }
   if (T > 0 && (!q || !k || !v || !g || !beta || !o)) return PBGDN_ERR_INVALID_ARGUMENT;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v)) return PBGDN_ERR_INVALID_ARGUMENT;
   if (!workspace || !aligned16(workspace) ||
@@ -150,23 +165,96 @@ extern "C" int pbgdn_chunk_fwd(const void *q, const void *k, const void *v, int 
   }
   const long total = static_cast<long>(V / pbgdn::VT) * Hv * num_seqs;
   if (total > 0x7fffffffL) return PBGDN_ERR_UNSUPPORTED;
-  const long records = pbgdn::chunk_records(static_cast<long>(B) * T, num_seqs);
+  records = chunk_records(static_cast<long>(B) * T, num_seqs);
   // The scan's sequence groups (scan_groups): a chained workgroup pays
   // ~1 µs per sequence boundary instead of a pipeline fill and drain, and the
   // unchained kernel's step is ~10% shorter.
-  pbgdn::DeviceShape shape;
-  if (!pbgdn::device_shape(shape)) return PBGDN_ERR_LAUNCH;
-  const int pairs = (V / pbgdn::VT) * Hv;
-  const int groups = pbgdn::scan_groups(static_cast<long>(B) * T, num_seqs, pairs, shape.cus);
-  pbgdn::ChunkParams p{q, k, v, g, beta, beta_dtype, h0, ht, state_dtype, state_idx, has_initial_state,
-                       num_states, cu_seqlens, o, static_cast<unsigned char *>(workspace), T, Hk, Hv, V,
-                       num_seqs, groups, scale, shape.cus, shape.xcds};
+  DeviceShape shape;
+  if (!device_shape(shape)) return PBGDN_ERR_LAUNCH;
+  const int pairs = (V / VT) * Hv;
+  const int groups = scan_groups(static_cast<long>(B) * T, num_seqs, pairs, shape.cus);
+  p = ChunkParams{q, k, v, g, beta, beta_dtype, h0, ht, state_dtype, state_idx, has_initial_state,
+                  num_states, cu_seqlens, o, static_cast<unsigned char *>(workspace), T, Hk, Hv, V,
+                  num_seqs, groups, scale, shape.cus, shape.xcds, nullptr, 0, nullptr, 0.f};
+  return PBGDN_OK;
+}
+
+}  // namespace
+}  // namespace pbgdn
+
+extern "C" int pbgdn_chunk_fwd(const void *q, const void *k, const void *v, int in_dtype, const float *g,
+                               const void *beta, int beta_dtype, const void *h0, void *ht, int state_dtype,
+                               const int32_t *state_idx, const uint8_t *has_initial_state, int num_states,
+                               const int32_t *cu_seqlens, int num_seqs, void *o, int out_dtype, int B, int T,
+                               int Hk, int Hv, int K, int V, float scale, int chunk, void *workspace,
+                               size_t workspace_bytes, void *stream) {
+  pbgdn::ChunkParams p;
+  long records = 0;
+  bool empty = false;
+  const int st = pbgdn::chunk_setup(q, k, v, in_dtype, g, beta, beta_dtype, h0, ht, state_dtype, state_idx,
+                                    has_initial_state, num_states, cu_seqlens, num_seqs, o, out_dtype, B, T, Hk,
+                                    Hv, K, V, scale, chunk, workspace, workspace_bytes, p, records, empty);
+  if (st != PBGDN_OK || empty) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (K) {
     case 64: return pbgdn::dispatch_in<64>(p, records, in_dtype, out_dtype, s);
     case 128: return pbgdn::dispatch_in<128>(p, records, in_dtype, out_dtype, s);
     default: return PBGDN_ERR_UNSUPPORTED;
   }
+}
+
+// The prefill followed by the layer epilogue. Where the wide scan takes the
+// call (16-bit inputs, K = V = 128, enough workgroups) and the gate is in the
+// inputs' dtype and hs in it or float32, the scan applies the epilogue to each
+// chunk's O and writes hs; o is not touched. Otherwise o receives the
+// operator's output (in the inputs' dtype) and pbgdn_epilogue_fwd runs after.
+extern "C" int pbgdn_chunk_layer_fwd(const void *q, const void *k, const void *v, int in_dtype, const float *g,
+                                     const void *beta, int beta_dtype, const void *h0, void *ht, int state_dtype,
+                                     const int32_t *state_idx, const uint8_t *has_initial_state, int num_states,
+                                     const int32_t *cu_seqlens, int num_seqs, const void *gate, long gate_stride,
+                                     int gate_dtype, const float *o_norm, float eps, void *hs, int hs_dtype,
+                                     void *o, int B, int T, int Hk, int Hv, int K, int V, float scale, int chunk,
+                                     void *workspace, size_t workspace_bytes, void *stream) {
+  using pbgdn::aligned16;
+  using pbgdn::valid_dtype;
+  if (!valid_dtype(gate_dtype) || !valid_dtype(hs_dtype) || !(eps >= 0.f)) return PBGDN_ERR_INVALID_ARGUMENT;
+  if (Hv > 0 && V > 0 && (gate_stride < static_cast<long>(Hv) * V || gate_stride % 8 != 0)) {
+    return PBGDN_ERR_INVALID_ARGUMENT;
+  }
+  if (!(V == 64 || V == 128)) return PBGDN_ERR_UNSUPPORTED;  // the epilogue's value widths
+  if (B > 0 && T > 0 && (!gate || !o_norm || !hs || !aligned16(gate) || !aligned16(hs))) {
+    return PBGDN_ERR_INVALID_ARGUMENT;
+  }
+  const bool fusable = K == 128 && V == 128 && (in_dtype == PBGDN_BF16 || in_dtype == PBGDN_F16) &&
+                       gate_dtype == in_dtype && (hs_dtype == PBGDN_F32 || hs_dtype == in_dtype) &&
+                       static_cast<long>(pbgdn::CH) * gate_stride * 2 <= 0x7fffffffL;
+  pbgdn::ChunkParams p;
+  long records = 0;
+  bool empty = false;
+  if (fusable) {
+    const int st = pbgdn::chunk_setup(q, k, v, in_dtype, g, beta, beta_dtype, h0, ht, state_dtype, state_idx,
+                                      has_initial_state, num_states, cu_seqlens, num_seqs, hs, in_dtype, B, T, Hk,
+                                      Hv, K, V, scale, chunk, workspace, workspace_bytes, p, records, empty);
+    if (st != PBGDN_OK || empty) return st;
+    if (in_dtype == PBGDN_BF16 ? pbgdn::wide_eligible<128, pbgdn::u16>(p)
+                               : pbgdn::wide_eligible<128, pbgdn::half_t>(p)) {
+      p.gate = gate;
+      p.gate_stride = gate_stride;
+      p.o_norm = o_norm;
+      p.eps = eps;
+      hipStream_t s = static_cast<hipStream_t>(stream);
+      return in_dtype == PBGDN_BF16 ? pbgdn::run_chunk_epilogue<pbgdn::u16>(p, records, hs_dtype, s)
+                                    : pbgdn::run_chunk_epilogue<pbgdn::half_t>(p, records, hs_dtype, s);
+    }
+  }
+  // Two passes: o in the inputs' dtype, then the epilogue.
+  if (B > 0 && T > 0 && (!o || !aligned16(o))) return PBGDN_ERR_INVALID_ARGUMENT;
+  const int st = pbgdn_chunk_fwd(q, k, v, in_dtype, g, beta, beta_dtype, h0, ht, state_dtype, state_idx,
+                                 has_initial_state, num_states, cu_seqlens, num_seqs, o, in_dtype, B, T, Hk, Hv, K,
+                                 V, scale, chunk, workspace, workspace_bytes, stream);
+  if (st != PBGDN_OK) return st;
+  return pbgdn_epilogue_fwd(o, in_dtype, gate, gate_stride, gate_dtype, o_norm, eps, hs, hs_dtype, B, T, Hv, V,
+                            stream);
 }
 
 // The prefill of pbgdn_chunk_fwd with the workspace taken from this device's

@@ -95,6 +95,12 @@ struct ChunkParams {
   int seq_groups;  // the scan's sequence groups (a workgroup runs one group's sequences back to back)
   float scale;
   int cus, xcds;   // the device's compute units and XCDs (device.hpp)
+  // The layer's epilogue, when the scan applies it (the wide scan at V = 128):
+  // o is then hs = RMSNorm(o) o_norm SiLU(gate) per (token, value head).
+  const void *gate;   // [T, gate_stride] in the inputs' dtype, head h at columns h V ..
+  long gate_stride;   // elements per token row
+  const float *o_norm;
+  float eps;
 };
 
 // Sequence s (wave-uniform): first token and end. cu_seqlens is read through
@@ -372,7 +378,7 @@ template <int K, typename TIn>
 int launch_prep(const ChunkParams &p, long records, hipStream_t stream);
 template <int K, typename TIn, typename TOut>
 int launch_scan(const ChunkParams &p, hipStream_t stream);
-template <int K, typename TIn, typename TOut>
+template <int K, typename TIn, typename TOut, bool EPI>
 int launch_wide(const ChunkParams &p, hipStream_t stream);
 
 }  // namespace pbgdn

@@ -57,6 +57,7 @@
 //   chunk n+1, barrier; loads of chunk n+2 are issued (into buffers chunk n-1,
 //   or for Q and V chunk n, used); C: the state update; O of chunk n, stored.
 #include "chunk.hpp"
+#include "layer_math.hpp"
 
 namespace pbgdn {
 namespace {
@@ -77,7 +78,9 @@ struct WideLayout {
   static constexpr int Q_OFF = K_OFF + 3 * MAT;              // [2] Q
   static constexpr int R_OFF = Q_OFF + 2 * MAT;              // [3] record
   static constexpr int V_OFF = R_OFF + 3 * REC_BYTES;        // [2] V
-  static constexpr int BYTES = V_OFF + 2 * VMAT;
+  static constexpr int P_OFF = V_OFF + 2 * VMAT;             // epilogue: [CH tokens][WT waves] sums of squares
+  static constexpr int N_OFF = P_OFF + CH * WT * 4;          // epilogue: o_norm of the 128 columns
+  static constexpr int BYTES = N_OFF + WCOLS * 4;
   __device__ static constexpr int kmat(int b3) { return K_OFF + b3 * MAT; }
   __device__ static constexpr int qmat(int b2) { return Q_OFF + b2 * MAT; }
   __device__ static constexpr int rec(int b3) { return R_OFF + b3 * REC_BYTES; }
@@ -89,7 +92,50 @@ struct WideLayout {
 __host__ __device__ constexpr int swz(int r) { return 4 * (r & 3) + ((r >> 2) & 3); }
 __host__ __device__ constexpr int vswz(int r) { return 2 * (r & 3) + 8 * ((r >> 2) & 1); }
 
-template <int K, typename TIn, typename TOut>
+// Lane swaps between two registers (lane group g = lanes 16 g .. 16 g + 15):
+// swap32 exchanges lanes 32-63 of a with lanes 0-31 of b, swap16 groups 1 and 3
+// of a with groups 0 and 2 of b. Written as assembly: the compiler's builtins
+// for these instructions (__builtin_amdgcn_permlane{16,32}_swap) return the
+// first result in both elements of their pair with this ROCm's clang. The
+// nops give the two wait states between a VALU write and the swap's read, and
+// between the swap and the next VALU read of its registers.
+__device__ __forceinline__ void swap32(float &a, float &b) {
+  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap16(float &a, float &b) {
+  asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+
+// The wave's per-token sums over its 16 columns: lane (g, c) holds x[r], a
+// partial of token 16 r + c; returns, in lane (g, c), the sum over the four
+// lane groups for token 16 g + c (a reduce-scatter: swap32 pairs lane groups
+// g and g ^ 2, swap16 g and g ^ 1).
+__device__ __forceinline__ float rows_reduce(const float (&x)[4]) {
+  // lanes 0-31 keep tokens 16 r + c of r = 0, 1, lanes 32-63 those of r = 2, 3
+  float a0 = x[0], a2 = x[2], a1 = x[1], a3 = x[3];
+  swap32(a0, a2);
+  swap32(a1, a3);
+  float w0 = a0 + a2;  // r = 0 (lanes < 32) or 2
+  float w1 = a1 + a3;  // r = 1 or 3
+  swap16(w0, w1);
+  return w0 + w1;
+}
+
+// The inverse movement: lane (g, c) holds y for token 16 g + c; returns in
+// every lane (g, c) the four values of tokens 16 r + c, r = 0..3.
+__device__ __forceinline__ void rows_gather(float y, float (&out)[4]) {
+  float e = y, o = y;
+  swap16(e, o);  // e: the value of group g & 2, o: of group (g & 2) + 1
+  float e2 = e, o2 = o;
+  swap32(e, e2);  // e: group 0, e2: group 2
+  swap32(o, o2);  // o: group 1, o2: group 3
+  out[0] = e;
+  out[1] = o;
+  out[2] = e2;
+  out[3] = o2;
+}
+
+template <int K, typename TIn, typename TOut, bool EPI>
 struct WideBlock {
   using L = WideLayout<K>;
   using Op = OpOf<TIn>;
@@ -101,9 +147,15 @@ struct WideBlock {
   static constexpr int DMA_REC = REC_BYTES / 1024;
   static constexpr int DMA_V = L::VMAT / 1024;
   static constexpr int OUT_STORES = 4;  // O stores a wave issues per chunk, after its loads
+  // staging loads a wave issues per chunk (issue_chunk): the K, Q and V
+  // instructions split evenly, the record's first DMA_REC % WT waves one more
+  static constexpr int DMA_WAVE_LO = 2 * (DMA_KQ / WT) + DMA_V / WT + DMA_REC / WT;
+  static_assert(DMA_REC % WT != 0, "two staging counts");
   static_assert(K == 128, "the wide scan is built for K = 128");
   static_assert(REC_BYTES % 1024 == 0 && DMA_KQ % WT == 0 && DMA_V % WT == 0, "whole DMA instructions per wave");
-  static_assert(sizeof(TIn) == 2 && sizeof(TOut) == 2, "16-bit inputs (staged as they are) and outputs");
+  static_assert(sizeof(TIn) == 2, "16-bit inputs (staged as they are)");
+  static_assert(sizeof(TOut) == 2 || (EPI && sizeof(TOut) == 4), "16-bit o; hs also in float32");
+  static constexpr int GATE_LOADS = EPI ? 4 : 0;  // gate loads a wave issues per chunk, at its start
   static_assert(L::BYTES <= 160 * 1024, "LDS");
 
   unsigned char *lds;
@@ -118,6 +170,7 @@ struct WideBlock {
   uint32_t vtr;      // V transposing read of row tile 0 (add 16 * VROW * r)
   uint32_t tbo0, tbo1;  // the two 8-byte halves of a Tb / QKD fragment row this lane reads
   uint32_t o_off;    // O: byte offset of this lane's piece (token c, columns v0 + 4g..) within a chunk
+  uint32_t g_off;    // gate: the same piece's byte offset from the chunk's first gate row (head h)
   uint32_t dma_kq;   // source offset of this lane's piece of K/Q DMA instruction `wave` within a chunk's rows
   uint32_t dma_v;    // same for V
   // The next chunk to stage (chunks are staged in order, each once): its
@@ -165,6 +218,7 @@ struct WideBlock {
     tbo0 = (16 * (g4 >> 1) + c16) * 16 + 8 * (g4 & 1);
     tbo1 = (16 * (2 + (g4 >> 1)) + c16) * 16 + 8 * (g4 & 1);
     o_off = (c16 * p.Hv * p.V + v0 + 4 * g4) * static_cast<uint32_t>(sizeof(TOut));
+    g_off = static_cast<uint32_t>((c16 * p.gate_stride + v0 + 4 * g4) * 2);
     // K/Q DMA instruction i covers rows 4i..4i+3, lane l filling row 4i + l/16
     // at position l%16 (piece (l%16) ^ swz(row)); this wave's are i = wave +
     // WT s, rows 32 s + 4 wave + l/16 (row & 15 = 4 (wave & 3) + l/16). V rows
@@ -323,6 +377,42 @@ struct WideBlock {
     return x;
   }
 
+  // The layer epilogue on O of a chunk (gated_deltanet.py:439-440): per token,
+  // o rsqrt(mean over the head's V columns of o^2 + eps) o_norm SiLU(gate).
+  // A token's 128 columns are spread over the 8 waves: each wave's sums go
+  // through LDS, with a second barrier (the single slot is free again once
+  // every wave has passed the next chunk's barrier).
+  __device__ __forceinline__ void epilogue(float4_t (&o)[4], v2u32_t (&graw)[4]) const {
+    float ss[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ss[r] = o[r][0] * o[r][0] + o[r][1] * o[r][1] + o[r][2] * o[r][2] + o[r][3] * o[r][3];
+    const float part = rows_reduce(ss);  // token 16 g + c, this wave's 16 columns
+    const uint32_t pt = L::P_OFF + (16 * g4 + c16) * (WT * 4);
+    *reinterpret_cast<float *>(lds + pt + 4 * wave) = part;
+    barrier();
+    const float4_t pa = ld<float4_t>(pt), pb = ld<float4_t>(pt + 16);
+    const float tot = (pa[0] + pa[1]) + (pa[2] + pa[3]) + ((pb[0] + pb[1]) + (pb[2] + pb[3]));
+    float rr[4];
+    rows_gather(__builtin_amdgcn_rsqf(tot * (1.f / WCOLS) + p.eps), rr);
+    const float4_t nrm = ld<float4_t>(L::N_OFF + (16 * wave + 4 * g4) * 4);
+    // the gate loads: older than the staging loads of chunk n + 2, which stay
+    // in flight (a wave's exact count: waiting on one of them costs a memory
+    // latency that the barrier above passes to every wave of the next chunk)
+    if (wave < DMA_REC % WT) {
+      wait_vm<DMA_WAVE_LO + 1>();
+    } else {
+      wait_vm<DMA_WAVE_LO>();
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      v2u32_t gr = graw[r];
+      asm volatile("" : "+v"(gr));  // after the wait
+      const float4_t gt = Op::bits_to_float(__builtin_bit_cast(i16x4_t, gr));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[r][i] *= rr[r] * nrm[i] * siluf(gt[i]);
+    }
+  }
+
   __device__ __forceinline__ void run() {
     load_state();
     if (nchunks <= 0) {
@@ -332,6 +422,10 @@ struct WideBlock {
     issue_chunk(0, 0);
     issue_chunk(1, 1);
     wait_vm<0>();
+    if constexpr (EPI) {
+      const int tid = threadIdx.x;
+      if (tid < WCOLS) *reinterpret_cast<float *>(lds + L::N_OFF + 4 * tid) = p.o_norm[col0 + tid];
+    }
     barrier();
     const bool early = wave < 4;  // issues its loads right after the barrier (else after the state update)
     // ring slots of chunks n (b3, b2) and n + 2 (i3, i2)
@@ -340,6 +434,11 @@ struct WideBlock {
     unsigned char *op = static_cast<unsigned char *>(p.o) + ((bos * p.Hv + h) * static_cast<long>(p.V)) * sizeof(TOut);
     const long ostride = static_cast<long>(p.Hv) * p.V * sizeof(TOut);  // bytes per token row
     long oleft = eos - bos;
+    // gate: chunk n's first row, columns of value head h
+    const unsigned char *gp = EPI ? static_cast<const unsigned char *>(p.gate) +
+                                        (bos * p.gate_stride + static_cast<long>(h) * p.V) * 2
+                                  : nullptr;
+    const long gstride = p.gate_stride * 2;  // bytes per gate row
     // Every LDS read is issued at least one group of products before its
     // first use: the scheduling fences (sched_barrier) keep the compiler from
     // moving a read down to its use, where the wave would wait out its latency.
@@ -354,6 +453,18 @@ struct WideBlock {
     }
     for (long n = 0; n < nchunks; ++n) {
       const uint32_t km = L::kmat(b3), qm = L::qmat(b2), rc = L::rec(b3), vm = L::vmat(b2);
+      // The gate of chunk n (rows 16 r + c, the lane's 4 columns), used at its
+      // O: issued first, so the whole step hides its latency.
+      v2u32_t graw[4];
+      if constexpr (EPI) {
+        const long rows = oleft < CH ? oleft : CH;
+        const u32x4_t_ rg = desc(gp, (rows - 1) * gstride + p.V * 2);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t off = g_off + static_cast<uint32_t>(16 * r) * static_cast<uint32_t>(gstride);
+          asm volatile("buffer_load_dwordx2 %0, %1, %2, 0 offen" : "=v"(graw[r]) : "v"(off), "s"(rg) : "memory");
+        }
+      }
       // lane bases of this chunk's reads
       const uint32_t rl = opaque(rc + REC_SC + 16 * g4);  // gamma, dec rows 4g..: + 64 r (+ table)
       const uint32_t rf0 = opaque(rc + tbo0), rf1 = opaque(rc + tbo1);
@@ -446,7 +557,7 @@ struct WideBlock {
       // O stores of chunk n-1, issued after them, may still be in flight),
       // every wave is past chunk n-1
       __builtin_amdgcn_sched_barrier(0);
-      wait_vm<OUT_STORES>();
+      wait_vm<OUT_STORES + GATE_LOADS>();
       barrier();
       if (early) issue_chunk(i3, i2);
       // ---- C: S <- gamma_63 S + K^T (dec U), token step ks outermost
@@ -516,36 +627,43 @@ struct WideBlock {
 #pragma unroll
         for (int r = 0; r < 4; ++r) o[r] *= up;
       }
+      if constexpr (EPI) epilogue(o, graw);
       const long rows = oleft < CH ? oleft : CH;  // >= 1: chunk n holds tokens
       const __amdgpu_buffer_rsrc_t ro = rsrc(op, (rows - 1) * ostride + p.V * static_cast<long>(sizeof(TOut)));
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const O4 x4 = Op::from(o[r]);
-        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32_t, x4), ro,
-                                              o_off + 16 * r * static_cast<uint32_t>(ostride), 0, 0);
+        const uint32_t off = o_off + 16 * r * static_cast<uint32_t>(ostride);
+        if constexpr (sizeof(TOut) == 4) {
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32_t, o[r]), ro, off, 0, 0);
+        } else {
+          const O4 x4 = Op::from(o[r]);
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32_t, x4), ro, off, 0, 0);
+        }
       }
       op += CH * ostride;
       oleft -= CH;
+      if constexpr (EPI) gp += CH * gstride;
     }
     store_state();
   }
 };
 
 // Two waves per SIMD: 256 registers each.
-template <int K, typename TIn, typename TOut>
+template <int K, typename TIn, typename TOut, bool EPI>
 __global__ __launch_bounds__(WNT) __attribute__((amdgpu_waves_per_eu(2, 2))) void wide_kernel(ChunkParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  WideBlock<K, TIn, TOut> blk(smem_raw, p);
+  WideBlock<K, TIn, TOut, EPI> blk(smem_raw, p);
   blk.run();
 }
 
 }  // namespace
 
-template <int K, typename TIn, typename TOut>
+template <int K, typename TIn, typename TOut, bool EPI>
 int launch_wide(const ChunkParams &p, hipStream_t stream) {
   static std::atomic<bool> configured[MAX_DEVICES];  // the attribute is set per device
   const size_t smem = WideLayout<K>::BYTES;
-  auto kernel = wide_kernel<K, TIn, TOut>;
+  auto kernel = wide_kernel<K, TIn, TOut, EPI>;
+  if (EPI && (p.V != WCOLS || !p.gate || !p.o_norm)) return PBGDN_ERR_INVALID_ARGUMENT;
   if (!smem_configured(reinterpret_cast<const void *>(kernel), smem, configured)) return PBGDN_ERR_LAUNCH;
   const long total = static_cast<long>(p.V / WCOLS) * p.Hv * p.num_seqs;
   if (total > 0x7fffffffL) return PBGDN_ERR_UNSUPPORTED;
@@ -553,7 +671,11 @@ int launch_wide(const ChunkParams &p, hipStream_t stream) {
   return hipGetLastError() == hipSuccess ? PBGDN_OK : PBGDN_ERR_LAUNCH;
 }
 
-template int launch_wide<128, u16, u16>(const ChunkParams &, hipStream_t);
-template int launch_wide<128, half_t, half_t>(const ChunkParams &, hipStream_t);
+template int launch_wide<128, u16, u16, false>(const ChunkParams &, hipStream_t);
+template int launch_wide<128, half_t, half_t, false>(const ChunkParams &, hipStream_t);
+template int launch_wide<128, u16, u16, true>(const ChunkParams &, hipStream_t);
+template int launch_wide<128, u16, float, true>(const ChunkParams &, hipStream_t);
+template int launch_wide<128, half_t, half_t, true>(const ChunkParams &, hipStream_t);
+template int launch_wide<128, half_t, float, true>(const ChunkParams &, hipStream_t);
 
 }  // namespace pbgdn

@@ -60,22 +60,34 @@ __device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, bf16x2_t{static_cast<__bf16>(lo), static_cast<__bf16>(hi)});
 }
 
+// A 16-byte store; STREAM: non-temporal (outputs read next by another kernel,
+// far more bytes than the caches hold).
+template <bool STREAM, typename T>
+__device__ __forceinline__ void put16(T *dst, const T &x) {
+  if constexpr (STREAM) {
+    __builtin_nontemporal_store(x, dst);
+  } else {
+    *dst = x;
+  }
+}
+
+template <bool STREAM = false>
 __device__ __forceinline__ void store8(void *p, long i, int dtype, const float (&x)[8]) {
   if (dtype == PBGDN_F32) {
-    *reinterpret_cast<float4_t *>(static_cast<float *>(p) + i) = float4_t{x[0], x[1], x[2], x[3]};
-    *reinterpret_cast<float4_t *>(static_cast<float *>(p) + i + 4) = float4_t{x[4], x[5], x[6], x[7]};
+    put16<STREAM>(reinterpret_cast<float4_t *>(static_cast<float *>(p) + i), float4_t{x[0], x[1], x[2], x[3]});
+    put16<STREAM>(reinterpret_cast<float4_t *>(static_cast<float *>(p) + i + 4), float4_t{x[4], x[5], x[6], x[7]});
   } else if (dtype == PBGDN_BF16) {
-    uint4 u;  // v_cvt_pk_bf16_f32: round to nearest even, as float_to_bf16_bits
-    u.x = bf16_pair(x[0], x[1]);
-    u.y = bf16_pair(x[2], x[3]);
-    u.z = bf16_pair(x[4], x[5]);
-    u.w = bf16_pair(x[6], x[7]);
-    *reinterpret_cast<uint4 *>(static_cast<u16 *>(p) + i) = u;
+    v4u32_t u;  // v_cvt_pk_bf16_f32: round to nearest even, as float_to_bf16_bits
+    u[0] = bf16_pair(x[0], x[1]);
+    u[1] = bf16_pair(x[2], x[3]);
+    u[2] = bf16_pair(x[4], x[5]);
+    u[3] = bf16_pair(x[6], x[7]);
+    put16<STREAM>(reinterpret_cast<v4u32_t *>(static_cast<u16 *>(p) + i), u);
   } else {
     half8_t h;
 #pragma unroll
     for (int e = 0; e < 8; ++e) h[e] = static_cast<half_t>(x[e]);
-    *reinterpret_cast<half8_t *>(static_cast<half_t *>(p) + i) = h;
+    put16<STREAM>(reinterpret_cast<half8_t *>(static_cast<half_t *>(p) + i), h);
   }
 }
 
@@ -140,11 +152,14 @@ __device__ __forceinline__ void decode8(const Raw8 &r, int dtype, float (&x)[8])
 }
 // Raw load of 8 elements at byte offset `off` of a buffer resource (32 bytes
 // when WIDE, else 16): offsets at or past the resource's size read zeros.
-template <bool WIDE>
+// STREAM: non-temporal (inputs read once).
+template <bool WIDE, bool STREAM = false>
 __device__ __forceinline__ Raw8 load_raw8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  constexpr int AUX = STREAM ? 2 : 0;
   Raw8 x;
-  x.a = buf_load16(r, off);
-  x.b = WIDE ? buf_load16(r, off + 16) : uint4{0u, 0u, 0u, 0u};
+  x.a = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX));
+  x.b = WIDE ? __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off + 16, 0, AUX))
+             : uint4{0u, 0u, 0u, 0u};
   return x;
 }
 
@@ -471,7 +486,12 @@ struct EpilogueParams {
 // g, g + G, ... (G = groups per workgroup); all loads issue before any use.
 constexpr int EPI_ROWS = 1;
 
-template <typename TO, typename TG, int V>
+// A call moving more bytes than this (o and gate in, the output out) streams
+// them with non-temporal hints; smaller calls keep them cacheable, since their
+// o was most likely just written by the scan and is still in the caches.
+constexpr long EPILOGUE_STREAM_BYTES = 192L << 20;
+
+template <typename TO, typename TG, int V, bool STREAM>
 __global__ __launch_bounds__(LNT) void epilogue_kernel(EpilogueParams p) {
   constexpr int LANES = V / 8;             // lanes per (token, head) row
   constexpr int GROUPS = LNT / LANES;      // row groups per workgroup
@@ -487,8 +507,8 @@ __global__ __launch_bounds__(LNT) void epilogue_kernel(EpilogueParams p) {
     const bool live = row < p.rows;
     const uint32_t token = static_cast<uint32_t>(row) / static_cast<uint32_t>(p.Hv);
     const uint32_t h = static_cast<uint32_t>(row) - token * static_cast<uint32_t>(p.Hv);
-    ro8[j] = load_raw8<sizeof(TO) == 4>(ro, live ? static_cast<uint32_t>((row * V + c0) * sizeof(TO)) : OUT_OF_RANGE);
-    rg8[j] = load_raw8<sizeof(TG) == 4>(
+    ro8[j] = load_raw8<sizeof(TO) == 4, STREAM>(ro, live ? static_cast<uint32_t>((row * V + c0) * sizeof(TO)) : OUT_OF_RANGE);
+    rg8[j] = load_raw8<sizeof(TG) == 4, STREAM>(
         rg, live ? static_cast<uint32_t>((token * p.gate_stride + h * V + c0) * sizeof(TG)) : OUT_OF_RANGE);
   }
   float nrm[8];
@@ -508,24 +528,28 @@ __global__ __launch_bounds__(LNT) void epilogue_kernel(EpilogueParams p) {
     float y[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) y[e] = o[e] * r * nrm[e] * siluf(gt[e]);
-    if (row < p.rows) store8(p.out, row * V + c0, p.out_dtype, y);
+    if (row < p.rows) store8<STREAM>(p.out, row * V + c0, p.out_dtype, y);
   }
 }
 
-template <typename TO, int V>
+template <typename TO, int V, bool STREAM>
 void launch_epilogue_v(int gate_dtype, dim3 grid, hipStream_t st, const EpilogueParams &prm) {
   switch (gate_dtype) {
-    case PBGDN_F32: hipLaunchKernelGGL((epilogue_kernel<TO, float, V>), grid, dim3(LNT), 0, st, prm); break;
-    case PBGDN_BF16: hipLaunchKernelGGL((epilogue_kernel<TO, u16, V>), grid, dim3(LNT), 0, st, prm); break;
-    default: hipLaunchKernelGGL((epilogue_kernel<TO, half_t, V>), grid, dim3(LNT), 0, st, prm); break;
+    case PBGDN_F32: hipLaunchKernelGGL((epilogue_kernel<TO, float, V, STREAM>), grid, dim3(LNT), 0, st, prm); break;
+    case PBGDN_BF16: hipLaunchKernelGGL((epilogue_kernel<TO, u16, V, STREAM>), grid, dim3(LNT), 0, st, prm); break;
+    default: hipLaunchKernelGGL((epilogue_kernel<TO, half_t, V, STREAM>), grid, dim3(LNT), 0, st, prm); break;
   }
 }
 template <typename TO>
 void launch_epilogue(int gate_dtype, dim3 grid, hipStream_t st, const EpilogueParams &prm) {
+  const long elem_out = prm.out_dtype == PBGDN_F32 ? 4 : 2, elem_gate = gate_dtype == PBGDN_F32 ? 4 : 2;
+  const bool stream = prm.rows * prm.V * (static_cast<long>(sizeof(TO)) + elem_gate + elem_out) > EPILOGUE_STREAM_BYTES;
   if (prm.V == 64) {
-    launch_epilogue_v<TO, 64>(gate_dtype, grid, st, prm);
+    stream ? launch_epilogue_v<TO, 64, true>(gate_dtype, grid, st, prm)
+           : launch_epilogue_v<TO, 64, false>(gate_dtype, grid, st, prm);
   } else {
-    launch_epilogue_v<TO, 128>(gate_dtype, grid, st, prm);
+    stream ? launch_epilogue_v<TO, 128, true>(gate_dtype, grid, st, prm)
+           : launch_epilogue_v<TO, 128, false>(gate_dtype, grid, st, prm);
   }
 }
 

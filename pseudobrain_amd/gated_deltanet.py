@@ -175,12 +175,11 @@ def _fp32_range_scale(v, h0):
     return torch.exp2(-torch.nan_to_num(e, nan=0.0, posinf=0.0))
 
 
-def _chunk_fwd(q, k, v, g, beta, scale: float, h0=None, cu_seqlens=None, *,
-               out_dtype: torch.dtype | None = None, output_final_state: bool = True,
-               out: torch.Tensor | None = None):
-    batch, length, hk, hv, dk, dv = _shapes(q, k, v, g, beta)
-    if out_dtype is not None and out_dtype not in (torch.float32, q.dtype):
-        raise ValueError(f"chunk kernel writes o as float32 or q's dtype ({q.dtype}), not {out_dtype}")
+def _chunk_args(q, k, v, g, beta, h0, cu_seqlens):
+    """Checked operands of a chunk-kernel call: (shapes, device, q, k, v, g, beta,
+    h0 as contiguous fp32 or None, cu_seqlens as int32 or None, N)."""
+    shapes = _shapes(q, k, v, g, beta)
+    batch, length, hk, hv, dk, dv = shapes
     dev = _require_device(q, k, v, g, beta, h0, cu_seqlens)
     if dk not in CHUNK_HEAD_DIMS or dv % 16:
         raise ValueError(f"chunk kernel supports K in {CHUNK_HEAD_DIMS} and V a multiple of 16")
@@ -198,6 +197,16 @@ def _chunk_fwd(q, k, v, g, beta, scale: float, h0=None, cu_seqlens=None, *,
         if h0.shape != (nseq, hv, dk, dv):
             raise ValueError(f"initial state must be [N,Hv,K,V] = {(nseq, hv, dk, dv)}")
         h0 = h0.to(torch.float32).contiguous()
+    return shapes, dev, q, k, v, g, beta, h0, cu_seqlens, nseq
+
+
+def _chunk_fwd(q, k, v, g, beta, scale: float, h0=None, cu_seqlens=None, *,
+               out_dtype: torch.dtype | None = None, output_final_state: bool = True,
+               out: torch.Tensor | None = None):
+    if out_dtype is not None and out_dtype not in (torch.float32, q.dtype):
+        raise ValueError(f"chunk kernel writes o as float32 or q's dtype ({q.dtype}), not {out_dtype}")
+    shapes, dev, q, k, v, g, beta, h0, cu_seqlens, nseq = _chunk_args(q, k, v, g, beta, h0, cu_seqlens)
+    batch, length, hk, hv, dk, dv = shapes
     down = None
     if q.dtype == torch.float32:
         down = _fp32_range_scale(v, h0)

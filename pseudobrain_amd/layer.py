@@ -11,6 +11,10 @@ epilogue of GatedDeltaNetLayer.forward (pseudobrain/gated_deltanet.py:403-441).
     layer_epilogue(o, gate, o_norm, eps)  ->  hs                      (:439-441)
         one kernel (pbgdn_epilogue_fwd): per-head RMSNorm x o_norm x SiLU(gate)
 
+For prefill, chunk_layer_fwd runs the operator and the epilogue as one call
+(pbgdn_chunk_layer_fwd): where the wide scan takes the call, the scan applies
+the epilogue to each chunk's output and writes hs directly.
+
 For decode (one token per sequence), decode_layer_step does all of it in one
 kernel (pbgdn_decode_layer_fwd), against slot pools of conv tails and states
 updated in place, the way a serving cache holds them.
@@ -28,7 +32,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .gated_deltanet import require_no_grad
+from .gated_deltanet import CHUNK, _chunk_args, _chunk_fwd, require_no_grad
 
 NORM_EPS = 1e-5           # gated_deltanet.py:72
 L2_MODES = ("max", "hf")  # gated_deltanet.py:57
@@ -261,6 +265,60 @@ def layer_epilogue(o: torch.Tensor, gate: torch.Tensor, o_norm: torch.Tensor, ep
         float(eps), _lib.ptr(out), codes[out_dtype], batch, length, hv, dv, _lib.stream_handle(dev))
     _lib.check(status, "pbgdn_epilogue_fwd")
     return out
+
+
+def chunk_layer_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
+                    scale: float, h0: torch.Tensor | None, gate: torch.Tensor, o_norm: torch.Tensor,
+                    eps: float = NORM_EPS, cu_seqlens: torch.Tensor | None = None, *,
+                    out_dtype: torch.dtype = torch.float32, output_final_state: bool = True):
+    """The layer core of a prefill (gated_deltanet.py:437-441): o, S =
+    gated_delta_rule(q, k, v, g, beta, scale, h0) followed by hs = o rsqrt(mean
+    (o^2) + eps) o_norm SiLU(gate), in one call (pbgdn_chunk_layer_fwd).
+    Arguments as chunk_fwd and layer_epilogue; returns (hs [B,T,Hv*V] in
+    out_dtype, final states [N,Hv,K,V] fp32 or None).
+
+    With bf16/fp16 q, k, v at K = V = 128 and enough (sequence, value head)
+    pairs for the wide scan, the epilogue is applied inside the scan (no o is
+    written or re-read); otherwise the operator writes o and the epilogue runs
+    as its own kernel. float32 inputs go through chunk_fwd (which scales them
+    into the kernels' range) and layer_epilogue."""
+    require_no_grad("chunk_layer_fwd", q, k, v, g, beta, h0, gate, o_norm)
+    codes = _lib.DTYPE_CODES
+    if out_dtype not in codes or gate.dtype not in codes:
+        raise ValueError("gate and out_dtype must be float32, bfloat16 or float16")
+    if q.dtype == torch.float32:
+        o, final = _chunk_fwd(q, k, v, g, beta, scale, h0, cu_seqlens, output_final_state=output_final_state)
+        return layer_epilogue(o, gate, o_norm, eps, out_dtype=out_dtype), final
+    shapes, dev, q, k, v, g, beta, h0, cu_seqlens, nseq = _chunk_args(q, k, v, g, beta, h0, cu_seqlens)
+    batch, length, hk, hv, dk, dv = shapes
+    if dv not in EPILOGUE_VALUE_DIMS:
+        raise ValueError(f"the epilogue supports value widths {EPILOGUE_VALUE_DIMS}")
+    if gate.shape != (batch, length, hv * dv):
+        raise ValueError(f"gate must be [B,T,Hv*V] = {(batch, length, hv * dv)}")
+    if not eps >= 0:
+        raise ValueError("eps must be >= 0")
+    if gate.device != dev:
+        raise ValueError("gate must be on the device of q")
+    norm = o_norm.to(device=dev, dtype=torch.float32).contiguous()
+    if norm.shape != (dv,):
+        raise ValueError(f"o_norm must be [{dv}]")
+    if (gate.stride(-1) != 1 or gate.stride(0) != gate.shape[1] * gate.stride(1) or gate.stride(1) % 8
+            or gate.data_ptr() % 16):  # one row stride across the batch, 16-byte row pieces
+        gate = gate.contiguous()
+    hs = torch.empty(batch, length, hv * dv, dtype=out_dtype, device=dev)
+    o = torch.empty(batch, length, hv, dv, dtype=q.dtype, device=dev)
+    final = torch.empty(nseq, hv, dk, dv, dtype=torch.float32, device=dev) if output_final_state else None
+    lib = _lib.lib()
+    ws_bytes = lib.pbgdn_chunk_workspace_size(batch, length, hv, nseq)
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    status = lib.pbgdn_chunk_layer_fwd(
+        _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), codes[q.dtype], _lib.ptr(g), _lib.ptr(beta), codes[beta.dtype],
+        _lib.ptr(h0), _lib.ptr(final), _lib.F32, None, None, 0, _lib.ptr(cu_seqlens), nseq,
+        _lib.ptr(gate), _rows(gate, "gate"), codes[gate.dtype], _lib.ptr(norm), float(eps), _lib.ptr(hs),
+        codes[out_dtype], _lib.ptr(o), batch, length, hk, hv, dk, dv, float(scale), CHUNK, _lib.ptr(workspace),
+        ws_bytes, _lib.stream_handle(dev))
+    _lib.check(status, "pbgdn_chunk_layer_fwd")
+    return hs, final
 
 
 def decode_layer_step(z: torch.Tensor, conv_state: torch.Tensor | None, conv_weight: torch.Tensor | None,

@@ -145,6 +145,30 @@ def test_epilogue(dv, o_dtype, gate_dtype, out_dtype):
     assert err <= tol
 
 
+def test_epilogue_streamed_matches_cached():
+    """A call moving more than 192 MiB (8,192 tokens x 32 heads x 128: 256 MiB
+    of o, gate and output) streams with non-temporal hints; its halves, below
+    that size, keep the cacheable path. Same arithmetic: equal bit for bit,
+    and within the tolerance of the oracle."""
+    gen = torch.Generator().manual_seed(44)
+    length, hv, dv = 8192, 32, 128
+    o = (torch.randn(1, length, hv, dv, generator=gen) * 0.3).to(torch.bfloat16)
+    z = torch.randn(1, length, 2 * hv * dv, generator=gen).to(torch.bfloat16)
+    gate = z[..., hv * dv:]
+    o_norm = torch.rand(dv, generator=gen) + 0.5
+    do, dz, dn = o.to(DEV), z.to(DEV), o_norm.to(DEV)
+    whole = layer_epilogue(do, dz[..., hv * dv:], dn, 1e-5, out_dtype=torch.float32)
+    halves = torch.cat([layer_epilogue(do[:, s], dz[:, s].contiguous()[..., hv * dv:], dn, 1e-5,
+                                       out_dtype=torch.float32)
+                        for s in (slice(0, length // 2), slice(length // 2, length))], dim=1)
+    torch.cuda.synchronize()
+    assert torch.equal(whole, halves)
+    ref = ol.layer_epilogue(to_numpy(o.float()), to_numpy(gate.float()), to_numpy(o_norm), 1e-5)
+    err = rel_err(whole, ref)
+    print(f"[epilogue streamed T={length}] rel_inf={err:.2e}", flush=True)
+    assert err <= F32_TOL
+
+
 def test_layer_prologue_operator_epilogue_against_the_oracle():
     """The whole GatedDeltaNetLayer core (gated_deltanet.py:415-441) at the
     Qwen3-Next head shape: fused prologue -> chunk operator -> fused epilogue
