@@ -92,20 +92,6 @@ struct WideLayout {
 __host__ __device__ constexpr int swz(int r) { return 4 * (r & 3) + ((r >> 2) & 3); }
 __host__ __device__ constexpr int vswz(int r) { return 2 * (r & 3) + 8 * ((r >> 2) & 1); }
 
-// Lane swaps between two registers (lane group g = lanes 16 g .. 16 g + 15):
-// swap32 exchanges lanes 32-63 of a with lanes 0-31 of b, swap16 groups 1 and 3
-// of a with groups 0 and 2 of b. Written as assembly: the compiler's builtins
-// for these instructions (__builtin_amdgcn_permlane{16,32}_swap) return the
-// first result in both elements of their pair with this ROCm's clang. The
-// nops give the two wait states between a VALU write and the swap's read, and
-// between the swap and the next VALU read of its registers.
-__device__ __forceinline__ void swap32(float &a, float &b) {
-  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
-}
-__device__ __forceinline__ void swap16(float &a, float &b) {
-  asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
-}
-
 // The wave's per-token sums over its 16 columns: lane (g, c) holds x[r], a
 // partial of token 16 r + c; returns, in lane (g, c), the sum over the four
 // lane groups for token 16 g + c (a reduce-scatter: swap32 pairs lane groups

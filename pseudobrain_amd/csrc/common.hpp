@@ -87,6 +87,66 @@ __device__ __forceinline__ float wave_sum(float x) {
 }
 
 // ---------------------------------------------------------------------------
+// Lane exchanges on the VALU (no LDS round trip). Lane group g = lanes
+// 16 g .. 16 g + 15.
+// ---------------------------------------------------------------------------
+// DPP move of a float inside 16-lane rows (every lane's source in its row).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over aligned groups of `width` lanes (1, 2, 4, 8 or 16) inside a 16-lane
+// row; every lane of a group gets the group's sum: a butterfly of DPP moves
+// (quad_perm [1,0,3,2] and [2,3,0,1], then row_half_mirror and row_mirror:
+// gfx9-family controls 0xb1, 0x4e, 0x141, 0x140).
+__device__ __forceinline__ float group_sum(float x, int width) {
+  if (width > 1) x += dpp_mov<0xb1>(x);
+  if (width > 2) x += dpp_mov<0x4e>(x);
+  if (width > 4) x += dpp_mov<0x141>(x);
+  if (width > 8) x += dpp_mov<0x140>(x);
+  return x;
+}
+
+// swap32 exchanges lanes 32-63 of a with lanes 0-31 of b; swap16 lane groups
+// 1 and 3 of a with groups 0 and 2 of b (v_permlane32_swap,
+// v_permlane16_swap). Written as assembly: this ROCm's clang builtins for them
+// (__builtin_amdgcn_permlane{16,32}_swap) return the first result in both
+// elements of their pair. The nops give the two wait states between a VALU
+// write and the swap's read, and between the swap and the next VALU read.
+__device__ __forceinline__ void swap32(float &a, float &b) {
+  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap16(float &a, float &b) {
+  asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+// x + x of lane ^ 32, and of lane ^ 16, in every lane.
+__device__ __forceinline__ float add_xor32(float x) {
+  float a = x, b = x;
+  swap32(a, b);
+  return a + b;
+}
+__device__ __forceinline__ float add_xor16(float x) {
+  float a = x, b = x;
+  swap16(a, b);
+  return a + b;
+}
+// Sum over the lanes congruent to this one modulo CG (a power of two): every
+// lane gets its class's sum. Within a row, DPP rotations by 8, 4, 2, 1 lanes
+// (row_ror, controls 0x128, 0x124, 0x122, 0x121); across rows the swaps.
+template <int CG>
+__device__ __forceinline__ float sum_mod_lanes(float x) {
+  static_assert(CG >= 1 && CG <= 64 && (CG & (CG - 1)) == 0, "a power of two up to 64");
+  if constexpr (CG <= 8) x += dpp_mov<0x128>(x);
+  if constexpr (CG <= 4) x += dpp_mov<0x124>(x);
+  if constexpr (CG <= 2) x += dpp_mov<0x122>(x);
+  if constexpr (CG <= 1) x += dpp_mov<0x121>(x);
+  if constexpr (CG <= 16) x = add_xor16(x);
+  if constexpr (CG <= 32) x = add_xor32(x);
+  return x;
+}
+
+// ---------------------------------------------------------------------------
 // MFMA wrappers. Lane layouts (l = lane, g = l >> 4, c = l & 15):
 //   16x16x32 f16: A[m=c][k-slots 8g..8g+7], B[k-slots 8g..8g+7][n=c]
 //   16x16x16 f16: A[m=c][k-slots 4g..4g+3], B[k-slots 4g..4g+3][n=c]

@@ -211,13 +211,11 @@ __global__ __launch_bounds__(DNT, (sizeof(TS) == 2 ? 5 : 4)) void decode_layer_k
 #pragma unroll
       for (int j = 0; j < RPT; ++j) asm volatile("" : "+v"(raw[j]));
     }
+    // the wave's row groups (lanes congruent modulo CG), on the VALU
 #pragma unroll
-    for (int off = CG; off < 64; off <<= 1) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        pk[c] += __shfl_xor(pk[c], off, 64);
-        pq[c] += __shfl_xor(pq[c], off, 64);
-      }
+    for (int c = 0; c < 4; ++c) {
+      pk[c] = sum_mod_lanes<CG>(pk[c]);
+      pq[c] = sum_mod_lanes<CG>(pq[c]);
     }
     if (lane < CG) {  // lane % CG == cg, and lane < CG selects the wave's first row group
       red_k[wave][lane] = pk;
@@ -240,8 +238,9 @@ __global__ __launch_bounds__(DNT, (sizeof(TS) == 2 ? 5 : 4)) void decode_layer_k
     // Epilogue: RMSNorm over the head's V outputs (the CG lanes of a row
     // group hold them), times o_norm, times SiLU(gate).
     float ss = out[0] * out[0] + out[1] * out[1] + out[2] * out[2] + out[3] * out[3];
-#pragma unroll
-    for (int off = 1; off < CG; off <<= 1) ss += __shfl_xor(ss, off, 64);
+    ss = group_sum(ss, CG < 16 ? CG : 16);  // the row group's CG consecutive lanes
+    if constexpr (CG == 32) ss = add_xor16(ss);
+    static_assert(CG <= 32, "a row group within half a wave");
     const float r = rsqrtf(ss * (1.f / V) + p.eps);
     if (rg == 0) {
       const long o_base = hs_row + static_cast<long>(h) * V + 4 * cg;

@@ -163,16 +163,6 @@ __device__ __forceinline__ Raw8 load_raw8(__amdgpu_buffer_rsrc_t r, uint32_t off
   return x;
 }
 
-// Sum over groups of `width` lanes (a power of two up to 16), inside a
-// 16-lane row.
-__device__ __forceinline__ float group_sum(float x, int width) {
-#pragma unroll
-  for (int off = 1; off < 16; off <<= 1) {  // a fixed trip count: no loop inside the callers' unrolled loops
-    if (off < width) x += __shfl_xor(x, off, 64);
-  }
-  return x;
-}
-
 struct PrologueParams {
   const void *qkv, *decay, *tail;
   void *tail_out;
@@ -233,7 +223,7 @@ struct OutLane {
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) ss += y[e] * y[e];
-    ss = group_sum(ss, head_lanes);
+    ss = group_sum(ss, head_lanes);  // DPP: a shuffle's LDS trip and wait per step sat on every token's path
     if (!store) return false;
     if (kind < 2) {
       constexpr float l2_eps = 1e-6f;

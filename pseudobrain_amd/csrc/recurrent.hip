@@ -195,13 +195,11 @@ __global__ __launch_bounds__(256, (recurrent_wg_per_cu<K, VW, ONE, ONE && sizeof
 #pragma unroll
       for (int j = 0; j < RPT; ++j) asm volatile("" : "+v"(raw[j]));
     }
+    // the wave's row groups (lanes congruent modulo CG), on the VALU
 #pragma unroll
-    for (int off = CG; off < 64; off <<= 1) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        pk[c] += __shfl_xor(pk[c], off, 64);
-        pq[c] += __shfl_xor(pq[c], off, 64);
-      }
+    for (int c = 0; c < 4; ++c) {
+      pk[c] = sum_mod_lanes<CG>(pk[c]);
+      pq[c] = sum_mod_lanes<CG>(pq[c]);
     }
     if (lane < CG) {  // lane % CG == cg, and lane < CG selects the wave's first row group
       red_k[wave][lane] = pk;
