@@ -273,17 +273,23 @@ __global__ __launch_bounds__(LNT) void prologue_kernel(PrologueParams p) {
   const long seq_row = static_cast<long>(b) * p.T;
   const long chans = static_cast<long>(p.units) * 8;
   // Every row this lane needs is loaded unconditionally through a buffer
-  // resource that spans exactly this sequence's rows; a row outside it (or a
-  // dead lane) gets an out-of-range offset and reads zeros. No load then
-  // waits on a branch merge: they all issue back to back.
-  const auto rq = rsrc(static_cast<const TIn *>(p.qkv) + seq_row * p.qkv_stride,
-                       (static_cast<long>(p.T - 1) * p.qkv_stride + chans) * static_cast<long>(sizeof(TIn)));
+  // resource that spans exactly the sequence's rows this tile reads (from
+  // base_row, the tile's first halo row or the sequence's first); a row
+  // outside it (or a dead lane) gets an out-of-range offset and reads zeros.
+  // No load then waits on a branch merge: they all issue back to back, and
+  // the offsets stay small however long the sequence.
+  const int base_row = max(t_tile - HALO, 0);
+  const int end_row = min(t_tile + TT, p.T);
+  const auto rq = rsrc(static_cast<const TIn *>(p.qkv) + (seq_row + base_row) * p.qkv_stride,
+                       (static_cast<long>(end_row - 1 - base_row) * p.qkv_stride + chans) *
+                           static_cast<long>(sizeof(TIn)));
   Raw8 raw[HALO + TPL];  // rows t_first - HALO ..
 #pragma unroll
   for (int m = 0; m < HALO + TPL; ++m) {
     const int t = t_first - HALO + m;
     const uint32_t off = live && t >= 0 && t < p.T
-                             ? (static_cast<uint32_t>(t) * static_cast<uint32_t>(p.qkv_stride) + c0) * sizeof(TIn)
+                             ? (static_cast<uint32_t>(t - base_row) * static_cast<uint32_t>(p.qkv_stride) + c0) *
+                                   sizeof(TIn)
                              : OUT_OF_RANGE;
     raw[m] = load_raw8<sizeof(TIn) == 4>(rq, off);
   }
@@ -348,15 +354,22 @@ __global__ __launch_bounds__(LNT) void edge_kernel(PrologueParams p) {
     len = min(max(0L, static_cast<long>(p.cu_seqlens[s + 1]) - bos), p.T - bos);
   }
   const long slot = p.slot_idx ? static_cast<long>(p.slot_idx[s]) : static_cast<long>(s);
-  const auto rq = rsrc(static_cast<const TIn *>(p.qkv) + bos * p.qkv_stride,
-                       len > 0 ? ((len - 1) * p.qkv_stride + chans) * static_cast<long>(sizeof(TIn)) : 0);
-  auto row_off = [&](long j) -> uint32_t {  // byte offset of the sequence's row j, channel c0
-    return live && j < len ? static_cast<uint32_t>((j * p.qkv_stride + c0) * static_cast<long>(sizeof(TIn)))
-                           : OUT_OF_RANGE;
+  // Two resources: the sequence's first TAIL rows, and its last TAIL rows
+  // (from row `last0`), so the offsets stay small however long the sequence.
+  const long head_rows = min(len, static_cast<long>(TAIL));
+  const long last0 = max(len - TAIL, 0L);
+  const auto r_head = rsrc(static_cast<const TIn *>(p.qkv) + bos * p.qkv_stride,
+                           head_rows > 0 ? ((head_rows - 1) * p.qkv_stride + chans) * static_cast<long>(sizeof(TIn))
+                                         : 0);
+  const auto r_last = rsrc(static_cast<const TIn *>(p.qkv) + (bos + last0) * p.qkv_stride,
+                           len > 0 ? ((len - 1 - last0) * p.qkv_stride + chans) * static_cast<long>(sizeof(TIn)) : 0);
+  auto row_off = [&](long j) -> uint32_t {  // byte offset of row j within a resource starting at row 0 or last0
+    return live && j >= 0 && j < TAIL ? static_cast<uint32_t>((j * p.qkv_stride + c0) * static_cast<long>(sizeof(TIn)))
+                                      : OUT_OF_RANGE;
   };
   float old[TAIL][8], x[TAIL][8];  // the old tail; the sequence's first TAIL inputs
 #pragma unroll
-  for (int j = 0; j < TAIL; ++j) decode8<TIn>(load_raw8<sizeof(TIn) == 4>(rq, row_off(j)), x[j]);
+  for (int j = 0; j < TAIL; ++j) decode8<TIn>(load_raw8<sizeof(TIn) == 4>(r_head, row_off(j)), x[j]);
   const bool from_pool = live && slot >= 0 && slot < p.num_slots && !(p.has_initial && !p.has_initial[s]);
   if (!from_pool) {
 #pragma unroll
@@ -417,7 +430,7 @@ __global__ __launch_bounds__(LNT) void edge_kernel(PrologueParams p) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) nt[r][k] = old[e < TAIL ? e : 0][k];
     } else {
-      decode8<TIn>(load_raw8<sizeof(TIn) == 4>(rq, row_off(e - TAIL)), nt[r]);
+      decode8<TIn>(load_raw8<sizeof(TIn) == 4>(r_last, row_off(e - TAIL - last0)), nt[r]);
     }
   }
   if (p.tail_vec == 1) {
@@ -487,19 +500,26 @@ __global__ __launch_bounds__(LNT) void epilogue_kernel(EpilogueParams p) {
   constexpr int GROUPS = LNT / LANES;      // row groups per workgroup
   const int tid = threadIdx.x;
   const int c0 = 8 * (tid % LANES);
-  const long row0 = static_cast<long>(blockIdx.x) * GROUPS * EPI_ROWS + tid / LANES;
-  const auto ro = rsrc(p.o, p.rows * V * static_cast<long>(sizeof(TO)));
-  const auto rg = rsrc(p.gate, (p.rows / p.Hv) * p.gate_stride * static_cast<long>(sizeof(TG)));
+  // The workgroup's rows, from its first (r0) and its first token (tk0): the
+  // buffer offsets stay small however many rows the call has.
+  const long r0 = static_cast<long>(blockIdx.x) * GROUPS * EPI_ROWS;
+  const long r_end = min(r0 + GROUPS * EPI_ROWS, p.rows);
+  const long tk0 = r0 / p.Hv;
+  const long row0 = r0 + tid / LANES;
+  const auto ro = rsrc(static_cast<const TO *>(p.o) + r0 * V, (r_end - r0) * V * static_cast<long>(sizeof(TO)));
+  const auto rg = rsrc(static_cast<const TG *>(p.gate) + tk0 * p.gate_stride,
+                       ((r_end - 1) / p.Hv - tk0 + 1) * p.gate_stride * static_cast<long>(sizeof(TG)));
   Raw8 ro8[EPI_ROWS], rg8[EPI_ROWS];
 #pragma unroll
   for (int j = 0; j < EPI_ROWS; ++j) {
     const long row = row0 + static_cast<long>(j) * GROUPS;
     const bool live = row < p.rows;
-    const uint32_t token = static_cast<uint32_t>(row) / static_cast<uint32_t>(p.Hv);
-    const uint32_t h = static_cast<uint32_t>(row) - token * static_cast<uint32_t>(p.Hv);
-    ro8[j] = load_raw8<sizeof(TO) == 4, STREAM>(ro, live ? static_cast<uint32_t>((row * V + c0) * sizeof(TO)) : OUT_OF_RANGE);
+    const long token = row / p.Hv;
+    const long h = row - token * p.Hv;
+    ro8[j] = load_raw8<sizeof(TO) == 4, STREAM>(
+        ro, live ? static_cast<uint32_t>(((row - r0) * V + c0) * sizeof(TO)) : OUT_OF_RANGE);
     rg8[j] = load_raw8<sizeof(TG) == 4, STREAM>(
-        rg, live ? static_cast<uint32_t>((token * p.gate_stride + h * V + c0) * sizeof(TG)) : OUT_OF_RANGE);
+        rg, live ? static_cast<uint32_t>(((token - tk0) * p.gate_stride + h * V + c0) * sizeof(TG)) : OUT_OF_RANGE);
   }
   float nrm[8];
 #pragma unroll
@@ -565,9 +585,10 @@ extern "C" int pbgdn_prologue_fwd(const void *qkv, long qkv_stride, const void *
   if (!(K == 64 || K == 128) || V % 8 != 0 || conv > MAX_CONV) return PBGDN_ERR_UNSUPPORTED;
   const long channels = 2L * Hk * K + static_cast<long>(Hv) * V;
   if (qkv_stride < channels || decay_stride < 2L * Hv || qkv_stride % 8 != 0) return PBGDN_ERR_INVALID_ARGUMENT;
-  // A sequence's rows are addressed with 32-bit byte offsets below the out-of-range marker.
+  // A tile's rows (and the ends of a sequence) are addressed with 32-bit byte
+  // offsets from their first row, below the out-of-range marker.
   const long in_elem = in_dtype == PBGDN_F32 ? 4 : 2;
-  if (static_cast<long>(T) * qkv_stride * in_elem > 0x7ffffff0L - 64) return PBGDN_ERR_UNSUPPORTED;
+  if (static_cast<long>(TT + MAX_CONV) * qkv_stride * in_elem > 0x7ffffff0L - 64) return PBGDN_ERR_UNSUPPORTED;
   if (static_cast<long>(B) * T == 0) return PBGDN_OK;
   const bool has_tail = conv > 1;
   if (!qkv || !decay || !a_log || !dt_bias || !q || !k || !v || !g || !beta || (conv > 0 && !conv_weight) ||
@@ -615,7 +636,7 @@ extern "C" int pbgdn_prologue_varlen_fwd(const void *qkv, long qkv_stride, const
   const long channels = 2L * Hk * K + static_cast<long>(Hv) * V;
   if (qkv_stride < channels || decay_stride < 2L * Hv || qkv_stride % 8 != 0) return PBGDN_ERR_INVALID_ARGUMENT;
   const long in_elem = in_dtype == PBGDN_F32 ? 4 : 2;
-  if (static_cast<long>(T) * qkv_stride * in_elem > 0x7ffffff0L - 64) return PBGDN_ERR_UNSUPPORTED;
+  if (static_cast<long>(TT + MAX_CONV) * qkv_stride * in_elem > 0x7ffffff0L - 64) return PBGDN_ERR_UNSUPPORTED;
   if (num_seqs == 0) return T == 0 ? PBGDN_OK : PBGDN_ERR_INVALID_ARGUMENT;
   const bool has_tail = conv > 1;
   if (!cu_seqlens || !qkv || !decay || !a_log || !dt_bias || !q || !k || !v || !g || !beta ||
@@ -660,10 +681,10 @@ extern "C" int pbgdn_epilogue_fwd(const void *o, int o_dtype, const void *gate, 
   if (!o || !gate || !o_norm || !out || !aligned16(o) || !aligned16(gate) || !aligned16(out)) {
     return PBGDN_ERR_INVALID_ARGUMENT;
   }
-  // 32-bit byte offsets below the out-of-range marker for o and the gate rows
-  const long o_bytes = rows * V * (o_dtype == PBGDN_F32 ? 4 : 2);
-  const long g_bytes = static_cast<long>(B) * T * gate_stride * (gate_dtype == PBGDN_F32 ? 4 : 2);
-  if (o_bytes > 0x7ffffff0L - 64 || g_bytes > 0x7ffffff0L - 64) return PBGDN_ERR_UNSUPPORTED;
+  // 32-bit byte offsets below the out-of-range marker for a workgroup's gate
+  // rows: its LNT / (V / 8) rows span at most that many tokens plus one
+  const long wg_tokens = LNT / (V / 8) + 1;
+  if (wg_tokens * gate_stride * (gate_dtype == PBGDN_F32 ? 4 : 2) > 0x7ffffff0L - 64) return PBGDN_ERR_UNSUPPORTED;
   EpilogueParams prm{o, gate, o_norm, out, gate_stride, o_dtype, gate_dtype, out_dtype, rows, Hv, V, eps};
   const long rows_per_wg = LNT / (V / 8) * EPI_ROWS;
   const long blocks = (rows + rows_per_wg - 1) / rows_per_wg;

@@ -42,9 +42,16 @@ DECODE_HEAD_DIMS = (64, 128)
 MAX_CONV = 4
 
 
+def _dense_rows(x: torch.Tensor) -> bool:
+    """Token rows of one stride across the batch, unit column stride (a column
+    or token slice of a contiguous [B,T,C] tensor; with B = 1 the batch stride
+    is not used, so a token slice of one batch row qualifies)."""
+    return x.stride(-1) == 1 and (x.shape[0] <= 1 or x.stride(0) == x.shape[1] * x.stride(1))
+
+
 def _rows(x: torch.Tensor, name: str) -> int:
     """Row stride (elements per token) of a [B,T,C] tensor or column slice of one."""
-    if x.ndim != 3 or x.stride(-1) != 1 or x.stride(0) != x.shape[1] * x.stride(1):
+    if x.ndim != 3 or not _dense_rows(x):
         raise ValueError(f"{name} must be a [B,T,C] tensor with unit column stride and dense rows "
                          "(a column slice of a contiguous projection is fine)")
     return x.stride(1)
@@ -81,7 +88,7 @@ def layer_prologue(z: torch.Tensor, tail: torch.Tensor | None, conv_weight: torc
     if z.ndim != 3 or z.shape[-1] != channels + vwidth + 2 * value_heads:
         raise ValueError(f"z must be [B,T,{channels + vwidth + 2 * value_heads}] "
                          "([q | k | v | gate | a | b])")
-    if z.stride(-1) != 1 or z.stride(0) != z.shape[1] * z.stride(1):
+    if not _dense_rows(z):
         z = z.contiguous()  # the kernel addresses token rows of one stride across the batch
     qkv, gate, decay = z.split((channels, vwidth, 2 * value_heads), dim=-1)
     batch, length, _ = z.shape
@@ -257,8 +264,8 @@ def layer_epilogue(o: torch.Tensor, gate: torch.Tensor, o_norm: torch.Tensor, ep
     if norm.shape != (dv,):
         raise ValueError(f"o_norm must be [{dv}]")
     out = torch.empty(batch, length, hv * dv, dtype=out_dtype, device=dev)
-    if (gate.stride(-1) != 1 or gate.stride(0) != gate.shape[1] * gate.stride(1) or gate.stride(1) % 8
-            or gate.data_ptr() % 16):  # one row stride across the batch, 16-byte row pieces
+    # one row stride across the batch, 16-byte row pieces
+    if not _dense_rows(gate) or gate.stride(1) % 8 or gate.data_ptr() % 16:
         gate = gate.contiguous()
     status = _lib.lib().pbgdn_epilogue_fwd(
         _lib.ptr(o), codes[o.dtype], _lib.ptr(gate), _rows(gate, "gate"), codes[gate.dtype], _lib.ptr(norm),
@@ -302,8 +309,8 @@ def chunk_layer_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.
     norm = o_norm.to(device=dev, dtype=torch.float32).contiguous()
     if norm.shape != (dv,):
         raise ValueError(f"o_norm must be [{dv}]")
-    if (gate.stride(-1) != 1 or gate.stride(0) != gate.shape[1] * gate.stride(1) or gate.stride(1) % 8
-            or gate.data_ptr() % 16):  # one row stride across the batch, 16-byte row pieces
+    # one row stride across the batch, 16-byte row pieces
+    if not _dense_rows(gate) or gate.stride(1) % 8 or gate.data_ptr() % 16:
         gate = gate.contiguous()
     hs = torch.empty(batch, length, hv * dv, dtype=out_dtype, device=dev)
     o = torch.empty(batch, length, hv, dv, dtype=q.dtype, device=dev)

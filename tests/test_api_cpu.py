@@ -124,3 +124,15 @@ def test_head_widths_route_to_kernels_that_run():
     assert torch.count_nonzero(p[..., 5:, :]) == 0 and torch.count_nonzero(p[..., :, 7:]) == 0
     # float64 (the reference's check precision) is not a device dtype: the gate says so
     assert not gd.hip_usable(torch.zeros(1, 2, 64, 64, dtype=torch.float64))
+
+
+def test_layer_row_stride_accepts_token_slices_of_one_batch_row():
+    """The layer kernels address token rows of one stride across the batch:
+    a token slice of a single batch row keeps the full tensor's batch stride,
+    which a batch of one never uses, so it passes; with B = 2 it does not."""
+    from pseudobrain_amd.layer import _rows
+    z = torch.empty(1, 100, 64)
+    assert _rows(z[:, 10:60], "z") == 64
+    assert _rows(z[:, 10:60, 16:48], "z") == 64  # a column slice as well
+    with pytest.raises(ValueError, match="dense rows"):
+        _rows(torch.empty(2, 100, 64)[:, 10:60], "z")

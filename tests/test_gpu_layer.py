@@ -169,6 +169,63 @@ def test_epilogue_streamed_matches_cached():
     assert err <= F32_TOL
 
 
+def test_prologue_past_2gib_equals_two_calls():
+    """98,304 tokens of the Qwen3-Next projection (24,704 bytes a row: 2.4 GB,
+    past 32-bit byte offsets from the sequence's start) in one call equal two
+    calls with the tail carried, bit for bit; its last tokens match the oracle
+    run on them with the rows before them as the tail."""
+    heads, dk, vheads, dv, conv = 16, 128, 32, 128, 4
+    length = 98304
+    channels = 2 * heads * dk + vheads * dv
+    gen = torch.Generator(device=DEV).manual_seed(60)
+    z = torch.randn(1, length, channels + vheads * dv + 2 * vheads, device=DEV, generator=gen).to(torch.bfloat16)
+    assert z.shape[1] * z.stride(1) * 2 > 2 ** 31
+    _, tail, w, a_log, dtb = make_layer_inputs(1, 1, heads, dk, vheads, dv, conv, torch.bfloat16, seed=61)
+    tail, w, a_log, dtb = [x.to(DEV) for x in (tail, w, a_log, dtb)]
+    whole = layer_prologue(z, tail, w, a_log, dtb, heads, dk, vheads, dv)
+    half = length // 2
+    first = layer_prologue(z[:, :half], tail, w, a_log, dtb, heads, dk, vheads, dv)
+    second = layer_prologue(z[:, half:], first[6], w, a_log, dtb, heads, dk, vheads, dv)
+    torch.cuda.synchronize()
+    for i in range(5):
+        assert torch.equal(torch.cat([first[i], second[i]], dim=1), whole[i]), i
+    assert torch.equal(second[6], whole[6])
+    last = 8
+    zs = z[:, length - last:].cpu()
+    ts = z[:, length - last - (conv - 1):length - last, :channels].float().cpu()
+    rq, rk, rv, rg, rb, rt = oracle_prologue(zs, ts, w.cpu(), a_log.cpu(), dtb.cpu(), heads, dk, vheads, dv, "max")
+    got = [x[:, length - last:] for x in whole[:5]]
+    errs = [rel_err(g_, r_) for g_, r_ in zip(got, (rq, rk, rv, rg, rb))]
+    print(f"[prologue T={length}] last tokens " + " ".join(f"{e:.2e}" for e in errs), flush=True)
+    assert max(errs[:3]) <= LOW_TOL and max(errs[3:]) <= F32_TOL
+    np.testing.assert_array_equal(to_numpy(whole[6].float()), rt.astype(np.float32))
+
+
+def test_epilogue_past_2gib_equals_two_calls():
+    """270,336 tokens x 32 heads x 128 (o 2.2 GB in bf16, past 32-bit byte
+    offsets from its start) in one call equal two calls, bit for bit; the last
+    rows match the oracle."""
+    length, hv, dv = 270336, 32, 128
+    gen = torch.Generator(device=DEV).manual_seed(62)
+    o = (torch.randn(1, length, hv, dv, device=DEV, generator=gen) * 0.3).to(torch.bfloat16)
+    gate = torch.randn(1, length, hv * dv, device=DEV, generator=gen).to(torch.bfloat16)
+    o_norm = torch.rand(dv, device=DEV, generator=gen) + 0.5
+    assert o.numel() * 2 > 2 ** 31
+    whole = layer_epilogue(o, gate, o_norm, 1e-5, out_dtype=torch.float32)
+    half = length // 2
+    parts = torch.cat([layer_epilogue(o[:, :half], gate[:, :half], o_norm, 1e-5, out_dtype=torch.float32),
+                       layer_epilogue(o[:, half:], gate[:, half:], o_norm, 1e-5, out_dtype=torch.float32)], dim=1)
+    torch.cuda.synchronize()
+    assert torch.equal(whole, parts)
+    del parts
+    last = 16
+    ref = ol.layer_epilogue(to_numpy(o[:, length - last:].float()), to_numpy(gate[:, length - last:].float()),
+                            to_numpy(o_norm), 1e-5)
+    err = rel_err(whole[:, length - last:], ref)
+    print(f"[epilogue T={length}] last rows rel_inf={err:.2e}", flush=True)
+    assert err <= F32_TOL
+
+
 def test_layer_prologue_operator_epilogue_against_the_oracle():
     """The whole GatedDeltaNetLayer core (gated_deltanet.py:415-441) at the
     Qwen3-Next head shape: fused prologue -> chunk operator -> fused epilogue
