@@ -43,6 +43,7 @@ import argparse
 import json
 import multiprocessing
 import re
+import statistics
 import sys
 import time
 
