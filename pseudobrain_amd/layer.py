@@ -32,7 +32,8 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .gated_deltanet import CHUNK, _chunk_args, _chunk_fwd, require_no_grad
+from .gated_deltanet import (CHUNK, _chunk_args, _chunk_fwd, _require_device, _state_pool, chunk_fwd_slots,
+                             require_no_grad)
 
 NORM_EPS = 1e-5           # gated_deltanet.py:72
 L2_MODES = ("max", "hf")  # gated_deltanet.py:57
@@ -290,13 +291,60 @@ def chunk_layer_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.
     as its own kernel. float32 inputs go through chunk_fwd (which scales them
     into the kernels' range) and layer_epilogue."""
     require_no_grad("chunk_layer_fwd", q, k, v, g, beta, h0, gate, o_norm)
-    codes = _lib.DTYPE_CODES
-    if out_dtype not in codes or gate.dtype not in codes:
-        raise ValueError("gate and out_dtype must be float32, bfloat16 or float16")
+    _epilogue_dtypes(gate, out_dtype)
     if q.dtype == torch.float32:
         o, final = _chunk_fwd(q, k, v, g, beta, scale, h0, cu_seqlens, output_final_state=output_final_state)
         return layer_epilogue(o, gate, o_norm, eps, out_dtype=out_dtype), final
     shapes, dev, q, k, v, g, beta, h0, cu_seqlens, nseq = _chunk_args(q, k, v, g, beta, h0, cu_seqlens)
+    batch, length, hk, hv, dk, dv = shapes
+    final = torch.empty(nseq, hv, dk, dv, dtype=torch.float32, device=dev) if output_final_state else None
+    hs = _chunk_layer(shapes, dev, q, k, v, g, beta, scale, cu_seqlens, nseq, gate, o_norm, eps, out_dtype,
+                      h0, final, _lib.F32, None, None, 0)
+    return hs, final
+
+
+def chunk_layer_fwd_slots(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
+                          scale: float, states: torch.Tensor, state_idx: torch.Tensor, gate: torch.Tensor,
+                          o_norm: torch.Tensor, eps: float = NORM_EPS, cu_seqlens: torch.Tensor | None = None,
+                          has_initial_state: torch.Tensor | None = None, *,
+                          out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """chunk_layer_fwd against a pool of state slots, as chunk_fwd_slots
+    (vLLM's per-request slots): sequence n starts from states[state_idx[n]]
+    (zeros where has_initial_state[n] is False or the slot is outside the
+    pool) and its final state goes back to that slot in the pool's dtype.
+    Returns hs [B,T,Hv*V] in out_dtype."""
+    require_no_grad("chunk_layer_fwd_slots", q, k, v, g, beta, states, gate, o_norm)
+    _epilogue_dtypes(gate, out_dtype)
+    if q.dtype == torch.float32:
+        o = chunk_fwd_slots(q, k, v, g, beta, scale, states, state_idx, cu_seqlens, has_initial_state)
+        return layer_epilogue(o, gate, o_norm, eps, out_dtype=out_dtype)
+    shapes, dev, q, k, v, g, beta, _, cu_seqlens, nseq = _chunk_args(q, k, v, g, beta, None, cu_seqlens)
+    batch, length, hk, hv, dk, dv = shapes
+    _require_device(states, state_idx, has_initial_state)
+    _state_pool(states, hv, dk, dv)
+    if states.device != dev:
+        raise ValueError("states must be on the device of q")
+    if state_idx.shape != (nseq,):
+        raise ValueError(f"state_idx must be [N] = [{nseq}]")
+    state_idx = state_idx.to(device=dev, dtype=torch.int32).contiguous()
+    if has_initial_state is not None:
+        if has_initial_state.shape != (nseq,):
+            raise ValueError(f"has_initial_state must be [N] = [{nseq}]")
+        has_initial_state = has_initial_state.to(device=dev, dtype=torch.uint8).contiguous()
+    return _chunk_layer(shapes, dev, q, k, v, g, beta, scale, cu_seqlens, nseq, gate, o_norm, eps, out_dtype,
+                        states, states, _lib.DTYPE_CODES[states.dtype], state_idx, has_initial_state,
+                        states.shape[0])
+
+
+def _epilogue_dtypes(gate, out_dtype):
+    codes = _lib.DTYPE_CODES
+    if out_dtype not in codes or gate.dtype not in codes:
+        raise ValueError("gate and out_dtype must be float32, bfloat16 or float16")
+
+
+def _chunk_layer(shapes, dev, q, k, v, g, beta, scale, cu_seqlens, nseq, gate, o_norm, eps, out_dtype,
+                 h0, ht, state_code, state_idx, has_initial_state, num_states):
+    """pbgdn_chunk_layer_fwd on checked operands; returns hs."""
     batch, length, hk, hv, dk, dv = shapes
     if dv not in EPILOGUE_VALUE_DIMS:
         raise ValueError(f"the epilogue supports value widths {EPILOGUE_VALUE_DIMS}")
@@ -312,20 +360,20 @@ def chunk_layer_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.
     # one row stride across the batch, 16-byte row pieces
     if not _dense_rows(gate) or gate.stride(1) % 8 or gate.data_ptr() % 16:
         gate = gate.contiguous()
+    codes = _lib.DTYPE_CODES
     hs = torch.empty(batch, length, hv * dv, dtype=out_dtype, device=dev)
     o = torch.empty(batch, length, hv, dv, dtype=q.dtype, device=dev)
-    final = torch.empty(nseq, hv, dk, dv, dtype=torch.float32, device=dev) if output_final_state else None
     lib = _lib.lib()
     ws_bytes = lib.pbgdn_chunk_workspace_size(batch, length, hv, nseq)
     workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     status = lib.pbgdn_chunk_layer_fwd(
         _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), codes[q.dtype], _lib.ptr(g), _lib.ptr(beta), codes[beta.dtype],
-        _lib.ptr(h0), _lib.ptr(final), _lib.F32, None, None, 0, _lib.ptr(cu_seqlens), nseq,
-        _lib.ptr(gate), _rows(gate, "gate"), codes[gate.dtype], _lib.ptr(norm), float(eps), _lib.ptr(hs),
-        codes[out_dtype], _lib.ptr(o), batch, length, hk, hv, dk, dv, float(scale), CHUNK, _lib.ptr(workspace),
-        ws_bytes, _lib.stream_handle(dev))
+        _lib.ptr(h0), _lib.ptr(ht), state_code, _lib.ptr(state_idx), _lib.ptr(has_initial_state), num_states,
+        _lib.ptr(cu_seqlens), nseq, _lib.ptr(gate), _rows(gate, "gate"), codes[gate.dtype], _lib.ptr(norm),
+        float(eps), _lib.ptr(hs), codes[out_dtype], _lib.ptr(o), batch, length, hk, hv, dk, dv, float(scale),
+        CHUNK, _lib.ptr(workspace), ws_bytes, _lib.stream_handle(dev))
     _lib.check(status, "pbgdn_chunk_layer_fwd")
-    return hs, final
+    return hs
 
 
 def decode_layer_step(z: torch.Tensor, conv_state: torch.Tensor | None, conv_weight: torch.Tensor | None,

@@ -15,7 +15,7 @@ import torch
 
 from oracle import layer as ol
 from pseudobrain_amd import gated_deltanet as gd
-from pseudobrain_amd.layer import chunk_layer_fwd, layer_epilogue
+from pseudobrain_amd.layer import chunk_layer_fwd, chunk_layer_fwd_slots, layer_epilogue
 from pseudobrain_amd.workloads import cu_seqlens_of, generate, to_numpy
 from tests.gpu_util import O_TOL, S_TOL, oracle, rel_err
 
@@ -106,3 +106,33 @@ def test_two_pass_shapes(batch, length, dv, gate_dtype):
 def test_float32_inputs():
     """float32 q, k, v go through chunk_fwd's range scaling and layer_epilogue."""
     check("fp32 inputs", layer_case(2, 150, 16, 32, 128, torch.float32, seed=12, v_scale=1e4))
+
+
+@pytest.mark.parametrize("state_dtype", [torch.float32, torch.bfloat16])
+def test_fused_with_state_slots(state_dtype):
+    """chunk_layer_fwd_slots: sequences start from their slots of a pool (a new
+    request without an initial state, a -1 slot) and write their final states
+    back in the pool's dtype; the other slots keep their contents."""
+    lengths = [100, 70, 0, 150]
+    n = len(lengths)
+    q, k, v, g, beta, _, gate, o_norm = layer_case(1, sum(lengths), 16, 32, 128, torch.bfloat16, 21, nstates=n)
+    pool = (torch.randn(9, 32, 128, 128, generator=torch.Generator().manual_seed(22)) * 0.02).to(state_dtype)
+    slots = torch.tensor([5, 0, 7, -1], dtype=torch.int32)
+    has_init = torch.tensor([1, 0, 1, 1], dtype=torch.uint8)
+    cu = cu_seqlens_of(lengths)
+    dpool = pool.to(DEV)
+    dev = [x.to(DEV) for x in (q, k, v, g, beta, gate, o_norm)]
+    with torch.no_grad():
+        hs = chunk_layer_fwd_slots(*dev[:5], 128 ** -0.5, dpool, slots.to(DEV), dev[5], dev[6], EPS, cu.to(DEV),
+                                   has_init.to(DEV))
+    torch.cuda.synchronize()
+    init = torch.stack([pool[5].float(), torch.zeros(32, 128, 128), pool[7].float(), torch.zeros(32, 128, 128)])
+    o_ref, s_ref = oracle(q, k, v, g, beta, 128 ** -0.5, init, cu_seqlens=cu)
+    hs_ref = ol.layer_epilogue(o_ref, to_numpy(gate.float()), to_numpy(o_norm), EPS)
+    got = dpool.cpu().float()
+    e_hs, e_s = rel_err(hs, hs_ref.reshape(hs.shape)), rel_err(got[[5, 0, 7]], s_ref[:3])
+    s_tol = S_TOL if state_dtype == torch.float32 else 1e-2
+    print(f"[fused slots {state_dtype}] hs rel_inf={e_hs:.2e} S rel_inf={e_s:.2e}", flush=True)
+    assert e_hs <= O_TOL and e_s <= s_tol
+    untouched = [1, 2, 3, 4, 6, 8]
+    assert torch.equal(dpool.cpu()[untouched], pool[untouched])
