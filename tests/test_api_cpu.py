@@ -100,6 +100,12 @@ def test_entry_points_without_backward_refuse_grad_before_anything_runs():
     with pytest.raises(RuntimeError, match="decode_layer_step has no backward"):
         layer.decode_layer_step(z[:, 0], None, None, torch.zeros(4), torch.zeros(4),
                                 torch.zeros(1, 4, 64, 64), torch.ones(64, requires_grad=True), 2, 64, 4, 64)
+    gate = torch.randn(q.shape[0], q.shape[1], v.shape[2] * v.shape[3])
+    with pytest.raises(RuntimeError, match="chunk_layer_fwd has no backward"):
+        layer.chunk_layer_fwd(q, k, v, g, beta, 0.1, h0, gate, torch.ones(v.shape[3]))
+    with pytest.raises(RuntimeError, match="chunk_layer_fwd_slots has no backward"):
+        layer.chunk_layer_fwd_slots(q, k, v, g, beta, 0.1, h0, torch.zeros(1, dtype=torch.int32), gate,
+                                    torch.ones(v.shape[3]))
     # under no_grad the guard is silent (and the CPU tensors are then refused)
     with torch.no_grad(), pytest.raises(RuntimeError, match="ROCm devices only"):
         gd.chunk_fwd(q, k, v, g, beta, 0.1, h0)
