@@ -222,9 +222,12 @@ extern "C" int pbgdn_chunk_layer_fwd(const void *q, const void *k, const void *v
     return PBGDN_ERR_INVALID_ARGUMENT;
   }
   if (!(V == 64 || V == 128)) return PBGDN_ERR_UNSUPPORTED;  // the epilogue's value widths
-  if (B > 0 && T > 0 && (!gate || !o_norm || !hs || !aligned16(gate) || !aligned16(hs))) {
-    return PBGDN_ERR_INVALID_ARGUMENT;
+  if (static_cast<long>(B) * T == 0) {  // no tokens: the final states only (h0 carried over)
+    return pbgdn_chunk_fwd(q, k, v, in_dtype, g, beta, beta_dtype, h0, ht, state_dtype, state_idx,
+                           has_initial_state, num_states, cu_seqlens, num_seqs, o, in_dtype, B, T, Hk, Hv, K, V,
+                           scale, chunk, workspace, workspace_bytes, stream);
   }
+  if (!gate || !o_norm || !hs || !aligned16(gate) || !aligned16(hs)) return PBGDN_ERR_INVALID_ARGUMENT;
   const bool fusable = K == 128 && V == 128 && (in_dtype == PBGDN_BF16 || in_dtype == PBGDN_F16) &&
                        gate_dtype == in_dtype && (hs_dtype == PBGDN_F32 || hs_dtype == in_dtype) &&
                        static_cast<long>(pbgdn::CH) * gate_stride * 2 <= 0x7fffffffL;
@@ -248,7 +251,7 @@ extern "C" int pbgdn_chunk_layer_fwd(const void *q, const void *k, const void *v
     }
   }
   // Two passes: o in the inputs' dtype, then the epilogue.
-  if (B > 0 && T > 0 && (!o || !aligned16(o))) return PBGDN_ERR_INVALID_ARGUMENT;
+  if (!o || !aligned16(o)) return PBGDN_ERR_INVALID_ARGUMENT;
   const int st = pbgdn_chunk_fwd(q, k, v, in_dtype, g, beta, beta_dtype, h0, ht, state_dtype, state_idx,
                                  has_initial_state, num_states, cu_seqlens, num_seqs, o, in_dtype, B, T, Hk, Hv, K,
                                  V, scale, chunk, workspace, workspace_bytes, stream);

@@ -46,7 +46,10 @@ MAX_CONV = 4
 def _dense_rows(x: torch.Tensor) -> bool:
     """Token rows of one stride across the batch, unit column stride (a column
     or token slice of a contiguous [B,T,C] tensor; with B = 1 the batch stride
-    is not used, so a token slice of one batch row qualifies)."""
+    is not used, so a token slice of one batch row qualifies, and an empty
+    tensor addresses no rows at all)."""
+    if x.numel() == 0:  # no rows are addressed
+        return True
     return x.stride(-1) == 1 and (x.shape[0] <= 1 or x.stride(0) == x.shape[1] * x.stride(1))
 
 

@@ -136,3 +136,14 @@ def test_fused_with_state_slots(state_dtype):
     assert e_hs <= O_TOL and e_s <= s_tol
     untouched = [1, 2, 3, 4, 6, 8]
     assert torch.equal(dpool.cpu()[untouched], pool[untouched])
+
+
+def test_no_tokens_carries_the_initial_states():
+    """T = 0 with 8 sequences (a batch the wide scan would take): hs is empty
+    and the final states are the initial ones."""
+    q, k, v, g, beta, h0, gate, o_norm = [x.to(DEV) for x in layer_case(8, 0, 16, 32, 128, torch.bfloat16, 30)]
+    with torch.no_grad():
+        hs, s = chunk_layer_fwd(q, k, v, g, beta, 128 ** -0.5, h0, gate, o_norm, EPS)
+    torch.cuda.synchronize()
+    assert hs.shape == (8, 0, 32 * 128)
+    assert torch.equal(s, h0)
