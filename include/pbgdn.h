@@ -123,9 +123,11 @@ const char *pbgdn_status_string(int status);
  * Ranges: the products run on fp16/bf16 MFMA operands with fp32 accumulation;
  * a chunk whose intermediate V - gamma K S leaves the fp16 range is scaled by
  * a power of two internally. With in_dtype F32, q and k enter as fp16
- * (|q|, |k| < 65504) and the state as an fp16 high/low pair (v and the state
- * within about +-4096); scale v and h0 by a power of two to meet that and
- * scale o and ht back (the recurrence is linear in v and h0).
+ * (|q|, |k| < 65504) and the state as an fp16 high/low pair; the call first
+ * computes on the device the power of two that brings max |v| and max |h0|
+ * (over the states it reads) within 1024, runs on the scaled v and h0 and
+ * scales o and ht back, exactly (the recurrence is linear in v and h0), so
+ * any finite float32 v and h0 are in range.
  */
 int pbgdn_chunk_fwd(const void *q, const void *k, const void *v, int in_dtype,
                     const float *g, const void *beta, int beta_dtype,
@@ -175,7 +177,8 @@ int pbgdn_chunk_layer_fwd(const void *q, const void *k, const void *v,
 /*
  * Bytes of workspace pbgdn_chunk_fwd needs for a call with these sizes
  * (B * T tokens in num_seqs sequences, Hv value heads): about 13 KiB per
- * 64-token chunk and value head. 0 for invalid sizes. No reference
+ * 64-token chunk and value head, plus 4 KiB (float32 inputs' range scale).
+ * 0 for invalid sizes. No reference
  * counterpart: the reference materialises the same per-chunk tensors
  * (gated_deltanet.py:143-157) with torch allocations.
  */

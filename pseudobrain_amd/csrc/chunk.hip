@@ -119,10 +119,85 @@ int scratch_for_stream(hipStream_t stream, unsigned char **out) {
 }  // namespace
 }  // namespace pbgdn
 
+namespace pbgdn {
+namespace {
+
+// float32 inputs enter the kernels' products as fp16-based operands (q, k as
+// fp16, v and the state as bf16 or fp16 high/low pairs), so v and the initial
+// states are brought within RANGE_LIMIT by a power of two first: the
+// recurrence is linear in (v, h0), and o and the final states of the scaled
+// inputs are the scaled results, exactly. Two small kernels compute it into
+// the workspace's tail (RANGE_BLOCKS partial maxima, then the scale), read by
+// the scan.
+constexpr float RANGE_LIMIT = 1024.f;
+constexpr int RANGE_BLOCKS = 512;
+constexpr long RANGE_TAIL_BYTES = 4096;
+static_assert((RANGE_BLOCKS + 1) * 4 <= RANGE_TAIL_BYTES, "range tail");
+
+struct RangeParams {
+  const float *v;
+  long nv;                      // elements of v
+  const void *h0;               // initial states or a pool of them (may be NULL)
+  int state_dtype;
+  const int32_t *state_idx;     // as ChunkParams
+  const uint8_t *has_initial_state;
+  int num_states, num_seqs;
+  long state_elems;             // Hv K V
+  float *part;                  // [RANGE_BLOCKS]
+};
+
+// Partial maxima of |v| and of |the initial states the call reads| (NaNs
+// are passed over; an infinity makes the scale 1).
+__global__ __launch_bounds__(256) void range_max_kernel(RangeParams p) {
+  float m = 0.f;
+  const long stride = static_cast<long>(gridDim.x) * 256;
+  for (long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x; i < p.nv; i += stride) m = fmaxf(m, fabsf(p.v[i]));
+  if (p.h0) {
+    for (int n = 0; n < p.num_seqs; ++n) {
+      const long slot = p.state_idx ? static_cast<long>(p.state_idx[n]) : static_cast<long>(n);
+      if ((p.state_idx && (slot < 0 || slot >= p.num_states)) || (p.has_initial_state && !p.has_initial_state[n])) {
+        continue;
+      }
+      for (long e = static_cast<long>(blockIdx.x) * 256 + threadIdx.x; e < p.state_elems; e += stride) {
+        m = fmaxf(m, fabsf(load_elem(p.h0, slot * p.state_elems + e, p.state_dtype)));
+      }
+    }
+  }
+  m = wave_max(m);
+  __shared__ float wm[4];
+  if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) p.part[blockIdx.x] = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+}
+
+// The scale: 2^-e with e = max(0, ceil(log2(max / RANGE_LIMIT))); 1 for a
+// maximum that is not finite.
+__global__ __launch_bounds__(256) void range_scale_kernel(const float *part, float *scale) {
+  float m = 0.f;
+  for (int i = threadIdx.x; i < RANGE_BLOCKS; i += 256) m = fmaxf(m, part[i]);
+  m = wave_max(m);
+  __shared__ float wm[4];
+  if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    m = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+    float down = 1.f;
+    if (__builtin_isfinite(m) && m > RANGE_LIMIT) {
+      int e = 0;
+      const float mant = frexpf(m / RANGE_LIMIT, &e);  // m / RANGE_LIMIT = mant 2^e, mant in [0.5, 1)
+      down = ldexpf(1.f, mant == 0.5f ? 1 - e : -e);   // 2^-ceil(log2(m / RANGE_LIMIT))
+    }
+    *scale = down;
+  }
+}
+
+}  // namespace
+}  // namespace pbgdn
+
 extern "C" size_t pbgdn_chunk_workspace_size(int B, int T, int Hv, int num_seqs) {
   if (B < 0 || T < 0 || Hv <= 0 || num_seqs < 0) return 0;
   const long records = pbgdn::chunk_records(static_cast<long>(B) * T, num_seqs);
-  return static_cast<size_t>(records) * Hv * pbgdn::REC_BYTES;
+  return static_cast<size_t>(records) * Hv * pbgdn::REC_BYTES + pbgdn::RANGE_TAIL_BYTES;
 }
 
 namespace pbgdn {
@@ -175,7 +250,7 @@ int chunk_setup(const void *q, const void *k, const void *v, int in_dtype, const
   const int groups = scan_groups(static_cast<long>(B) * T, num_seqs, pairs, shape.cus);
   p = ChunkParams{q, k, v, g, beta, beta_dtype, h0, ht, state_dtype, state_idx, has_initial_state,
                   num_states, cu_seqlens, o, static_cast<unsigned char *>(workspace), T, Hk, Hv, V,
-                  num_seqs, groups, scale, shape.cus, shape.xcds, nullptr, 0, nullptr, 0.f};
+                  num_seqs, groups, scale, shape.cus, shape.xcds, nullptr, 0, nullptr, 0.f, nullptr};
   return PBGDN_OK;
 }
 
@@ -196,6 +271,15 @@ extern "C" int pbgdn_chunk_fwd(const void *q, const void *k, const void *v, int 
                                     Hv, K, V, scale, chunk, workspace, workspace_bytes, p, records, empty);
   if (st != PBGDN_OK || empty) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (in_dtype == PBGDN_F32) {  // the range scale of v and the initial states, into the workspace's tail
+    float *part = reinterpret_cast<float *>(static_cast<unsigned char *>(workspace) + records * Hv * pbgdn::REC_BYTES);
+    pbgdn::RangeParams rp{static_cast<const float *>(v), static_cast<long>(B) * T * Hv * V, h0, state_dtype,
+                          state_idx, has_initial_state, num_states, num_seqs, static_cast<long>(Hv) * K * V, part};
+    hipLaunchKernelGGL(pbgdn::range_max_kernel, dim3(pbgdn::RANGE_BLOCKS), dim3(256), 0, s, rp);
+    hipLaunchKernelGGL(pbgdn::range_scale_kernel, dim3(1), dim3(256), 0, s, part, part + pbgdn::RANGE_BLOCKS);
+    if (hipGetLastError() != hipSuccess) return PBGDN_ERR_LAUNCH;
+    p.in_scale = part + pbgdn::RANGE_BLOCKS;
+  }
   switch (K) {
     case 64: return pbgdn::dispatch_in<64>(p, records, in_dtype, out_dtype, s);
     case 128: return pbgdn::dispatch_in<128>(p, records, in_dtype, out_dtype, s);

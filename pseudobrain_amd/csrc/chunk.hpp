@@ -101,6 +101,9 @@ struct ChunkParams {
   long gate_stride;   // elements per token row
   const float *o_norm;
   float eps;
+  // float32 inputs: the power of two that brings v and the initial states
+  // into the kernels' range (a device scalar written before the scan), or NULL
+  const float *in_scale;
 };
 
 // Sequence s (wave-uniform): first token and end. cu_seqlens is read through

@@ -138,9 +138,11 @@ struct ScanStage {
   uint32_t src[UPT];  // byte offset of the unit in its source (OUT_OF_RANGE if none)
   uint32_t dst[UPT];  // LDS byte offset of the unit within a chunk buffer
   bool v_wave;        // this loader wave's slot SLOT_V unit is V (else record); wave-uniform
+  float vscale;       // fp32 inputs: V's range scale (a power of two)
 
-  __device__ __forceinline__ void init(const ChunkParams &p, int l) {
+  __device__ __forceinline__ void init(const ChunkParams &p, int l, float in_down) {
     v_wave = __builtin_amdgcn_readfirstlane(l & ~63) < V_UNITS;
+    vscale = in_down;
 #pragma unroll
     for (int i = 0; i < UPT; ++i) {
       const int u = l + NLT * i;
@@ -210,11 +212,11 @@ struct ScanStage {
   __device__ __forceinline__ void store_unit(unsigned char *buf, const Regs &r, int l, int i) const {
     if (l + NLT * i >= UNITS) return;
     unsigned char *d = buf + dst[i];
-    if (EPU == 4 && i == SLOT_V && v_wave) {  // fp32 V: bf16 high and low parts (fp32 range)
+    if (EPU == 4 && i == SLOT_V && v_wave) {  // fp32 V, range-scaled: bf16 high and low parts
       const uint4 x = r.u[i];
       bf16x4_t hi, lo;
       OpOf<u16>::split(float4_t{__uint_as_float(x.x), __uint_as_float(x.y), __uint_as_float(x.z),
-                                __uint_as_float(x.w)}, hi, lo);
+                                __uint_as_float(x.w)} * vscale, hi, lo);
       *reinterpret_cast<bf16x4_t *>(d) = hi;
       *reinterpret_cast<bf16x4_t *>(d + (L::V16LO_OFF - L::V16_OFF)) = lo;
     } else if (EPU == 4 && i < SLOT_V) {
@@ -294,6 +296,9 @@ struct ScanBlock {
     long t0, eos, rec;  // this chunk's first token, s's end, this chunk's record
   } cc, lc, oc;
   float4_t sacc;
+  // fp32 inputs: v and the initial states enter scaled by in_down (a power of
+  // two, so exactly), o and the final states leave scaled back; 1 otherwise
+  float in_down, in_up;
   Stage stage;
   typename Stage::Regs regs[2];
   uint4 h0r[2][2];  // chained streams: loader thread's 16-byte units of a chunk's initial state, per register set
@@ -317,8 +322,13 @@ struct ScanBlock {
     s_begin = static_cast<int>(static_cast<long>(grp) * p.num_seqs / p.seq_groups);
     s_end = static_cast<int>(static_cast<long>(grp + 1) * p.num_seqs / p.seq_groups);
     sacc = float4_t{0.f, 0.f, 0.f, 0.f};
+    in_down = 1.f;
+    if constexpr (sizeof(TIn) == 4) {
+      if (p.in_scale) in_down = *p.in_scale;  // written by the range kernels earlier on the stream
+    }
+    in_up = 1.f / in_down;
     if (wave >= NCW) {
-      stage.init(p, lt);
+      stage.init(p, lt, in_down);
       constexpr int upr = VT * sizeof(TOut) / 16;  // units per output row
       out_src = lt < OUT_UNITS ? 16 * lt : 0;
       out_dst = lt < OUT_UNITS ? ((lt / upr) * p.Hv * p.V + (lt % upr) * (16 / sizeof(TOut))) * sizeof(TOut)
@@ -465,14 +475,15 @@ struct ScanBlock {
 #pragma unroll
       for (int i = 0; i < 4; ++i) x[i] = load_elem(p.h0, base + static_cast<long>(16 * kt + 4 * g4 + i) * p.V, p.state_dtype);
     }
-    return x;
+    return x * in_down;
   }
   __device__ __forceinline__ void final_state(int s, int kt, float4_t x) const {
     const long slot = slot_of(s);
     if (p.ht && in_pool(slot)) {
       const long base = (slot * p.Hv + h) * K * p.V + v0 + c16;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) store_elem(p.ht, base + static_cast<long>(16 * kt + 4 * g4 + i) * p.V, p.state_dtype, x[i]);
+      for (int i = 0; i < 4; ++i)
+        store_elem(p.ht, base + static_cast<long>(16 * kt + 4 * g4 + i) * p.V, p.state_dtype, x[i] * in_up);
     }
   }
   // sacc -> the S^T high/low operand copies in LDS (key tile kt).
@@ -514,6 +525,7 @@ struct ScanBlock {
                                                 : static_cast<float>(__builtin_bit_cast(half_t, x));
       }
     }
+    sacc *= in_down;
     final_state(done, kt, fin);
     put_state(kt);
   }
@@ -538,6 +550,13 @@ struct ScanBlock {
   __device__ __forceinline__ half8_t rec_frag(int b, int mat, int r, int kk) const {
     return ld<half8_t>(L::rec(b) + mat + frag_index(r, kk) * FRAG_BYTES + lane * 16);
   }
+  // The second contraction step's fragment f of row tile r. Rows of tiles 0
+  // and 1 vanish past column 31, so theirs is zero: every wave issues both
+  // products with no branch between them and the first read of the result.
+  // (With a branch around the second product, hipcc placed reads after the
+  // join fewer wait states behind it than a 16x16x32 product needs, and read
+  // stale result registers.)
+  static __device__ __forceinline__ half8_t second_step(const half8_t &f, int r) { return r >= 2 ? f : half8_t{}; }
 
   // Operands are read from LDS one phase before the phase that uses them, so
   // that each phase waits only for what the previous phase produced. The two
@@ -613,7 +632,7 @@ struct ScanBlock {
         slo[kk] = ld<O8>(L::SL + kp_frag + 64 * kk);
       }
       f0 = rec_frag(b, REC_TB, r, 0);
-      f1 = rec_frag(b, REC_TB, r, 1);  // row tiles 0, 1: unused
+      f1 = second_step(rec_frag(b, REC_TB, r, 1), r);
       dd = rec_rows(b, SC_DEC, r);
       float4_t acc = {0.f, 0.f, 0.f, 0.f}, acl = acc;
 #pragma unroll
@@ -643,17 +662,19 @@ struct ScanBlock {
       // multiply tile t (tokens 8g.. of step kk: tile 2 kk + g/2) take
       // d / downs[t] (a power of two, at most 1)
       const float d = fminf(fminf(downs[0], downs[1]), fminf(downs[2], downs[3]));
+      const float rd = d < 1.f ? 1.f / d : 1.f;
       if (d < 1.f) {
         const int t = g4 >> 1;
         f0 *= static_cast<half_t>(d / downs[t]);
         f1 *= static_cast<half_t>(d / downs[2 + t]);
       }
+      // no branch between the products and their first reads
       float4_t u = mfma32(f0, x0, float4_t{0.f, 0.f, 0.f, 0.f});
-      if (r >= 2) u = mfma32(f1, x1, u);
+      u = mfma32(f1, x1, u);
       const uint32_t o = sp_tile + 32 * r;
       st(L::ut(b) + o, to_half4(u));  // U' = U d, for O of this chunk
       if (wave == 0 && lane == 0) st(L::RS + 16 + 4 * b, d);
-      if (d < 1.f) u *= 1.f / d;
+      u *= rd;
       const float4_t du = u * dd;
       const O4 hi = Op::from(du);
       st(L::UH + o, hi);
@@ -683,11 +704,13 @@ struct ScanBlock {
     const int r = wave & 3;
     // U^T of the chunk holds U d (d its range scale, usually 1): O = (scale gamma Q S d + QKD U d) / d
     const float d = ld<float>(L::RS + 16 + 4 * ob);
+    const float rd = (d < 1.f ? 1.f / d : 1.f) * in_up;  // powers of two: exact
     float4_t o = qs * gs;
     if (d < 1.f) o *= d;
+    // no branch between the products and their first reads
     o = mfma32(f0, ld<half8_t>(L::ut(ob) + sp_frag), o);
-    if (r >= 2) o = mfma32(f1, ld<half8_t>(L::ut(ob) + sp_frag + 64), o);
-    if (d < 1.f) o *= 1.f / d;
+    o = mfma32(f1, ld<half8_t>(L::ut(ob) + sp_frag + 64), o);
+    o *= rd;
 #pragma unroll
     for (int i = 0; i < 4; ++i) st(L::ot(ob) + ((16 * r + 4 * g4 + i) * VT + c16) * sizeof(TOut), out_elem<TOut>(o[i]));
   }
@@ -716,7 +739,7 @@ struct ScanBlock {
     block_sync();
     {
       const half8_t n0 = rec_frag(b, REC_QKD, r, 0);
-      const half8_t n1 = rec_frag(b, REC_QKD, r, 1);  // row tiles 0, 1: unused
+      const half8_t n1 = second_step(rec_frag(b, REC_QKD, r, 1), r);
       const float4_t ngs = rec_rows(b, SC_GSC, r);
       if constexpr (NKT > 4) fetch_kt(b, kt);
       if (n > 0) out_tile(b ^ 1, qs_prev, gs, f0, f1);

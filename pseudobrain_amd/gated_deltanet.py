@@ -158,23 +158,6 @@ def chunk_fwd(q, k, v, g, beta, scale: float, h0=None, cu_seqlens=None, *,
                       output_final_state=output_final_state, out=out)
 
 
-# fp32 inputs enter the chunk kernels' products as fp16 (include/pbgdn.h);
-# v and the initial state are brought inside FP32_INPUT_LIMIT by a power of two.
-FP32_INPUT_LIMIT = 1024.0
-
-
-def _fp32_range_scale(v, h0):
-    """2^-e (e >= 0, a 0-dim device tensor): the least power that brings
-    max(|v|, |h0|) to at most FP32_INPUT_LIMIT. The recurrence is linear in
-    (v, h0), so o and the final state of the scaled inputs are the scaled
-    results, exactly (powers of two)."""
-    amax = v.abs().amax()
-    if h0 is not None:
-        amax = torch.maximum(amax, h0.abs().amax())
-    e = torch.clamp(torch.ceil(torch.log2(amax / FP32_INPUT_LIMIT)), min=0.0)
-    return torch.exp2(-torch.nan_to_num(e, nan=0.0, posinf=0.0))
-
-
 def _chunk_args(q, k, v, g, beta, h0, cu_seqlens):
     """Checked operands of a chunk-kernel call: (shapes, device, q, k, v, g, beta,
     h0 as contiguous fp32 or None, cu_seqlens as int32 or None, N)."""
@@ -207,12 +190,8 @@ def _chunk_fwd(q, k, v, g, beta, scale: float, h0=None, cu_seqlens=None, *,
         raise ValueError(f"chunk kernel writes o as float32 or q's dtype ({q.dtype}), not {out_dtype}")
     shapes, dev, q, k, v, g, beta, h0, cu_seqlens, nseq = _chunk_args(q, k, v, g, beta, h0, cu_seqlens)
     batch, length, hk, hv, dk, dv = shapes
-    down = None
-    if q.dtype == torch.float32:
-        down = _fp32_range_scale(v, h0)
-        v = (v * down).contiguous()
-        if h0 is not None:
-            h0 = (h0 * down).contiguous()
+    # (float32 inputs: the library scales v and h0 into its products' range
+    # on the device and the results back, include/pbgdn.h)
     out_dtype = q.dtype if out_dtype is None else out_dtype
     if out is None:
         out = torch.empty(batch, length, hv, dv, dtype=out_dtype, device=dev)
@@ -229,32 +208,7 @@ def _chunk_fwd(q, k, v, g, beta, scale: float, h0=None, cu_seqlens=None, *,
         _lib.ptr(out), codes[out_dtype], batch, length, hk, hv, dk, dv, float(scale), CHUNK,
         _lib.ptr(workspace), ws_bytes, _lib.stream_handle(dev))
     _lib.check(status, "pbgdn_chunk_fwd")
-    if down is not None:
-        out.div_(down)
-        if final is not None:
-            final.div_(down)
     return out, final
-
-
-def _chunk_slots_fp32(q, k, v, g, beta, scale, states, state_idx, cu_seqlens, has_initial_state, out_dtype, out):
-    """chunk_fwd_slots for fp32 inputs: the slots' states are gathered into an
-    initial state, the prefill runs through _chunk_fwd (which scales fp32
-    inputs into range), and the final states go back to their slots."""
-    nseq = cu_seqlens.numel() - 1 if cu_seqlens is not None else q.shape[0]
-    if state_idx.shape != (nseq,):
-        raise ValueError(f"state_idx must be [N] = [{nseq}]")
-    idx = state_idx.to(device=states.device, dtype=torch.long)
-    valid = (idx >= 0) & (idx < states.shape[0])
-    start = valid.clone()
-    if has_initial_state is not None:
-        if has_initial_state.shape != (nseq,):
-            raise ValueError(f"has_initial_state must be [N] = [{nseq}]")
-        start &= has_initial_state.to(device=states.device, dtype=torch.bool)
-    h0 = states[idx.clamp(0, states.shape[0] - 1)].float() * start.view(-1, 1, 1, 1)
-    o, final = _chunk_fwd(q, k, v, g, beta, scale, h0, cu_seqlens, out_dtype=out_dtype, out=out)
-    rows = idx[valid]
-    states[rows] = final[valid].to(states.dtype)
-    return o
 
 
 def _state_pool(states, hv, dk, dv):
@@ -282,9 +236,6 @@ def chunk_fwd_slots(q, k, v, g, beta, scale: float, states, state_idx, cu_seqlen
     if dk not in CHUNK_HEAD_DIMS or dv % 16:
         raise ValueError(f"chunk kernel supports K in {CHUNK_HEAD_DIMS} and V a multiple of 16")
     _state_pool(states, hv, dk, dv)
-    if q.dtype == torch.float32:  # through _chunk_fwd, which keeps fp32 inputs in range
-        return _chunk_slots_fp32(q, k, v, g, beta, scale, states, state_idx, cu_seqlens, has_initial_state,
-                                 out_dtype, out)
     q, k, v, g, beta = _operands(q, k, v, g, beta)
     if cu_seqlens is not None:
         if batch != 1:

@@ -141,11 +141,12 @@ def test_stream_probe_empty_is_ok():
 def test_chunk_workspace_size():
     lib = _lib.lib()
     rec = 13 * 1024  # bytes per (64-token chunk, value head) record
+    tail = 4096      # float32 inputs' range scale and its partial maxima
     # B*T tokens in N sequences: floor(B*T / 64) + N + 1 chunk records per value head
-    assert lib.pbgdn_chunk_workspace_size(1, 32768, 32, 1) == (512 + 2) * 32 * rec
-    assert lib.pbgdn_chunk_workspace_size(1, 262144, 32, 8) == (4096 + 9) * 32 * rec
-    assert lib.pbgdn_chunk_workspace_size(4, 100, 2, 4) == (6 + 5) * 2 * rec
-    assert lib.pbgdn_chunk_workspace_size(1, 0, 4, 1) == 2 * 4 * rec
+    assert lib.pbgdn_chunk_workspace_size(1, 32768, 32, 1) == (512 + 2) * 32 * rec + tail
+    assert lib.pbgdn_chunk_workspace_size(1, 262144, 32, 8) == (4096 + 9) * 32 * rec + tail
+    assert lib.pbgdn_chunk_workspace_size(4, 100, 2, 4) == (6 + 5) * 2 * rec + tail
+    assert lib.pbgdn_chunk_workspace_size(1, 0, 4, 1) == 2 * 4 * rec + tail
     assert lib.pbgdn_chunk_workspace_size(-1, 10, 4, 1) == 0
     assert lib.pbgdn_chunk_workspace_size(1, 10, 0, 1) == 0
 
