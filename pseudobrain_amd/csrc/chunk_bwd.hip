@@ -78,6 +78,30 @@ __device__ __forceinline__ float4_t tile_mm(float4_t acc, FA a, FB b) {
   return acc;
 }
 
+// The same sum with k grouped per lane: in each block of 16 k, lane group g
+// supplies k = 4g .. 4g+3 over four products (the products sum over all k,
+// so which k a step carries is free). a4(i, k) and b4(k, j) return the four
+// values a(i, k..k+3) and b(k..k+3, j): one 128-bit LDS read where they are
+// contiguous (ld4), else four reads 16 lanes x 4 groups wide that fall in
+// distinct banks for the padded strides used here (ld4s). U blocks unrolled.
+template <int KD, int U = 4, typename FA, typename FB>
+__device__ __forceinline__ float4_t tile_mm4(float4_t acc, FA a4, FB b4) {
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15, g = lane >> 4;
+#pragma unroll U
+  for (int kb = 0; kb < KD; kb += 16) {
+    const float4_t a = a4(c, kb + 4 * g), b = b4(kb + 4 * g, c);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = mfma_f32(a[j], b[j], acc);
+  }
+  return acc;
+}
+
+__device__ __forceinline__ float4_t ld4(const float *p) { return *reinterpret_cast<const float4_t *>(p); }
+__device__ __forceinline__ float4_t ld4s(const float *p, int stride) {
+  return float4_t{p[0], p[stride], p[2 * stride], p[3 * stride]};
+}
+
 __device__ __forceinline__ float4_t zero4() { return float4_t{0.f, 0.f, 0.f, 0.f}; }
 
 template <typename T>
@@ -114,38 +138,83 @@ __device__ __forceinline__ void decode16(const uint4 &u, float *x) {
   }
 }
 
+// Element idx of an LDS array of TIn, as float.
+template <typename TIn>
+__device__ __forceinline__ float ld_el(const TIn *m, int idx) {
+  if constexpr (sizeof(TIn) == 4) {
+    return m[idx];
+  } else if constexpr (dtype_of_bwd<TIn>() == PBGDN_BF16) {
+    return __uint_as_float(static_cast<uint32_t>(m[idx]) << 16);
+  } else {
+    return static_cast<float>(m[idx]);
+  }
+}
+
+// Four consecutive elements of TIn (idx a multiple of 4; one 8- or 16-byte
+// LDS read), and four elements `stride` apart, as float.
+template <typename TIn>
+__device__ __forceinline__ float4_t ld4e(const TIn *m, int idx) {
+  if constexpr (sizeof(TIn) == 4) {
+    return ld4(reinterpret_cast<const float *>(m) + idx);
+  } else {
+    const uint2 w = *reinterpret_cast<const uint2 *>(m + idx);
+    if constexpr (dtype_of_bwd<TIn>() == PBGDN_BF16) {
+      return float4_t{__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u), __uint_as_float(w.y << 16),
+                      __uint_as_float(w.y & 0xffff0000u)};
+    } else {
+      return float4_t{static_cast<float>(__builtin_bit_cast(half_t, static_cast<u16>(w.x & 0xffffu))),
+                      static_cast<float>(__builtin_bit_cast(half_t, static_cast<u16>(w.x >> 16))),
+                      static_cast<float>(__builtin_bit_cast(half_t, static_cast<u16>(w.y & 0xffffu))),
+                      static_cast<float>(__builtin_bit_cast(half_t, static_cast<u16>(w.y >> 16)))};
+    }
+  }
+}
+
+template <typename TIn>
+__device__ __forceinline__ float4_t ld4es(const TIn *m, int idx, int stride) {
+  return float4_t{ld_el(m, idx), ld_el(m, idx + stride), ld_el(m, idx + 2 * stride), ld_el(m, idx + 3 * stride)};
+}
+
+typedef __bf16 bh8_t __attribute__((ext_vector_type(8)));
+
+// x = hi + lo, each rounded to bf16 in turn (16 significant bits together),
+// as packed bf16 pairs: element j in bits 16 (j & 1) of word j >> 1. (The
+// words are taken apart with integer shifts: reading the elements of a
+// __bf16 vector one by one compiled to element 0 four times.)
+__device__ __forceinline__ void split_bf16(float4_t x, v2u32_t &hi, v2u32_t &lo) {
+  hi = __builtin_bit_cast(v2u32_t, __builtin_convertvector(x, bf16x4_t));
+  const float4_t back = {__uint_as_float(hi[0] << 16), __uint_as_float(hi[0] & 0xffff0000u),
+                         __uint_as_float(hi[1] << 16), __uint_as_float(hi[1] & 0xffff0000u)};
+  lo = __builtin_bit_cast(v2u32_t, __builtin_convertvector(x - back, bf16x4_t));
+}
+
+// bf16 MFMA: acc (16x16) += A (16x32) B (32x16). Lane l, c = l & 15, g = l >> 4:
+// A[m=c][k=8g..8g+7], B[k=8g..8g+7][n=c]; acc[r] is D[row 4g + r][col c].
+__device__ __forceinline__ float4_t mfma_bf16(bh8_t a, bh8_t b, float4_t acc) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+}
+
+// Rows row0 .. row0+15 of a [64][ldr] bf16 array (exact inputs) times a
+// state tile given as its transpose in two bf16 parts, hiT + loT ([16][lds],
+// x = hi + lo to 16 bits): sum over k < KD, on bf16 MFMA with fp32
+// accumulation. Both operands are read k-contiguous, 16 bytes a lane.
+template <int KD>
+__device__ __forceinline__ float4_t rows_times_state(const u16 *rows, int ldr, int row0, const u16 *hiT,
+                                                     const u16 *loT, int ldt) {
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 2
+  for (int kb = 0; kb < KD; kb += 32) {
+    const bh8_t a = *reinterpret_cast<const bh8_t *>(rows + (row0 + c) * ldr + kb + 8 * g);
+    acc = mfma_bf16(a, *reinterpret_cast<const bh8_t *>(hiT + c * ldt + kb + 8 * g), acc);
+    acc = mfma_bf16(a, *reinterpret_cast<const bh8_t *>(loT + c * ldt + kb + 8 * g), acc);
+  }
+  return acc;
+}
+
 // Workspace records of (batch b, value head h, chunk i).
 __device__ __forceinline__ long rec(const BwdParams &p, int b, int h, int i) {
   return (static_cast<long>(b) * p.Hv + h) * p.n + i;
-}
-
-// Rows t0 .. t0+63 of a [B,T,H,W] tensor of TIn (head hd, columns col0 ..
-// col0+COLS-1) into LDS as float, zero past T: 16-byte loads, all issued
-// before the first LDS write. W and col0 keep every row piece 16-byte aligned.
-template <typename TIn, int COLS>
-__device__ __forceinline__ void load_rows_vec(float *dst, int ld, const void *src, const BwdParams &p, int b, int t0,
-                                              int heads, int hd, int width, int col0) {
-  constexpr int EPP = 16 / sizeof(TIn), PPR = COLS / EPP, TOTAL = BC * PPR, PER = (TOTAL + BNT - 1) / BNT;
-  const unsigned char *base = static_cast<const unsigned char *>(src);
-  uint4 raw[PER];
-#pragma unroll
-  for (int m = 0; m < PER; ++m) {
-    const int e = threadIdx.x + BNT * m, row = e / PPR, part = e % PPR, t = t0 + row;
-    const long off = (((static_cast<long>(b) * p.T + t) * heads + hd) * width + col0) * static_cast<long>(sizeof(TIn));
-    raw[m] = e < TOTAL && t < p.T ? *reinterpret_cast<const uint4 *>(base + off + part * 16) : uint4{0u, 0u, 0u, 0u};
-  }
-#pragma unroll
-  for (int m = 0; m < PER; ++m) {
-    const int e = threadIdx.x + BNT * m, row = e / PPR, part = e % PPR;
-    if (e < TOTAL) {
-      float x[EPP];
-      decode16<TIn>(raw[m], x);
-#pragma unroll
-      for (int j = 0; j < EPP; j += 4) {
-        *reinterpret_cast<float4_t *>(&dst[row * ld + part * EPP + j]) = float4_t{x[j], x[j + 1], x[j + 2], x[j + 3]};
-      }
-    }
-  }
 }
 
 // A 64 x 64 float32 record (T) into LDS rows of LC floats.
@@ -177,43 +246,9 @@ __device__ __forceinline__ void load_decays(const BwdParams &p, int b, int h, in
   }
 }
 
-// A (strict lower) and M (lower, scaled) of one chunk from K K^T and Q K^T;
-// wave w writes rows 16w .. 16w+15.
-template <int K, bool WITH_A>
-__device__ __forceinline__ void form_a_m(const BwdParams &p, const float *sq, const float *sk, const float *sc,
-                                         const float *sbeta, float *sa, float *sm) {
-  constexpr int LK = K + 4;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 15, g4 = lane >> 4;
-  for (int tc = 0; tc < 4; ++tc) {
-    auto bk = [&](int kk, int j) { return sk[(16 * tc + j) * LK + kk]; };
-    float4_t kk_acc = zero4();
-    if constexpr (WITH_A) kk_acc = tile_mm<K>(kk_acc, [&](int r, int kk) { return sk[(16 * wave + r) * LK + kk]; }, bk);
-    const float4_t qk_acc = tile_mm<K>(zero4(), [&](int r, int kk) { return sq[(16 * wave + r) * LK + kk]; }, bk);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = 16 * wave + 4 * g4 + r, s = 16 * tc + c;
-      const float d = t >= s ? expf(sc[t] - sc[s]) : 0.f;
-      if constexpr (WITH_A) sa[t * LC + s] = t > s ? sbeta[t] * kk_acc[r] * d : 0.f;
-      sm[t * LC + s] = p.scale * qk_acc[r] * d;
-    }
-  }
-}
-
 // ---------------------------------------------------------------------------
 // Per (chunk, value head): T, dU0 = M^T dO, J = scale (Gamma Q)^T dO, c.
 // ---------------------------------------------------------------------------
-// Element idx of an LDS array of TIn, as float.
-template <typename TIn>
-__device__ __forceinline__ float ld_el(const TIn *m, int idx) {
-  if constexpr (sizeof(TIn) == 4) {
-    return m[idx];
-  } else if constexpr (dtype_of_bwd<TIn>() == PBGDN_BF16) {
-    return __uint_as_float(static_cast<uint32_t>(m[idx]) << 16);
-  } else {
-    return static_cast<float>(m[idx]);
-  }
-}
-
 // Rows t0 .. t0+63 of a [B,T,H,W] tensor of TIn (head hd, columns 0 ..
 // COLS-1) into LDS as they are (16-byte pieces; rows of ld elements, ld a
 // multiple of 16 bytes), zero past T.
@@ -273,11 +308,11 @@ __global__ __launch_bounds__(BNT) void bwd_local_kernel(BwdParams p) {
     p.ws_c[rec(p, b, h, i) * BC + lane] = x;
   }
   __syncthreads();
-  auto krow = [&](int kk, int j, int tc) { return ld_el(sk, (16 * tc + j) * LK + kk); };
+  auto krow = [&](int kk, int j, int tc) { return ld4e(sk, (16 * tc + j) * LK + kk); };
   // A = strict_lower(beta_t (K K^T) o D), rows 16w .. of this wave
   for (int tc = 0; tc < 4; ++tc) {
-    const float4_t kk_acc = tile_mm<K>(zero4(), [&](int r, int kk) { return ld_el(sk, (16 * wave + r) * LK + kk); },
-                                       [&](int kk, int j) { return krow(kk, j, tc); });
+    const float4_t kk_acc = tile_mm4<K>(zero4(), [&](int r, int kk) { return ld4e(sk, (16 * wave + r) * LK + kk); },
+                                        [&](int kk, int j) { return krow(kk, j, tc); });
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = 16 * wave + 4 * g4 + r, s2 = 16 * tc + c;
@@ -327,8 +362,8 @@ __global__ __launch_bounds__(BNT) void bwd_local_kernel(BwdParams p) {
   for (int e = tid; e < BC * BC; e += BNT) wt[e] = sa[(e / BC) * LC + e % BC];
   __syncthreads();  // T is out: M = scale (Q K^T) o D takes its place
   for (int tc = 0; tc < 4; ++tc) {
-    const float4_t qk_acc = tile_mm<K>(zero4(), [&](int r, int kk) { return ld_el(sq, (16 * wave + r) * LK + kk); },
-                                       [&](int kk, int j) { return krow(kk, j, tc); });
+    const float4_t qk_acc = tile_mm4<K>(zero4(), [&](int r, int kk) { return ld4e(sq, (16 * wave + r) * LK + kk); },
+                                        [&](int kk, int j) { return krow(kk, j, tc); });
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = 16 * wave + 4 * g4 + r, s2 = 16 * tc + c;
@@ -340,8 +375,12 @@ __global__ __launch_bounds__(BNT) void bwd_local_kernel(BwdParams p) {
   float *wu = p.ws_dU0 + rec(p, b, h, i) * BC * V;
   for (int tile = wave; tile < 4 * (V / 16); tile += 4) {
     const int tr = tile & 3, tv = tile >> 2;
-    const float4_t acc = tile_mm<BC>(zero4(), [&](int r, int s2) { return sa[s2 * LC + 16 * tr + r]; },
-                                     [&](int s2, int col) { return ld_el(sdo, s2 * LV + 16 * tv + col); });
+    const float4_t acc = tile_mm4<BC>(zero4(), [&](int r, int s2) { return ld4s(&sa[s2 * LC + 16 * tr + r], LC); },
+                                      [&](int s2, int col) {
+                                        const int e = s2 * LV + 16 * tv + col;
+                                        return float4_t{ld_el(sdo, e), ld_el(sdo, e + LV), ld_el(sdo, e + 2 * LV),
+                                                        ld_el(sdo, e + 3 * LV)};
+                                      });
 #pragma unroll
     for (int r = 0; r < 4; ++r) wu[(16 * tr + 4 * g4 + r) * V + 16 * tv + c] = acc[r];
   }
@@ -349,8 +388,17 @@ __global__ __launch_bounds__(BNT) void bwd_local_kernel(BwdParams p) {
   float *wj = p.ws_J + rec(p, b, h, i) * static_cast<long>(K) * V;
   for (int tile = wave; tile < (K / 16) * (V / 16); tile += 4) {
     const int tk = tile % (K / 16), tv = tile / (K / 16);
-    const float4_t acc = tile_mm<BC>(zero4(), [&](int r, int t) { return ld_el(sq, t * LK + 16 * tk + r) * sgam[t]; },
-                                     [&](int t, int col) { return ld_el(sdo, t * LV + 16 * tv + col); });
+    const float4_t acc = tile_mm4<BC>(
+        zero4(),
+        [&](int r, int t) {
+          const int e = t * LK + 16 * tk + r;
+          return float4_t{ld_el(sq, e), ld_el(sq, e + LK), ld_el(sq, e + 2 * LK), ld_el(sq, e + 3 * LK)} *
+                 ld4(&sgam[t]);
+        },
+        [&](int t, int col) {
+          const int e = t * LV + 16 * tv + col;
+          return float4_t{ld_el(sdo, e), ld_el(sdo, e + LV), ld_el(sdo, e + 2 * LV), ld_el(sdo, e + 3 * LV)};
+        });
 #pragma unroll
     for (int r = 0; r < 4; ++r) wj[(16 * tk + 4 * g4 + r) * V + 16 * tv + c] = p.scale * acc[r];
   }
@@ -492,8 +540,8 @@ __device__ __forceinline__ void state_pass(const BwdParams &p, float *lds, int b
     if (i + 1 < p.n) stage.load(p, b, h, hk, i + 1, v0);
     __syncthreads();
     // X = V - Gamma K S (rows 16w ..)
-    const float4_t ks = tile_mm<K>(zero4(), [&](int r, int kk) { return sk[(16 * wave + r) * LK + kk]; },
-                                   [&](int kk, int col) { return ss[kk * LT + col]; });
+    const float4_t ks = tile_mm4<K>(zero4(), [&](int r, int kk) { return ld4(&sk[(16 * wave + r) * LK + kk]); },
+                                    [&](int kk, int col) { return ld4s(&ss[kk * LT + col], LT); });
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = 16 * wave + 4 * g4 + r;
@@ -501,8 +549,9 @@ __device__ __forceinline__ void state_pass(const BwdParams &p, float *lds, int b
     }
     __syncthreads();
     // U = T diag(beta) X
-    const float4_t u = tile_mm<BC>(zero4(), [&](int r, int s2) { return st[(16 * wave + r) * LC + s2] * sbeta[s2]; },
-                                   [&](int s2, int col) { return sx[s2 * LT + col]; });
+    const float4_t u = tile_mm4<BC>(
+        zero4(), [&](int r, int s2) { return ld4(&st[(16 * wave + r) * LC + s2]) * ld4(&sbeta[s2]); },
+        [&](int s2, int col) { return ld4s(&sx[s2 * LT + col], LT); });
 #pragma unroll
     for (int r = 0; r < 4; ++r) su[(16 * wave + 4 * g4 + r) * LT + c] = u[r];
     __syncthreads();
@@ -511,8 +560,8 @@ __device__ __forceinline__ void state_pass(const BwdParams &p, float *lds, int b
 #pragma unroll
     for (int m = 0; m < PER; ++m) {
       const int k0 = 16 * (wave + 4 * m);
-      const float4_t y = tile_mm<BC>(zero4(), [&](int r, int t) { return sk[t * LK + k0 + r] * se[t]; },
-                                     [&](int t, int col) { return su[t * LT + col]; });
+      const float4_t y = tile_mm4<BC>(zero4(), [&](int r, int t) { return ld4s(&sk[t * LK + k0 + r], LK) * ld4(&se[t]); },
+                                      [&](int t, int col) { return ld4s(&su[t * LT + col], LT); });
 #pragma unroll
       for (int r = 0; r < 4; ++r) s[m][r] = gam_c * s[m][r] + y[r];
     }
@@ -564,8 +613,8 @@ __device__ __forceinline__ void adjoint_pass(const BwdParams &p, float *lds, int
     if (i > 0) stage.load(p, b, h, hk, i - 1, v0);
     __syncthreads();
     // dU = dU0 + E K dS'
-    const float4_t kd = tile_mm<K>(zero4(), [&](int r, int kk) { return sk[(16 * wave + r) * LK + kk]; },
-                                   [&](int kk, int col) { return sds[kk * LT + col]; });
+    const float4_t kd = tile_mm4<K>(zero4(), [&](int r, int kk) { return ld4(&sk[(16 * wave + r) * LK + kk]); },
+                                    [&](int kk, int col) { return ld4s(&sds[kk * LT + col], LT); });
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = 16 * wave + 4 * g4 + r;
@@ -573,9 +622,9 @@ __device__ __forceinline__ void adjoint_pass(const BwdParams &p, float *lds, int
     }
     __syncthreads();
     // dX = (T diag(beta))^T dU
-    const float4_t dx = tile_mm<BC>(
-        zero4(), [&](int r, int s2) { return st[s2 * LC + 16 * wave + r] * sbeta[16 * wave + r]; },
-        [&](int s2, int col) { return sdu[s2 * LT + col]; });
+    const float4_t dx = tile_mm4<BC>(
+        zero4(), [&](int r, int s2) { return ld4s(&st[s2 * LC + 16 * wave + r], LC) * sbeta[16 * wave + r]; },
+        [&](int s2, int col) { return ld4s(&sdu[s2 * LT + col], LT); });
 #pragma unroll
     for (int r = 0; r < 4; ++r) sdx[(16 * wave + 4 * g4 + r) * LT + c] = dx[r];
     __syncthreads();
@@ -584,8 +633,8 @@ __device__ __forceinline__ void adjoint_pass(const BwdParams &p, float *lds, int
 #pragma unroll
     for (int m = 0; m < PER; ++m) {
       const int k0 = 16 * (wave + 4 * m);
-      const float4_t y = tile_mm<BC>(zero4(), [&](int r, int t) { return sk[t * LK + k0 + r] * sgam[t]; },
-                                     [&](int t, int col) { return sdx[t * LT + col]; });
+      const float4_t y = tile_mm4<BC>(zero4(), [&](int r, int t) { return ld4s(&sk[t * LK + k0 + r], LK) * ld4(&sgam[t]); },
+                                      [&](int t, int col) { return ld4s(&sdx[t * LT + col], LT); });
 #pragma unroll
       for (int r = 0; r < 4; ++r) ds[m][r] = gam_c * ds[m][r] + jv[m][r] - y[r];
     }
@@ -637,9 +686,13 @@ constexpr int GNT = 512;
 
 template <int K, int V, typename TIn>
 __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
-  constexpr int LK = K + 4, KT = K / 16, KH = KT / 2;
+  constexpr int LK = K + 16 / sizeof(TIn), KT = K / 16, KH = KT / 2, LS = K + 8;
+  // bf16 inputs: K S, K dS' and Q S on bf16 MFMA (q, k exact; the state
+  // tiles as high + low parts); other input types on the fp32 MFMA
+  constexpr bool BF = std::is_same<TIn, u16>::value;
   extern __shared__ __align__(16) float lds[];
-  float *sq = lds, *sk = sq + BC * LK, *st = sk + BC * LK, *sm = st + BC * LC;
+  TIn *sq = reinterpret_cast<TIn *>(lds), *sk = sq + BC * LK;  // q, k rows as they are
+  float *st = reinterpret_cast<float *>(sk + BC * LK), *sm = st + BC * LC;
   float *area = sm + BC * LC;  // the value-column tiles, then three C x C matrices
   float *ss = area, *sds = ss + K * LT, *sx = sds + K * LT, *sdo = sx + BC * LT, *su = sdo + BC * LT;
   float *sdu = su + BC * LT, *sdx = sdu + BC * LT;
@@ -647,6 +700,9 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
   float *vec = area + (3 * BC * LC > 2 * K * LT + 5 * BC * LT ? 3 * BC * LC : 2 * K * LT + 5 * BC * LT);
   float *sc = vec, *sgam = sc + BC, *se = sgam + BC, *sbeta = se + BC;
   float *sdgam = sbeta + BC, *sde = sdgam + BC, *sdc = sde + BC, *sdb = sdc + BC, *sred = sdb + BC;
+  // bf16 inputs: the tile's S^T and dS'^T as high and low bf16 parts, [16][LS]
+  u16 *shT = reinterpret_cast<u16 *>(sred + GNT / 64 + 8), *slT = shT + 16 * LS, *dhT = slT + 16 * LS,
+      *dlT = dhT + 16 * LS;
   const int i = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 15, g4 = lane >> 4;
   const int half = wave >> 2, tw = 16 * (wave & 3);  // column half; this wave's token rows
@@ -654,8 +710,8 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
   const int hk = h / (p.Hv / p.Hk);
   const int t0 = i * BC;
   if (tid < BNT) {  // the loads run on the first four waves
-    load_rows_vec<TIn, K>(sq, LK, p.q, p, b, t0, p.Hk, hk, K, 0);
-    load_rows_vec<TIn, K>(sk, LK, p.k, p, b, t0, p.Hk, hk, K, 0);
+    load_rows_raw<TIn, K>(sq, LK, p.q, p, b, t0, p.Hk, hk, K);
+    load_rows_raw<TIn, K>(sk, LK, p.k, p, b, t0, p.Hk, hk, K);
     load_t(st, p.ws_T + rec(p, b, h, i) * BC * BC);
     load_decays(p, b, h, i, sc, sgam, se, sbeta);
     if (tid < BC) {
@@ -668,8 +724,8 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
   __syncthreads();
   // M = scale (Q K^T) o D, this wave's rows and column tiles 2 half, 2 half + 1
   for (int tc = 2 * half; tc < 2 * half + 2; ++tc) {
-    const float4_t qk = tile_mm<K, 4>(zero4(), [&](int r, int kk) { return sq[(tw + r) * LK + kk]; },
-                                   [&](int kk, int j) { return sk[(16 * tc + j) * LK + kk]; });
+    const float4_t qk = tile_mm4<K>(zero4(), [&](int r, int kk) { return ld4e(sq, (tw + r) * LK + kk); },
+                                 [&](int kk, int j) { return ld4e(sk, (16 * tc + j) * LK + kk); });
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = tw + 4 * g4 + r, s2 = 16 * tc + c;
@@ -714,6 +770,22 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
       const int e = tid + BNT * m;
       *reinterpret_cast<float4_t *>(&ss[(e >> 2) * LT + 4 * (e & 3)]) = rs[m];
       *reinterpret_cast<float4_t *>(&sds[(e >> 2) * LT + 4 * (e & 3)]) = rd[m];
+      if constexpr (BF) {  // column c0 + j of the tile -> row c0 + j of the transposes
+        const int kk = e >> 2, c0 = 4 * (e & 3);
+        v2u32_t hi, lo;
+        split_bf16(rs[m], hi, lo);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          shT[(c0 + j) * LS + kk] = static_cast<u16>(hi[j >> 1] >> (16 * (j & 1)));
+          slT[(c0 + j) * LS + kk] = static_cast<u16>(lo[j >> 1] >> (16 * (j & 1)));
+        }
+        split_bf16(rd[m], hi, lo);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          dhT[(c0 + j) * LS + kk] = static_cast<u16>(hi[j >> 1] >> (16 * (j & 1)));
+          dlT[(c0 + j) * LS + kk] = static_cast<u16>(lo[j >> 1] >> (16 * (j & 1)));
+        }
+      }
     }
     if (tid < BC * PPR) {
       float x[EPP], y[EPP];
@@ -727,8 +799,9 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
       }
     }
   };
-  auto rows_of = [&](const float *m2, int ld) { return [=](int r, int kk) { return m2[(tw + r) * ld + kk]; }; };
-  auto state_cols = [&](const float *m2) { return [=](int kk, int col) { return m2[kk * LT + col]; }; };
+  auto rows_of = [&](const float *m2, int ld) { return [=](int r, int kk) { return ld4(&m2[(tw + r) * ld + kk]); }; };
+  auto in_rows = [&](const TIn *m2) { return [=](int r, int kk) { return ld4e(m2, (tw + r) * LK + kk); }; };
+  auto state_cols = [&](const float *m2) { return [=](int kk, int col) { return ld4s(&m2[kk * LT + col], LT); }; };
   fetch(0);
   for (int v0 = 0; v0 < V; v0 += 16) {
     __syncthreads();  // the previous tile's readers are done (and sm is complete)
@@ -737,24 +810,35 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
     __syncthreads();
     float4_t ks = zero4(), kd = zero4();
     if (chain) {
-      ks = tile_mm<K, 4>(zero4(), rows_of(sk, LK), state_cols(ss));
-      kd = tile_mm<K, 4>(zero4(), rows_of(sk, LK), state_cols(sds));
+      if constexpr (BF) {
+        ks = rows_times_state<K>(sk, LK, tw, shT, slT, LS);
+        kd = rows_times_state<K>(sk, LK, tw, dhT, dlT, LS);
+      } else {
+        ks = tile_mm4<K>(zero4(), in_rows(sk), state_cols(ss));
+        kd = tile_mm4<K>(zero4(), in_rows(sk), state_cols(sds));
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int t = tw + 4 * g4 + r;
         sx[t * LT + c] -= sgam[t] * ks[r];  // X = V - Gamma K S
       }
     } else {
-      const float4_t qs = tile_mm<K, 4>(zero4(), rows_of(sq, LK), state_cols(ss));
+      float4_t qs;
+      if constexpr (BF) {
+        qs = rows_times_state<K>(sq, LK, tw, shT, slT, LS);
+      } else {
+        qs = tile_mm4<K>(zero4(), in_rows(sq), state_cols(ss));
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) dgam_r[r] += p.scale * qs[r] * sdo[(tw + 4 * g4 + r) * LT + c];
     }
     __syncthreads();
     if (chain) {
-      const float4_t u = tile_mm<BC, 4>(zero4(), [&](int r, int s2) { return st[(tw + r) * LC + s2] * sbeta[s2]; },
-                                     [&](int s2, int col) { return sx[s2 * LT + col]; });
-      float4_t du = tile_mm<BC, 4>(zero4(), [&](int r, int s2) { return sm[s2 * LC + tw + r]; },
-                                [&](int s2, int col) { return sdo[s2 * LT + col]; });
+      const float4_t u = tile_mm4<BC>(
+          zero4(), [&](int r, int s2) { return ld4(&st[(tw + r) * LC + s2]) * ld4(&sbeta[s2]); },
+          [&](int s2, int col) { return ld4s(&sx[s2 * LT + col], LT); });
+      float4_t du = tile_mm4<BC>(zero4(), [&](int r, int s2) { return ld4s(&sm[s2 * LC + tw + r], LC); },
+                                 [&](int s2, int col) { return ld4s(&sdo[s2 * LT + col], LT); });
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int t = tw + 4 * g4 + r;
@@ -766,9 +850,9 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
     }
     __syncthreads();
     if (chain) {
-      const float4_t dx = tile_mm<BC, 4>(
-          zero4(), [&](int r, int s2) { return st[s2 * LC + tw + r] * sbeta[tw + r]; },
-          [&](int s2, int col) { return sdu[s2 * LT + col]; });
+      const float4_t dx = tile_mm4<BC>(
+          zero4(), [&](int r, int s2) { return ld4s(&st[s2 * LC + tw + r], LC) * sbeta[tw + r]; },
+          [&](int s2, int col) { return ld4s(&sdu[s2 * LT + col], LT); });
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int t = tw + 4 * g4 + r;
@@ -786,18 +870,19 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
       const int tc = 2 * half + m;
-      dtb[m] = tile_mm<16, 4>(dtb[m], rows_of(sdu, LT), [&](int j, int col) { return sx[(16 * tc + col) * LT + j]; });
-      dm[m] = tile_mm<16, 4>(dm[m], rows_of(sdo, LT), [&](int j, int col) { return su[(16 * tc + col) * LT + j]; });
+      dtb[m] = tile_mm4<16>(dtb[m], rows_of(sdu, LT), [&](int j, int col) { return ld4(&sx[(16 * tc + col) * LT + j]); });
+      dm[m] = tile_mm4<16>(dm[m], rows_of(sdo, LT), [&](int j, int col) { return ld4(&su[(16 * tc + col) * LT + j]); });
     }
     // dQ += scale Gamma dO S^T;  dK += E U dS'^T - Gamma dX S^T (this wave's half of the key tiles)
 #pragma unroll
     for (int m = 0; m < KH; ++m) {
       const int kt = half * KH + m;
-      auto s_t = [&](int j, int col) { return ss[(16 * kt + col) * LT + j]; };
-      dq[m] = tile_mm<16, 4>(dq[m], [&](int r, int j) { return sdo[(tw + r) * LT + j] * sgam[tw + r] * p.scale; }, s_t);
-      dk[m] = tile_mm<16, 4>(dk[m], [&](int r, int j) { return su[(tw + r) * LT + j] * se[tw + r]; },
-                          [&](int j, int col) { return sds[(16 * kt + col) * LT + j]; });
-      dk[m] = tile_mm<16, 4>(dk[m], [&](int r, int j) { return -sdx[(tw + r) * LT + j] * sgam[tw + r]; }, s_t);
+      auto s_t = [&](int j, int col) { return ld4(&ss[(16 * kt + col) * LT + j]); };
+      dq[m] = tile_mm4<16>(dq[m], [&](int r, int j) { return ld4(&sdo[(tw + r) * LT + j]) * sgam[tw + r] * p.scale; },
+                           s_t);
+      dk[m] = tile_mm4<16>(dk[m], [&](int r, int j) { return ld4(&su[(tw + r) * LT + j]) * se[tw + r]; },
+                           [&](int j, int col) { return ld4(&sds[(16 * kt + col) * LT + j]); });
+      dk[m] = tile_mm4<16>(dk[m], [&](int r, int j) { return ld4(&sdx[(tw + r) * LT + j]) * -sgam[tw + r]; }, s_t);
     }
   }
   // per-token sums over the value columns (both halves add into sdgam)
@@ -835,8 +920,8 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
 #pragma unroll
   for (int m = 0; m < 2; ++m) {
     const int tc = 2 * half + m;
-    w4[m] = tile_mm<BC, 4>(zero4(), [&](int r, int u2) { return st[u2 * LC + tw + r]; },
-                        [&](int u2, int col) { return b2[u2 * LC + 16 * tc + col]; });
+    w4[m] = tile_mm4<BC>(zero4(), [&](int r, int u2) { return ld4s(&st[u2 * LC + tw + r], LC); },
+                         [&](int u2, int col) { return ld4s(&b2[u2 * LC + 16 * tc + col], LC); });
   }
   __syncthreads();
 #pragma unroll
@@ -850,10 +935,10 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
 #pragma unroll
   for (int m = 0; m < 2; ++m) {
     const int tc = 2 * half + m;
-    const float4_t da = tile_mm<BC, 4>(zero4(), [&](int r, int u2) { return b2[(tw + r) * LC + u2]; },
-                                    [&](int u2, int col) { return st[(16 * tc + col) * LC + u2]; });
-    const float4_t gk = tile_mm<K, 4>(zero4(), [&](int r, int kk) { return sk[(tw + r) * LK + kk]; },
-                                   [&](int kk, int col) { return sk[(16 * tc + col) * LK + kk]; });
+    const float4_t da = tile_mm4<BC>(zero4(), [&](int r, int u2) { return ld4(&b2[(tw + r) * LC + u2]); },
+                                     [&](int u2, int col) { return ld4(&st[(16 * tc + col) * LC + u2]); });
+    const float4_t gk = tile_mm4<K>(zero4(), [&](int r, int kk) { return ld4e(sk, (tw + r) * LK + kk); },
+                                    [&](int kk, int col) { return ld4e(sk, (16 * tc + col) * LK + kk); });
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = tw + 4 * g4 + r, s2 = 16 * tc + c;
@@ -877,11 +962,11 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
 #pragma unroll
   for (int m = 0; m < KH; ++m) {
     const int kt = half * KH + m;
-    auto kcol = [&](int s2, int col) { return sk[s2 * LK + 16 * kt + col]; };
-    dq[m] = tile_mm<BC, 4>(dq[m], [&](int r, int s2) { return b1[(tw + r) * LC + s2]; }, kcol);
-    dk[m] = tile_mm<BC, 4>(dk[m], [&](int r, int s2) { return b1[s2 * LC + tw + r]; },
-                        [&](int s2, int col) { return sq[s2 * LK + 16 * kt + col]; });
-    dk[m] = tile_mm<BC, 4>(dk[m], [&](int r, int s2) { return b3[(tw + r) * LC + s2]; }, kcol);
+    auto kcol = [&](int s2, int col) { return ld4es(sk, s2 * LK + 16 * kt + col, LK); };
+    dq[m] = tile_mm4<BC>(dq[m], [&](int r, int s2) { return ld4(&b1[(tw + r) * LC + s2]); }, kcol);
+    dk[m] = tile_mm4<BC>(dk[m], [&](int r, int s2) { return ld4s(&b1[s2 * LC + tw + r], LC); },
+                         [&](int s2, int col) { return ld4es(sq, s2 * LK + 16 * kt + col, LK); });
+    dk[m] = tile_mm4<BC>(dk[m], [&](int r, int s2) { return ld4(&b3[(tw + r) * LC + s2]); }, kcol);
   }
   // dq, dk: straight to the output without GQA, else per value head in float32
   const bool direct = p.Hk == p.Hv;
@@ -945,11 +1030,12 @@ __global__ __launch_bounds__(BNT) void bwd_gqa_reduce_kernel(BwdParams p) {
 // LDS bytes of each kernel.
 template <int K>
 constexpr size_t scan_lds() { return sizeof(float) * (BC * (K + 4) + BC * LC + K * LT + 2 * BC * LT + 4 * BC); }
-template <int K>
+template <int K, typename TIn>
 constexpr size_t grad_lds() {
-  return sizeof(float) * (2 * BC * (K + 4) + 2 * BC * LC +
-                          (3 * BC * LC > 2 * K * LT + 5 * BC * LT ? 3 * BC * LC : 2 * K * LT + 5 * BC * LT) +
-                          8 * BC + GNT / 64);
+  return sizeof(TIn) * 2 * BC * (K + 16 / sizeof(TIn)) +
+         sizeof(float) * (2 * BC * LC + (3 * BC * LC > 2 * K * LT + 5 * BC * LT ? 3 * BC * LC : 2 * K * LT + 5 * BC * LT) +
+                          8 * BC + GNT / 64 + 8) +
+         (std::is_same<TIn, u16>::value ? sizeof(u16) * 4 * 16 * (K + 8) : 0);
 }
 
 template <typename Kern>
@@ -964,7 +1050,7 @@ int launch(Kern kernel, dim3 grid, size_t lds, hipStream_t st, const BwdParams &
 
 template <int K, int V>
 int run_backward(const BwdParams &p, hipStream_t st) {
-  static_assert(grad_lds<K>() <= 160 * 1024 && local_lds<K, V, float>() <= 160 * 1024, "LDS budget");
+  static_assert(grad_lds<K, float>() <= 160 * 1024 && grad_lds<K, u16>() <= 160 * 1024 && local_lds<K, V, float>() <= 160 * 1024, "LDS budget");
   const dim3 per_chunk(p.n, p.Hv, p.B), per_tile2((V / 16) * p.Hv * 2 * p.B);
   int rc = PBGDN_OK;
   if (p.n > 0) {
@@ -983,9 +1069,9 @@ int run_backward(const BwdParams &p, hipStream_t st) {
   }
   if (rc == PBGDN_OK && p.n > 0) {
     switch (p.in_dtype) {
-      case PBGDN_F32: rc = launch(bwd_grad_kernel<K, V, float>, per_chunk, grad_lds<K>(), st, p, GNT); break;
-      case PBGDN_BF16: rc = launch(bwd_grad_kernel<K, V, u16>, per_chunk, grad_lds<K>(), st, p, GNT); break;
-      default: rc = launch(bwd_grad_kernel<K, V, half_t>, per_chunk, grad_lds<K>(), st, p, GNT); break;
+      case PBGDN_F32: rc = launch(bwd_grad_kernel<K, V, float>, per_chunk, grad_lds<K, float>(), st, p, GNT); break;
+      case PBGDN_BF16: rc = launch(bwd_grad_kernel<K, V, u16>, per_chunk, grad_lds<K, u16>(), st, p, GNT); break;
+      default: rc = launch(bwd_grad_kernel<K, V, half_t>, per_chunk, grad_lds<K, half_t>(), st, p, GNT); break;
     }
   }
   if (rc == PBGDN_OK && p.n > 0 && p.Hk != p.Hv) {
