@@ -212,6 +212,20 @@ __device__ __forceinline__ float4_t rows_times_state(const u16 *rows, int ldr, i
   return acc;
 }
 
+// Rows a0 .. a0+15 of one [64][ld] bf16 array times the transpose of rows
+// b0 .. b0+15 of another (exact inputs, sum over k < KD) on bf16 MFMA.
+template <int KD>
+__device__ __forceinline__ float4_t rows_times_rows(const u16 *a, const u16 *b, int ld, int a0, int b0) {
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 2
+  for (int kb = 0; kb < KD; kb += 32) {
+    acc = mfma_bf16(*reinterpret_cast<const bh8_t *>(a + (a0 + c) * ld + kb + 8 * g),
+                    *reinterpret_cast<const bh8_t *>(b + (b0 + c) * ld + kb + 8 * g), acc);
+  }
+  return acc;
+}
+
 // Workspace records of (batch b, value head h, chunk i).
 __device__ __forceinline__ long rec(const BwdParams &p, int b, int h, int i) {
   return (static_cast<long>(b) * p.Hv + h) * p.n + i;
@@ -311,8 +325,13 @@ __global__ __launch_bounds__(BNT) void bwd_local_kernel(BwdParams p) {
   auto krow = [&](int kk, int j, int tc) { return ld4e(sk, (16 * tc + j) * LK + kk); };
   // A = strict_lower(beta_t (K K^T) o D), rows 16w .. of this wave
   for (int tc = 0; tc < 4; ++tc) {
-    const float4_t kk_acc = tile_mm4<K>(zero4(), [&](int r, int kk) { return ld4e(sk, (16 * wave + r) * LK + kk); },
-                                        [&](int kk, int j) { return krow(kk, j, tc); });
+    float4_t kk_acc;
+    if constexpr (std::is_same<TIn, u16>::value) {
+      kk_acc = rows_times_rows<K>(sk, sk, LK, 16 * wave, 16 * tc);
+    } else {
+      kk_acc = tile_mm4<K>(zero4(), [&](int r, int kk) { return ld4e(sk, (16 * wave + r) * LK + kk); },
+                           [&](int kk, int j) { return krow(kk, j, tc); });
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = 16 * wave + 4 * g4 + r, s2 = 16 * tc + c;
@@ -362,8 +381,13 @@ __global__ __launch_bounds__(BNT) void bwd_local_kernel(BwdParams p) {
   for (int e = tid; e < BC * BC; e += BNT) wt[e] = sa[(e / BC) * LC + e % BC];
   __syncthreads();  // T is out: M = scale (Q K^T) o D takes its place
   for (int tc = 0; tc < 4; ++tc) {
-    const float4_t qk_acc = tile_mm4<K>(zero4(), [&](int r, int kk) { return ld4e(sq, (16 * wave + r) * LK + kk); },
-                                        [&](int kk, int j) { return krow(kk, j, tc); });
+    float4_t qk_acc;
+    if constexpr (std::is_same<TIn, u16>::value) {
+      qk_acc = rows_times_rows<K>(sq, sk, LK, 16 * wave, 16 * tc);
+    } else {
+      qk_acc = tile_mm4<K>(zero4(), [&](int r, int kk) { return ld4e(sq, (16 * wave + r) * LK + kk); },
+                           [&](int kk, int j) { return krow(kk, j, tc); });
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = 16 * wave + 4 * g4 + r, s2 = 16 * tc + c;
@@ -724,8 +748,13 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
   __syncthreads();
   // M = scale (Q K^T) o D, this wave's rows and column tiles 2 half, 2 half + 1
   for (int tc = 2 * half; tc < 2 * half + 2; ++tc) {
-    const float4_t qk = tile_mm4<K>(zero4(), [&](int r, int kk) { return ld4e(sq, (tw + r) * LK + kk); },
-                                 [&](int kk, int j) { return ld4e(sk, (16 * tc + j) * LK + kk); });
+    float4_t qk;
+    if constexpr (BF) {
+      qk = rows_times_rows<K>(sq, sk, LK, tw, 16 * tc);
+    } else {
+      qk = tile_mm4<K>(zero4(), [&](int r, int kk) { return ld4e(sq, (tw + r) * LK + kk); },
+                       [&](int kk, int j) { return ld4e(sk, (16 * tc + j) * LK + kk); });
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = tw + 4 * g4 + r, s2 = 16 * tc + c;
@@ -937,8 +966,13 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
     const int tc = 2 * half + m;
     const float4_t da = tile_mm4<BC>(zero4(), [&](int r, int u2) { return ld4(&b2[(tw + r) * LC + u2]); },
                                      [&](int u2, int col) { return ld4(&st[(16 * tc + col) * LC + u2]); });
-    const float4_t gk = tile_mm4<K>(zero4(), [&](int r, int kk) { return ld4e(sk, (tw + r) * LK + kk); },
-                                    [&](int kk, int col) { return ld4e(sk, (16 * tc + col) * LK + kk); });
+    float4_t gk;
+    if constexpr (BF) {
+      gk = rows_times_rows<K>(sk, sk, LK, tw, 16 * tc);
+    } else {
+      gk = tile_mm4<K>(zero4(), [&](int r, int kk) { return ld4e(sk, (tw + r) * LK + kk); },
+                       [&](int kk, int col) { return ld4e(sk, (16 * tc + col) * LK + kk); });
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = tw + 4 * g4 + r, s2 = 16 * tc + c;
