@@ -482,19 +482,25 @@ struct ScanStage {
     }
   }
 
-  // K rows, T, the decays and the tile into LDS (sk, st, vectors, tile).
-  __device__ __forceinline__ void store(float *sk, float *st, float *sc, float *sgam, float *se, float *sbeta,
+  // K rows, T, the decays and the tile into LDS (sk, st, vectors, tile). K
+  // rows go in as they are for bf16 inputs (rows of K + 8), else as float
+  // (rows of K + 4).
+  __device__ __forceinline__ void store(void *sk, float *st, float *sc, float *sgam, float *se, float *sbeta,
                                         float *tile) const {
-    constexpr int LK = K + 4;
     const int tid = threadIdx.x;
 #pragma unroll
     for (int m = 0; m < KP; ++m) {
       const int e = tid + BNT * m, row = e / ROW16, part = e % ROW16;
-      float x[EPP];
-      decode16<TIn>(kr[m], x);
+      if constexpr (std::is_same<TIn, u16>::value) {
+        *reinterpret_cast<uint4 *>(static_cast<u16 *>(sk) + row * (K + 8) + part * EPP) = kr[m];
+      } else {
+        float x[EPP];
+        decode16<TIn>(kr[m], x);
 #pragma unroll
-      for (int j = 0; j < EPP; j += 4) {
-        *reinterpret_cast<float4_t *>(&sk[row * LK + part * EPP + j]) = float4_t{x[j], x[j + 1], x[j + 2], x[j + 3]};
+        for (int j = 0; j < EPP; j += 4) {
+          *reinterpret_cast<float4_t *>(static_cast<float *>(sk) + row * (K + 4) + part * EPP + j) =
+              float4_t{x[j], x[j + 1], x[j + 2], x[j + 3]};
+        }
       }
     }
 #pragma unroll
@@ -530,10 +536,70 @@ struct ScanStage {
 // start. Wave w holds key-row tiles w, w+4 (K/64 of them) of the state. The
 // next chunk's inputs load during each step.
 // ---------------------------------------------------------------------------
+// LDS of one scan workgroup. bf16 inputs: K rows as they are and the state
+// tile as its transpose in bf16 high/low parts (for K S on bf16 MFMA); other
+// inputs: K rows and the state tile in float.
+template <int K, typename TIn>
+struct ScanLds {
+  static constexpr bool BF = std::is_same<TIn, u16>::value;
+  static constexpr int LK = BF ? K + 8 : K + 4, LS = K + 8;
+  static constexpr size_t K_BYTES = BF ? sizeof(u16) * BC * LK : sizeof(float) * BC * LK;
+  static constexpr size_t S_BYTES = BF ? sizeof(u16) * 2 * 16 * LS : sizeof(float) * K * LT;
+  static constexpr size_t BYTES = K_BYTES + sizeof(float) * BC * LC + S_BYTES + sizeof(float) * (2 * BC * LT + 4 * BC);
+};
+
+// K rows (row0 + r) times the state tile kept in LDS: bf16 MFMA on the high
+// and low parts of its transpose, or the fp32 MFMA on the float tile.
+template <int K, typename TIn>
+__device__ __forceinline__ float4_t k_times_state(const void *sk, int row0, const void *sstate) {
+  using L = ScanLds<K, TIn>;
+  if constexpr (L::BF) {
+    const u16 *hiT = static_cast<const u16 *>(sstate);
+    return rows_times_state<K>(static_cast<const u16 *>(sk), L::LK, row0, hiT, hiT + 16 * L::LS, L::LS);
+  } else {
+    const float *kf = static_cast<const float *>(sk), *sf = static_cast<const float *>(sstate);
+    return tile_mm4<K>(zero4(), [&](int r, int kk) { return ld4(&kf[(row0 + r) * L::LK + kk]); },
+                       [&](int kk, int col) { return ld4s(&sf[kk * LT + col], LT); });
+  }
+}
+
+// Rows kk0 .. kk0+3 (4 g4 + 16 m ..) of the state tile, column c, into LDS: the
+// float tile, or the high/low parts of its transpose (8 bytes each).
+template <int K, typename TIn>
+__device__ __forceinline__ void put_state_rows(void *sstate, int kk0, int c, float4_t x) {
+  using L = ScanLds<K, TIn>;
+  if constexpr (L::BF) {
+    u16 *hiT = static_cast<u16 *>(sstate);
+    v2u32_t hi, lo;
+    split_bf16(x, hi, lo);
+    *reinterpret_cast<v2u32_t *>(hiT + c * L::LS + kk0) = hi;
+    *reinterpret_cast<v2u32_t *>(hiT + 16 * L::LS + c * L::LS + kk0) = lo;
+  } else {
+    float *sf = static_cast<float *>(sstate);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sf[(kk0 + r) * LT + c] = x[r];
+  }
+}
+
+// (diag(w) K)^T rows k0 + r, four tokens t .. t+3 of the K rows in LDS.
+template <int K, typename TIn>
+__device__ __forceinline__ float4_t k_cols(const void *sk, int t, int col) {
+  using L = ScanLds<K, TIn>;
+  if constexpr (L::BF) {
+    return ld4es(static_cast<const u16 *>(sk), t * L::LK + col, L::LK);
+  } else {
+    return ld4s(static_cast<const float *>(sk) + t * L::LK + col, L::LK);
+  }
+}
+
 template <int K, typename TIn>
 __device__ __forceinline__ void state_pass(const BwdParams &p, float *lds, int b, int h, int v0) {
-  constexpr int LK = K + 4, PER = K / 64;
-  float *sk = lds, *st = sk + BC * LK, *ss = st + BC * LC, *sx = ss + K * LT, *su = sx + BC * LT;
+  using L = ScanLds<K, TIn>;
+  constexpr int PER = K / 64;
+  unsigned char *base = reinterpret_cast<unsigned char *>(lds);
+  void *sk = base, *ss = base + L::K_BYTES + sizeof(float) * BC * LC;
+  float *st = reinterpret_cast<float *>(base + L::K_BYTES);
+  float *sx = reinterpret_cast<float *>(static_cast<unsigned char *>(ss) + L::S_BYTES), *su = sx + BC * LT;
   float *sc = su + BC * LT, *sgam = sc + BC, *se = sgam + BC, *sbeta = se + BC;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 15, g4 = lane >> 4;
   const int hk = h / (p.Hv / p.Hk);
@@ -557,15 +623,14 @@ __device__ __forceinline__ void state_pass(const BwdParams &p, float *lds, int b
       for (int r = 0; r < 4; ++r) {
         const int kk = 16 * (wave + 4 * m) + 4 * g4 + r;
         ws[static_cast<long>(kk) * p.V + v0 + c] = s[m][r];
-        ss[kk * LT + c] = s[m][r];
       }
+      put_state_rows<K, TIn>(ss, 16 * (wave + 4 * m) + 4 * g4, c, s[m]);
     }
     stage.store(sk, st, sc, sgam, se, sbeta, sx);
     if (i + 1 < p.n) stage.load(p, b, h, hk, i + 1, v0);
     __syncthreads();
     // X = V - Gamma K S (rows 16w ..)
-    const float4_t ks = tile_mm4<K>(zero4(), [&](int r, int kk) { return ld4(&sk[(16 * wave + r) * LK + kk]); },
-                                    [&](int kk, int col) { return ld4s(&ss[kk * LT + col], LT); });
+    const float4_t ks = k_times_state<K, TIn>(sk, 16 * wave, ss);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = 16 * wave + 4 * g4 + r;
@@ -584,7 +649,7 @@ __device__ __forceinline__ void state_pass(const BwdParams &p, float *lds, int b
 #pragma unroll
     for (int m = 0; m < PER; ++m) {
       const int k0 = 16 * (wave + 4 * m);
-      const float4_t y = tile_mm4<BC>(zero4(), [&](int r, int t) { return ld4s(&sk[t * LK + k0 + r], LK) * ld4(&se[t]); },
+      const float4_t y = tile_mm4<BC>(zero4(), [&](int r, int t) { return k_cols<K, TIn>(sk, t, k0 + r) * ld4(&se[t]); },
                                       [&](int t, int col) { return ld4s(&su[t * LT + col], LT); });
 #pragma unroll
       for (int r = 0; r < 4; ++r) s[m][r] = gam_c * s[m][r] + y[r];
@@ -599,8 +664,12 @@ __device__ __forceinline__ void state_pass(const BwdParams &p, float *lds, int b
 // ---------------------------------------------------------------------------
 template <int K, typename TIn>
 __device__ __forceinline__ void adjoint_pass(const BwdParams &p, float *lds, int b, int h, int v0) {
-  constexpr int LK = K + 4, PER = K / 64;
-  float *sk = lds, *st = sk + BC * LK, *sds = st + BC * LC, *sdu = sds + K * LT, *sdx = sdu + BC * LT;
+  using L = ScanLds<K, TIn>;
+  constexpr int PER = K / 64;
+  unsigned char *base = reinterpret_cast<unsigned char *>(lds);
+  void *sk = base, *sds = base + L::K_BYTES + sizeof(float) * BC * LC;
+  float *st = reinterpret_cast<float *>(base + L::K_BYTES);
+  float *sdu = reinterpret_cast<float *>(static_cast<unsigned char *>(sds) + L::S_BYTES), *sdx = sdu + BC * LT;
   float *sc = sdx + BC * LT, *sgam = sc + BC, *se = sgam + BC, *sbeta = se + BC;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 15, g4 = lane >> 4;
   const int hk = h / (p.Hv / p.Hk);
@@ -624,8 +693,8 @@ __device__ __forceinline__ void adjoint_pass(const BwdParams &p, float *lds, int
       for (int r = 0; r < 4; ++r) {
         const int kk = 16 * (wave + 4 * m) + 4 * g4 + r;
         wds[static_cast<long>(kk) * p.V + v0 + c] = ds[m][r];
-        sds[kk * LT + c] = ds[m][r];
       }
+      put_state_rows<K, TIn>(sds, 16 * (wave + 4 * m) + 4 * g4, c, ds[m]);
     }
     stage.store(sk, st, sc, sgam, se, sbeta, sdu);
     float jv[PER][4];
@@ -637,8 +706,7 @@ __device__ __forceinline__ void adjoint_pass(const BwdParams &p, float *lds, int
     if (i > 0) stage.load(p, b, h, hk, i - 1, v0);
     __syncthreads();
     // dU = dU0 + E K dS'
-    const float4_t kd = tile_mm4<K>(zero4(), [&](int r, int kk) { return ld4(&sk[(16 * wave + r) * LK + kk]); },
-                                    [&](int kk, int col) { return ld4s(&sds[kk * LT + col], LT); });
+    const float4_t kd = k_times_state<K, TIn>(sk, 16 * wave, sds);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = 16 * wave + 4 * g4 + r;
@@ -657,7 +725,7 @@ __device__ __forceinline__ void adjoint_pass(const BwdParams &p, float *lds, int
 #pragma unroll
     for (int m = 0; m < PER; ++m) {
       const int k0 = 16 * (wave + 4 * m);
-      const float4_t y = tile_mm4<BC>(zero4(), [&](int r, int t) { return ld4s(&sk[t * LK + k0 + r], LK) * ld4(&sgam[t]); },
+      const float4_t y = tile_mm4<BC>(zero4(), [&](int r, int t) { return k_cols<K, TIn>(sk, t, k0 + r) * ld4(&sgam[t]); },
                                       [&](int t, int col) { return ld4s(&sdx[t * LT + col], LT); });
 #pragma unroll
       for (int r = 0; r < 4; ++r) ds[m][r] = gam_c * ds[m][r] + jv[m][r] - y[r];
@@ -1062,8 +1130,8 @@ __global__ __launch_bounds__(BNT) void bwd_gqa_reduce_kernel(BwdParams p) {
 }
 
 // LDS bytes of each kernel.
-template <int K>
-constexpr size_t scan_lds() { return sizeof(float) * (BC * (K + 4) + BC * LC + K * LT + 2 * BC * LT + 4 * BC); }
+template <int K, typename TIn>
+constexpr size_t scan_lds() { return ScanLds<K, TIn>::BYTES; }
 template <int K, typename TIn>
 constexpr size_t grad_lds() {
   return sizeof(TIn) * 2 * BC * (K + 16 / sizeof(TIn)) +
@@ -1096,9 +1164,9 @@ int run_backward(const BwdParams &p, hipStream_t st) {
   }
   if (rc == PBGDN_OK) {  // both scans in one launch (with T = 0 only the reverse one writes: dh0 = dht)
     switch (p.in_dtype) {
-      case PBGDN_F32: rc = launch(bwd_scans_kernel<K, float>, per_tile2, scan_lds<K>(), st, p); break;
-      case PBGDN_BF16: rc = launch(bwd_scans_kernel<K, u16>, per_tile2, scan_lds<K>(), st, p); break;
-      default: rc = launch(bwd_scans_kernel<K, half_t>, per_tile2, scan_lds<K>(), st, p); break;
+      case PBGDN_F32: rc = launch(bwd_scans_kernel<K, float>, per_tile2, scan_lds<K, float>(), st, p); break;
+      case PBGDN_BF16: rc = launch(bwd_scans_kernel<K, u16>, per_tile2, scan_lds<K, u16>(), st, p); break;
+      default: rc = launch(bwd_scans_kernel<K, half_t>, per_tile2, scan_lds<K, half_t>(), st, p); break;
     }
   }
   if (rc == PBGDN_OK && p.n > 0) {
