@@ -791,7 +791,11 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
   float *b1 = area, *b2 = b1 + BC * LC, *b3 = b2 + BC * LC;
   float *vec = area + (3 * BC * LC > 2 * K * LT + 5 * BC * LT ? 3 * BC * LC : 2 * K * LT + 5 * BC * LT);
   float *sc = vec, *sgam = sc + BC, *se = sgam + BC, *sbeta = se + BC;
-  float *sdgam = sbeta + BC, *sde = sdgam + BC, *sdc = sde + BC, *sdb = sdc + BC, *sred = sdb + BC;
+  float *sdgam = sbeta + BC, *sde = sdgam + BC;
+  // per-wave sums of the dc and dbeta terms: over this wave's token rows
+  // [wave][16] and over its two column tiles [wave][32]
+  float *prc = sde + BC, *prb = prc + 16 * (GNT / 64), *pcc = prb + 16 * (GNT / 64), *pcb = pcc + 32 * (GNT / 64);
+  float *sred = pcb + 32 * (GNT / 64);
   // bf16 inputs: the tile's S^T and dS'^T as high and low bf16 parts, [16][LS]
   u16 *shT = reinterpret_cast<u16 *>(sred + GNT / 64 + 8), *slT = shT + 16 * LS, *dhT = slT + 16 * LS,
       *dlT = dhT + 16 * LS;
@@ -809,8 +813,6 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
     if (tid < BC) {
       sdgam[tid] = 0.f;
       sde[tid] = 0.f;
-      sdc[tid] = 0.f;
-      sdb[tid] = 0.f;
     }
   }
   __syncthreads();
@@ -994,7 +996,10 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
   dgc = wave_sum(dgc);
   if (lane == 0) sred[wave] = dgc;
   __syncthreads();  // the value tiles are dead: the area now holds b1, b2, b3
-  // dM o Mt into b1 (and its dc terms); dT = dTb diag(beta) into b2 (and dbeta)
+  // dM o Mt into b1 (and its dc terms); dT = dTb diag(beta) into b2 (and
+  // dbeta). The dc and dbeta terms of token t are summed in registers: rc, rb
+  // for this lane's rows t = tw + 4 g4 + r, cc, cb for its columns 16 tc + c.
+  float rc[4] = {0.f, 0.f, 0.f, 0.f}, rb[4] = {0.f, 0.f, 0.f, 0.f}, cc[2] = {0.f, 0.f}, cb[2] = {0.f, 0.f};
 #pragma unroll
   for (int m = 0; m < 2; ++m) {
     const int tc = 2 * half + m;
@@ -1005,10 +1010,10 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
       const float dmv = t >= s2 ? dm[m][r] : 0.f;
       b1[t * LC + s2] = dmv * d;
       const float dcv = dmv * sm[t * LC + s2];
-      atomicAdd(&sdc[t], dcv);
-      atomicAdd(&sdc[s2], -dcv);
+      rc[r] += dcv;
+      cc[m] -= dcv;
       b2[t * LC + s2] = dtb[m][r] * sbeta[s2];
-      atomicAdd(&sdb[s2], dtb[m][r] * st[t * LC + s2]);
+      cb[m] += dtb[m][r] * st[t * LC + s2];
     }
   }
   __syncthreads();
@@ -1049,14 +1054,32 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
         const float dav = -da[r];
         const float av = sbeta[t] * gk[r] * d;
         const float hv = dav * sbeta[t] * d;
-        atomicAdd(&sdb[t], dav * gk[r] * d);
-        atomicAdd(&sdc[t], dav * av);
-        atomicAdd(&sdc[s2], -dav * av);
+        rb[r] += dav * gk[r] * d;
+        rc[r] += dav * av;
+        cc[m] -= dav * av;
         b3[t * LC + s2] = hv;
         b3[s2 * LC + t] = hv;
       } else if (t == s2) {
         b3[t * LC + s2] = 0.f;
       }
+    }
+  }
+  // the sums over this wave's lanes: a row's over its 16 column lanes, a
+  // column's over its 4 row groups
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float x = group_sum(rc[r], 16), y = group_sum(rb[r], 16);
+    if (c == 0) {
+      prc[16 * wave + 4 * g4 + r] = x;
+      prb[16 * wave + 4 * g4 + r] = y;
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    const float x = add_xor32(add_xor16(cc[m])), y = add_xor32(add_xor16(cb[m]));
+    if (g4 == 0) {
+      pcc[32 * wave + 16 * m + c] = x;
+      pcb[32 * wave + 16 * m + c] = y;
     }
   }
   __syncthreads();
@@ -1092,7 +1115,16 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
   __syncthreads();
   if (wave == 0) {  // dc -> dg = reverse cumulative sum within the chunk
     const int t = lane;
-    float dcv = sdc[t] + sdgam[t] * sgam[t] - sde[t] * se[t];
+    // token t's terms: rows t of waves t/16 and t/16 + 4, columns t of the
+    // four waves of column half t/32
+    float dct = prc[16 * (t >> 4) + (t & 15)] + prc[16 * ((t >> 4) + 4) + (t & 15)];
+    float dbt = prb[16 * (t >> 4) + (t & 15)] + prb[16 * ((t >> 4) + 4) + (t & 15)];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      dct += pcc[32 * (4 * (t >> 5) + w) + (t & 31)];
+      dbt += pcb[32 * (4 * (t >> 5) + w) + (t & 31)];
+    }
+    float dcv = dct + sdgam[t] * sgam[t] - sde[t] * se[t];
     const float tail = wave_sum(sde[t] * se[t]);
     float gc = 0.f;
 #pragma unroll
@@ -1106,7 +1138,7 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
     if (t0 + t < p.T) {
       const long o = (static_cast<long>(b) * p.T + t0 + t) * p.Hv + h;
       p.dg[o] = dcv;
-      store_elem(p.dbeta, o, p.beta_dtype, sdb[t]);
+      store_elem(p.dbeta, o, p.beta_dtype, dbt);
     }
   }
 }
@@ -1136,7 +1168,7 @@ template <int K, typename TIn>
 constexpr size_t grad_lds() {
   return sizeof(TIn) * 2 * BC * (K + 16 / sizeof(TIn)) +
          sizeof(float) * (2 * BC * LC + (3 * BC * LC > 2 * K * LT + 5 * BC * LT ? 3 * BC * LC : 2 * K * LT + 5 * BC * LT) +
-                          8 * BC + GNT / 64 + 8) +
+                          6 * BC + 96 * (GNT / 64) + GNT / 64 + 8) +
          (std::is_same<TIn, u16>::value ? sizeof(u16) * 4 * 16 * (K + 8) : 0);
 }
 
