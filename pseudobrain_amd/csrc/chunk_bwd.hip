@@ -485,7 +485,7 @@ struct ScanStage {
   // K rows, T, the decays and the tile into LDS (sk, st, vectors, tile). K
   // rows go in as they are for bf16 inputs (rows of K + 8), else as float
   // (rows of K + 4).
-  __device__ __forceinline__ void store(void *sk, float *st, float *sc, float *sgam, float *se, float *sbeta,
+  __device__ __forceinline__ void store(void *sk, void *st, float *sc, float *sgam, float *se, float *sbeta,
                                         float *tile) const {
     const int tid = threadIdx.x;
 #pragma unroll
@@ -506,7 +506,15 @@ struct ScanStage {
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const int e = tid + BNT * m;
-      *reinterpret_cast<float4_t *>(&st[(e >> 4) * LC + 4 * (e & 15)]) = tr[m];
+      if constexpr (std::is_same<TIn, u16>::value) {  // T as bf16 high/low rows of BC + 8
+        u16 *th = static_cast<u16 *>(st);
+        v2u32_t hi, lo;
+        split_bf16(tr[m], hi, lo);
+        *reinterpret_cast<v2u32_t *>(th + (e >> 4) * (BC + 8) + 4 * (e & 15)) = hi;
+        *reinterpret_cast<v2u32_t *>(th + BC * (BC + 8) + (e >> 4) * (BC + 8) + 4 * (e & 15)) = lo;
+      } else {
+        *reinterpret_cast<float4_t *>(static_cast<float *>(st) + (e >> 4) * LC + 4 * (e & 15)) = tr[m];
+      }
     }
     if (tid < BC) {
       const float last = __shfl(cv, BC - 1, 64);
@@ -542,11 +550,97 @@ struct ScanStage {
 template <int K, typename TIn>
 struct ScanLds {
   static constexpr bool BF = std::is_same<TIn, u16>::value;
-  static constexpr int LK = BF ? K + 8 : K + 4, LS = K + 8;
+  static constexpr int LK = BF ? K + 8 : K + 4, LS = K + 8, LB = BC + 8;
+  // K rows; T (bf16: high and low parts, rows of LB); the state tile (bf16:
+  // its transpose, high and low); the step's V or dU0 tile in float; the
+  // tiles the next products read (bf16: two transposed high/low pairs
+  // [16][LB], float: one [64][LT] tile); decay vectors.
   static constexpr size_t K_BYTES = BF ? sizeof(u16) * BC * LK : sizeof(float) * BC * LK;
+  static constexpr size_t T_BYTES = BF ? sizeof(u16) * 2 * BC * LB : sizeof(float) * BC * LC;
   static constexpr size_t S_BYTES = BF ? sizeof(u16) * 2 * 16 * LS : sizeof(float) * K * LT;
-  static constexpr size_t BYTES = K_BYTES + sizeof(float) * BC * LC + S_BYTES + sizeof(float) * (2 * BC * LT + 4 * BC);
+  static constexpr size_t A_BYTES = BF ? sizeof(u16) * 2 * 2 * 16 * LB : sizeof(float) * BC * LT;
+  static constexpr size_t OFF_T = K_BYTES, OFF_S = OFF_T + T_BYTES, OFF_TILE = OFF_S + S_BYTES,
+                          OFF_A = OFF_TILE + sizeof(float) * BC * LT, OFF_VEC = OFF_A + A_BYTES;
+  static constexpr size_t BYTES = OFF_VEC + sizeof(float) * 4 * BC;
 };
+
+typedef short bw_i16x4_t __attribute__((ext_vector_type(4)));
+
+// x (rows k0 .. k0+3 of column c) into a transposed pair of bf16 tiles
+// (high at hiT, low 16 rows of ld after it): 8 bytes each.
+__device__ __forceinline__ void put_t_pair(u16 *hiT, int ld, int k0, int c, float4_t x) {
+  v2u32_t hi, lo;
+  split_bf16(x, hi, lo);
+  *reinterpret_cast<v2u32_t *>(hiT + c * ld + k0) = hi;
+  *reinterpret_cast<v2u32_t *>(hiT + 16 * ld + c * ld + k0) = lo;
+}
+
+// Rows row0 .. row0+15 of an A pair (high ah, low al; rows of lda) times a B
+// pair given transposed (bh, bl: [16][ldb]), over k < KD: A_hi B_hi + A_hi
+// B_lo + A_lo B_hi on bf16 MFMA (fp32 accurate to about 2^-16).
+template <int KD>
+__device__ __forceinline__ float4_t pair_times_pair(const u16 *ah, const u16 *al, int lda, int row0, const u16 *bh,
+                                                    const u16 *bl, int ldb) {
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kb = 0; kb < KD; kb += 32) {
+    const bh8_t a_h = *reinterpret_cast<const bh8_t *>(ah + (row0 + c) * lda + kb + 8 * g);
+    const bh8_t a_l = *reinterpret_cast<const bh8_t *>(al + (row0 + c) * lda + kb + 8 * g);
+    const bh8_t b_h = *reinterpret_cast<const bh8_t *>(bh + c * ldb + kb + 8 * g);
+    const bh8_t b_l = *reinterpret_cast<const bh8_t *>(bl + c * ldb + kb + 8 * g);
+    acc = mfma_bf16(a_h, b_h, acc);
+    acc = mfma_bf16(a_h, b_l, acc);
+    acc = mfma_bf16(a_l, b_h, acc);
+  }
+  return acc;
+}
+
+// The A fragment of columns col0 .. col0+15 of a row-major bf16 array (rows
+// of ld) taken as rows, contraction rows k0 + 8g .. k0 + 8g + 7: two
+// transposing reads (lanes 4k .. 4k+3 of group g address row k0 + 8g + k
+// (+ 4), 8 bytes at column col0 + 4 (c & 3); lane c receives column col0 + c).
+__device__ __forceinline__ bh8_t tr_frag(const u16 *m, int ld, int k0, int col0) {
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  const u16 *a = m + (k0 + 8 * g + (c >> 2)) * ld + col0 + 4 * (c & 3);
+  const bw_i16x4_t lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) bw_i16x4_t *)(a));
+  const bw_i16x4_t hi4 =
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) bw_i16x4_t *)(a + 4 * ld));
+  return __builtin_bit_cast(bh8_t, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// (columns k0 .. k0+15 of the K rows)^T times a B pair given transposed,
+// over the 64 tokens: K is exact in bf16, so two products per step.
+__device__ __forceinline__ float4_t kt_times_pair(const u16 *sk, int ldk, int k0, const u16 *bh, const u16 *bl,
+                                                  int ldb) {
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ts = 0; ts < BC; ts += 32) {
+    const bh8_t a = tr_frag(sk, ldk, ts, k0);
+    acc = mfma_bf16(a, *reinterpret_cast<const bh8_t *>(bh + c * ldb + ts + 8 * g), acc);
+    acc = mfma_bf16(a, *reinterpret_cast<const bh8_t *>(bl + c * ldb + ts + 8 * g), acc);
+  }
+  return acc;
+}
+
+// (columns col0 .. col0+15 of T)^T, T a high/low pair of rows of ldt, times
+// a B pair given transposed, over the 64 rows of T.
+__device__ __forceinline__ float4_t tt_times_pair(const u16 *th, const u16 *tl, int ldt, int col0, const u16 *bh,
+                                                  const u16 *bl, int ldb) {
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ts = 0; ts < BC; ts += 32) {
+    const bh8_t a_h = tr_frag(th, ldt, ts, col0), a_l = tr_frag(tl, ldt, ts, col0);
+    const bh8_t b_h = *reinterpret_cast<const bh8_t *>(bh + c * ldb + ts + 8 * g);
+    const bh8_t b_l = *reinterpret_cast<const bh8_t *>(bl + c * ldb + ts + 8 * g);
+    acc = mfma_bf16(a_h, b_h, acc);
+    acc = mfma_bf16(a_h, b_l, acc);
+    acc = mfma_bf16(a_l, b_h, acc);
+  }
+  return acc;
+}
 
 // K rows (row0 + r) times the state tile kept in LDS: bf16 MFMA on the high
 // and low parts of its transpose, or the fp32 MFMA on the float tile.
@@ -595,12 +689,13 @@ __device__ __forceinline__ float4_t k_cols(const void *sk, int t, int col) {
 template <int K, typename TIn>
 __device__ __forceinline__ void state_pass(const BwdParams &p, float *lds, int b, int h, int v0) {
   using L = ScanLds<K, TIn>;
-  constexpr int PER = K / 64;
+  constexpr int PER = K / 64, LB = L::LB;
   unsigned char *base = reinterpret_cast<unsigned char *>(lds);
-  void *sk = base, *ss = base + L::K_BYTES + sizeof(float) * BC * LC;
-  float *st = reinterpret_cast<float *>(base + L::K_BYTES);
-  float *sx = reinterpret_cast<float *>(static_cast<unsigned char *>(ss) + L::S_BYTES), *su = sx + BC * LT;
-  float *sc = su + BC * LT, *sgam = sc + BC, *se = sgam + BC, *sbeta = se + BC;
+  void *sk = base, *st = base + L::OFF_T, *ss = base + L::OFF_S;
+  float *sx = reinterpret_cast<float *>(base + L::OFF_TILE), *su = reinterpret_cast<float *>(base + L::OFF_A);
+  float *sc = reinterpret_cast<float *>(base + L::OFF_VEC), *sgam = sc + BC, *se = sgam + BC, *sbeta = se + BC;
+  // bf16 inputs: (beta X)^T and (E U)^T as high/low pairs
+  u16 *xT = reinterpret_cast<u16 *>(base + L::OFF_A), *uT = xT + 2 * 16 * LB;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 15, g4 = lane >> 4;
   const int hk = h / (p.Hv / p.Hk);
   const long kv = (static_cast<long>(b) * p.Hv + h) * K * p.V;
@@ -631,26 +726,51 @@ __device__ __forceinline__ void state_pass(const BwdParams &p, float *lds, int b
     __syncthreads();
     // X = V - Gamma K S (rows 16w ..)
     const float4_t ks = k_times_state<K, TIn>(sk, 16 * wave, ss);
+    if constexpr (L::BF) {
+      float4_t xb;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = 16 * wave + 4 * g4 + r;
-      sx[t * LT + c] -= sgam[t] * ks[r];
+      for (int r = 0; r < 4; ++r) {
+        const int t = 16 * wave + 4 * g4 + r;
+        xb[r] = (sx[t * LT + c] - sgam[t] * ks[r]) * sbeta[t];
+      }
+      put_t_pair(xT, LB, 16 * wave + 4 * g4, c, xb);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = 16 * wave + 4 * g4 + r;
+        sx[t * LT + c] -= sgam[t] * ks[r];
+      }
     }
     __syncthreads();
     // U = T diag(beta) X
-    const float4_t u = tile_mm4<BC>(
-        zero4(), [&](int r, int s2) { return ld4(&st[(16 * wave + r) * LC + s2]) * ld4(&sbeta[s2]); },
-        [&](int s2, int col) { return ld4s(&sx[s2 * LT + col], LT); });
+    if constexpr (L::BF) {
+      const u16 *th = static_cast<const u16 *>(st);
+      const float4_t u = pair_times_pair<BC>(th, th + BC * LB, LB, 16 * wave, xT, xT + 16 * LB, LB);
+      float4_t eu;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) su[(16 * wave + 4 * g4 + r) * LT + c] = u[r];
+      for (int r = 0; r < 4; ++r) eu[r] = se[16 * wave + 4 * g4 + r] * u[r];
+      put_t_pair(uT, LB, 16 * wave + 4 * g4, c, eu);
+    } else {
+      const float *stf = static_cast<const float *>(st);
+      const float4_t u = tile_mm4<BC>(
+          zero4(), [&](int r, int s2) { return ld4(&stf[(16 * wave + r) * LC + s2]) * ld4(&sbeta[s2]); },
+          [&](int s2, int col) { return ld4s(&sx[s2 * LT + col], LT); });
+#pragma unroll
+      for (int r = 0; r < 4; ++r) su[(16 * wave + 4 * g4 + r) * LT + c] = u[r];
+    }
     __syncthreads();
     // S = gamma_C S + K^T E U
     const float gam_c = sgam[BC - 1];
 #pragma unroll
     for (int m = 0; m < PER; ++m) {
       const int k0 = 16 * (wave + 4 * m);
-      const float4_t y = tile_mm4<BC>(zero4(), [&](int r, int t) { return k_cols<K, TIn>(sk, t, k0 + r) * ld4(&se[t]); },
-                                      [&](int t, int col) { return ld4s(&su[t * LT + col], LT); });
+      float4_t y;
+      if constexpr (L::BF) {
+        y = kt_times_pair(static_cast<const u16 *>(sk), L::LK, k0, uT, uT + 16 * LB, LB);
+      } else {
+        y = tile_mm4<BC>(zero4(), [&](int r, int t) { return k_cols<K, TIn>(sk, t, k0 + r) * ld4(&se[t]); },
+                         [&](int t, int col) { return ld4s(&su[t * LT + col], LT); });
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) s[m][r] = gam_c * s[m][r] + y[r];
     }
@@ -665,12 +785,13 @@ __device__ __forceinline__ void state_pass(const BwdParams &p, float *lds, int b
 template <int K, typename TIn>
 __device__ __forceinline__ void adjoint_pass(const BwdParams &p, float *lds, int b, int h, int v0) {
   using L = ScanLds<K, TIn>;
-  constexpr int PER = K / 64;
+  constexpr int PER = K / 64, LB = L::LB;
   unsigned char *base = reinterpret_cast<unsigned char *>(lds);
-  void *sk = base, *sds = base + L::K_BYTES + sizeof(float) * BC * LC;
-  float *st = reinterpret_cast<float *>(base + L::K_BYTES);
-  float *sdu = reinterpret_cast<float *>(static_cast<unsigned char *>(sds) + L::S_BYTES), *sdx = sdu + BC * LT;
-  float *sc = sdx + BC * LT, *sgam = sc + BC, *se = sgam + BC, *sbeta = se + BC;
+  void *sk = base, *st = base + L::OFF_T, *sds = base + L::OFF_S;
+  float *sdu = reinterpret_cast<float *>(base + L::OFF_TILE), *sdx = reinterpret_cast<float *>(base + L::OFF_A);
+  float *sc = reinterpret_cast<float *>(base + L::OFF_VEC), *sgam = sc + BC, *se = sgam + BC, *sbeta = se + BC;
+  // bf16 inputs: dU^T and (Gamma dX)^T as high/low pairs
+  u16 *duT = reinterpret_cast<u16 *>(base + L::OFF_A), *gxT = duT + 2 * 16 * LB;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 15, g4 = lane >> 4;
   const int hk = h / (p.Hv / p.Hk);
   const long kv = (static_cast<long>(b) * p.Hv + h) * K * p.V;
@@ -707,26 +828,54 @@ __device__ __forceinline__ void adjoint_pass(const BwdParams &p, float *lds, int
     __syncthreads();
     // dU = dU0 + E K dS'
     const float4_t kd = k_times_state<K, TIn>(sk, 16 * wave, sds);
+    if constexpr (L::BF) {
+      float4_t du;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = 16 * wave + 4 * g4 + r;
-      sdu[t * LT + c] += se[t] * kd[r];
+      for (int r = 0; r < 4; ++r) {
+        const int t = 16 * wave + 4 * g4 + r;
+        du[r] = sdu[t * LT + c] + se[t] * kd[r];
+      }
+      put_t_pair(duT, LB, 16 * wave + 4 * g4, c, du);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = 16 * wave + 4 * g4 + r;
+        sdu[t * LT + c] += se[t] * kd[r];
+      }
     }
     __syncthreads();
     // dX = (T diag(beta))^T dU
-    const float4_t dx = tile_mm4<BC>(
-        zero4(), [&](int r, int s2) { return ld4s(&st[s2 * LC + 16 * wave + r], LC) * sbeta[16 * wave + r]; },
-        [&](int s2, int col) { return ld4s(&sdu[s2 * LT + col], LT); });
+    if constexpr (L::BF) {
+      const u16 *th = static_cast<const u16 *>(st);
+      const float4_t dx = tt_times_pair(th, th + BC * LB, LB, 16 * wave, duT, duT + 16 * LB, LB);
+      float4_t gx;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sdx[(16 * wave + 4 * g4 + r) * LT + c] = dx[r];
+      for (int r = 0; r < 4; ++r) {
+        const int t = 16 * wave + 4 * g4 + r;
+        gx[r] = sgam[t] * (sbeta[t] * dx[r]);
+      }
+      put_t_pair(gxT, LB, 16 * wave + 4 * g4, c, gx);
+    } else {
+      const float *stf = static_cast<const float *>(st);
+      const float4_t dx = tile_mm4<BC>(
+          zero4(), [&](int r, int s2) { return ld4s(&stf[s2 * LC + 16 * wave + r], LC) * sbeta[16 * wave + r]; },
+          [&](int s2, int col) { return ld4s(&sdu[s2 * LT + col], LT); });
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sdx[(16 * wave + 4 * g4 + r) * LT + c] = dx[r];
+    }
     __syncthreads();
     // dS = gamma_C dS' + J - (Gamma K)^T dX
     const float gam_c = sgam[BC - 1];
 #pragma unroll
     for (int m = 0; m < PER; ++m) {
       const int k0 = 16 * (wave + 4 * m);
-      const float4_t y = tile_mm4<BC>(zero4(), [&](int r, int t) { return k_cols<K, TIn>(sk, t, k0 + r) * ld4(&sgam[t]); },
-                                      [&](int t, int col) { return ld4s(&sdx[t * LT + col], LT); });
+      float4_t y;
+      if constexpr (L::BF) {
+        y = kt_times_pair(static_cast<const u16 *>(sk), L::LK, k0, gxT, gxT + 16 * LB, LB);
+      } else {
+        y = tile_mm4<BC>(zero4(), [&](int r, int t) { return k_cols<K, TIn>(sk, t, k0 + r) * ld4(&sgam[t]); },
+                         [&](int t, int col) { return ld4s(&sdx[t * LT + col], LT); });
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) ds[m][r] = gam_c * ds[m][r] + jv[m][r] - y[r];
     }
