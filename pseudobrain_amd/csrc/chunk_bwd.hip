@@ -609,6 +609,23 @@ __device__ __forceinline__ bh8_t tr_frag(const u16 *m, int ld, int k0, int col0)
   return __builtin_bit_cast(bh8_t, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
+// bf16 MFMA with four k per lane: acc (16x16) += A (16x16) B (16x16); lane l,
+// c = l & 15, g = l >> 4: A[m=c][k=4g..4g+3], B[k=4g..4g+3][n=c].
+__device__ __forceinline__ float4_t mfma_bf16_k16(bw_i16x4_t a, bw_i16x4_t b, float4_t acc) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc, 0, 0, 0);
+}
+
+// Rows 4g .. 4g+3 of column col0 + c of a row-major 16-bit array (rows of
+// ld) in lane (c, g): one transposing read (lanes 4k .. 4k+3 of group g
+// address row 4g + k, 8 bytes at column col0 + 4 (c & 3)). Taken from a
+// transposed tile M^T it is the A or B operand of M's rows col0 .. col0+15
+// with k the 16 rows of M^T.
+__device__ __forceinline__ bw_i16x4_t tr4(const u16 *m, int ld, int col0) {
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) bw_i16x4_t *)(m + (4 * g + (c >> 2)) * ld + col0 + 4 * (c & 3)));
+}
+
 // (columns k0 .. k0+15 of the K rows)^T times a B pair given transposed,
 // over the 64 tokens: K is exact in bf16, so two products per step.
 __device__ __forceinline__ float4_t kt_times_pair(const u16 *sk, int ldk, int k0, const u16 *bh, const u16 *bl,
@@ -925,6 +942,16 @@ __global__ __launch_bounds__(BNT) void bwd_scans_kernel(BwdParams p) {
 // ---------------------------------------------------------------------------
 constexpr int GNT = 512;
 
+// Floats of the gradient kernel's area: the value-column tiles during the
+// loop over them (bf16 inputs: S, dS', V/X, dU in float, five transposed bf16
+// pairs and the dO rows; else seven float tiles), then the three C x C
+// matrices.
+template <int K, bool BF>
+constexpr int grad_area() {
+  constexpr int tiles = BF ? 2 * K * LT + 2 * BC * LT + (5 * 2 * 16 * (BC + 8) + BC * 24) / 2 : 2 * K * LT + 5 * BC * LT;
+  return 3 * BC * LC > tiles ? 3 * BC * LC : tiles;
+}
+
 template <int K, int V, typename TIn>
 __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
   constexpr int LK = K + 16 / sizeof(TIn), KT = K / 16, KH = KT / 2, LS = K + 8;
@@ -937,8 +964,15 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
   float *area = sm + BC * LC;  // the value-column tiles, then three C x C matrices
   float *ss = area, *sds = ss + K * LT, *sx = sds + K * LT, *sdo = sx + BC * LT, *su = sdo + BC * LT;
   float *sdu = su + BC * LT, *sdx = sdu + BC * LT;
+  // bf16 inputs: the per-tile products take their operands from transposed
+  // bf16 high/low pairs [16][LB] (X^T, dU^T, U^T, (E U)^T, (-Gamma dX)^T) and dO
+  // rows as they are [64][LO]; sdu follows sx and these replace sdo, su, sdx
+  constexpr int LB = BC + 8, LO = 16 + 8, PAIR = 2 * 16 * LB;
+  if constexpr (BF) sdu = sx + BC * LT;
+  u16 *xT = reinterpret_cast<u16 *>(sdu + BC * LT), *duT = xT + PAIR, *uT = duT + PAIR, *euT = uT + PAIR,
+      *gxT = euT + PAIR, *sdo16 = gxT + PAIR;
   float *b1 = area, *b2 = b1 + BC * LC, *b3 = b2 + BC * LC;
-  float *vec = area + (3 * BC * LC > 2 * K * LT + 5 * BC * LT ? 3 * BC * LC : 2 * K * LT + 5 * BC * LT);
+  float *vec = area + grad_area<K, BF>();
   float *sc = vec, *sgam = sc + BC, *se = sgam + BC, *sbeta = se + BC;
   float *sdgam = sbeta + BC, *sde = sdgam + BC;
   // per-wave sums of the dc and dbeta terms: over this wave's token rows
@@ -1040,10 +1074,13 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
       decode16<TIn>(rv, x);
       decode16<TIn>(ro, y);
       const int row = tid / PPR, part = tid % PPR;
+      if constexpr (BF) *reinterpret_cast<uint4 *>(sdo16 + row * LO + part * EPP) = ro;
 #pragma unroll
       for (int j = 0; j < EPP; j += 4) {
         *reinterpret_cast<float4_t *>(&sx[row * LT + part * EPP + j]) = float4_t{x[j], x[j + 1], x[j + 2], x[j + 3]};
-        *reinterpret_cast<float4_t *>(&sdo[row * LT + part * EPP + j]) = float4_t{y[j], y[j + 1], y[j + 2], y[j + 3]};
+        if constexpr (!BF) {
+          *reinterpret_cast<float4_t *>(&sdo[row * LT + part * EPP + j]) = float4_t{y[j], y[j + 1], y[j + 2], y[j + 3]};
+        }
       }
     }
   };
@@ -1065,11 +1102,14 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
         ks = tile_mm4<K>(zero4(), in_rows(sk), state_cols(ss));
         kd = tile_mm4<K>(zero4(), in_rows(sk), state_cols(sds));
       }
+      float4_t xv;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int t = tw + 4 * g4 + r;
-        sx[t * LT + c] -= sgam[t] * ks[r];  // X = V - Gamma K S
+        xv[r] = sx[t * LT + c] - sgam[t] * ks[r];  // X = V - Gamma K S
+        sx[t * LT + c] = xv[r];
       }
+      if constexpr (BF) put_t_pair(xT, LB, tw + 4 * g4, c, xv);
     } else {
       float4_t qs;
       if constexpr (BF) {
@@ -1078,7 +1118,10 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
         qs = tile_mm4<K>(zero4(), in_rows(sq), state_cols(ss));
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) dgam_r[r] += p.scale * qs[r] * sdo[(tw + 4 * g4 + r) * LT + c];
+      for (int r = 0; r < 4; ++r) {
+        const int t = tw + 4 * g4 + r;
+        dgam_r[r] += p.scale * qs[r] * (BF ? ld_el(sdo16, t * LO + c) : sdo[t * LT + c]);
+      }
     }
     __syncthreads();
     if (chain) {
@@ -1086,14 +1129,27 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
           zero4(), [&](int r, int s2) { return ld4(&st[(tw + r) * LC + s2]) * ld4(&sbeta[s2]); },
           [&](int s2, int col) { return ld4s(&sx[s2 * LT + col], LT); });
       float4_t du = tile_mm4<BC>(zero4(), [&](int r, int s2) { return ld4s(&sm[s2 * LC + tw + r], LC); },
-                                 [&](int s2, int col) { return ld4s(&sdo[s2 * LT + col], LT); });
+                                 [&](int s2, int col) {
+                                   if constexpr (BF) {
+                                     return ld4es(sdo16, s2 * LO + col, LO);
+                                   } else {
+                                     return ld4s(&sdo[s2 * LT + col], LT);
+                                   }
+                                 });
+      float4_t eu;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int t = tw + 4 * g4 + r;
-        su[t * LT + c] = u[r];
+        if constexpr (!BF) su[t * LT + c] = u[r];
+        eu[r] = se[t] * u[r];
         de_r[r] += kd[r] * u[r];
         du[r] += se[t] * kd[r];
         sdu[t * LT + c] = du[r];
+      }
+      if constexpr (BF) {
+        put_t_pair(uT, LB, tw + 4 * g4, c, u);
+        put_t_pair(euT, LB, tw + 4 * g4, c, eu);
+        put_t_pair(duT, LB, tw + 4 * g4, c, du);
       }
     }
     __syncthreads();
@@ -1101,36 +1157,80 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
       const float4_t dx = tile_mm4<BC>(
           zero4(), [&](int r, int s2) { return ld4s(&st[s2 * LC + tw + r], LC) * sbeta[tw + r]; },
           [&](int s2, int col) { return ld4s(&sdu[s2 * LT + col], LT); });
+      float4_t gx;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int t = tw + 4 * g4 + r;
-        sdx[t * LT + c] = dx[r];
+        if constexpr (!BF) sdx[t * LT + c] = dx[r];
+        gx[r] = -sgam[t] * dx[r];
         if (t0 + t < p.T) {
           store_elem(p.dv, ((static_cast<long>(b) * p.T + t0 + t) * p.Hv + h) * V + v0 + c, p.in_dtype, dx[r]);
         }
         dgam_r[r] -= ks[r] * dx[r];
       }
+      if constexpr (BF) put_t_pair(gxT, LB, tw + 4 * g4, c, gx);
     }
     for (int e = tid; e < K * 16; e += GNT) dgc += ss[(e >> 4) * LT + (e & 15)] * sds[(e >> 4) * LT + (e & 15)];
     __syncthreads();
     // C x C products over these 16 columns (this wave's two column tiles):
-    // dTb += dU X^T, dM += dO U^T
+    // dTb += dU X^T, dM += dO U^T; then dQ += scale Gamma dO S^T (bf16
+    // inputs: the row scale after the loop), dK += E U dS'^T - Gamma dX S^T
+    // (this wave's half of the key tiles)
+    if constexpr (BF) {
+      // A operands of this wave's rows: dU, E U, -Gamma dX pairs, dO as it is
+      const bw_i16x4_t du_h = tr4(duT, LB, tw), du_l = tr4(duT + 16 * LB, LB, tw);
+      const bw_i16x4_t eu_h = tr4(euT, LB, tw), eu_l = tr4(euT + 16 * LB, LB, tw);
+      const bw_i16x4_t gx_h = tr4(gxT, LB, tw), gx_l = tr4(gxT + 16 * LB, LB, tw);
+      const bw_i16x4_t dof = *reinterpret_cast<const bw_i16x4_t *>(sdo16 + (tw + c) * LO + 4 * g4);
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const int tc = 2 * half + m;
-      dtb[m] = tile_mm4<16>(dtb[m], rows_of(sdu, LT), [&](int j, int col) { return ld4(&sx[(16 * tc + col) * LT + j]); });
-      dm[m] = tile_mm4<16>(dm[m], rows_of(sdo, LT), [&](int j, int col) { return ld4(&su[(16 * tc + col) * LT + j]); });
+      for (int m = 0; m < 2; ++m) {
+        const int tc = 2 * half + m;
+        const bw_i16x4_t x_h = tr4(xT, LB, 16 * tc), x_l = tr4(xT + 16 * LB, LB, 16 * tc);
+        const bw_i16x4_t u_h = tr4(uT, LB, 16 * tc), u_l = tr4(uT + 16 * LB, LB, 16 * tc);
+        dtb[m] = mfma_bf16_k16(du_h, x_h, dtb[m]);
+        dtb[m] = mfma_bf16_k16(du_h, x_l, dtb[m]);
+        dtb[m] = mfma_bf16_k16(du_l, x_h, dtb[m]);
+        dm[m] = mfma_bf16_k16(dof, u_h, dm[m]);
+        dm[m] = mfma_bf16_k16(dof, u_l, dm[m]);
+      }
+#pragma unroll
+      for (int m = 0; m < KH; ++m) {
+        const int kt = half * KH + m;
+        const bw_i16x4_t s_h = tr4(shT, LS, 16 * kt), s_l = tr4(slT, LS, 16 * kt);
+        const bw_i16x4_t d_h = tr4(dhT, LS, 16 * kt), d_l = tr4(dlT, LS, 16 * kt);
+        dq[m] = mfma_bf16_k16(dof, s_h, dq[m]);
+        dq[m] = mfma_bf16_k16(dof, s_l, dq[m]);
+        dk[m] = mfma_bf16_k16(eu_h, d_h, dk[m]);
+        dk[m] = mfma_bf16_k16(eu_h, d_l, dk[m]);
+        dk[m] = mfma_bf16_k16(eu_l, d_h, dk[m]);
+        dk[m] = mfma_bf16_k16(gx_h, s_h, dk[m]);
+        dk[m] = mfma_bf16_k16(gx_h, s_l, dk[m]);
+        dk[m] = mfma_bf16_k16(gx_l, s_h, dk[m]);
+      }
+    } else {
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const int tc = 2 * half + m;
+        dtb[m] = tile_mm4<16>(dtb[m], rows_of(sdu, LT), [&](int j, int col) { return ld4(&sx[(16 * tc + col) * LT + j]); });
+        dm[m] = tile_mm4<16>(dm[m], rows_of(sdo, LT), [&](int j, int col) { return ld4(&su[(16 * tc + col) * LT + j]); });
+      }
+#pragma unroll
+      for (int m = 0; m < KH; ++m) {
+        const int kt = half * KH + m;
+        auto s_t = [&](int j, int col) { return ld4(&ss[(16 * kt + col) * LT + j]); };
+        dq[m] = tile_mm4<16>(dq[m], [&](int r, int j) { return ld4(&sdo[(tw + r) * LT + j]) * sgam[tw + r] * p.scale; },
+                             s_t);
+        dk[m] = tile_mm4<16>(dk[m], [&](int r, int j) { return ld4(&su[(tw + r) * LT + j]) * se[tw + r]; },
+                             [&](int j, int col) { return ld4(&sds[(16 * kt + col) * LT + j]); });
+        dk[m] = tile_mm4<16>(dk[m], [&](int r, int j) { return ld4(&sdx[(tw + r) * LT + j]) * -sgam[tw + r]; }, s_t);
+      }
     }
-    // dQ += scale Gamma dO S^T;  dK += E U dS'^T - Gamma dX S^T (this wave's half of the key tiles)
+  }
+  if constexpr (BF) {  // dQ's row scale, scale Gamma
 #pragma unroll
     for (int m = 0; m < KH; ++m) {
-      const int kt = half * KH + m;
-      auto s_t = [&](int j, int col) { return ld4(&ss[(16 * kt + col) * LT + j]); };
-      dq[m] = tile_mm4<16>(dq[m], [&](int r, int j) { return ld4(&sdo[(tw + r) * LT + j]) * sgam[tw + r] * p.scale; },
-                           s_t);
-      dk[m] = tile_mm4<16>(dk[m], [&](int r, int j) { return ld4(&su[(tw + r) * LT + j]) * se[tw + r]; },
-                           [&](int j, int col) { return ld4(&sds[(16 * kt + col) * LT + j]); });
-      dk[m] = tile_mm4<16>(dk[m], [&](int r, int j) { return ld4(&sdx[(tw + r) * LT + j]) * -sgam[tw + r]; }, s_t);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dq[m][r] *= sgam[tw + 4 * g4 + r] * p.scale;
     }
   }
   // per-token sums over the value columns (both halves add into sdgam)
@@ -1316,8 +1416,8 @@ constexpr size_t scan_lds() { return ScanLds<K, TIn>::BYTES; }
 template <int K, typename TIn>
 constexpr size_t grad_lds() {
   return sizeof(TIn) * 2 * BC * (K + 16 / sizeof(TIn)) +
-         sizeof(float) * (2 * BC * LC + (3 * BC * LC > 2 * K * LT + 5 * BC * LT ? 3 * BC * LC : 2 * K * LT + 5 * BC * LT) +
-                          6 * BC + 96 * (GNT / 64) + GNT / 64 + 8) +
+         sizeof(float) * (2 * BC * LC + grad_area<K, std::is_same<TIn, u16>::value>() + 6 * BC + 96 * (GNT / 64) +
+                          GNT / 64 + 8) +
          (std::is_same<TIn, u16>::value ? sizeof(u16) * 4 * 16 * (K + 8) : 0);
 }
 

@@ -22,7 +22,7 @@ from pseudobrain_amd import build
 
 SOURCES = ("chunk_prep.hip", "chunk_scan.hip", "chunk_wide.hip", "chunk_bwd.hip")
 NEED = {"v_mfma_f32_16x16x32_f16": 8, "v_mfma_f32_16x16x32_bf16": 8, "v_mfma_f32_16x16x16_f16": 8,
-        "v_mfma_f32_16x16x4_f32": 10}
+        "v_mfma_f32_16x16x16_bf16": 8, "v_mfma_f32_16x16x4_f32": 10}
 _REG = re.compile(r"\bv\[(\d+):(\d+)\]|\bv(\d+)\b")
 _STORES = ("ds_write", "ds_add", "global_store", "buffer_store", "global_atomic", "buffer_atomic", "flat_store")
 
