@@ -24,8 +24,11 @@
 //   bwd_grad_kernel      per (chunk, value head): dq, dk, dv, dbeta, dg
 //   bwd_gqa_reduce_kernel  dq, dk summed over the value heads of a key head
 //
-// Everything is float32: operands staged in LDS, products on the 16x16x4 fp32
-// MFMA (the same peak as fp32 FMA on this chip, with far fewer LDS reads).
+// Accumulation is float32. With bf16 inputs the products of inputs and states
+// run on bf16 MFMA, a float32 operand entering as a high/low pair of bf16
+// parts (A B_hi + A B_lo, or three products when both are paired: about
+// 2^-16 relative); the rest, and every product for fp16 / fp32 inputs, on the
+// 16x16x4 fp32 MFMA with four consecutive k per lane group.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
