@@ -229,6 +229,108 @@ __device__ __forceinline__ float4_t rows_times_rows(const u16 *a, const u16 *b, 
   return acc;
 }
 
+typedef short bw_i16x4_t __attribute__((ext_vector_type(4)));
+
+// x (rows k0 .. k0+3 of column c) into a transposed pair of bf16 tiles
+// (high at hiT, low 16 rows of ld after it): 8 bytes each.
+__device__ __forceinline__ void put_t_pair(u16 *hiT, int ld, int k0, int c, float4_t x) {
+  v2u32_t hi, lo;
+  split_bf16(x, hi, lo);
+  *reinterpret_cast<v2u32_t *>(hiT + c * ld + k0) = hi;
+  *reinterpret_cast<v2u32_t *>(hiT + 16 * ld + c * ld + k0) = lo;
+}
+
+// Rows row0 .. row0+15 of an A pair (high ah, low al; rows of lda) times a B
+// pair given transposed (bh, bl: [16][ldb]), over k < KD: A_hi B_hi + A_hi
+// B_lo + A_lo B_hi on bf16 MFMA (fp32 accurate to about 2^-16).
+template <int KD>
+__device__ __forceinline__ float4_t pair_times_pair(const u16 *ah, const u16 *al, int lda, int row0, const u16 *bh,
+                                                    const u16 *bl, int ldb) {
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kb = 0; kb < KD; kb += 32) {
+    const bh8_t a_h = *reinterpret_cast<const bh8_t *>(ah + (row0 + c) * lda + kb + 8 * g);
+    const bh8_t a_l = *reinterpret_cast<const bh8_t *>(al + (row0 + c) * lda + kb + 8 * g);
+    const bh8_t b_h = *reinterpret_cast<const bh8_t *>(bh + c * ldb + kb + 8 * g);
+    const bh8_t b_l = *reinterpret_cast<const bh8_t *>(bl + c * ldb + kb + 8 * g);
+    acc = mfma_bf16(a_h, b_h, acc);
+    acc = mfma_bf16(a_h, b_l, acc);
+    acc = mfma_bf16(a_l, b_h, acc);
+  }
+  return acc;
+}
+
+// The A fragment of columns col0 .. col0+15 of a row-major bf16 array (rows
+// of ld) taken as rows, contraction rows k0 + 8g .. k0 + 8g + 7: two
+// transposing reads (lanes 4k .. 4k+3 of group g address row k0 + 8g + k
+// (+ 4), 8 bytes at column col0 + 4 (c & 3); lane c receives column col0 + c).
+__device__ __forceinline__ bh8_t tr_frag(const u16 *m, int ld, int k0, int col0) {
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  const u16 *a = m + (k0 + 8 * g + (c >> 2)) * ld + col0 + 4 * (c & 3);
+  const bw_i16x4_t lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) bw_i16x4_t *)(a));
+  const bw_i16x4_t hi4 =
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) bw_i16x4_t *)(a + 4 * ld));
+  return __builtin_bit_cast(bh8_t, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// bf16 MFMA with four k per lane: acc (16x16) += A (16x16) B (16x16); lane l,
+// c = l & 15, g = l >> 4: A[m=c][k=4g..4g+3], B[k=4g..4g+3][n=c].
+__device__ __forceinline__ float4_t mfma_bf16_k16(bw_i16x4_t a, bw_i16x4_t b, float4_t acc) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc, 0, 0, 0);
+}
+
+// Rows 4g .. 4g+3 of column col0 + c of a row-major 16-bit array (rows of
+// ld) in lane (c, g): one transposing read (lanes 4k .. 4k+3 of group g
+// address row 4g + k, 8 bytes at column col0 + 4 (c & 3)). Taken from a
+// transposed tile M^T it is the A or B operand of M's rows col0 .. col0+15
+// with k the 16 rows of M^T.
+__device__ __forceinline__ bw_i16x4_t tr4(const u16 *m, int ld, int col0) {
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) bw_i16x4_t *)(m + (4 * g + (c >> 2)) * ld + col0 + 4 * (c & 3)));
+}
+
+// (columns k0 .. k0+15 of the K rows)^T times a B pair given transposed,
+// over the 64 tokens: K is exact in bf16, so two products per step.
+__device__ __forceinline__ float4_t kt_times_pair(const u16 *sk, int ldk, int k0, const u16 *bh, const u16 *bl,
+                                                  int ldb) {
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ts = 0; ts < BC; ts += 32) {
+    const bh8_t a = tr_frag(sk, ldk, ts, k0);
+    acc = mfma_bf16(a, *reinterpret_cast<const bh8_t *>(bh + c * ldb + ts + 8 * g), acc);
+    acc = mfma_bf16(a, *reinterpret_cast<const bh8_t *>(bl + c * ldb + ts + 8 * g), acc);
+  }
+  return acc;
+}
+
+// (columns col0 .. col0+15 of T)^T, T a high/low pair of rows of ldt, times
+// a B pair given transposed, over the 64 rows of T.
+__device__ __forceinline__ float4_t tt_times_pair(const u16 *th, const u16 *tl, int ldt, int col0, const u16 *bh,
+                                                  const u16 *bl, int ldb) {
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ts = 0; ts < BC; ts += 32) {
+    const bh8_t a_h = tr_frag(th, ldt, ts, col0), a_l = tr_frag(tl, ldt, ts, col0);
+    const bh8_t b_h = *reinterpret_cast<const bh8_t *>(bh + c * ldb + ts + 8 * g);
+    const bh8_t b_l = *reinterpret_cast<const bh8_t *>(bl + c * ldb + ts + 8 * g);
+    acc = mfma_bf16(a_h, b_h, acc);
+    acc = mfma_bf16(a_h, b_l, acc);
+    acc = mfma_bf16(a_l, b_h, acc);
+  }
+  return acc;
+}
+
+// Round to the nearest bf16 (ties to even) of a finite float, as its bits.
+__device__ __forceinline__ u16 bf16_bits(float x) {
+  uint32_t u = __float_as_uint(x);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<u16>(u >> 16);
+}
+
 // Workspace records of (batch b, value head h, chunk i).
 __device__ __forceinline__ long rec(const BwdParams &p, int b, int h, int i) {
   return (static_cast<long>(b) * p.Hv + h) * p.n + i;
@@ -304,6 +406,11 @@ __global__ __launch_bounds__(BNT) void bwd_local_kernel(BwdParams p) {
   TIn *sq = reinterpret_cast<TIn *>(lds), *sk = sq + BC * LK, *sdo = sk + BC * LK;
   float *sa = reinterpret_cast<float *>(sdo + BC * LV);
   float *sc = sa + BC * LC, *sgam = sc + BC, *sbeta = sgam + BC, *sr = sbeta + BC;
+  // bf16 inputs: M as a bf16 high/low pair (rows of LM) in sa's bytes, and
+  // dU0, J on bf16 MFMA
+  constexpr bool BF = std::is_same<TIn, u16>::value;
+  constexpr int LM = LC;
+  u16 *mh = reinterpret_cast<u16 *>(sa);
   const int i = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 15, g4 = lane >> 4;
   const int hk = h / (p.Hv / p.Hk);
@@ -394,13 +501,34 @@ __global__ __launch_bounds__(BNT) void bwd_local_kernel(BwdParams p) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = 16 * wave + 4 * g4 + r, s2 = 16 * tc + c;
-      sa[t * LC + s2] = t >= s2 ? p.scale * qk_acc[r] * expf(sc[t] - sc[s2]) : 0.f;
+      const float mv = t >= s2 ? p.scale * qk_acc[r] * expf(sc[t] - sc[s2]) : 0.f;
+      if constexpr (BF) {  // M as a bf16 high/low pair, rows of LM, in sa's bytes
+        const u16 hi = bf16_bits(mv);
+        mh[t * LM + s2] = hi;
+        mh[BC * LM + t * LM + s2] = bf16_bits(mv - __uint_as_float(static_cast<uint32_t>(hi) << 16));
+      } else {
+        sa[t * LC + s2] = mv;
+      }
     }
   }
   __syncthreads();
   // dU0 = M^T dO: tiles (row tile, 16-column tile)
   float *wu = p.ws_dU0 + rec(p, b, h, i) * BC * V;
-  for (int tile = wave; tile < 4 * (V / 16); tile += 4) {
+  if constexpr (BF) {  // M^T fragments and dO's columns by transposing reads
+    for (int tile = wave; tile < 4 * (V / 16); tile += 4) {
+      const int tr = tile & 3, tv = tile >> 2;
+      float4_t acc = zero4();
+#pragma unroll
+      for (int ts = 0; ts < BC; ts += 32) {
+        const bh8_t d = tr_frag(sdo, LV, ts, 16 * tv);
+        acc = mfma_bf16(tr_frag(mh, LM, ts, 16 * tr), d, acc);
+        acc = mfma_bf16(tr_frag(mh + BC * LM, LM, ts, 16 * tr), d, acc);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) wu[(16 * tr + 4 * g4 + r) * V + 16 * tv + c] = acc[r];
+    }
+  }
+  for (int tile = wave; tile < (BF ? 0 : 4 * (V / 16)); tile += 4) {
     const int tr = tile & 3, tv = tile >> 2;
     const float4_t acc = tile_mm4<BC>(zero4(), [&](int r, int s2) { return ld4s(&sa[s2 * LC + 16 * tr + r], LC); },
                                       [&](int s2, int col) {
@@ -413,7 +541,39 @@ __global__ __launch_bounds__(BNT) void bwd_local_kernel(BwdParams p) {
   }
   // J = scale (Gamma Q)^T dO: K x V
   float *wj = p.ws_J + rec(p, b, h, i) * static_cast<long>(K) * V;
-  for (int tile = wave; tile < (K / 16) * (V / 16); tile += 4) {
+  if constexpr (BF) {
+    // per column tile of this wave: (Gamma dO)'s columns as bf16 pairs once,
+    // then every key tile's Q^T fragments (transposing reads of the q rows)
+    for (int tv = wave; tv < V / 16; tv += 4) {
+      bh8_t bh[2], bl[2];
+#pragma unroll
+      for (int s8 = 0; s8 < 2; ++s8) {
+        const v4u32_t w = __builtin_bit_cast(v4u32_t, tr_frag(sdo, LV, 32 * s8, 16 * tv));
+        const float4_t g0 = ld4(&sgam[32 * s8 + 8 * g4]), g1 = ld4(&sgam[32 * s8 + 8 * g4 + 4]);
+        const float4_t x0 = float4_t{__uint_as_float(w[0] << 16), __uint_as_float(w[0] & 0xffff0000u),
+                                     __uint_as_float(w[1] << 16), __uint_as_float(w[1] & 0xffff0000u)} * g0;
+        const float4_t x1 = float4_t{__uint_as_float(w[2] << 16), __uint_as_float(w[2] & 0xffff0000u),
+                                     __uint_as_float(w[3] << 16), __uint_as_float(w[3] & 0xffff0000u)} * g1;
+        v2u32_t h0, l0, h1, l1;
+        split_bf16(x0, h0, l0);
+        split_bf16(x1, h1, l1);
+        bh[s8] = __builtin_bit_cast(bh8_t, v4u32_t{h0[0], h0[1], h1[0], h1[1]});
+        bl[s8] = __builtin_bit_cast(bh8_t, v4u32_t{l0[0], l0[1], l1[0], l1[1]});
+      }
+      for (int tk = 0; tk < K / 16; ++tk) {
+        float4_t acc = zero4();
+#pragma unroll
+        for (int s8 = 0; s8 < 2; ++s8) {
+          const bh8_t a = tr_frag(sq, LK, 32 * s8, 16 * tk);
+          acc = mfma_bf16(a, bh[s8], acc);
+          acc = mfma_bf16(a, bl[s8], acc);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) wj[(16 * tk + 4 * g4 + r) * V + 16 * tv + c] = p.scale * acc[r];
+      }
+    }
+  }
+  for (int tile = wave; tile < (BF ? 0 : (K / 16) * (V / 16)); tile += 4) {
     const int tk = tile % (K / 16), tv = tile / (K / 16);
     const float4_t acc = tile_mm4<BC>(
         zero4(),
@@ -566,101 +726,6 @@ struct ScanLds {
                           OFF_A = OFF_TILE + sizeof(float) * BC * LT, OFF_VEC = OFF_A + A_BYTES;
   static constexpr size_t BYTES = OFF_VEC + sizeof(float) * 4 * BC;
 };
-
-typedef short bw_i16x4_t __attribute__((ext_vector_type(4)));
-
-// x (rows k0 .. k0+3 of column c) into a transposed pair of bf16 tiles
-// (high at hiT, low 16 rows of ld after it): 8 bytes each.
-__device__ __forceinline__ void put_t_pair(u16 *hiT, int ld, int k0, int c, float4_t x) {
-  v2u32_t hi, lo;
-  split_bf16(x, hi, lo);
-  *reinterpret_cast<v2u32_t *>(hiT + c * ld + k0) = hi;
-  *reinterpret_cast<v2u32_t *>(hiT + 16 * ld + c * ld + k0) = lo;
-}
-
-// Rows row0 .. row0+15 of an A pair (high ah, low al; rows of lda) times a B
-// pair given transposed (bh, bl: [16][ldb]), over k < KD: A_hi B_hi + A_hi
-// B_lo + A_lo B_hi on bf16 MFMA (fp32 accurate to about 2^-16).
-template <int KD>
-__device__ __forceinline__ float4_t pair_times_pair(const u16 *ah, const u16 *al, int lda, int row0, const u16 *bh,
-                                                    const u16 *bl, int ldb) {
-  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
-  float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int kb = 0; kb < KD; kb += 32) {
-    const bh8_t a_h = *reinterpret_cast<const bh8_t *>(ah + (row0 + c) * lda + kb + 8 * g);
-    const bh8_t a_l = *reinterpret_cast<const bh8_t *>(al + (row0 + c) * lda + kb + 8 * g);
-    const bh8_t b_h = *reinterpret_cast<const bh8_t *>(bh + c * ldb + kb + 8 * g);
-    const bh8_t b_l = *reinterpret_cast<const bh8_t *>(bl + c * ldb + kb + 8 * g);
-    acc = mfma_bf16(a_h, b_h, acc);
-    acc = mfma_bf16(a_h, b_l, acc);
-    acc = mfma_bf16(a_l, b_h, acc);
-  }
-  return acc;
-}
-
-// The A fragment of columns col0 .. col0+15 of a row-major bf16 array (rows
-// of ld) taken as rows, contraction rows k0 + 8g .. k0 + 8g + 7: two
-// transposing reads (lanes 4k .. 4k+3 of group g address row k0 + 8g + k
-// (+ 4), 8 bytes at column col0 + 4 (c & 3); lane c receives column col0 + c).
-__device__ __forceinline__ bh8_t tr_frag(const u16 *m, int ld, int k0, int col0) {
-  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
-  const u16 *a = m + (k0 + 8 * g + (c >> 2)) * ld + col0 + 4 * (c & 3);
-  const bw_i16x4_t lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) bw_i16x4_t *)(a));
-  const bw_i16x4_t hi4 =
-      __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) bw_i16x4_t *)(a + 4 * ld));
-  return __builtin_bit_cast(bh8_t, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
-}
-
-// bf16 MFMA with four k per lane: acc (16x16) += A (16x16) B (16x16); lane l,
-// c = l & 15, g = l >> 4: A[m=c][k=4g..4g+3], B[k=4g..4g+3][n=c].
-__device__ __forceinline__ float4_t mfma_bf16_k16(bw_i16x4_t a, bw_i16x4_t b, float4_t acc) {
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc, 0, 0, 0);
-}
-
-// Rows 4g .. 4g+3 of column col0 + c of a row-major 16-bit array (rows of
-// ld) in lane (c, g): one transposing read (lanes 4k .. 4k+3 of group g
-// address row 4g + k, 8 bytes at column col0 + 4 (c & 3)). Taken from a
-// transposed tile M^T it is the A or B operand of M's rows col0 .. col0+15
-// with k the 16 rows of M^T.
-__device__ __forceinline__ bw_i16x4_t tr4(const u16 *m, int ld, int col0) {
-  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) bw_i16x4_t *)(m + (4 * g + (c >> 2)) * ld + col0 + 4 * (c & 3)));
-}
-
-// (columns k0 .. k0+15 of the K rows)^T times a B pair given transposed,
-// over the 64 tokens: K is exact in bf16, so two products per step.
-__device__ __forceinline__ float4_t kt_times_pair(const u16 *sk, int ldk, int k0, const u16 *bh, const u16 *bl,
-                                                  int ldb) {
-  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
-  float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int ts = 0; ts < BC; ts += 32) {
-    const bh8_t a = tr_frag(sk, ldk, ts, k0);
-    acc = mfma_bf16(a, *reinterpret_cast<const bh8_t *>(bh + c * ldb + ts + 8 * g), acc);
-    acc = mfma_bf16(a, *reinterpret_cast<const bh8_t *>(bl + c * ldb + ts + 8 * g), acc);
-  }
-  return acc;
-}
-
-// (columns col0 .. col0+15 of T)^T, T a high/low pair of rows of ldt, times
-// a B pair given transposed, over the 64 rows of T.
-__device__ __forceinline__ float4_t tt_times_pair(const u16 *th, const u16 *tl, int ldt, int col0, const u16 *bh,
-                                                  const u16 *bl, int ldb) {
-  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
-  float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int ts = 0; ts < BC; ts += 32) {
-    const bh8_t a_h = tr_frag(th, ldt, ts, col0), a_l = tr_frag(tl, ldt, ts, col0);
-    const bh8_t b_h = *reinterpret_cast<const bh8_t *>(bh + c * ldb + ts + 8 * g);
-    const bh8_t b_l = *reinterpret_cast<const bh8_t *>(bl + c * ldb + ts + 8 * g);
-    acc = mfma_bf16(a_h, b_h, acc);
-    acc = mfma_bf16(a_h, b_l, acc);
-    acc = mfma_bf16(a_l, b_h, acc);
-  }
-  return acc;
-}
 
 // K rows (row0 + r) times the state tile kept in LDS: bf16 MFMA on the high
 // and low parts of its transpose, or the fp32 MFMA on the float tile.
