@@ -331,6 +331,13 @@ __device__ __forceinline__ u16 bf16_bits(float x) {
   return static_cast<u16>(u >> 16);
 }
 
+// x as a bf16 high/low pair: element e of the high array, e + lo_off of the low.
+__device__ __forceinline__ void put_pair1(u16 *m, int lo_off, int e, float x) {
+  const u16 hi = bf16_bits(x);
+  m[e] = hi;
+  m[lo_off + e] = bf16_bits(x - __uint_as_float(static_cast<uint32_t>(hi) << 16));
+}
+
 // Workspace records of (batch b, value head h, chunk i).
 __device__ __forceinline__ long rec(const BwdParams &p, int b, int h, int i) {
   return (static_cast<long>(b) * p.Hv + h) * p.n + i;
@@ -1013,11 +1020,12 @@ constexpr int GNT = 512;
 // Floats of the gradient kernel's area: the value-column tiles during the
 // loop over them (bf16 inputs: S, dS', V/X, dU in float, five transposed bf16
 // pairs and the dO rows; else seven float tiles), then the three C x C
-// matrices.
+// matrices (bf16 inputs: one in float, two as bf16 pairs of rows BC + 8).
 template <int K, bool BF>
 constexpr int grad_area() {
   constexpr int tiles = BF ? 2 * K * LT + 2 * BC * LT + (5 * 2 * 16 * (BC + 8) + BC * 24) / 2 : 2 * K * LT + 5 * BC * LT;
-  return 3 * BC * LC > tiles ? 3 * BC * LC : tiles;
+  constexpr int tri = BF ? BC * LC + 2 * BC * (BC + 8) : 3 * BC * LC;
+  return tri > tiles ? tri : tiles;
 }
 
 template <int K, int V, typename TIn>
@@ -1040,6 +1048,10 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
   u16 *xT = reinterpret_cast<u16 *>(sdu + BC * LT), *duT = xT + PAIR, *uT = duT + PAIR, *euT = uT + PAIR,
       *gxT = euT + PAIR, *sdo16 = gxT + PAIR;
   float *b1 = area, *b2 = b1 + BC * LC, *b3 = b2 + BC * LC;
+  // bf16 inputs: b2 in float first, then dM o Mt (b1) and H + H^T (b3) as
+  // bf16 high/low pairs, rows of LB
+  if constexpr (BF) b2 = area;
+  u16 *b1p = reinterpret_cast<u16 *>(area + BC * LC), *b3p = b1p + 2 * BC * LB;
   float *vec = area + grad_area<K, BF>();
   float *sc = vec, *sgam = sc + BC, *se = sgam + BC, *sbeta = se + BC;
   float *sdgam = sbeta + BC, *sde = sdgam + BC;
@@ -1325,7 +1337,11 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
       const int t = tw + 4 * g4 + r, s2 = 16 * tc + c;
       const float d = t >= s2 ? p.scale * expf(sc[t] - sc[s2]) : 0.f;
       const float dmv = t >= s2 ? dm[m][r] : 0.f;
-      b1[t * LC + s2] = dmv * d;
+      if constexpr (BF) {
+        put_pair1(b1p, BC * LB, t * LB + s2, dmv * d);
+      } else {
+        b1[t * LC + s2] = dmv * d;
+      }
       const float dcv = dmv * sm[t * LC + s2];
       rc[r] += dcv;
       cc[m] -= dcv;
@@ -1374,10 +1390,19 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
         rb[r] += dav * gk[r] * d;
         rc[r] += dav * av;
         cc[m] -= dav * av;
-        b3[t * LC + s2] = hv;
-        b3[s2 * LC + t] = hv;
+        if constexpr (BF) {
+          put_pair1(b3p, BC * LB, t * LB + s2, hv);
+          put_pair1(b3p, BC * LB, s2 * LB + t, hv);
+        } else {
+          b3[t * LC + s2] = hv;
+          b3[s2 * LC + t] = hv;
+        }
       } else if (t == s2) {
-        b3[t * LC + s2] = 0.f;
+        if constexpr (BF) {
+          put_pair1(b3p, BC * LB, t * LB + s2, 0.f);
+        } else {
+          b3[t * LC + s2] = 0.f;
+        }
       }
     }
   }
@@ -1401,8 +1426,28 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
   }
   __syncthreads();
   // dQ += (dM o Mt) K;  dK += (dM o Mt)^T Q + (H + H^T) K
+  if constexpr (BF) {  // K and Q columns by transposing reads (exact), the C x C pairs by rows or transposing reads
 #pragma unroll
-  for (int m = 0; m < KH; ++m) {
+    for (int ts = 0; ts < BC; ts += 32) {
+      const int o = (tw + c) * LB + ts + 8 * g4;
+      const bh8_t a1h = *reinterpret_cast<const bh8_t *>(b1p + o), a1l = *reinterpret_cast<const bh8_t *>(b1p + BC * LB + o);
+      const bh8_t a3h = *reinterpret_cast<const bh8_t *>(b3p + o), a3l = *reinterpret_cast<const bh8_t *>(b3p + BC * LB + o);
+      const bh8_t t1h = tr_frag(b1p, LB, ts, tw), t1l = tr_frag(b1p + BC * LB, LB, ts, tw);
+#pragma unroll
+      for (int m = 0; m < KH; ++m) {
+        const int kt = half * KH + m;
+        const bh8_t kf = tr_frag(sk, LK, ts, 16 * kt), qf = tr_frag(sq, LK, ts, 16 * kt);
+        dq[m] = mfma_bf16(a1h, kf, dq[m]);
+        dq[m] = mfma_bf16(a1l, kf, dq[m]);
+        dk[m] = mfma_bf16(t1h, qf, dk[m]);
+        dk[m] = mfma_bf16(t1l, qf, dk[m]);
+        dk[m] = mfma_bf16(a3h, kf, dk[m]);
+        dk[m] = mfma_bf16(a3l, kf, dk[m]);
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < (BF ? 0 : KH); ++m) {
     const int kt = half * KH + m;
     auto kcol = [&](int s2, int col) { return ld4es(sk, s2 * LK + 16 * kt + col, LK); };
     dq[m] = tile_mm4<BC>(dq[m], [&](int r, int s2) { return ld4(&b1[(tw + r) * LC + s2]); }, kcol);
