@@ -331,6 +331,11 @@ __device__ __forceinline__ u16 bf16_bits(float x) {
   return static_cast<u16>(u >> 16);
 }
 
+// The value of a bf16 high/low pair.
+__device__ __forceinline__ float pair_val(const u16 *m, int lo_off, int e) {
+  return __uint_as_float(static_cast<uint32_t>(m[e]) << 16) + __uint_as_float(static_cast<uint32_t>(m[lo_off + e]) << 16);
+}
+
 // x as a bf16 high/low pair: element e of the high array, e + lo_off of the low.
 __device__ __forceinline__ void put_pair1(u16 *m, int lo_off, int e, float x) {
   const u16 hi = bf16_bits(x);
@@ -353,6 +358,22 @@ __device__ __forceinline__ void load_t(float *st, const float *src) {
   for (int m = 0; m < 4; ++m) {
     const int e = threadIdx.x + BNT * m;
     *reinterpret_cast<float4_t *>(&st[(e >> 4) * LC + 4 * (e & 15)]) = raw[m];
+  }
+}
+
+// A 64 x 64 float32 record (T) into LDS as a bf16 high/low pair of rows ld.
+__device__ __forceinline__ void load_t_pair(u16 *tp, int ld, const float *src) {
+  const float4_t *w = reinterpret_cast<const float4_t *>(src);
+  float4_t raw[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) raw[m] = w[threadIdx.x + BNT * m];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int e = threadIdx.x + BNT * m;
+    v2u32_t hi, lo;
+    split_bf16(raw[m], hi, lo);
+    *reinterpret_cast<v2u32_t *>(tp + (e >> 4) * ld + 4 * (e & 15)) = hi;
+    *reinterpret_cast<v2u32_t *>(tp + BC * ld + (e >> 4) * ld + 4 * (e & 15)) = lo;
   }
 }
 
@@ -1023,8 +1044,8 @@ constexpr int GNT = 512;
 // matrices (bf16 inputs: one in float, two as bf16 pairs of rows BC + 8).
 template <int K, bool BF>
 constexpr int grad_area() {
-  constexpr int tiles = BF ? 2 * K * LT + 2 * BC * LT + (5 * 2 * 16 * (BC + 8) + BC * 24) / 2 : 2 * K * LT + 5 * BC * LT;
-  constexpr int tri = BF ? BC * LC + 2 * BC * (BC + 8) : 3 * BC * LC;
+  constexpr int tiles = BF ? 2 * K * LT + 2 * BC * LT + (6 * 2 * 16 * (BC + 8) + BC * 24) / 2 : 2 * K * LT + 5 * BC * LT;
+  constexpr int tri = BF ? 3 * BC * (BC + 8) : 3 * BC * LC;
   return tri > tiles ? tri : tiles;
 }
 
@@ -1035,23 +1056,25 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
   // tiles as high + low parts); other input types on the fp32 MFMA
   constexpr bool BF = std::is_same<TIn, u16>::value;
   extern __shared__ __align__(16) float lds[];
+  constexpr int LB = BC + 8, LO = 16 + 8, PAIR = 2 * 16 * LB;
+  // T and M: float rows of LC, or (bf16 inputs) bf16 high/low pairs of rows LB
+  constexpr int TSZ = BF ? BC * LB : BC * LC;
   TIn *sq = reinterpret_cast<TIn *>(lds), *sk = sq + BC * LK;  // q, k rows as they are
-  float *st = reinterpret_cast<float *>(sk + BC * LK), *sm = st + BC * LC;
-  float *area = sm + BC * LC;  // the value-column tiles, then three C x C matrices
+  float *st = reinterpret_cast<float *>(sk + BC * LK), *sm = st + TSZ;
+  u16 *tp = reinterpret_cast<u16 *>(st), *mp = reinterpret_cast<u16 *>(sm);
+  float *area = sm + TSZ;  // the value-column tiles, then three C x C matrices
   float *ss = area, *sds = ss + K * LT, *sx = sds + K * LT, *sdo = sx + BC * LT, *su = sdo + BC * LT;
   float *sdu = su + BC * LT, *sdx = sdu + BC * LT;
   // bf16 inputs: the per-tile products take their operands from transposed
-  // bf16 high/low pairs [16][LB] (X^T, dU^T, U^T, (E U)^T, (-Gamma dX)^T) and dO
-  // rows as they are [64][LO]; sdu follows sx and these replace sdo, su, sdx
-  constexpr int LB = BC + 8, LO = 16 + 8, PAIR = 2 * 16 * LB;
+  // bf16 high/low pairs [16][LB] (X^T, dU^T, U^T, (E U)^T, (-Gamma dX)^T,
+  // (beta X)^T) and dO rows as they are [64][LO]; sdu follows sx and these
+  // replace sdo, su, sdx
   if constexpr (BF) sdu = sx + BC * LT;
   u16 *xT = reinterpret_cast<u16 *>(sdu + BC * LT), *duT = xT + PAIR, *uT = duT + PAIR, *euT = uT + PAIR,
-      *gxT = euT + PAIR, *sdo16 = gxT + PAIR;
+      *gxT = euT + PAIR, *bxT = gxT + PAIR, *sdo16 = bxT + PAIR;
   float *b1 = area, *b2 = b1 + BC * LC, *b3 = b2 + BC * LC;
-  // bf16 inputs: b2 in float first, then dM o Mt (b1) and H + H^T (b3) as
-  // bf16 high/low pairs, rows of LB
-  if constexpr (BF) b2 = area;
-  u16 *b1p = reinterpret_cast<u16 *>(area + BC * LC), *b3p = b1p + 2 * BC * LB;
+  // bf16 inputs: dT (then W), dM o Mt and H + H^T as bf16 high/low pairs, rows of LB
+  u16 *b2p = reinterpret_cast<u16 *>(area), *b1p = b2p + 2 * BC * LB, *b3p = b1p + 2 * BC * LB;
   float *vec = area + grad_area<K, BF>();
   float *sc = vec, *sgam = sc + BC, *se = sgam + BC, *sbeta = se + BC;
   float *sdgam = sbeta + BC, *sde = sdgam + BC;
@@ -1071,7 +1094,11 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
   if (tid < BNT) {  // the loads run on the first four waves
     load_rows_raw<TIn, K>(sq, LK, p.q, p, b, t0, p.Hk, hk, K);
     load_rows_raw<TIn, K>(sk, LK, p.k, p, b, t0, p.Hk, hk, K);
-    load_t(st, p.ws_T + rec(p, b, h, i) * BC * BC);
+    if constexpr (BF) {
+      load_t_pair(tp, LB, p.ws_T + rec(p, b, h, i) * BC * BC);
+    } else {
+      load_t(st, p.ws_T + rec(p, b, h, i) * BC * BC);
+    }
     load_decays(p, b, h, i, sc, sgam, se, sbeta);
     if (tid < BC) {
       sdgam[tid] = 0.f;
@@ -1091,7 +1118,12 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = tw + 4 * g4 + r, s2 = 16 * tc + c;
-      sm[t * LC + s2] = t >= s2 ? p.scale * qk[r] * expf(sc[t] - sc[s2]) : 0.f;
+      const float mv = t >= s2 ? p.scale * qk[r] * expf(sc[t] - sc[s2]) : 0.f;
+      if constexpr (BF) {
+        put_pair1(mp, BC * LB, t * LB + s2, mv);
+      } else {
+        sm[t * LC + s2] = mv;
+      }
     }
   }
 
@@ -1189,7 +1221,10 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
         xv[r] = sx[t * LT + c] - sgam[t] * ks[r];  // X = V - Gamma K S
         sx[t * LT + c] = xv[r];
       }
-      if constexpr (BF) put_t_pair(xT, LB, tw + 4 * g4, c, xv);
+      if constexpr (BF) {
+        put_t_pair(xT, LB, tw + 4 * g4, c, xv);
+        put_t_pair(bxT, LB, tw + 4 * g4, c, xv * ld4(&sbeta[tw + 4 * g4]));
+      }
     } else {
       float4_t qs;
       if constexpr (BF) {
@@ -1205,17 +1240,22 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
     }
     __syncthreads();
     if (chain) {
-      const float4_t u = tile_mm4<BC>(
-          zero4(), [&](int r, int s2) { return ld4(&st[(tw + r) * LC + s2]) * ld4(&sbeta[s2]); },
-          [&](int s2, int col) { return ld4s(&sx[s2 * LT + col], LT); });
-      float4_t du = tile_mm4<BC>(zero4(), [&](int r, int s2) { return ld4s(&sm[s2 * LC + tw + r], LC); },
-                                 [&](int s2, int col) {
-                                   if constexpr (BF) {
-                                     return ld4es(sdo16, s2 * LO + col, LO);
-                                   } else {
-                                     return ld4s(&sdo[s2 * LT + col], LT);
-                                   }
-                                 });
+      float4_t u, du;
+      if constexpr (BF) {  // U = T (beta X), dU0 part M^T dO (M^T, dO columns by transposing reads)
+        u = pair_times_pair<BC>(tp, tp + BC * LB, LB, tw, bxT, bxT + 16 * LB, LB);
+        du = zero4();
+#pragma unroll
+        for (int ts = 0; ts < BC; ts += 32) {
+          const bh8_t dof = tr_frag(sdo16, LO, ts, 0);
+          du = mfma_bf16(tr_frag(mp, LB, ts, tw), dof, du);
+          du = mfma_bf16(tr_frag(mp + BC * LB, LB, ts, tw), dof, du);
+        }
+      } else {
+        u = tile_mm4<BC>(zero4(), [&](int r, int s2) { return ld4(&st[(tw + r) * LC + s2]) * ld4(&sbeta[s2]); },
+                         [&](int s2, int col) { return ld4s(&sx[s2 * LT + col], LT); });
+        du = tile_mm4<BC>(zero4(), [&](int r, int s2) { return ld4s(&sm[s2 * LC + tw + r], LC); },
+                          [&](int s2, int col) { return ld4s(&sdo[s2 * LT + col], LT); });
+      }
       float4_t eu;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -1234,9 +1274,15 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
     }
     __syncthreads();
     if (chain) {
-      const float4_t dx = tile_mm4<BC>(
-          zero4(), [&](int r, int s2) { return ld4s(&st[s2 * LC + tw + r], LC) * sbeta[tw + r]; },
-          [&](int s2, int col) { return ld4s(&sdu[s2 * LT + col], LT); });
+      float4_t dx;
+      if constexpr (BF) {  // dX = diag(beta) T^T dU
+        dx = tt_times_pair(tp, tp + BC * LB, LB, tw, duT, duT + 16 * LB, LB);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dx[r] *= sbeta[tw + 4 * g4 + r];
+      } else {
+        dx = tile_mm4<BC>(zero4(), [&](int r, int s2) { return ld4s(&st[s2 * LC + tw + r], LC) * sbeta[tw + r]; },
+                          [&](int s2, int col) { return ld4s(&sdu[s2 * LT + col], LT); });
+      }
       float4_t gx;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -1342,11 +1388,15 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
       } else {
         b1[t * LC + s2] = dmv * d;
       }
-      const float dcv = dmv * sm[t * LC + s2];
+      const float dcv = dmv * (BF ? pair_val(mp, BC * LB, t * LB + s2) : sm[t * LC + s2]);
       rc[r] += dcv;
       cc[m] -= dcv;
-      b2[t * LC + s2] = dtb[m][r] * sbeta[s2];
-      cb[m] += dtb[m][r] * st[t * LC + s2];
+      if constexpr (BF) {
+        put_pair1(b2p, BC * LB, t * LB + s2, dtb[m][r] * sbeta[s2]);
+      } else {
+        b2[t * LC + s2] = dtb[m][r] * sbeta[s2];
+      }
+      cb[m] += dtb[m][r] * (BF ? pair_val(tp, BC * LB, t * LB + s2) : st[t * LC + s2]);
     }
   }
   __syncthreads();
@@ -1355,14 +1405,33 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
 #pragma unroll
   for (int m = 0; m < 2; ++m) {
     const int tc = 2 * half + m;
-    w4[m] = tile_mm4<BC>(zero4(), [&](int r, int u2) { return ld4s(&st[u2 * LC + tw + r], LC); },
-                         [&](int u2, int col) { return ld4s(&b2[u2 * LC + 16 * tc + col], LC); });
+    if constexpr (BF) {  // T^T and dT's columns by transposing reads of the pairs
+      w4[m] = zero4();
+#pragma unroll
+      for (int ts = 0; ts < BC; ts += 32) {
+        const bh8_t th = tr_frag(tp, LB, ts, tw), tl = tr_frag(tp + BC * LB, LB, ts, tw);
+        const bh8_t dh = tr_frag(b2p, LB, ts, 16 * tc), dl = tr_frag(b2p + BC * LB, LB, ts, 16 * tc);
+        w4[m] = mfma_bf16(th, dh, w4[m]);
+        w4[m] = mfma_bf16(th, dl, w4[m]);
+        w4[m] = mfma_bf16(tl, dh, w4[m]);
+      }
+    } else {
+      w4[m] = tile_mm4<BC>(zero4(), [&](int r, int u2) { return ld4s(&st[u2 * LC + tw + r], LC); },
+                           [&](int u2, int col) { return ld4s(&b2[u2 * LC + 16 * tc + col], LC); });
+    }
   }
   __syncthreads();
 #pragma unroll
   for (int m = 0; m < 2; ++m) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) b2[(tw + 4 * g4 + r) * LC + 16 * (2 * half + m) + c] = w4[m][r];
+    for (int r = 0; r < 4; ++r) {
+      const int e = (tw + 4 * g4 + r) * (BF ? LB : LC) + 16 * (2 * half + m) + c;
+      if constexpr (BF) {
+        put_pair1(b2p, BC * LB, e, w4[m][r]);
+      } else {
+        b2[e] = w4[m][r];
+      }
+    }
   }
   __syncthreads();
   // dA = -W T^T (strict lower): H = dA beta_t D, stored as H + H^T in b3
@@ -1370,8 +1439,13 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
 #pragma unroll
   for (int m = 0; m < 2; ++m) {
     const int tc = 2 * half + m;
-    const float4_t da = tile_mm4<BC>(zero4(), [&](int r, int u2) { return ld4(&b2[(tw + r) * LC + u2]); },
-                                     [&](int u2, int col) { return ld4(&st[(16 * tc + col) * LC + u2]); });
+    float4_t da;
+    if constexpr (BF) {  // W rows times T rows (both pairs)
+      da = pair_times_pair<BC>(b2p, b2p + BC * LB, LB, tw, tp + 16 * tc * LB, tp + BC * LB + 16 * tc * LB, LB);
+    } else {
+      da = tile_mm4<BC>(zero4(), [&](int r, int u2) { return ld4(&b2[(tw + r) * LC + u2]); },
+                        [&](int u2, int col) { return ld4(&st[(16 * tc + col) * LC + u2]); });
+    }
     float4_t gk;
     if constexpr (BF) {
       gk = rows_times_rows<K>(sk, sk, LK, tw, 16 * tc);
@@ -1529,8 +1603,8 @@ constexpr size_t scan_lds() { return ScanLds<K, TIn>::BYTES; }
 template <int K, typename TIn>
 constexpr size_t grad_lds() {
   return sizeof(TIn) * 2 * BC * (K + 16 / sizeof(TIn)) +
-         sizeof(float) * (2 * BC * LC + grad_area<K, std::is_same<TIn, u16>::value>() + 6 * BC + 96 * (GNT / 64) +
-                          GNT / 64 + 8) +
+         sizeof(float) * (2 * (std::is_same<TIn, u16>::value ? BC * (BC + 8) : BC * LC) +
+                          grad_area<K, std::is_same<TIn, u16>::value>() + 6 * BC + 96 * (GNT / 64) + GNT / 64 + 8) +
          (std::is_same<TIn, u16>::value ? sizeof(u16) * 4 * 16 * (K + 8) : 0);
 }
 
