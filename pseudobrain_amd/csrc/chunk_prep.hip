@@ -80,6 +80,7 @@ struct PrepBlock {
   unsigned char *lds;
   const ChunkParams &p;
   int tid, lane, c16, g4, wave, group_heads, hpi, hgroups, jscan;
+  bool nt = false;  // record stores non-temporal (a large call)
   Inputs in;
   float4_t rk[3], rq[3];  // raw K K^T and Q K^T of this wave's tile pairs
   uint32_t kp_frag, sp_frag, sp_tile, at_lane, tr_a;
@@ -327,7 +328,12 @@ struct PrepBlock {
       const int kk = fi < 2 ? 0 : ((fi - 2) & 1);
       const uint32_t src = (f < NFRAG ? L::TB : L::QKD) + 16 * r * L::SPB + sp_frag + 64 * kk;
       const uint32_t dst = (f < NFRAG ? REC_TB : REC_QKD) + fi * FRAG_BYTES + lane * 16;
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, ld<half8_t>(src)), rr, dst, 0, 0);
+      const u32x4_t x = __builtin_bit_cast(u32x4_t, ld<half8_t>(src));
+      if (nt) {
+        __builtin_amdgcn_raw_buffer_store_b128(x, rr, dst, 0, 2);
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b128(x, rr, dst, 0, 0);
+      }
     }
     const uint32_t sc = L::SC + jh * L::SC_HEAD;
     const float gam = ld<float>(sc + L::GAM + lane * 4);
@@ -335,7 +341,11 @@ struct PrepBlock {
                       : wave == 1 ? p.scale * gam
                       : ld<float>(sc + (wave == 2 ? L::DEC : L::CUM) + lane * 4);
     const uint32_t dst = REC_SC + 256 * wave + lane * 4;  // SC_GAM, SC_GSC, SC_DEC, c
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, val), rr, dst, 0, 0);
+    if (nt) {
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, val), rr, dst, 0, 2);
+    } else {
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, val), rr, dst, 0, 0);
+    }
   }
 
   // Blocks (0, 1) and (2, 3) of Tb and QKD lie above the diagonal inside the
@@ -399,13 +409,16 @@ struct PrepBlock {
 };
 
 template <int K, typename TIn>
-__global__ __launch_bounds__(PNT, prep_wg_per_cu<TIn>()) void prep_kernel(ChunkParams p, int items) {
+__global__ __launch_bounds__(PNT, prep_wg_per_cu<TIn>()) void prep_kernel(ChunkParams p, int items, int nt) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   PrepBlock<K, TIn> blk(smem_raw, p);
+  blk.nt = nt != 0;
   blk.run(items);
 }
 
 }  // namespace
+
+constexpr long REC_STREAM_BYTES = 64L << 20;
 
 template <int K, typename TIn>
 int launch_prep(const ChunkParams &p, long records, hipStream_t stream) {
@@ -417,7 +430,10 @@ int launch_prep(const ChunkParams &p, long records, hipStream_t stream) {
   const long items = records * (p.Hv / hpi);
   if (items > 0x3fffffffL) return PBGDN_ERR_UNSUPPORTED;  // item numbers are 32-bit
   const long grid = prep_grid(items, p.cus, prep_wg_per_cu<TIn>(), p.xcds);
-  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(PNT), smem, stream, p, static_cast<int>(items));
+  // Records of a large call are written non-temporally: measured on the
+  // 32,768-token call (213 MB of records), the scan then reads them 2% faster.
+  const int nt = records * p.Hv * static_cast<long>(REC_BYTES) > REC_STREAM_BYTES ? 1 : 0;
+  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(PNT), smem, stream, p, static_cast<int>(items), nt);
   return hipGetLastError() == hipSuccess ? PBGDN_OK : PBGDN_ERR_LAUNCH;
 }
 
