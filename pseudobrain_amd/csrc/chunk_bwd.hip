@@ -57,7 +57,7 @@ struct BwdParams {
   float *dg;
   void *dbeta;
   float *dh0;
-  float *ws_T, *ws_c, *ws_dU0, *ws_J, *ws_S, *ws_dS, *ws_dq, *ws_dk;
+  float *ws_T, *ws_c, *ws_beta, *ws_dU0, *ws_J, *ws_S, *ws_dS, *ws_dq, *ws_dk;
   int in_dtype, beta_dtype;
   int B, T, Hk, Hv, K, V, n;
   float scale;
@@ -394,7 +394,8 @@ __device__ __forceinline__ void load_decays(const BwdParams &p, int b, int h, in
 }
 
 // ---------------------------------------------------------------------------
-// Per (chunk, value head): T, dU0 = M^T dO, J = scale (Gamma Q)^T dO, c.
+// Per (chunk, value head): T, dU0 = M^T dO, J = scale (Gamma Q)^T dO, c and
+// beta as float.
 // ---------------------------------------------------------------------------
 // Rows t0 .. t0+63 of a [B,T,H,W] tensor of TIn (head hd, columns 0 ..
 // COLS-1) into LDS as they are (16-byte pieces; rows of ld elements, ld a
@@ -456,8 +457,10 @@ __global__ __launch_bounds__(BNT) void bwd_local_kernel(BwdParams p) {
     }
     sc[lane] = x;
     sgam[lane] = expf(x);
-    sbeta[lane] = t < p.T ? load_elem(p.beta, (static_cast<long>(b) * p.T + t) * p.Hv + h, p.beta_dtype) : 0.f;
+    const float bt = t < p.T ? load_elem(p.beta, (static_cast<long>(b) * p.T + t) * p.Hv + h, p.beta_dtype) : 0.f;
+    sbeta[lane] = bt;
     p.ws_c[rec(p, b, h, i) * BC + lane] = x;
+    p.ws_beta[rec(p, b, h, i) * BC + lane] = bt;
   }
   __syncthreads();
   auto krow = [&](int kk, int j, int tc) { return ld4e(sk, (16 * tc + j) * LK + kk); };
@@ -644,18 +647,20 @@ struct ScanStage {
     const unsigned char *kb = static_cast<const unsigned char *>(p.k);
 #pragma unroll
     for (int m = 0; m < KP; ++m) {
-      const int e = tid + BNT * m, row = e / ROW16, part = e % ROW16, t = t0 + row;
-      const long off = ((static_cast<long>(b) * p.T + t) * p.Hk + hk) * K * static_cast<long>(sizeof(TIn)) + part * 16;
-      kr[m] = t < p.T ? *reinterpret_cast<const uint4 *>(kb + off) : uint4{0u, 0u, 0u, 0u};
+      // rows clamped into the sequence and zeroed after: every path issues
+      // the same loads, so the waits for them can be partial
+      const int e = tid + BNT * m, row = e / ROW16, part = e % ROW16, t = t0 + row, tc = t < p.T ? t : p.T - 1;
+      const long off = ((static_cast<long>(b) * p.T + tc) * p.Hk + hk) * K * static_cast<long>(sizeof(TIn)) + part * 16;
+      const uint4 kx = *reinterpret_cast<const uint4 *>(kb + off);
+      kr[m] = t < p.T ? kx : uint4{0u, 0u, 0u, 0u};
     }
     const float4_t *wt = reinterpret_cast<const float4_t *>(p.ws_T + r * BC * BC);
 #pragma unroll
     for (int m = 0; m < 4; ++m) tr[m] = wt[tid + BNT * m];
-    if (tid < BC) {
-      cv = p.ws_c[r * BC + tid];
-      bv = t0 + tid < p.T ? load_elem(p.beta, (static_cast<long>(b) * p.T + t0 + tid) * p.Hv + h, p.beta_dtype)
-                          : 0.f;
-    }
+    // every lane loads (wave 0's values are used): c and beta as float from
+    // the workspace, no load that only some paths issue
+    cv = p.ws_c[r * BC + (tid & (BC - 1))];
+    bv = p.ws_beta[r * BC + (tid & (BC - 1))];
     if constexpr (!ADJ) {
       const int row = tid / TILE16, part = tid % TILE16, t = t0 + row;
       const unsigned char *vb = static_cast<const unsigned char *>(p.v);
@@ -1655,7 +1660,7 @@ int run_backward(const BwdParams &p, hipStream_t st) {
 
 // Workspace floats per (batch, value head, chunk), and the GQA scratch.
 long ws_record_floats(int K, int V) {
-  return static_cast<long>(BC) * BC + BC + static_cast<long>(BC) * V + 3L * K * V;
+  return static_cast<long>(BC) * BC + 2 * BC + static_cast<long>(BC) * V + 3L * K * V;
 }
 
 }  // namespace
@@ -1716,7 +1721,8 @@ extern "C" int pbgdn_chunk_bwd(const void *q, const void *k, const void *v, int 
   p.dh0 = dh0;
   p.ws_T = ws;
   p.ws_c = p.ws_T + recs * BC * BC;
-  p.ws_dU0 = p.ws_c + recs * BC;
+  p.ws_beta = p.ws_c + recs * BC;
+  p.ws_dU0 = p.ws_beta + recs * BC;
   p.ws_J = p.ws_dU0 + recs * BC * V;
   p.ws_S = p.ws_J + recs * K * V;
   p.ws_dS = p.ws_S + recs * K * V;

@@ -334,11 +334,11 @@ def test_chunk_bwd_rejects_bad_arguments(over, code):
 
 
 def test_chunk_bwd_workspace_size():
-    """Per (batch, value head, chunk): T (64 x 64), c (64), dU0 (64 x V) and
-    the start state, end adjoint and J (K x V each) in float32; with GQA also
-    dq and dk per value head; plus 256 bytes of slack."""
+    """Per (batch, value head, chunk): T (64 x 64), c and beta (64 each), dU0
+    (64 x V) and the start state, end adjoint and J (K x V each) in float32;
+    with GQA also dq and dk per value head; plus 256 bytes of slack."""
     size = _lib.lib().pbgdn_chunk_bwd_workspace_size
-    per_record = 64 * 64 + 64 + 64 * 128 + 3 * 128 * 128
+    per_record = 64 * 64 + 2 * 64 + 64 * 128 + 3 * 128 * 128
     assert size(2, 100, 4, 4, 128, 128) == 2 * 4 * 2 * per_record * 4 + 256
     assert size(1, 64, 2, 4, 128, 128) == (4 * per_record + 2 * 64 * 4 * 128) * 4 + 256
     assert size(1, 0, 1, 1, 64, 64) == 256
