@@ -378,18 +378,18 @@ __device__ __forceinline__ void load_t_pair(u16 *tp, int ld, const float *src) {
 }
 
 // c (in-chunk cumulative log decay), e^c, e^(c_last - c) and beta of one chunk,
-// from the workspace record (c) and beta; rows past T have beta 0.
+// from the workspace record (c, and beta as float: 0 past T). Every lane
+// loads; the first wave stores.
 __device__ __forceinline__ void load_decays(const BwdParams &p, int b, int h, int i, float *sc, float *sgam, float *se,
                                             float *sbeta) {
   const int tid = threadIdx.x;
+  const long r = rec(p, b, h, i) * BC;
+  const float c = p.ws_c[r + (tid & (BC - 1))], last = p.ws_c[r + BC - 1], bt = p.ws_beta[r + (tid & (BC - 1))];
   if (tid < BC) {
-    const float c = p.ws_c[rec(p, b, h, i) * BC + tid];
-    const float last = p.ws_c[rec(p, b, h, i) * BC + BC - 1];
-    const int t = i * BC + tid;
     sc[tid] = c;
     sgam[tid] = expf(c);
     se[tid] = expf(last - c);
-    sbeta[tid] = t < p.T ? load_elem(p.beta, (static_cast<long>(b) * p.T + t) * p.Hv + h, p.beta_dtype) : 0.f;
+    sbeta[tid] = bt;
   }
 }
 
@@ -398,26 +398,36 @@ __device__ __forceinline__ void load_decays(const BwdParams &p, int b, int h, in
 // beta as float.
 // ---------------------------------------------------------------------------
 // Rows t0 .. t0+63 of a [B,T,H,W] tensor of TIn (head hd, columns 0 ..
-// COLS-1) into LDS as they are (16-byte pieces; rows of ld elements, ld a
-// multiple of 16 bytes), zero past T.
+// COLS-1) as 16-byte pieces in registers, then into LDS as they are (rows of
+// ld elements, ld a multiple of 16 bytes), zero past T. Every lane issues the
+// same loads (rows clamped into the sequence, zeroed after), so a kernel can
+// issue several tensors' rows before its first wait, and that wait is one
+// round trip rather than one per tensor.
 template <typename TIn, int COLS>
-__device__ __forceinline__ void load_rows_raw(TIn *dst, int ld, const void *src, const BwdParams &p, int b, int t0,
-                                              int heads, int hd, int width) {
-  constexpr int EPP = 16 / sizeof(TIn), PPR = COLS / EPP, TOTAL = BC * PPR, PER = (TOTAL + BNT - 1) / BNT;
-  const unsigned char *base = static_cast<const unsigned char *>(src);
+struct RawRows {
+  static constexpr int EPP = 16 / sizeof(TIn), PPR = COLS / EPP, TOTAL = BC * PPR, PER = TOTAL / BNT;
+  static_assert(TOTAL % BNT == 0, "whole pieces per thread");
   uint4 raw[PER];
+
+  __device__ __forceinline__ void load(const void *src, const BwdParams &p, int b, int t0, int heads, int hd,
+                                       int width) {
+    const unsigned char *base = static_cast<const unsigned char *>(src);
 #pragma unroll
-  for (int m = 0; m < PER; ++m) {
-    const int e = threadIdx.x + BNT * m, row = e / PPR, part = e % PPR, t = t0 + row;
-    const long off = ((static_cast<long>(b) * p.T + t) * heads + hd) * width * static_cast<long>(sizeof(TIn));
-    raw[m] = e < TOTAL && t < p.T ? *reinterpret_cast<const uint4 *>(base + off + part * 16) : uint4{0u, 0u, 0u, 0u};
+    for (int m = 0; m < PER; ++m) {
+      const int e = threadIdx.x + BNT * m, row = e / PPR, part = e % PPR, t = t0 + row, tc = t < p.T ? t : p.T - 1;
+      const long off = ((static_cast<long>(b) * p.T + tc) * heads + hd) * width * static_cast<long>(sizeof(TIn));
+      const uint4 x = *reinterpret_cast<const uint4 *>(base + off + part * 16);
+      raw[m] = t < p.T ? x : uint4{0u, 0u, 0u, 0u};
+    }
   }
+  __device__ __forceinline__ void put(TIn *dst, int ld) const {
 #pragma unroll
-  for (int m = 0; m < PER; ++m) {
-    const int e = threadIdx.x + BNT * m, row = e / PPR, part = e % PPR;
-    if (e < TOTAL) *reinterpret_cast<uint4 *>(&dst[row * ld + part * EPP]) = raw[m];
+    for (int m = 0; m < PER; ++m) {
+      const int e = threadIdx.x + BNT * m, row = e / PPR, part = e % PPR;
+      *reinterpret_cast<uint4 *>(&dst[row * ld + part * EPP]) = raw[m];
+    }
   }
-}
+};
 
 // q, k and dO stay in LDS in the input dtype (converted on read), and M is
 // formed in A's place once T has been written out: 72 KiB for 16-bit inputs at
@@ -444,9 +454,16 @@ __global__ __launch_bounds__(BNT) void bwd_local_kernel(BwdParams p) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 15, g4 = lane >> 4;
   const int hk = h / (p.Hv / p.Hk);
   const int t0 = i * BC;
-  load_rows_raw<TIn, K>(sq, LK, p.q, p, b, t0, p.Hk, hk, K);
-  load_rows_raw<TIn, K>(sk, LK, p.k, p, b, t0, p.Hk, hk, K);
-  load_rows_raw<TIn, V>(sdo, LV, p.dout, p, b, t0, p.Hv, h, V);
+  {
+    RawRows<TIn, K> rq, rk;
+    RawRows<TIn, V> rd;
+    rq.load(p.q, p, b, t0, p.Hk, hk, K);
+    rk.load(p.k, p, b, t0, p.Hk, hk, K);
+    rd.load(p.dout, p, b, t0, p.Hv, h, V);
+    rq.put(sq, LK);
+    rk.put(sk, LK);
+    rd.put(sdo, LV);
+  }
   if (wave == 0) {  // inclusive cumulative sum of g over the chunk (zero past T)
     const int t = t0 + lane;
     float x = t < p.T ? p.g[(static_cast<long>(b) * p.T + t) * p.Hv + h] : 0.f;
@@ -1097,8 +1114,11 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
   const int hk = h / (p.Hv / p.Hk);
   const int t0 = i * BC;
   if (tid < BNT) {  // the loads run on the first four waves
-    load_rows_raw<TIn, K>(sq, LK, p.q, p, b, t0, p.Hk, hk, K);
-    load_rows_raw<TIn, K>(sk, LK, p.k, p, b, t0, p.Hk, hk, K);
+    RawRows<TIn, K> rq, rk;
+    rq.load(p.q, p, b, t0, p.Hk, hk, K);
+    rk.load(p.k, p, b, t0, p.Hk, hk, K);
+    rq.put(sq, LK);
+    rk.put(sk, LK);
     if constexpr (BF) {
       load_t_pair(tp, LB, p.ws_T + rec(p, b, h, i) * BC * BC);
     } else {
