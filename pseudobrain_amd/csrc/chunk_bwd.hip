@@ -331,6 +331,20 @@ __device__ __forceinline__ u16 bf16_bits(float x) {
   return static_cast<u16>(u >> 16);
 }
 
+// Element i of an output of the kernel's input type from float, with the
+// rounding store_elem applies for that dtype, chosen at compile time (no
+// branch on the runtime dtype around each store).
+template <typename TIn>
+__device__ __forceinline__ void store_el(void *p, long i, float x) {
+  if constexpr (sizeof(TIn) == 4) {
+    static_cast<float *>(p)[i] = x;
+  } else if constexpr (std::is_same<TIn, u16>::value) {
+    static_cast<u16 *>(p)[i] = float_to_bf16_bits(x);
+  } else {
+    static_cast<half_t *>(p)[i] = static_cast<half_t>(x);
+  }
+}
+
 // The value of a bf16 high/low pair.
 __device__ __forceinline__ float pair_val(const u16 *m, int lo_off, int e) {
   return __uint_as_float(static_cast<uint32_t>(m[e]) << 16) + __uint_as_float(static_cast<uint32_t>(m[lo_off + e]) << 16);
@@ -1315,7 +1329,7 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
         if constexpr (!BF) sdx[t * LT + c] = dx[r];
         gx[r] = -sgam[t] * dx[r];
         if (t0 + t < p.T) {
-          store_elem(p.dv, ((static_cast<long>(b) * p.T + t0 + t) * p.Hv + h) * V + v0 + c, p.in_dtype, dx[r]);
+          store_el<TIn>(p.dv, ((static_cast<long>(b) * p.T + t0 + t) * p.Hv + h) * V + v0 + c, dx[r]);
         }
         dgam_r[r] -= ks[r] * dx[r];
       }
@@ -1564,8 +1578,8 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
       if (t >= p.T) continue;
       if (direct) {
         const long o = ((static_cast<long>(b) * p.T + t) * p.Hk + hk) * K + kk;
-        store_elem(p.dq, o, p.in_dtype, dq[m][r]);
-        store_elem(p.dk, o, p.in_dtype, dk[m][r]);
+        store_el<TIn>(p.dq, o, dq[m][r]);
+        store_el<TIn>(p.dk, o, dk[m][r]);
       } else {
         const long o = ((static_cast<long>(b) * p.T + t) * p.Hv + h) * K + kk;
         p.ws_dq[o] = dq[m][r];
