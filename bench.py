@@ -505,13 +505,14 @@ def bench_layer_core(steps, warmup=3, rounds=3):
     return {"layer_core_ungraded": out}
 
 
-def bench_decode_layer(batch, steps, warmup=10, state_dtype=None):
+def bench_decode_layer(batch, steps, warmup=10, state_dtype=None, conv_dtype=None):
     """The fused decode step of the whole layer (pbgdn_decode_layer_fwd) at the
     Qwen3-Next layer shape for `batch` sequences of one token, state and conv
     pools updated in place, against the same step as three launches (the
     layer prologue, the recurrent step, the epilogue). HBM roofline of the
     fused step: the state read and written, the projection row read, the conv
-    tail read and written, hs written."""
+    tail read and written, hs written. `conv_dtype` is the conv tail's dtype
+    (float32 by default)."""
     import torch
     from pseudobrain_amd.layer import decode_layer_step, layer_epilogue, layer_prologue
     gen = torch.Generator().manual_seed(1)
@@ -519,7 +520,7 @@ def bench_decode_layer(batch, steps, warmup=10, state_dtype=None):
     channels = 2 * hk * dk + hv * dv
     width = channels + hv * dv + 2 * hv
     z = torch.randn(batch, width, generator=gen).to(torch.bfloat16).cuda()
-    pool = torch.randn(batch, conv - 1, channels, generator=gen).cuda()
+    pool = torch.randn(batch, conv - 1, channels, generator=gen).to(conv_dtype or torch.float32).cuda()
     weight = ((torch.rand(channels, conv, generator=gen) * 2 - 1) / 2).cuda()
     a_log = torch.empty(hv).uniform_(0, 16, generator=gen).log().cuda()
     dt_bias = (torch.randn(hv, generator=gen) - 4).cuda()
@@ -538,7 +539,8 @@ def bench_decode_layer(batch, steps, warmup=10, state_dtype=None):
 
     sec, ksec = timed_steps(fused, steps, warmup)
     sec3, ksec3 = timed_steps(three, steps, warmup)
-    nbytes = (2 * batch * hv * dk * dv * state.element_size() + batch * width * 2 + 2 * batch * (conv - 1) * channels * 4
+    nbytes = (2 * batch * hv * dk * dv * state.element_size() + batch * width * 2
+              + 2 * batch * (conv - 1) * channels * pool.element_size()
               + batch * hv * dv * 4)
     gbs = nbytes / ksec / 1e9
     return {"batch": batch, "state_dtype": str(state.dtype).replace("torch.", ""), "steps": steps,
@@ -679,6 +681,8 @@ def main(argv=None):
             result["decode_layer_b64"] = bench_decode_layer(64, 200)
             result["decode_layer_b64"]["roofline"]["traffic"] = measured_traffic("decode_layer_b64")
             result["decode_layer_b64_bf16_state"] = bench_decode_layer(64, 200, state_dtype=torch.bfloat16)
+            # the conv tail in the projection's dtype, as a serving cache holds it
+            result["decode_layer_b64_bf16_tail"] = bench_decode_layer(64, 200, conv_dtype=torch.bfloat16)
     if not args.no_backward:
         result["backward"] = bench_backward()
     if not args.no_long:

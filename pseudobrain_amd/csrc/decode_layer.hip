@@ -78,6 +78,18 @@ __device__ float conv_channel(const DecodeLayerParams &p, long slot, long c, flo
   return siluf(acc);
 }
 
+// conv_channel for a bf16 input and a bf16 tail of DECODE_MAX_CONV taps: the
+// tail rows' bits (oldest first) and x's, summed in conv_channel's order (a
+// bf16 value rounds through bf16 to itself).
+__device__ __forceinline__ float conv4_bf16(const float *w, u16 a, u16 b, u16 c, u16 x) {
+  float acc = 0.f;
+  acc += w[0] * bf16_bits_to_float(a);
+  acc += w[1] * bf16_bits_to_float(b);
+  acc += w[2] * bf16_bits_to_float(c);
+  acc += w[3] * bf16_bits_to_float(x);
+  return siluf(acc);
+}
+
 // CP: the state's cache policy (state_io.hpp).
 template <int K, int V, typename TS, int CP>
 __global__ __launch_bounds__(DNT, (sizeof(TS) == 2 ? 5 : 4)) void decode_layer_kernel(DecodeLayerParams p) {
@@ -149,22 +161,64 @@ __global__ __launch_bounds__(DNT, (sizeof(TS) == 2 ? 5 : 4)) void decode_layer_k
   // k of the key head (convolution, SiLU, L2 norm over the head), then v,
   // SiLU(gate) and the decay/beta gates of each value head of the group.
   float yq = 0.f, yk = 0.f;
-  if (tid < K) {
-    const long cq = static_cast<long>(hk) * K + tid;
-    const long ck = qk_width + cq;
-    yq = conv_channel(p, slot, cq, load_elem(p.z, zrow + cq, p.in_dtype));
-    yk = conv_channel(p, slot, ck, load_elem(p.z, zrow + ck, p.in_dtype));
-  }
   const long v0 = 2 * qk_width + static_cast<long>(hk) * group * V;  // the group's v channels
-  for (int e = tid; e < group * V; e += DNT) {
-    sv[e] = conv_channel(p, slot, v0 + e, load_elem(p.z, zrow + v0 + e, p.in_dtype));
-    sgate[e] = siluf(load_elem(p.z, zrow + channels + static_cast<long>(hk) * group * V + e, p.in_dtype));
-  }
-  if (tid < group) {
-    const int h = hk * group + tid;
-    const long ab = zrow + channels + static_cast<long>(p.Hv) * V + h;
-    salpha[tid] = expf(-expf(p.a_log[h]) * softplusf(load_elem(p.z, ab, p.in_dtype) + p.dt_bias[h]));
-    sbeta[tid] = sigmoidf(load_elem(p.z, ab + p.Hv, p.in_dtype));
+  if (p.in_dtype == PBGDN_BF16 && p.conv_dtype == PBGDN_BF16 && p.conv == DECODE_MAX_CONV) {
+    // The bf16 serving case: a channel's loads (typed, no branch on a runtime
+    // dtype between them) all issue before their first use, so a thread waits
+    // once per channel group instead of once per load; the tail shifts by
+    // copying bits.
+    const u16 *z16 = static_cast<const u16 *>(p.z);
+    u16 *cs = static_cast<u16 *>(p.conv_state);
+    const long rs = p.conv_rs;
+    if (tid < K) {
+      const long cq = static_cast<long>(hk) * K + tid, ck = qk_width + cq;
+      const long bq = slot * p.conv_ss + cq * p.conv_cs, bk = slot * p.conv_ss + ck * p.conv_cs;
+      const u16 zq = z16[zrow + cq], zk = z16[zrow + ck];
+      const u16 q0 = cs[bq], q1 = cs[bq + rs], q2 = cs[bq + 2 * rs];
+      const u16 k0 = cs[bk], k1 = cs[bk + rs], k2 = cs[bk + 2 * rs];
+      yq = conv4_bf16(p.conv_weight + cq * DECODE_MAX_CONV, q0, q1, q2, zq);
+      yk = conv4_bf16(p.conv_weight + ck * DECODE_MAX_CONV, k0, k1, k2, zk);
+      cs[bq] = q1;
+      cs[bq + rs] = q2;
+      cs[bq + 2 * rs] = zq;
+      cs[bk] = k1;
+      cs[bk + rs] = k2;
+      cs[bk + 2 * rs] = zk;
+    }
+    for (int e = tid; e < group * V; e += DNT) {
+      const long cv = v0 + e, bv = slot * p.conv_ss + cv * p.conv_cs;
+      const u16 zv = z16[zrow + cv], zg = z16[zrow + channels + static_cast<long>(hk) * group * V + e];
+      const u16 a0 = cs[bv], a1 = cs[bv + rs], a2 = cs[bv + 2 * rs];
+      sv[e] = conv4_bf16(p.conv_weight + cv * DECODE_MAX_CONV, a0, a1, a2, zv);
+      sgate[e] = siluf(bf16_bits_to_float(zg));
+      cs[bv] = a1;
+      cs[bv + rs] = a2;
+      cs[bv + 2 * rs] = zv;
+    }
+    if (tid < group) {
+      const int h = hk * group + tid;
+      const long ab = zrow + channels + static_cast<long>(p.Hv) * V + h;
+      const float za = bf16_bits_to_float(z16[ab]), zb = bf16_bits_to_float(z16[ab + p.Hv]);
+      salpha[tid] = expf(-expf(p.a_log[h]) * softplusf(za + p.dt_bias[h]));
+      sbeta[tid] = sigmoidf(zb);
+    }
+  } else {
+    if (tid < K) {
+      const long cq = static_cast<long>(hk) * K + tid;
+      const long ck = qk_width + cq;
+      yq = conv_channel(p, slot, cq, load_elem(p.z, zrow + cq, p.in_dtype));
+      yk = conv_channel(p, slot, ck, load_elem(p.z, zrow + ck, p.in_dtype));
+    }
+    for (int e = tid; e < group * V; e += DNT) {
+      sv[e] = conv_channel(p, slot, v0 + e, load_elem(p.z, zrow + v0 + e, p.in_dtype));
+      sgate[e] = siluf(load_elem(p.z, zrow + channels + static_cast<long>(hk) * group * V + e, p.in_dtype));
+    }
+    if (tid < group) {
+      const int h = hk * group + tid;
+      const long ab = zrow + channels + static_cast<long>(p.Hv) * V + h;
+      salpha[tid] = expf(-expf(p.a_log[h]) * softplusf(load_elem(p.z, ab, p.in_dtype) + p.dt_bias[h]));
+      sbeta[tid] = sigmoidf(load_elem(p.z, ab + p.Hv, p.in_dtype));
+    }
   }
   const float pq2 = wave_sum(yq * yq);
   const float pk2 = wave_sum(yk * yk);

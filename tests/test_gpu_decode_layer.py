@@ -113,6 +113,17 @@ def test_decode_step_bf16_pools_channel_major_hf():
                   out_dtype=torch.bfloat16)
 
 
+def test_decode_step_qwen3next_bf16_tail():
+    """The Qwen3-Next shape with the conv pool in bf16, row-major, as a
+    serving cache holds it (the kernel's bf16 path: typed loads, the tail
+    shifted by copying bits; the new tail is checked bit for bit), fp32 state,
+    a padded (-1) entry."""
+    args = make(64, 70, 16, 128, 32, 128, 4, seed=75, conv_dtype=torch.bfloat16)
+    idx = torch.randperm(70, generator=torch.Generator().manual_seed(76))[:64].tolist()
+    idx[9] = -1
+    run_and_check("decode layer B=64 bf16 tail", args, idx, 16, 128, 32, 128)
+
+
 @pytest.mark.parametrize("conv", [0, 1, 2])
 @pytest.mark.parametrize("dk,dv,heads,vheads", [(64, 64, 2, 2), (64, 128, 2, 8), (128, 64, 4, 8)])
 def test_decode_step_shapes(conv, dk, dv, heads, vheads):
