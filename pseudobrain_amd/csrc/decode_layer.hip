@@ -78,16 +78,36 @@ __device__ float conv_channel(const DecodeLayerParams &p, long slot, long c, flo
   return siluf(acc);
 }
 
-// conv_channel for a bf16 input and a bf16 tail of DECODE_MAX_CONV taps: the
-// tail rows' bits (oldest first) and x's, summed in conv_channel's order (a
-// bf16 value rounds through bf16 to itself).
-__device__ __forceinline__ float conv4_bf16(const float *w, u16 a, u16 b, u16 c, u16 x) {
+// conv_channel for a bf16 input and DECODE_MAX_CONV taps: the tail rows
+// (oldest first, already rounded through bf16) and x, summed in
+// conv_channel's order.
+__device__ __forceinline__ float conv4(const float *w, float a, float b, float c, float x) {
   float acc = 0.f;
-  acc += w[0] * bf16_bits_to_float(a);
-  acc += w[1] * bf16_bits_to_float(b);
-  acc += w[2] * bf16_bits_to_float(c);
-  acc += w[3] * bf16_bits_to_float(x);
+  acc += w[0] * a;
+  acc += w[1] * b;
+  acc += w[2] * c;
+  acc += w[3] * x;
   return siluf(acc);
+}
+
+// A tail element of type TC (bf16 bits or float) as conv_channel reads it
+// for a bf16 input (rounded through bf16), and a value stored back as
+// store_elem would store it.
+template <typename TC>
+__device__ __forceinline__ float tail_in(TC x) {
+  if constexpr (std::is_same<TC, u16>::value) {
+    return bf16_bits_to_float(x);
+  } else {
+    return bf16_bits_to_float(float_to_bf16_bits(x));
+  }
+}
+template <typename TC>
+__device__ __forceinline__ TC tail_out(float x) {
+  if constexpr (std::is_same<TC, u16>::value) {
+    return float_to_bf16_bits(x);
+  } else {
+    return x;
+  }
 }
 
 // CP: the state's cache policy (state_io.hpp).
@@ -162,38 +182,43 @@ __global__ __launch_bounds__(DNT, (sizeof(TS) == 2 ? 5 : 4)) void decode_layer_k
   // SiLU(gate) and the decay/beta gates of each value head of the group.
   float yq = 0.f, yk = 0.f;
   const long v0 = 2 * qk_width + static_cast<long>(hk) * group * V;  // the group's v channels
-  if (p.in_dtype == PBGDN_BF16 && p.conv_dtype == PBGDN_BF16 && p.conv == DECODE_MAX_CONV) {
-    // The bf16 serving case: a channel's loads (typed, no branch on a runtime
-    // dtype between them) all issue before their first use, so a thread waits
-    // once per channel group instead of once per load; the tail shifts by
-    // copying bits.
+  // The serving cases, a bf16 projection with a bf16 or float32 tail of
+  // DECODE_MAX_CONV taps: a channel's loads (typed, no branch on a runtime
+  // dtype between them) all issue before their first use, so a thread waits
+  // once per channel group instead of once per load. Same values as the
+  // general path below.
+  auto typed_inputs = [&](auto tag) {
+    using TC = decltype(tag);
     const u16 *z16 = static_cast<const u16 *>(p.z);
-    u16 *cs = static_cast<u16 *>(p.conv_state);
+    TC *cs = static_cast<TC *>(p.conv_state);
     const long rs = p.conv_rs;
     if (tid < K) {
       const long cq = static_cast<long>(hk) * K + tid, ck = qk_width + cq;
       const long bq = slot * p.conv_ss + cq * p.conv_cs, bk = slot * p.conv_ss + ck * p.conv_cs;
       const u16 zq = z16[zrow + cq], zk = z16[zrow + ck];
-      const u16 q0 = cs[bq], q1 = cs[bq + rs], q2 = cs[bq + 2 * rs];
-      const u16 k0 = cs[bk], k1 = cs[bk + rs], k2 = cs[bk + 2 * rs];
-      yq = conv4_bf16(p.conv_weight + cq * DECODE_MAX_CONV, q0, q1, q2, zq);
-      yk = conv4_bf16(p.conv_weight + ck * DECODE_MAX_CONV, k0, k1, k2, zk);
-      cs[bq] = q1;
-      cs[bq + rs] = q2;
-      cs[bq + 2 * rs] = zq;
-      cs[bk] = k1;
-      cs[bk + rs] = k2;
-      cs[bk + 2 * rs] = zk;
+      const TC q0 = cs[bq], q1 = cs[bq + rs], q2 = cs[bq + 2 * rs];
+      const TC k0 = cs[bk], k1 = cs[bk + rs], k2 = cs[bk + 2 * rs];
+      const float xq = bf16_bits_to_float(zq), xk = bf16_bits_to_float(zk);
+      const float fq1 = tail_in(q1), fq2 = tail_in(q2), fk1 = tail_in(k1), fk2 = tail_in(k2);
+      yq = conv4(p.conv_weight + cq * DECODE_MAX_CONV, tail_in(q0), fq1, fq2, xq);
+      yk = conv4(p.conv_weight + ck * DECODE_MAX_CONV, tail_in(k0), fk1, fk2, xk);
+      cs[bq] = tail_out<TC>(fq1);
+      cs[bq + rs] = tail_out<TC>(fq2);
+      cs[bq + 2 * rs] = tail_out<TC>(xq);
+      cs[bk] = tail_out<TC>(fk1);
+      cs[bk + rs] = tail_out<TC>(fk2);
+      cs[bk + 2 * rs] = tail_out<TC>(xk);
     }
     for (int e = tid; e < group * V; e += DNT) {
       const long cv = v0 + e, bv = slot * p.conv_ss + cv * p.conv_cs;
       const u16 zv = z16[zrow + cv], zg = z16[zrow + channels + static_cast<long>(hk) * group * V + e];
-      const u16 a0 = cs[bv], a1 = cs[bv + rs], a2 = cs[bv + 2 * rs];
-      sv[e] = conv4_bf16(p.conv_weight + cv * DECODE_MAX_CONV, a0, a1, a2, zv);
+      const TC a0 = cs[bv], a1 = cs[bv + rs], a2 = cs[bv + 2 * rs];
+      const float xv = bf16_bits_to_float(zv), f1 = tail_in(a1), f2 = tail_in(a2);
+      sv[e] = conv4(p.conv_weight + cv * DECODE_MAX_CONV, tail_in(a0), f1, f2, xv);
       sgate[e] = siluf(bf16_bits_to_float(zg));
-      cs[bv] = a1;
-      cs[bv + rs] = a2;
-      cs[bv + 2 * rs] = zv;
+      cs[bv] = tail_out<TC>(f1);
+      cs[bv + rs] = tail_out<TC>(f2);
+      cs[bv + 2 * rs] = tail_out<TC>(xv);
     }
     if (tid < group) {
       const int h = hk * group + tid;
@@ -202,6 +227,12 @@ __global__ __launch_bounds__(DNT, (sizeof(TS) == 2 ? 5 : 4)) void decode_layer_k
       salpha[tid] = expf(-expf(p.a_log[h]) * softplusf(za + p.dt_bias[h]));
       sbeta[tid] = sigmoidf(zb);
     }
+  };
+  const bool typed = p.in_dtype == PBGDN_BF16 && p.conv == DECODE_MAX_CONV;
+  if (typed && p.conv_dtype == PBGDN_BF16) {
+    typed_inputs(u16{});
+  } else if (typed && p.conv_dtype == PBGDN_F32) {
+    typed_inputs(float{});
   } else {
     if (tid < K) {
       const long cq = static_cast<long>(hk) * K + tid;
