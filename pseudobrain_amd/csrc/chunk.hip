@@ -126,11 +126,9 @@ namespace {
 // fp16, v and the state as bf16 or fp16 high/low pairs), so v and the initial
 // states are brought within RANGE_LIMIT by a power of two first: the
 // recurrence is linear in (v, h0), and o and the final states of the scaled
-// inputs are the scaled results, exactly. Two small kernels compute it into
-// the workspace's tail (RANGE_BLOCKS partial maxima, then the scale), read by
-// the scan.
-constexpr float RANGE_LIMIT = 1024.f;
-constexpr int RANGE_BLOCKS = 512;
+// inputs are the scaled results, exactly. range_max_kernel writes
+// RANGE_BLOCKS partial maxima into the workspace's tail; the prep kernel's
+// first wave reduces them into the scale after them, which the scan reads.
 constexpr long RANGE_TAIL_BYTES = 4096;
 static_assert((RANGE_BLOCKS + 1) * 4 <= RANGE_TAIL_BYTES, "range tail");
 
@@ -168,27 +166,6 @@ __global__ __launch_bounds__(256) void range_max_kernel(RangeParams p) {
   if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
   __syncthreads();
   if (threadIdx.x == 0) p.part[blockIdx.x] = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
-}
-
-// The scale: 2^-e with e = max(0, ceil(log2(max / RANGE_LIMIT))); 1 for a
-// maximum that is not finite.
-__global__ __launch_bounds__(256) void range_scale_kernel(const float *part, float *scale) {
-  float m = 0.f;
-  for (int i = threadIdx.x; i < RANGE_BLOCKS; i += 256) m = fmaxf(m, part[i]);
-  m = wave_max(m);
-  __shared__ float wm[4];
-  if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    m = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
-    float down = 1.f;
-    if (__builtin_isfinite(m) && m > RANGE_LIMIT) {
-      int e = 0;
-      const float mant = frexpf(m / RANGE_LIMIT, &e);  // m / RANGE_LIMIT = mant 2^e, mant in [0.5, 1)
-      down = ldexpf(1.f, mant == 0.5f ? 1 - e : -e);   // 2^-ceil(log2(m / RANGE_LIMIT))
-    }
-    *scale = down;
-  }
 }
 
 }  // namespace
@@ -250,7 +227,7 @@ int chunk_setup(const void *q, const void *k, const void *v, int in_dtype, const
   const int groups = scan_groups(static_cast<long>(B) * T, num_seqs, pairs, shape.cus);
   p = ChunkParams{q, k, v, g, beta, beta_dtype, h0, ht, state_dtype, state_idx, has_initial_state,
                   num_states, cu_seqlens, o, static_cast<unsigned char *>(workspace), T, Hk, Hv, V,
-                  num_seqs, groups, scale, shape.cus, shape.xcds, nullptr, 0, nullptr, 0.f, nullptr};
+                  num_seqs, groups, scale, shape.cus, shape.xcds, nullptr, 0, nullptr, 0.f, nullptr, nullptr};
   return PBGDN_OK;
 }
 
@@ -276,8 +253,8 @@ extern "C" int pbgdn_chunk_fwd(const void *q, const void *k, const void *v, int 
     pbgdn::RangeParams rp{static_cast<const float *>(v), static_cast<long>(B) * T * Hv * V, h0, state_dtype,
                           state_idx, has_initial_state, num_states, num_seqs, static_cast<long>(Hv) * K * V, part};
     hipLaunchKernelGGL(pbgdn::range_max_kernel, dim3(pbgdn::RANGE_BLOCKS), dim3(256), 0, s, rp);
-    hipLaunchKernelGGL(pbgdn::range_scale_kernel, dim3(1), dim3(256), 0, s, part, part + pbgdn::RANGE_BLOCKS);
     if (hipGetLastError() != hipSuccess) return PBGDN_ERR_LAUNCH;
+    p.range_part = part;
     p.in_scale = part + pbgdn::RANGE_BLOCKS;
   }
   switch (K) {

@@ -104,7 +104,34 @@ struct ChunkParams {
   // float32 inputs: the power of two that brings v and the initial states
   // into the kernels' range (a device scalar written before the scan), or NULL
   const float *in_scale;
+  // float32 inputs: the RANGE_BLOCKS partial maxima the scale is made from
+  // (the prep kernel's first wave reduces them into *in_scale), or NULL
+  const float *range_part;
 };
+
+// float32 inputs' range scale: v and the initial states are brought within
+// RANGE_LIMIT by a power of two, from RANGE_BLOCKS partial maxima of their
+// magnitudes.
+constexpr float RANGE_LIMIT = 1024.f;
+constexpr int RANGE_BLOCKS = 512;
+
+// One wave: the scale 2^-e, e = max(0, ceil(log2(max / RANGE_LIMIT))), from
+// the partial maxima; 1 for a maximum that is not finite.
+__device__ __forceinline__ void range_scale_wave(const float *part, float *scale) {
+  const int lane = threadIdx.x & 63;
+  float m = 0.f;
+  for (int i = lane; i < RANGE_BLOCKS; i += 64) m = fmaxf(m, part[i]);
+  m = wave_max(m);
+  if (lane == 0) {
+    float down = 1.f;
+    if (__builtin_isfinite(m) && m > RANGE_LIMIT) {
+      int e = 0;
+      const float mant = frexpf(m / RANGE_LIMIT, &e);  // m / RANGE_LIMIT = mant 2^e, mant in [0.5, 1)
+      down = ldexpf(1.f, mant == 0.5f ? 1 - e : -e);   // 2^-ceil(log2(m / RANGE_LIMIT))
+    }
+    *scale = down;
+  }
+}
 
 // Sequence s (wave-uniform): first token and end. cu_seqlens is read through
 // the constant address space (it is not written during a call), so these are
