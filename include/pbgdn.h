@@ -44,8 +44,11 @@
  *     kernels; a 16-bit state is widened when it is read and rounded to
  *     nearest even when it is written;
  *   - launches are asynchronous on `stream` (a hipStream_t; NULL = the null
- *     stream); no host synchronisation; the kernels keep no global state and
- *     are safe to call from several threads;
+ *     stream); no host synchronisation; safe to call from several threads.
+ *     Nothing a call computes depends on earlier calls: the library keeps
+ *     only per-device facts it queries once (compute units, XCDs, kernel LDS
+ *     limits, the no-allocation scratch address), and the decode steps' cache
+ *     policy is the caller's state_policy argument;
  *   - return 0 (PBGDN_OK) or a PBGDN_ERR_* code; no exception crosses the ABI.
  */
 #ifndef PBGDN_H_
@@ -58,7 +61,7 @@
 extern "C" {
 #endif
 
-#define PBGDN_ABI_VERSION 10
+#define PBGDN_ABI_VERSION 11
 
 /* element types */
 #define PBGDN_F32 0
@@ -71,6 +74,24 @@ extern "C" {
 #define PBGDN_ERR_UNSUPPORTED 2      /* valid, but a head width / chunk this library has no kernel for */
 #define PBGDN_ERR_LAUNCH 3           /* the HIP launch failed (hipGetLastError) */
 #define PBGDN_ERR_SCRATCH 4          /* more workspace than pbgdn_chunk_fwd_noalloc's scratch holds */
+
+/* Cache policy of a decode step's state (pbgdn_recurrent_fwd at T = 1,
+ * pbgdn_decode_layer_fwd), named by the caller:
+ *   PBGDN_STATE_STREAM    the state comes from HBM and goes back past the
+ *                         last-level cache (non-temporal): a model whose
+ *                         layers each keep a pool steps a different pool every
+ *                         call, so no state is still cached when it is read
+ *                         again (float32 state, B = 64, Qwen3-Next heads: 69%
+ *                         of 8 TB/s, against 61% with cacheable accesses);
+ *   PBGDN_STATE_RESIDENT  the caller steps the same pool again before much
+ *                         else passes through the 256 MB last-level cache (one
+ *                         layer stepped in a loop): cacheable accesses keep it
+ *                         there (83% of 8 TB/s, against 71% streamed); taken
+ *                         only when the call moves at most 192 MiB of state,
+ *                         larger calls stream.
+ * The policy sets cache bits only: results are the same bit for bit. */
+#define PBGDN_STATE_STREAM 0
+#define PBGDN_STATE_RESIDENT 1
 
 /* Version of this ABI (PBGDN_ABI_VERSION). */
 int pbgdn_abi_version(void);
@@ -236,6 +257,9 @@ int pbgdn_chunk_fwd_noalloc(const void *q, const void *k, const void *v,
  *   state_dtype F32, BF16 or F16 (both state tensors); they must be aligned
  *               to 4 elements; q, k, v to 16 bytes, g and beta to 4 bytes
  *   o           [B, T, Hv, V]   dtype out_dtype
+ *   state_policy PBGDN_STATE_STREAM or PBGDN_STATE_RESIDENT (above): the
+ *               state's cache policy for a one-token step; calls of more than
+ *               one token read and write each state once and ignore it
  *
  * Supported: K in {32, 64, 128, 256}, V in {32, 64, 128, 256}.
  */
@@ -246,7 +270,7 @@ int pbgdn_recurrent_fwd(const void *q, const void *k, const void *v,
                         const int32_t *state_idx,
                         int num_states, void *o, int out_dtype, int B, int T,
                         int Hk, int Hv, int K, int V, float scale,
-                        void *stream);
+                        int state_policy, void *stream);
 
 /*
  * Speculative verify: the recurrent steps of pbgdn_recurrent_fwd over the T
@@ -441,6 +465,7 @@ size_t pbgdn_chunk_bwd_workspace_size(int B, int T, int Hk, int Hv, int K,
  *   o_norm      [V] float32; eps the RMSNorm epsilon (the reference's 1e-5)
  *   hs          [B, Hv V] out_dtype, written
  *   scale       query scale (K ** -0.5)
+ *   state_policy PBGDN_STATE_STREAM or PBGDN_STATE_RESIDENT (above)
  *
  * Supported: K, V in {64, 128}; conv 0..4; Hv a multiple of Hk, at most 8 Hk.
  */
@@ -453,7 +478,7 @@ int pbgdn_decode_layer_fwd(const void *z, long z_stride, int in_dtype,
                            const int32_t *state_idx, int num_states,
                            const float *o_norm, float eps, void *hs,
                            int out_dtype, int B, int Hk, int Hv, int K, int V,
-                           float scale, void *stream);
+                           float scale, int state_policy, void *stream);
 
 /*
  * Streaming copy of `bytes` from src to dst on `stream`: 16-byte non-temporal

@@ -13,10 +13,11 @@ import threading
 import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpbgdn.so")
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 F32, BF16, F16 = 0, 1, 2
 OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED, ERR_LAUNCH, ERR_SCRATCH = 0, 1, 2, 3, 4
+STATE_STREAM, STATE_RESIDENT = 0, 1  # PBGDN_STATE_*: a decode step's state cache policy
 NOALLOC_SCRATCH_BYTES = 64 << 20  # PBGDN_NOALLOC_SCRATCH_BYTES
 
 DTYPE_CODES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
@@ -35,7 +36,7 @@ SIGNATURES = {
     "pbgdn_chunk_fwd_noalloc": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _i, _vp, _i,
                                  _i, _i, _i, _i, _i, _i, _f, _i, _vp], _i),
     "pbgdn_recurrent_fwd": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _i, _vp, _i,
-                             _i, _i, _i, _i, _i, _i, _f, _vp], _i),
+                             _i, _i, _i, _i, _i, _i, _f, _i, _vp], _i),
     "pbgdn_recurrent_verify_fwd": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _i,
                                     _i, _i, _i, _i, _i, _i, _f, _vp], _i),
     "pbgdn_prologue_fwd": ([_vp, _l, _vp, _l, _i, _vp, _vp, _i, _vp, _i, _vp, _vp,
@@ -45,7 +46,7 @@ SIGNATURES = {
                                    _vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp],
                                   _i),
     "pbgdn_decode_layer_fwd": ([_vp, _l, _i, _vp, _i, _l, _l, _l, _vp, _i, _vp, _vp, _i, _vp, _i, _vp, _i,
-                                _vp, _f, _vp, _i, _i, _i, _i, _i, _i, _f, _vp], _i),
+                                _vp, _f, _vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp], _i),
     "pbgdn_chunk_bwd": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                          _vp, ctypes.c_size_t, _i, _i, _i, _i, _i, _i, _f, _vp], _i),
     "pbgdn_chunk_bwd_workspace_size": ([_i, _i, _i, _i, _i, _i], ctypes.c_size_t),

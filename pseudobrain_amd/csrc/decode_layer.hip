@@ -338,12 +338,12 @@ __global__ __launch_bounds__(DNT, (sizeof(TS) == 2 ? 5 : 4)) void decode_layer_k
   }
 }
 
-// Keeps the state cached or streams it as the decode step does
-// (state_likely_cached).
+// Keeps the state cached or streams it past the cache as the caller names it,
+// as the decode step does (pbgdn_recurrent_fwd).
 template <int K, int V, typename TS>
-int launch_decode_layer(const DecodeLayerParams &p, int B, hipStream_t stream) {
+int launch_decode_layer(const DecodeLayerParams &p, int B, int policy, hipStream_t stream) {
   const long moved = static_cast<long>(B) * p.Hv * K * V * static_cast<long>(sizeof(TS));
-  if (state_likely_cached(p.state, moved, STATE_CACHE_BYTES)) {
+  if (policy == PBGDN_STATE_RESIDENT && moved <= STATE_CACHE_BYTES) {
     hipLaunchKernelGGL((decode_layer_kernel<K, V, TS, STATE_CACHED>), dim3(p.Hk, B), dim3(DNT), 0, stream, p);
   } else {
     hipLaunchKernelGGL((decode_layer_kernel<K, V, TS, state_streamed<TS>()>), dim3(p.Hk, B), dim3(DNT), 0, stream, p);
@@ -352,11 +352,11 @@ int launch_decode_layer(const DecodeLayerParams &p, int B, hipStream_t stream) {
 }
 
 template <typename TS>
-int dispatch_decode_layer(const DecodeLayerParams &p, int B, int K, int V, hipStream_t stream) {
-  if (K == 64 && V == 64) return launch_decode_layer<64, 64, TS>(p, B, stream);
-  if (K == 64 && V == 128) return launch_decode_layer<64, 128, TS>(p, B, stream);
-  if (K == 128 && V == 64) return launch_decode_layer<128, 64, TS>(p, B, stream);
-  if (K == 128 && V == 128) return launch_decode_layer<128, 128, TS>(p, B, stream);
+int dispatch_decode_layer(const DecodeLayerParams &p, int B, int K, int V, int policy, hipStream_t stream) {
+  if (K == 64 && V == 64) return launch_decode_layer<64, 64, TS>(p, B, policy, stream);
+  if (K == 64 && V == 128) return launch_decode_layer<64, 128, TS>(p, B, policy, stream);
+  if (K == 128 && V == 64) return launch_decode_layer<128, 64, TS>(p, B, policy, stream);
+  if (K == 128 && V == 128) return launch_decode_layer<128, 128, TS>(p, B, policy, stream);
   return PBGDN_ERR_UNSUPPORTED;
 }
 
@@ -370,8 +370,12 @@ extern "C" int pbgdn_decode_layer_fwd(const void *z, long z_stride, int in_dtype
                                       const float *conv_weight, int conv, const float *a_log, const float *dt_bias,
                                       int l2_mode, void *state, int state_dtype, const int32_t *state_idx,
                                       int num_states, const float *o_norm, float eps, void *hs, int out_dtype, int B,
-                                      int Hk, int Hv, int K, int V, float scale, void *stream) {
+                                      int Hk, int Hv, int K, int V, float scale, int state_policy,
+                                      void *stream) {
   using pbgdn::valid_dtype;
+  if (!(state_policy == PBGDN_STATE_STREAM || state_policy == PBGDN_STATE_RESIDENT)) {
+    return PBGDN_ERR_INVALID_ARGUMENT;
+  }
   if (B < 0 || Hk <= 0 || Hv <= 0 || K <= 0 || V <= 0 || Hv % Hk != 0 || num_states < 0) {
     return PBGDN_ERR_INVALID_ARGUMENT;
   }
@@ -399,8 +403,8 @@ extern "C" int pbgdn_decode_layer_fwd(const void *z, long z_stride, int in_dtype
                              num_states, o_norm, eps, hs, out_dtype, Hk, Hv, scale};
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (state_dtype) {
-    case PBGDN_F32: return pbgdn::dispatch_decode_layer<float>(p, B, K, V, s);
-    case PBGDN_BF16: return pbgdn::dispatch_decode_layer<pbgdn::u16>(p, B, K, V, s);
-    default: return pbgdn::dispatch_decode_layer<pbgdn::half_t>(p, B, K, V, s);
+    case PBGDN_F32: return pbgdn::dispatch_decode_layer<float>(p, B, K, V, state_policy, s);
+    case PBGDN_BF16: return pbgdn::dispatch_decode_layer<pbgdn::u16>(p, B, K, V, state_policy, s);
+    default: return pbgdn::dispatch_decode_layer<pbgdn::half_t>(p, B, K, V, state_policy, s);
   }
 }

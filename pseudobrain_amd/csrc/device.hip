@@ -35,14 +35,6 @@ bool device_shape(DeviceShape &out) {
   return true;
 }
 
-bool state_likely_cached(const void *state, long moved, long cache_bytes) {
-  static std::atomic<uintptr_t> last[MAX_DEVICES];
-  const int dev = current_device();
-  if (dev < 0) return false;
-  const uintptr_t prev = last[dev].exchange(reinterpret_cast<uintptr_t>(state), std::memory_order_relaxed);
-  return prev == reinterpret_cast<uintptr_t>(state) && moved <= cache_bytes;
-}
-
 bool smem_configured(const void *kernel, size_t bytes, std::atomic<bool> *flags) {
   const int dev = current_device();
   if (dev < 0) return false;

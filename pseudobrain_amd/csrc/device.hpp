@@ -25,14 +25,6 @@ int current_device();
 // cannot report it.
 bool device_shape(DeviceShape &out);
 
-// Whether a decode call's state (at `state`, `moved` bytes read and written)
-// is likely still in the last-level cache: the previous decode call on this
-// device stepped the same pool and the call moves at most cache_bytes. A
-// model's layers each keep their own pool, so their consecutive calls alternate
-// pools and stream; a loop stepping one pool keeps it cached. Records `state`
-// for the next call.
-bool state_likely_cached(const void *state, long moved, long cache_bytes);
-
 // Raises `kernel`'s dynamic LDS limit to `bytes` on the current device, once
 // per device (`flags`: MAX_DEVICES entries kept by the caller); false when the
 // runtime refuses.

@@ -247,9 +247,9 @@ __global__ __launch_bounds__(256, (recurrent_wg_per_cu<K, VW, ONE, ONE && sizeof
   }
 }
 
-// The decode step streams its state past the cache when the call moves more
-// state than the cache keeps; otherwise (and for token loops, which move each
-// state once per call) it keeps the cached policy.
+// The decode step's state loads and stores take the cache policy the caller
+// names (cached or streamed past the last-level cache); token loops move each
+// state once per call and keep the cached policy.
 template <int K, int V, int VW, typename TS>
 static void launch_step(const RecurrentParams &p, int B, bool cached, hipStream_t stream) {
   const dim3 grid(p.Hv * (V / VW), B);
@@ -260,20 +260,22 @@ static void launch_step(const RecurrentParams &p, int B, bool cached, hipStream_
   }
 }
 
-// The decode step keeps its state cached when it likely still is (the same
-// pool as the previous step, small enough), and streams it past the cache
-// otherwise. A streamed float32 step over many head states splits each state's
-// columns over two workgroups (at B = 256, Hv = 32: 71% of HBM against 67%
-// whole; at B = 64 the whole state is faster). Token loops move each state
-// once per call and keep the cached policy.
+// The decode step keeps its state cached when the caller declares it resident
+// (PBGDN_STATE_RESIDENT: the same pool is stepped again before much else
+// passes through the cache) and the call moves at most STATE_CACHE_BYTES of
+// state; otherwise it streams the state past the cache. The launch shape
+// follows from the call's shape alone, so equal inputs give equal results
+// whatever the policy: a float32 step over 4,096 or more head states splits
+// each state's columns over two workgroups (streamed, at B = 256, Hv = 32:
+// 71% of HBM against 67% whole; at B = 64 the whole state is faster).
 template <int K, int V, typename TS>
-static int launch_recurrent(const RecurrentParams &p, int B, hipStream_t stream) {
+static int launch_recurrent(const RecurrentParams &p, int B, int policy, hipStream_t stream) {
   if (p.T == 1 && !p.token_state_idx) {
     const long moved = static_cast<long>(B) * p.Hv * K * V * static_cast<long>(sizeof(TS));
-    const bool cached = state_likely_cached(p.state_out, moved, STATE_CACHE_BYTES);
+    const bool cached = policy == PBGDN_STATE_RESIDENT && moved <= STATE_CACHE_BYTES;
     if constexpr (sizeof(TS) == 4 && V >= 128 && V % 64 == 0) {
-      if (!cached && static_cast<long>(B) * p.Hv >= 4096) {
-        launch_step<K, V, 64, TS>(p, B, false, stream);
+      if (static_cast<long>(B) * p.Hv >= 4096) {
+        launch_step<K, V, 64, TS>(p, B, cached, stream);
         return hipGetLastError() == hipSuccess ? PBGDN_OK : PBGDN_ERR_LAUNCH;
       }
     }
@@ -285,32 +287,32 @@ static int launch_recurrent(const RecurrentParams &p, int B, hipStream_t stream)
 }
 
 template <int K, typename TS>
-static int dispatch_v(const RecurrentParams &p, int B, int V, hipStream_t stream) {
+static int dispatch_v(const RecurrentParams &p, int B, int V, int policy, hipStream_t stream) {
   switch (V) {
-    case 32: return launch_recurrent<K, 32, TS>(p, B, stream);
-    case 64: return launch_recurrent<K, 64, TS>(p, B, stream);
-    case 128: return launch_recurrent<K, 128, TS>(p, B, stream);
-    case 256: return launch_recurrent<K, 256, TS>(p, B, stream);
+    case 32: return launch_recurrent<K, 32, TS>(p, B, policy, stream);
+    case 64: return launch_recurrent<K, 64, TS>(p, B, policy, stream);
+    case 128: return launch_recurrent<K, 128, TS>(p, B, policy, stream);
+    case 256: return launch_recurrent<K, 256, TS>(p, B, policy, stream);
     default: return PBGDN_ERR_UNSUPPORTED;
   }
 }
 
 template <typename TS>
-static int dispatch_k(const RecurrentParams &p, int B, int K, int V, hipStream_t stream) {
+static int dispatch_k(const RecurrentParams &p, int B, int K, int V, int policy, hipStream_t stream) {
   switch (K) {
-    case 32: return dispatch_v<32, TS>(p, B, V, stream);
-    case 64: return dispatch_v<64, TS>(p, B, V, stream);
-    case 128: return dispatch_v<128, TS>(p, B, V, stream);
-    case 256: return dispatch_v<256, TS>(p, B, V, stream);
+    case 32: return dispatch_v<32, TS>(p, B, V, policy, stream);
+    case 64: return dispatch_v<64, TS>(p, B, V, policy, stream);
+    case 128: return dispatch_v<128, TS>(p, B, V, policy, stream);
+    case 256: return dispatch_v<256, TS>(p, B, V, policy, stream);
     default: return PBGDN_ERR_UNSUPPORTED;
   }
 }
 
-int recurrent_fwd(const RecurrentParams &p, int state_dtype, int B, int K, int V, hipStream_t stream) {
+int recurrent_fwd(const RecurrentParams &p, int state_dtype, int B, int K, int V, int policy, hipStream_t stream) {
   switch (state_dtype) {
-    case PBGDN_F32: return dispatch_k<float>(p, B, K, V, stream);
-    case PBGDN_BF16: return dispatch_k<u16>(p, B, K, V, stream);
-    case PBGDN_F16: return dispatch_k<half_t>(p, B, K, V, stream);
+    case PBGDN_F32: return dispatch_k<float>(p, B, K, V, policy, stream);
+    case PBGDN_BF16: return dispatch_k<u16>(p, B, K, V, policy, stream);
+    case PBGDN_F16: return dispatch_k<half_t>(p, B, K, V, policy, stream);
     default: return PBGDN_ERR_INVALID_ARGUMENT;
   }
 }
@@ -339,8 +341,11 @@ extern "C" int pbgdn_recurrent_fwd(const void *q, const void *k, const void *v, 
                                    const int32_t *state_idx, int num_states, void *o,
                                    int out_dtype, int B,
                                    int T, int Hk, int Hv, int K, int V, float scale,
-                                   void *stream) {
+                                   int state_policy, void *stream) {
   if (B < 0 || T < 0 || Hk <= 0 || Hv <= 0 || K <= 0 || V <= 0 || Hv % Hk != 0) {
+    return PBGDN_ERR_INVALID_ARGUMENT;
+  }
+  if (!(state_policy == PBGDN_STATE_STREAM || state_policy == PBGDN_STATE_RESIDENT)) {
     return PBGDN_ERR_INVALID_ARGUMENT;
   }
   if (!valid_dtype(in_dtype) || !valid_dtype(out_dtype) || !valid_dtype(state_dtype) ||
@@ -358,7 +363,7 @@ extern "C" int pbgdn_recurrent_fwd(const void *q, const void *k, const void *v, 
   if (B > 65535) return PBGDN_ERR_UNSUPPORTED;
   pbgdn::RecurrentParams p{q, k, v, in_dtype, g, beta, beta_dtype, state_in, state_out,
                            state_idx, nullptr, num_states, o, out_dtype, T, Hk, Hv, scale};
-  return pbgdn::recurrent_fwd(p, state_dtype, B, K, V, static_cast<hipStream_t>(stream));
+  return pbgdn::recurrent_fwd(p, state_dtype, B, K, V, state_policy, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int pbgdn_recurrent_verify_fwd(const void *q, const void *k, const void *v, int in_dtype,
@@ -385,5 +390,5 @@ extern "C" int pbgdn_recurrent_verify_fwd(const void *q, const void *k, const vo
   if (B > 65535) return PBGDN_ERR_UNSUPPORTED;
   pbgdn::RecurrentParams p{q, k, v, in_dtype, g, beta, beta_dtype, state_in, states,
                            state_idx, token_state_idx, num_states, o, out_dtype, T, Hk, Hv, scale};
-  return pbgdn::recurrent_fwd(p, state_dtype, B, K, V, static_cast<hipStream_t>(stream));
+  return pbgdn::recurrent_fwd(p, state_dtype, B, K, V, PBGDN_STATE_STREAM, static_cast<hipStream_t>(stream));
 }

@@ -274,7 +274,7 @@ def chunk_fwd_slots(q, k, v, g, beta, scale: float, states, state_idx, cu_seqlen
 
 def recurrent_fwd(q, k, v, g, beta, scale: float, state_in, state_out=None, state_idx=None, *,
                   out_dtype: torch.dtype = torch.float32, out: torch.Tensor | None = None,
-                  token_state_idx: torch.Tensor | None = None):
+                  token_state_idx: torch.Tensor | None = None, state_resident: bool = False):
     """Launch pbgdn_recurrent_fwd: all T tokens through the per-step recurrence.
     state_out may be state_in (in place) or None (a new tensor). state_idx [B]
     int32 maps sequences to state slots (distinct; a slot outside the state
@@ -288,15 +288,21 @@ def recurrent_fwd(q, k, v, g, beta, scale: float, state_in, state_out=None, stat
     state_out (skipped when outside the state tensor); nothing else is
     written. With state_out None the new tensor starts as a copy of state_in,
     so the slots a call does not write keep their values there.
+
+    state_resident: the caller steps this state pool again before much else
+    passes through the GPU's 256 MB last-level cache (one layer stepped in a
+    loop), so a one-token step keeps it cacheable (PBGDN_STATE_RESIDENT); the
+    default streams it past the cache, as suits a model whose layers each keep
+    a pool. Cache bits only: the results are the same.
     Inference only (no backward)."""
     require_no_grad("recurrent_fwd", q, k, v, g, beta, state_in)
     return _recurrent_fwd(q, k, v, g, beta, scale, state_in, state_out, state_idx, out_dtype=out_dtype, out=out,
-                          token_state_idx=token_state_idx)
+                          token_state_idx=token_state_idx, state_resident=state_resident)
 
 
 def _recurrent_fwd(q, k, v, g, beta, scale: float, state_in, state_out=None, state_idx=None, *,
                    out_dtype: torch.dtype = torch.float32, out: torch.Tensor | None = None,
-                   token_state_idx: torch.Tensor | None = None):
+                   token_state_idx: torch.Tensor | None = None, state_resident: bool = False):
     batch, length, hk, hv, dk, dv = _shapes(q, k, v, g, beta)
     dev = _require_device(q, k, v, g, beta, state_in, state_out, state_idx)
     if dk not in RECURRENT_HEAD_DIMS or dv not in RECURRENT_HEAD_DIMS:
@@ -339,7 +345,7 @@ def _recurrent_fwd(q, k, v, g, beta, scale: float, state_in, state_out=None, sta
         _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), codes[q.dtype], _lib.ptr(g), _lib.ptr(beta),
         codes[beta.dtype], _lib.ptr(state_in), _lib.ptr(state_out), codes[state_in.dtype], _lib.ptr(state_idx),
         state_in.shape[0], _lib.ptr(out), codes[out.dtype], batch, length, hk, hv, dk, dv, float(scale),
-        _lib.stream_handle(dev))
+        _lib.STATE_RESIDENT if state_resident else _lib.STATE_STREAM, _lib.stream_handle(dev))
     _lib.check(status, "pbgdn_recurrent_fwd")
     return out, state_out
 
@@ -453,15 +459,17 @@ gated_delta_chunk.register_autograd(_chunk_grad, setup_context=_chunk_setup)
 
 @torch.library.custom_op("pbgdn::recurrent_step_", mutates_args=("state",),
                          schema="(Tensor q, Tensor k, Tensor v, Tensor g, Tensor beta, Tensor(a!) state, "
-                                "Tensor? state_idx, float scale) -> Tensor")
-def recurrent_step_(q, k, v, g, beta, state, state_idx, scale):
-    """Decode step(s) updating `state` [S,Hv,K,V] in place; o in q's dtype."""
-    out, _ = _recurrent_fwd(q, k, v, g, beta, scale, state, state, state_idx, out_dtype=q.dtype)
+                                "Tensor? state_idx, float scale, bool state_resident=False) -> Tensor")
+def recurrent_step_(q, k, v, g, beta, state, state_idx, scale, state_resident=False):
+    """Decode step(s) updating `state` [S,Hv,K,V] in place; o in q's dtype.
+    state_resident as recurrent_fwd's (the state's cache policy)."""
+    out, _ = _recurrent_fwd(q, k, v, g, beta, scale, state, state, state_idx, out_dtype=q.dtype,
+                            state_resident=state_resident)
     return out
 
 
 @recurrent_step_.register_fake
-def _(q, k, v, g, beta, state, state_idx, scale):
+def _(q, k, v, g, beta, state, state_idx, scale, state_resident=False):
     return q.new_empty(q.shape[0], q.shape[1], v.shape[2], v.shape[3])
 
 
@@ -565,21 +573,27 @@ def delta_rule_sequential(q, k, v, g, beta, scale, h0):
 
 
 def hip_usable(*tensors: torch.Tensor) -> bool:
-    """The device kernels apply (the fla_usable gate, gated_deltanet.py:189-197):
-    every tensor on the device, a dtype the kernels read (float32, bfloat16,
-    float16), and head widths K, V <= 256; when a gradient will be wanted, K,
-    V <= 128 (the chunk backward's widths), so that a training call the device
-    cannot differentiate stays on the reference's PyTorch path. tensors[0] is
-    the matrix state [..., K, V]. Raises if the tensors are on a GPU but the
+    """The chunkwise device prefill applies (the fla_usable gate,
+    gated_deltanet.py:189-197, which select_kernel consults only for calls
+    longer than SEQUENTIAL_MAX tokens): every tensor on the device, a dtype
+    the kernels read (float32, bfloat16, float16), a key width K <= 128 (the
+    chunk kernel's; wider keys would run token by token on the recurrent
+    kernel, so fla or the reference's chunked path keeps them) and a value
+    width V <= 256; when a gradient will be wanted, V <= 128 as well (the
+    chunk backward's widths), so that a training call the device cannot
+    differentiate stays on the reference's PyTorch path. tensors[0] is the
+    matrix state [..., K, V]. Raises if the tensors are on a GPU but the
     library is missing: a GPU caller never silently loses the kernel."""
     if not tensors or not all(t.is_cuda for t in tensors):
         return False
     if not all(t.dtype in _lib.DTYPE_CODES for t in tensors if t.is_floating_point()):
         return False
     state = tensors[0]
-    widths = [state.shape[-1]] + ([state.shape[-2]] if state.ndim >= 2 else [])
-    bound = BACKWARD_HEAD_DIMS[-1] if grad_needed(*tensors) else MAX_HEAD_DIM
-    if max(widths) > bound:
+    dv = state.shape[-1]
+    dk = state.shape[-2] if state.ndim >= 2 else 0
+    if dk > CHUNK_HEAD_DIMS[-1]:
+        return False
+    if dv > (BACKWARD_HEAD_DIMS[-1] if grad_needed(*tensors) else MAX_HEAD_DIM):
         return False
     _lib.lib()
     return True

@@ -383,7 +383,8 @@ def decode_layer_step(z: torch.Tensor, conv_state: torch.Tensor | None, conv_wei
                       A_log: torch.Tensor, dt_bias: torch.Tensor, state: torch.Tensor, o_norm: torch.Tensor,
                       heads: int, key_dim: int, value_heads: int, value_dim: int,
                       state_idx: torch.Tensor | None = None, l2norm: str = "max", eps: float = NORM_EPS, *,
-                      scale: float | None = None, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+                      scale: float | None = None, out_dtype: torch.dtype = torch.float32,
+                      state_resident: bool = False) -> torch.Tensor:
     """One decode token per sequence through GatedDeltaNetLayer.forward from the
     projection to hs (gated_deltanet.py:415-441) in one kernel: the short
     convolution against the carried tail, SiLU, q/k L2 norms, the gates, the
@@ -397,7 +398,8 @@ def decode_layer_step(z: torch.Tensor, conv_state: torch.Tensor | None, conv_wei
     states (float32, bfloat16 or float16), both updated in place at slot
     state_idx[b] (int32 [B], or None for slot b; a slot outside the pools
     touches nothing and gives zeros). Returns hs [B, value_heads*value_dim] in
-    out_dtype."""
+    out_dtype. state_resident: the state's cache policy, as recurrent_fwd's
+    (the default streams it, as a model whose layers each keep a pool needs)."""
     require_no_grad("decode_layer_step", z, conv_state, conv_weight, A_log, dt_bias, state, o_norm)
     if l2norm not in L2_MODES:
         raise ValueError(f"l2 normalization mode must be one of {L2_MODES}")
@@ -459,6 +461,6 @@ def decode_layer_step(z: torch.Tensor, conv_state: torch.Tensor | None, conv_wei
         _lib.ptr(a_log), _lib.ptr(dtb), L2_MODES.index(l2norm), _lib.ptr(state), codes[state.dtype],
         _lib.ptr(state_idx), state.shape[0], _lib.ptr(norm), float(eps), _lib.ptr(hs), codes[out_dtype], batch,
         heads, value_heads, key_dim, value_dim, float(key_dim ** -0.5 if scale is None else scale),
-        _lib.stream_handle(dev))
+        _lib.STATE_RESIDENT if state_resident else _lib.STATE_STREAM, _lib.stream_handle(dev))
     _lib.check(status, "pbgdn_decode_layer_fwd")
     return hs

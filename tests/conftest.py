@@ -28,3 +28,12 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+def pytest_terminal_summary(terminalreporter):
+    """The full-size oracle checks' errors (tests/gpu_util.SUMMARY), one line each."""
+    from tests import gpu_util
+    if gpu_util.SUMMARY:
+        terminalreporter.write_sep("-", "full-size workloads against the oracle (relative inf-norm errors)")
+        for line in gpu_util.SUMMARY:
+            terminalreporter.write_line(line)

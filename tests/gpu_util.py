@@ -36,3 +36,13 @@ def assert_parity(name, o, o_ref, s=None, s_ref=None, o_tol=O_TOL, s_tol=S_TOL):
     eo, es = report(name, o, o_ref, s, s_ref)
     assert np.isfinite(eo) and eo <= o_tol, f"{name}: output error {eo:.3e} > {o_tol}"
     assert np.isfinite(es) and es <= s_tol, f"{name}: state error {es:.3e} > {s_tol}"
+
+
+# Lines the full-size oracle checks (varlen and million-token workloads) add for
+# the session's closing summary (conftest.pytest_terminal_summary), so their
+# per-sequence and per-segment errors show in a quiet run's tail.
+SUMMARY: list[str] = []
+
+
+def summarize(line: str) -> None:
+    SUMMARY.append(line)

@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version_and_status_strings():
-    assert _lib.lib().pbgdn_abi_version() == _lib.ABI_VERSION == 10
+    assert _lib.lib().pbgdn_abi_version() == _lib.ABI_VERSION == 11
     header = open(HEADER).read()
     assert re.search(r"#define PBGDN_ABI_VERSION (\d+)", header).group(1) == str(_lib.ABI_VERSION)
     assert _lib.status_string(0) == "ok"
@@ -66,7 +66,7 @@ def test_chunk_fwd_noalloc_rejects_calls_beyond_its_scratch():
 def recurrent_call(**over):
     args = dict(q=FAKE, k=FAKE, v=FAKE, in_dtype=1, g=FAKE, beta=FAKE, beta_dtype=0, sin=FAKE,
                 sout=FAKE, sdt=0, idx=None, nstates=1, o=FAKE, out_dtype=1, B=1, T=1, Hk=16, Hv=32, K=128,
-                V=128, scale=0.1, stream=None)
+                V=128, scale=0.1, policy=_lib.STATE_STREAM, stream=None)
     args.update(over)
     return _lib.lib().pbgdn_recurrent_fwd(*args.values())
 
@@ -114,6 +114,8 @@ def test_chunk_fwd_empty_is_ok():
     (dict(K=48), _lib.ERR_UNSUPPORTED),
     (dict(V=512), _lib.ERR_UNSUPPORTED),
     (dict(B=70000, nstates=70000), _lib.ERR_UNSUPPORTED),
+    (dict(policy=2), _lib.ERR_INVALID_ARGUMENT),        # PBGDN_STATE_STREAM or PBGDN_STATE_RESIDENT
+    (dict(policy=-1, B=0), _lib.ERR_INVALID_ARGUMENT),
 ])
 def test_recurrent_fwd_rejects(over, code):
     assert recurrent_call(**over) == code
@@ -121,6 +123,13 @@ def test_recurrent_fwd_rejects(over, code):
 
 def test_recurrent_fwd_empty_is_ok():
     assert recurrent_call(B=0) == _lib.OK
+    assert recurrent_call(B=0, policy=_lib.STATE_RESIDENT) == _lib.OK
+
+
+def test_state_policy_codes_match_the_header():
+    header = open(HEADER).read()
+    assert int(re.search(r"#define PBGDN_STATE_STREAM (\d+)", header).group(1)) == _lib.STATE_STREAM
+    assert int(re.search(r"#define PBGDN_STATE_RESIDENT (\d+)", header).group(1)) == _lib.STATE_RESIDENT
 
 
 @pytest.mark.parametrize("src,dst,nbytes", [
@@ -245,7 +254,7 @@ def decode_layer_call(**over):
     args = dict(z=FAKE, z_stride=width, in_dtype=1, conv_state=FAKE, conv_dtype=0, css=3 * CH, crs=CH, ccs=1,
                 w=FAKE, conv=4, a_log=FAKE, dt_bias=FAKE, l2=0, state=FAKE, sdt=0, idx=None, nstates=64,
                 o_norm=FAKE, eps=1e-5, hs=FAKE, out_dtype=0, B=64, Hk=16, Hv=32, K=128, V=128, scale=0.1,
-                stream=None)
+                policy=_lib.STATE_STREAM, stream=None)
     args.update(over)
     return _lib.lib().pbgdn_decode_layer_fwd(*args.values())
 
@@ -264,6 +273,7 @@ def decode_layer_call(**over):
     (dict(Hk=2, z_stride=1 << 20), _lib.ERR_UNSUPPORTED),  # 16 value heads per key head: more than 8
     (dict(K=96), _lib.ERR_UNSUPPORTED),
     (dict(V=256, z_stride=1 << 20), _lib.ERR_UNSUPPORTED),
+    (dict(policy=7), _lib.ERR_INVALID_ARGUMENT),
 ])
 def test_decode_layer_fwd_rejects(over, code):
     assert decode_layer_call(**over) == code

@@ -157,3 +157,19 @@ def test_decode_steps_chain():
         assert e <= 1e-4
     assert rel_err(dstate.cpu()[idx], to_numpy(rstate[idx])) <= 1e-4
     np.testing.assert_array_equal(to_numpy(dpool.cpu()), to_numpy(rpool))
+
+
+def test_decode_step_state_policy_sets_cache_bits_only():
+    """The fused step under the default (streamed) and the resident state
+    policy: hs, the state pool and the conv pool equal bit for bit."""
+    heads, dk, vheads, dv = 16, 128, 32, 128
+    z, pool, weight, a_log, dt_bias, state, o_norm = make(64, 64, heads, dk, vheads, dv, 4, seed=90)
+    dz, dw, da, db, dn = z.to(DEV), weight.to(DEV), a_log.to(DEV), dt_bias.to(DEV), o_norm.to(DEV)
+    runs = []
+    for resident in (False, True):
+        dpool, dstate = pool.to(DEV), state.to(DEV)
+        hs = decode_layer_step(dz, dpool, dw, da, db, dstate, dn, heads, dk, vheads, dv, state_resident=resident)
+        torch.cuda.synchronize()
+        runs.append((hs, dstate, dpool))
+    for a, b in zip(runs[0], runs[1]):
+        assert torch.equal(a, b)

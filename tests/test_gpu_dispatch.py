@@ -60,7 +60,10 @@ def test_fused_backend_selects_and_runs_the_device_kernel(length, expect):
 def test_every_head_width_up_to_256_runs(dk, dv, hk, hv, length, kernel):
     q, k, v, g, beta, h0 = inputs(1, length, hk, hv, dk, dv, seed=dk + dv)
     dq, dk_, dv_, dg, db, dh = to_dev(q, k, v, g, beta, h0)
-    assert gd.hip_usable(dh, dq)
+    # the gate admits the chunk kernel's key widths only: a wider key would run
+    # token by token, so in the reference's wiring fla or chunked keeps it
+    assert gd.hip_usable(dh, dq) == (dk <= 128)
+    assert gd.select_kernel("fused", False, length, dh, dq) == ("hip" if dk <= 128 else "chunked")
     o, s = gd.gated_delta_rule(dq, dk_, dv_, dg, db, dk ** -0.5, dh, kernel=kernel)
     torch.cuda.synchronize()
     assert o.shape == (1, length, hv, dv) and s.shape == (1, hv, dk, dv)
@@ -137,11 +140,18 @@ def test_training_call_without_a_device_backward_raises():
     with torch.no_grad():
         o, _ = gd.gated_delta_rule(*leaves[:5], 0.0625, leaves[5], kernel="hip")
     assert not o.requires_grad
-    # the gate sends such training calls to the reference's PyTorch path
+    # the gate sends such calls (K = 256, above the chunk kernel's keys) to the
+    # reference's path, with or without a gradient
     assert not gd.hip_usable(leaves[5], leaves[0])
     assert gd.select_kernel("fused", False, 100, leaves[5], leaves[0]) == "chunked"
     with torch.no_grad():
-        assert gd.hip_usable(leaves[5], leaves[0])
+        assert not gd.hip_usable(leaves[5], leaves[0])
+    # a value width the chunk kernel takes but its backward does not: usable for
+    # inference only
+    wide_v = torch.zeros(1, 2, 64, 256, device=DEV, requires_grad=True)
+    assert not gd.hip_usable(wide_v, leaves[0])
+    with torch.no_grad():
+        assert gd.hip_usable(wide_v, leaves[0])
 
 
 def test_entry_points_without_backward_refuse_grad():

@@ -43,6 +43,32 @@ def test_decode_step_streamed_past_the_cache(batch, state_dtype):
     assert_parity(f"decode B={batch} {state_dtype} streamed", o, o_ref, state.float(), s_ref, s_tol=s_tol)
 
 
+@pytest.mark.parametrize("batch,state_dtype,dk", [(64, torch.float32, 128), (128, torch.float32, 128),
+                                                  (64, torch.bfloat16, 128), (256, torch.float32, 64)])
+def test_decode_state_policy_sets_cache_bits_only(batch, state_dtype, dk):
+    """The state's cache policy is the caller's (PBGDN_STATE_STREAM, the default,
+    or PBGDN_STATE_RESIDENT) and changes cache bits only: the same step under
+    either policy gives the same output and state bit for bit, twice in a row
+    (no call history), for whole-state and split (4,096+ head states) launches
+    and for a resident call small enough to be kept cached (B = 256 at K = 64:
+    128 MiB). Both match the oracle."""
+    q, k, v, g, beta, h0 = generate(batch, 1, 16, 32, dk, 128, torch.bfloat16, 0.02, seed=batch + dk)
+    h0 = h0.to(state_dtype)
+    o_ref, s_ref = oracle(q, k, v, g, beta, dk ** -0.5, h0.float(), "sequential")
+    dq, dk_, dv, dg, db, base = to_dev(q, k, v, g, beta, h0)
+    results = []
+    for resident in (False, True, True, False):
+        state = base.clone()
+        o = torch.ops.pbgdn.recurrent_step_(dq, dk_, dv, dg, db, state, None, dk ** -0.5, resident)
+        torch.cuda.synchronize()
+        results.append((o, state))
+    for o, state in results[1:]:
+        assert torch.equal(o, results[0][0]) and torch.equal(state, results[0][1])
+    s_tol = 1e-3 if state_dtype == torch.float32 else 1e-2
+    assert_parity(f"decode B={batch} K={dk} {state_dtype} either policy", results[0][0], o_ref,
+                  results[0][1].float(), s_ref, s_tol=s_tol)
+
+
 def test_stream_probe_copies():
     """pbgdn_stream_probe copies every byte (64 MiB plus a 16-byte tail piece)."""
     from pseudobrain_amd import _lib
