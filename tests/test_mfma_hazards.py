@@ -3,7 +3,9 @@ chunk_bwd), compiled for gfx950 with the library's own flags: along every
 control-flow path of every kernel, no instruction reads a v_mfma result
 fewer wait states after the product than hipcc itself places within one
 block for that product (8 for the 16x16x32 and 16x16x16 fp16 / bf16 forms, 10
-for 16x16x4 fp32; an s_nop N counts N + 1, any other instruction 1).
+for 16x16x4 fp32; an s_nop N counts N + 1, any other instruction 1). Results
+in VGPRs (v) and in accumulation registers (a, read back by v_accvgpr_read or
+as MFMA operands) are both followed.
 
 hipcc (ROCm 7.2) has emitted reads two to five wait states after a product
 issued inside a branch, when the read follows the join: the read then sees
@@ -23,17 +25,18 @@ from pseudobrain_amd import build
 SOURCES = ("chunk_prep.hip", "chunk_scan.hip", "chunk_wide.hip", "chunk_bwd.hip")
 NEED = {"v_mfma_f32_16x16x32_f16": 8, "v_mfma_f32_16x16x32_bf16": 8, "v_mfma_f32_16x16x16_f16": 8,
         "v_mfma_f32_16x16x16_bf16": 8, "v_mfma_f32_16x16x4_f32": 10}
-_REG = re.compile(r"\bv\[(\d+):(\d+)\]|\bv(\d+)\b")
+_REG = re.compile(r"\b([va])\[(\d+):(\d+)\]|\b([va])(\d+)\b")
 _STORES = ("ds_write", "ds_add", "global_store", "buffer_store", "global_atomic", "buffer_atomic", "flat_store")
 
 
 def vgprs(text):
+    """The vector registers an operand text names, as ('v', n) or ('a', n)."""
     out = set()
     for m in _REG.finditer(text):
-        if m.group(3) is not None:
-            out.add(int(m.group(3)))
+        if m.group(5) is not None:
+            out.add((m.group(4), int(m.group(5))))
         else:
-            out.update(range(int(m.group(1)), int(m.group(2)) + 1))
+            out.update((m.group(1), r) for r in range(int(m.group(2)), int(m.group(3)) + 1))
     return out
 
 
@@ -128,6 +131,23 @@ def test_checker_finds_a_read_after_a_join():
     assert len(hits) == 2 and {h[3] for h in hits} == {1, 2}
     good = bad.replace("s_nop 0", "s_nop 7")
     assert short_reads(good) == []
+
+
+def test_checker_follows_accumulation_registers():
+    """A product into accumulation registers, read back by v_accvgpr_read after
+    a join, is found as well; a product into other registers is not."""
+    bad = """_Zk:
+	v_mfma_f32_16x16x32_bf16 a[0:3], v[0:3], v[4:7], a[0:3]
+	s_cbranch_scc1 .LBB0_2
+	v_mov_b32_e32 v9, v8
+.LBB0_2:
+	v_accvgpr_read_b32 v12, a3
+	s_endpgm
+"""
+    hits = short_reads(bad)
+    assert {h[3] for h in hits} == {1, 2} and all("v_accvgpr_read" in h[2] for h in hits)
+    assert short_reads(bad.replace("a[0:3], v[0:3]", "a[4:7], v[0:3]")) == []
+    assert vgprs("a[2:3], v5") == {("a", 2), ("a", 3), ("v", 5)}
 
 
 def test_no_mfma_result_is_read_early():
