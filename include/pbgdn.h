@@ -61,7 +61,7 @@
 extern "C" {
 #endif
 
-#define PBGDN_ABI_VERSION 11
+#define PBGDN_ABI_VERSION 12
 
 /* element types */
 #define PBGDN_F32 0
@@ -177,10 +177,11 @@ int pbgdn_chunk_fwd(const void *q, const void *k, const void *v, int in_dtype,
  * When the wide scan takes the call (in_dtype BF16 or F16, K = V = 128, N x
  * Hv at least half the device's CUs, gate_dtype == in_dtype, hs_dtype F32 or
  * in_dtype), the scan applies the epilogue to each chunk's output in
- * registers (fp32, before any rounding) and writes hs: o is not touched and
- * the epilogue pass, with its read of o, is saved. Otherwise o is written in
- * in_dtype and the epilogue runs after it on the same stream. V must be 64 or
- * 128 (the epilogue's widths).
+ * registers (fp32, before any rounding) and writes hs: o is not touched (it
+ * may be NULL) and the epilogue pass, with its read of o, is saved. Otherwise
+ * o is written in in_dtype and the epilogue runs after it on the same stream.
+ * pbgdn_chunk_layer_fuses tells the two apart before the call. V must be 64
+ * or 128 (the epilogue's widths).
  */
 int pbgdn_chunk_layer_fwd(const void *q, const void *k, const void *v,
                           int in_dtype, const float *g, const void *beta,
@@ -234,6 +235,17 @@ int pbgdn_chunk_fwd_noalloc(const void *q, const void *k, const void *v,
                             const int32_t *cu_seqlens, int num_seqs, void *o,
                             int out_dtype, int B, int T, int Hk, int Hv, int K,
                             int V, float scale, int chunk, void *stream);
+
+/*
+ * 1 when pbgdn_chunk_layer_fwd with these arguments applies the epilogue
+ * inside the scan (its o argument then unused and allowed to be NULL), 0 when
+ * it writes o and runs the epilogue as a second pass (o required), on the
+ * current device; -1 for arguments pbgdn_chunk_layer_fwd would reject as
+ * invalid dtypes or widths. Lets a caller allocate o only when it is written.
+ * No reference counterpart (the reference always materialises o).
+ */
+int pbgdn_chunk_layer_fuses(int in_dtype, int gate_dtype, int hs_dtype, long gate_stride, int num_seqs, int Hv,
+                            int K, int V);
 
 /*
  * Fused recurrent steps: for each token, in one pass over the state,

@@ -85,6 +85,13 @@ bool valid_dtype(int d) { return d == PBGDN_F32 || d == PBGDN_BF16 || d == PBGDN
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// The dtypes and widths for which the wide scan can apply the layer epilogue
+// (then it does whenever it takes the call: wide_eligible).
+bool layer_fusable(int in_dtype, int gate_dtype, int hs_dtype, long gate_stride, int K, int V) {
+  return K == 128 && V == 128 && (in_dtype == PBGDN_BF16 || in_dtype == PBGDN_F16) && gate_dtype == in_dtype &&
+         (hs_dtype == PBGDN_F32 || hs_dtype == in_dtype) && static_cast<long>(CH) * gate_stride * 2 <= 0x7fffffffL;
+}
+
 // Device address of `scratch` per device ordinal, resolved once per device
 // (with that device current) on the first no-allocation call there.
 constexpr int MAX_DEVICES = 64;
@@ -289,9 +296,7 @@ extern "C" int pbgdn_chunk_layer_fwd(const void *q, const void *k, const void *v
                            scale, chunk, workspace, workspace_bytes, stream);
   }
   if (!gate || !o_norm || !hs || !aligned16(gate) || !aligned16(hs)) return PBGDN_ERR_INVALID_ARGUMENT;
-  const bool fusable = K == 128 && V == 128 && (in_dtype == PBGDN_BF16 || in_dtype == PBGDN_F16) &&
-                       gate_dtype == in_dtype && (hs_dtype == PBGDN_F32 || hs_dtype == in_dtype) &&
-                       static_cast<long>(pbgdn::CH) * gate_stride * 2 <= 0x7fffffffL;
+  const bool fusable = pbgdn::layer_fusable(in_dtype, gate_dtype, hs_dtype, gate_stride, K, V);
   pbgdn::ChunkParams p;
   long records = 0;
   bool empty = false;
@@ -319,6 +324,26 @@ extern "C" int pbgdn_chunk_layer_fwd(const void *q, const void *k, const void *v
   if (st != PBGDN_OK) return st;
   return pbgdn_epilogue_fwd(o, in_dtype, gate, gate_stride, gate_dtype, o_norm, eps, hs, hs_dtype, B, T, Hv, V,
                             stream);
+}
+
+extern "C" int pbgdn_chunk_layer_fuses(int in_dtype, int gate_dtype, int hs_dtype, long gate_stride, int num_seqs,
+                                       int Hv, int K, int V) {
+  using pbgdn::valid_dtype;
+  if (!valid_dtype(in_dtype) || !valid_dtype(gate_dtype) || !valid_dtype(hs_dtype) || num_seqs < 0 || Hv <= 0 ||
+      !(V == 64 || V == 128) || !(K == 64 || K == 128)) {
+    return -1;
+  }
+  if (!pbgdn::layer_fusable(in_dtype, gate_dtype, hs_dtype, gate_stride, K, V)) return 0;
+  pbgdn::DeviceShape shape;
+  if (!pbgdn::device_shape(shape)) return -1;
+  pbgdn::ChunkParams p{};
+  p.V = V;
+  p.Hv = Hv;
+  p.num_seqs = num_seqs;
+  p.cus = shape.cus;
+  const bool wide = in_dtype == PBGDN_BF16 ? pbgdn::wide_eligible<128, pbgdn::u16>(p)
+                                           : pbgdn::wide_eligible<128, pbgdn::half_t>(p);
+  return wide ? 1 : 0;
 }
 
 // The prefill of pbgdn_chunk_fwd with the workspace taken from this device's

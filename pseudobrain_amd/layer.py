@@ -365,14 +365,18 @@ def _chunk_layer(shapes, dev, q, k, v, g, beta, scale, cu_seqlens, nseq, gate, o
         gate = gate.contiguous()
     codes = _lib.DTYPE_CODES
     hs = torch.empty(batch, length, hv * dv, dtype=out_dtype, device=dev)
-    o = torch.empty(batch, length, hv, dv, dtype=q.dtype, device=dev)
     lib = _lib.lib()
+    # o only where the epilogue runs as a pass of its own (the wide scan writes hs itself)
+    gate_stride = _rows(gate, "gate")
+    fuses = lib.pbgdn_chunk_layer_fuses(codes[q.dtype], codes[gate.dtype], codes[out_dtype], gate_stride, nseq, hv,
+                                        dk, dv)
+    o = None if fuses == 1 else torch.empty(batch, length, hv, dv, dtype=q.dtype, device=dev)
     ws_bytes = lib.pbgdn_chunk_workspace_size(batch, length, hv, nseq)
     workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     status = lib.pbgdn_chunk_layer_fwd(
         _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), codes[q.dtype], _lib.ptr(g), _lib.ptr(beta), codes[beta.dtype],
         _lib.ptr(h0), _lib.ptr(ht), state_code, _lib.ptr(state_idx), _lib.ptr(has_initial_state), num_states,
-        _lib.ptr(cu_seqlens), nseq, _lib.ptr(gate), _rows(gate, "gate"), codes[gate.dtype], _lib.ptr(norm),
+        _lib.ptr(cu_seqlens), nseq, _lib.ptr(gate), gate_stride, codes[gate.dtype], _lib.ptr(norm),
         float(eps), _lib.ptr(hs), codes[out_dtype], _lib.ptr(o), batch, length, hk, hv, dk, dv, float(scale),
         CHUNK, _lib.ptr(workspace), ws_bytes, _lib.stream_handle(dev))
     _lib.check(status, "pbgdn_chunk_layer_fwd")

@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version_and_status_strings():
-    assert _lib.lib().pbgdn_abi_version() == _lib.ABI_VERSION == 11
+    assert _lib.lib().pbgdn_abi_version() == _lib.ABI_VERSION == 12
     header = open(HEADER).read()
     assert re.search(r"#define PBGDN_ABI_VERSION (\d+)", header).group(1) == str(_lib.ABI_VERSION)
     assert _lib.status_string(0) == "ok"
@@ -353,3 +353,16 @@ def test_chunk_bwd_workspace_size():
     assert size(1, 64, 2, 4, 128, 128) == (4 * per_record + 2 * 64 * 4 * 128) * 4 + 256
     assert size(1, 0, 1, 1, 64, 64) == 256
     assert size(-1, 64, 1, 1, 64, 64) == 0
+
+
+def test_chunk_layer_fuses_rejects_and_declines_without_a_device_call():
+    """The fusion query: -1 for arguments the layer prefill rejects, 0 for
+    dtypes and widths the wide scan's epilogue does not take (decided before
+    any device query)."""
+    q = _lib.lib().pbgdn_chunk_layer_fuses
+    assert q(9, _lib.BF16, _lib.F32, 4096, 1, 32, 128, 128) == -1       # dtype code
+    assert q(_lib.BF16, _lib.BF16, _lib.F32, 4096, 1, 32, 128, 96) == -1  # epilogue widths 64, 128
+    assert q(_lib.BF16, _lib.BF16, _lib.F32, 4096, -1, 32, 128, 128) == -1
+    assert q(_lib.F32, _lib.F32, _lib.F32, 4096, 8, 32, 128, 128) == 0    # float32 inputs: two passes
+    assert q(_lib.BF16, _lib.F16, _lib.F32, 4096, 8, 32, 128, 128) == 0   # gate in another dtype
+    assert q(_lib.BF16, _lib.BF16, _lib.F32, 4096, 8, 32, 64, 128) == 0   # K = 64

@@ -36,6 +36,17 @@ def test_wide_batch(batch, length, hk, hv, dtype):
     assert_parity(f"wide B={batch} T={length} Hk={hk}", o, o_ref, s, s_ref)
 
 
+def test_wide_two_column_groups_per_head():
+    """V = 256: two 128-column groups per value head (column offset 128, and
+    2 Hv / Hk workgroups per key head in the XCD grouping), 128 workgroups."""
+    q, k, v, g, beta, h0 = generate(2, 200, 16, 32, 128, 256, torch.bfloat16, 0.02, seed=11)
+    with torch.no_grad():
+        o, s = gd.chunk_fwd(*to_dev(q, k, v, g, beta), 128 ** -0.5, h0.to(DEV))
+    torch.cuda.synchronize()
+    o_ref, s_ref = oracle(q, k, v, g, beta, 128 ** -0.5, h0)
+    assert_parity("wide V=256", o, o_ref, s, s_ref)
+
+
 def test_wide_packed_sequences_with_empty_and_ragged_lengths():
     lengths = [200, 0, 1, 63, 64, 65, 129, 10]
     q, k, v, g, beta, h0 = generate(1, sum(lengths), 16, 32, 128, 128, torch.bfloat16, 0.02, seed=7,

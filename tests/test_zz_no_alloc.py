@@ -16,10 +16,10 @@ DEV = "cuda"
 
 
 def call(noalloc, q, k, v, g, beta, h0, cu, hk, hv, dk, dv, scale):
-    """One prefill through the C ABI; returns (o bf16, final states fp32)."""
+    """One prefill through the C ABI; returns (o in q's dtype, final states fp32)."""
     batch, length = q.shape[:2]
     nseq = batch if cu is None else cu.numel() - 1
-    o = torch.full((batch, length, hv, dv), float("nan"), dtype=torch.bfloat16, device=DEV)
+    o = torch.full((batch, length, hv, dv), float("nan"), dtype=q.dtype, device=DEV)
     ht = torch.full((nseq, hv, dk, dv), float("nan"), dtype=torch.float32, device=DEV)
     lib = _lib.lib()
     codes = _lib.DTYPE_CODES
@@ -38,11 +38,11 @@ def call(noalloc, q, k, v, g, beta, h0, cu, hk, hv, dk, dv, scale):
     return o, ht
 
 
-def case(length, hk, hv, dk, dv, seed, lengths=None):
+def case(length, hk, hv, dk, dv, seed, lengths=None, dtype=torch.bfloat16, v_scale=1.0):
     nseq = 1 if lengths is None else len(lengths)
-    q, k, v, g, beta, h0 = generate(1, length, hk, hv, dk, dv, torch.bfloat16, 0.02, seed=seed, nstates=nseq)
+    q, k, v, g, beta, h0 = generate(1, length, hk, hv, dk, dv, dtype, 0.02, seed=seed, nstates=nseq)
     cu = None if lengths is None else cu_seqlens_of(lengths)
-    return q, k, v, g, beta, h0, cu
+    return q, k, v * v_scale, g, beta, h0 * v_scale, cu
 
 
 @pytest.mark.parametrize("first,second", [
@@ -50,10 +50,13 @@ def case(length, hk, hv, dk, dv, seed, lengths=None):
     ((4096, 16, 32, 128, 128, 1, None), (1000, 16, 32, 128, 128, 2, None)),
     # packed sequences, then fewer and shorter ones with other heads
     ((3000, 4, 8, 128, 64, 3, [1000, 64, 0, 1936]), (700, 2, 4, 64, 128, 4, [300, 400])),
+    # float32 inputs (the range scale of v and h0 is reduced into the scratch's
+    # tail): v x 1e3, then a smaller call with v x 1e5 and other heads
+    ((2048, 4, 4, 64, 64, 5, None, torch.float32, 1e3), (900, 2, 4, 128, 64, 6, [500, 400], torch.float32, 1e5)),
 ])
 def test_noalloc_equals_the_workspace_entry_point(first, second):
-    for length, hk, hv, dk, dv, seed, lengths in (first, second):
-        q, k, v, g, beta, h0, cu = case(length, hk, hv, dk, dv, seed, lengths)
+    for length, hk, hv, dk, dv, seed, lengths, *more in (first, second):
+        q, k, v, g, beta, h0, cu = case(length, hk, hv, dk, dv, seed, lengths, *more)
         dev = [None if x is None else x.to(DEV) for x in (q, k, v, g, beta, h0, cu)]
         scale = dk ** -0.5
         print(f"[noalloc] T={length} Hk={hk} Hv={hv} K={dk} V={dv} seqs={lengths}", flush=True)
@@ -61,7 +64,7 @@ def test_noalloc_equals_the_workspace_entry_point(first, second):
         o, s = call(True, *dev, hk, hv, dk, dv, scale)
         assert torch.equal(o, o_ref), "outputs differ from pbgdn_chunk_fwd"
         assert torch.equal(s, s_ref), "final states differ from pbgdn_chunk_fwd"
-        if length <= 1000:  # and both meet the oracle
+        if length <= 1000 or q.dtype == torch.float32:  # and both meet the oracle
             o_or, s_or = oracle(q, k, v, g, beta, scale, h0, cu_seqlens=cu)
             assert_parity(f"noalloc T={length}", o, o_or, s, s_or)
 
