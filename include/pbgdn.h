@@ -61,7 +61,7 @@
 extern "C" {
 #endif
 
-#define PBGDN_ABI_VERSION 12
+#define PBGDN_ABI_VERSION 13
 
 /* element types */
 #define PBGDN_F32 0
@@ -135,7 +135,7 @@ const char *pbgdn_status_string(int status);
  *   scale       query scale (the reference passes K ** -0.5)
  *   chunk       must be 64 (CHUNK, gated_deltanet.py:49)
  *   workspace   device scratch of at least pbgdn_chunk_workspace_size(B, T,
- *               Hv, num_seqs) bytes, 16-byte aligned: per-chunk intermediates
+ *               Hv, num_seqs, in_dtype) bytes, 16-byte aligned: per-chunk intermediates
  *               (Tb, Q K^T o D, decays) passed from the first kernel of the
  *               call to the second; its contents need no initialisation and
  *               are dead when the call's work on `stream` completes
@@ -144,7 +144,10 @@ const char *pbgdn_status_string(int status);
  * Ranges: the products run on fp16/bf16 MFMA operands with fp32 accumulation;
  * a chunk whose intermediate V - gamma K S leaves the fp16 range is scaled by
  * a power of two internally. With in_dtype F32, q and k enter as fp16
- * (|q|, |k| < 65504) and the state as an fp16 high/low pair; the call first
+ * (|q|, |k| < 65504), the state as an fp16 high/low pair, and U = Tb X (the
+ * WY product that carries the state update) is formed from fp16 high/low
+ * pairs of Tb and X (final-state error ~3e-4 where single fp16 operands gave
+ * 7-9e-4); the call first
  * computes on the device the power of two that brings max |v| and max |h0|
  * (over the states it reads) within 1024, runs on the scaled v and h0 and
  * scales o and ht back, exactly (the recurrence is linear in v and h0), so
@@ -198,13 +201,14 @@ int pbgdn_chunk_layer_fwd(const void *q, const void *k, const void *v,
 
 /*
  * Bytes of workspace pbgdn_chunk_fwd needs for a call with these sizes
- * (B * T tokens in num_seqs sequences, Hv value heads): about 13 KiB per
- * 64-token chunk and value head, plus 4 KiB (float32 inputs' range scale).
- * 0 for invalid sizes. No reference
- * counterpart: the reference materialises the same per-chunk tensors
- * (gated_deltanet.py:143-157) with torch allocations.
+ * (B * T tokens in num_seqs sequences, Hv value heads) and input dtype: 13 KiB
+ * per 64-token chunk and value head for 16-bit inputs, 19 KiB for float32
+ * (the low part of Tb as well), plus 4 KiB (float32 inputs' range scale).
+ * 0 for invalid sizes or dtype. No reference counterpart: the reference
+ * materialises the same per-chunk tensors (gated_deltanet.py:143-157) with
+ * torch allocations.
  */
-size_t pbgdn_chunk_workspace_size(int B, int T, int Hv, int num_seqs);
+size_t pbgdn_chunk_workspace_size(int B, int T, int Hv, int num_seqs, int in_dtype);
 
 /* Bytes of device scratch each GPU holds for pbgdn_chunk_fwd_noalloc (64 MiB). */
 #define PBGDN_NOALLOC_SCRATCH_BYTES (64u << 20)
@@ -219,7 +223,7 @@ size_t pbgdn_chunk_workspace_size(int B, int T, int Hv, int num_seqs);
  *
  * Arguments, results and kernels are those of pbgdn_chunk_fwd; `stream` must
  * belong to the current device (PBGDN_ERR_INVALID_ARGUMENT otherwise). A call
- * whose pbgdn_chunk_workspace_size(B, T, Hv, num_seqs) exceeds
+ * whose pbgdn_chunk_workspace_size(B, T, Hv, num_seqs, in_dtype) exceeds
  * PBGDN_NOALLOC_SCRATCH_BYTES returns PBGDN_ERR_SCRATCH and launches nothing
  * (e.g. at Hv = 32 about 9,900 tokens in one sequence; at Hv = 16 twice that).
  * Every call on one GPU shares that GPU's array: calls whose work overlaps on

@@ -13,7 +13,7 @@ import threading
 import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpbgdn.so")
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 F32, BF16, F16 = 0, 1, 2
 OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED, ERR_LAUNCH, ERR_SCRATCH = 0, 1, 2, 3, 4
@@ -32,7 +32,7 @@ SIGNATURES = {
     "pbgdn_chunk_layer_fwd": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _i,
                                _vp, _l, _i, _vp, _f, _vp, _i, _vp,
                                _i, _i, _i, _i, _i, _i, _f, _i, _vp, ctypes.c_size_t, _vp], _i),
-    "pbgdn_chunk_workspace_size": ([_i, _i, _i, _i], ctypes.c_size_t),
+    "pbgdn_chunk_workspace_size": ([_i, _i, _i, _i, _i], ctypes.c_size_t),
     "pbgdn_chunk_layer_fuses": ([_i, _i, _i, _l, _i, _i, _i, _i], _i),
     "pbgdn_chunk_fwd_noalloc": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _i, _vp, _i,
                                  _i, _i, _i, _i, _i, _i, _f, _i, _vp], _i),

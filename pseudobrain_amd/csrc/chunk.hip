@@ -178,10 +178,10 @@ __global__ __launch_bounds__(256) void range_max_kernel(RangeParams p) {
 }  // namespace
 }  // namespace pbgdn
 
-extern "C" size_t pbgdn_chunk_workspace_size(int B, int T, int Hv, int num_seqs) {
-  if (B < 0 || T < 0 || Hv <= 0 || num_seqs < 0) return 0;
+extern "C" size_t pbgdn_chunk_workspace_size(int B, int T, int Hv, int num_seqs, int in_dtype) {
+  if (B < 0 || T < 0 || Hv <= 0 || num_seqs < 0 || !pbgdn::valid_dtype(in_dtype)) return 0;
   const long records = pbgdn::chunk_records(static_cast<long>(B) * T, num_seqs);
-  return static_cast<size_t>(records) * Hv * pbgdn::REC_BYTES + pbgdn::RANGE_TAIL_BYTES;
+  return static_cast<size_t>(records) * Hv * pbgdn::rec_bytes_of(in_dtype) + pbgdn::RANGE_TAIL_BYTES;
 }
 
 namespace pbgdn {
@@ -219,7 +219,7 @@ int chunk_setup(const void *q, const void *k, const void *v, int in_dtype, const
   if (T > 0 && (!q || !k || !v || !g || !beta || !o)) return PBGDN_ERR_INVALID_ARGUMENT;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v)) return PBGDN_ERR_INVALID_ARGUMENT;
   if (!workspace || !aligned16(workspace) ||
-      workspace_bytes < pbgdn_chunk_workspace_size(B, T, Hv, num_seqs)) {
+      workspace_bytes < pbgdn_chunk_workspace_size(B, T, Hv, num_seqs, in_dtype)) {
     return PBGDN_ERR_INVALID_ARGUMENT;
   }
   const long total = static_cast<long>(V / pbgdn::VT) * Hv * num_seqs;
@@ -256,7 +256,8 @@ extern "C" int pbgdn_chunk_fwd(const void *q, const void *k, const void *v, int 
   if (st != PBGDN_OK || empty) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (in_dtype == PBGDN_F32) {  // the range scale of v and the initial states, into the workspace's tail
-    float *part = reinterpret_cast<float *>(static_cast<unsigned char *>(workspace) + records * Hv * pbgdn::REC_BYTES);
+    float *part = reinterpret_cast<float *>(static_cast<unsigned char *>(workspace) +
+                                            records * Hv * pbgdn::rec_bytes_of(PBGDN_F32));
     pbgdn::RangeParams rp{static_cast<const float *>(v), static_cast<long>(B) * T * Hv * V, h0, state_dtype,
                           state_idx, has_initial_state, num_states, num_seqs, static_cast<long>(Hv) * K * V, part};
     hipLaunchKernelGGL(pbgdn::range_max_kernel, dim3(pbgdn::RANGE_BLOCKS), dim3(256), 0, s, rp);
@@ -358,7 +359,8 @@ extern "C" int pbgdn_chunk_fwd_noalloc(const void *q, const void *k, const void 
                                        const int32_t *cu_seqlens, int num_seqs, void *o, int out_dtype, int B,
                                        int T, int Hk, int Hv, int K, int V, float scale, int chunk,
                                        void *stream) {
-  if (pbgdn_chunk_workspace_size(B, T, Hv, num_seqs) > PBGDN_NOALLOC_SCRATCH_BYTES) return PBGDN_ERR_SCRATCH;
+  if (!pbgdn::valid_dtype(in_dtype)) return PBGDN_ERR_INVALID_ARGUMENT;
+  if (pbgdn_chunk_workspace_size(B, T, Hv, num_seqs, in_dtype) > PBGDN_NOALLOC_SCRATCH_BYTES) return PBGDN_ERR_SCRATCH;
   unsigned char *ws = nullptr;
   const int st = pbgdn::scratch_for_stream(static_cast<hipStream_t>(stream), &ws);
   if (st != PBGDN_OK) return st;

@@ -55,6 +55,9 @@ constexpr int VT = 16;                  // value columns per scan workgroup
 //            at fragment frag_index(r, kk); lane (g, c) holds
 //            Tb[16 r + c][32 kk + 8 g .. + 7]
 //   REC_QKD  the same for QKD = scale (Q K^T o D)
+//   REC_TBL  float32 inputs only: the low fp16 part of Tb (Tb - fp16(Tb)) in
+//            the layout of REC_TB, so that U = Tb X is formed to ~22 bits
+//            (REC_BYTES_F32 bytes a record)
 // Records are indexed (chunk record, value head); the chunk record of chunk j
 // of sequence s is rec_base(s) + j with rec_base(s) = floor(bos_s / 64) + s,
 // which is increasing in s, leaves room for every sequence's chunks, and is
@@ -66,6 +69,12 @@ constexpr int SC_GAM = 0, SC_GSC = 256, SC_DEC = 512;
 constexpr int REC_TB = 1024;
 constexpr int REC_QKD = REC_TB + NFRAG * FRAG_BYTES;
 constexpr int REC_BYTES = REC_QKD + NFRAG * FRAG_BYTES;
+constexpr int REC_TBL = REC_BYTES;
+constexpr int REC_BYTES_F32 = REC_TBL + NFRAG * FRAG_BYTES;
+// Bytes of a record for inputs of type TIn / of dtype code `in_dtype`.
+template <typename TIn>
+__host__ __device__ constexpr int rec_bytes() { return sizeof(TIn) == 4 ? REC_BYTES_F32 : REC_BYTES; }
+__host__ __device__ constexpr int rec_bytes_of(int in_dtype) { return in_dtype == PBGDN_F32 ? REC_BYTES_F32 : REC_BYTES; }
 
 __host__ __device__ constexpr int frag_index(int r, int kk) { return r < 2 ? r : 2 * r - 2 + kk; }
 

@@ -8,6 +8,7 @@
 //   Tb  = (I + A)^-1 diag(beta)                  as 16x16x32 fp16 A fragments
 //   QKD = scale (Q K^T o D), D inclusive        as 16x16x32 fp16 A fragments
 //   exp(c_t), scale exp(c_t), exp(c_63 - c_t)  fp32
+//   Tb - fp16(Tb)                               float32 inputs: the low part, as Tb
 //
 // A persistent grid of 4-wave workgroups walks the items: a chunk record and
 // HPI value heads that share a key head (HPI = 2 when the value heads per key
@@ -45,10 +46,11 @@ constexpr int prep_wg_per_cu() { return sizeof(TIn) == 4 ? 2 : 3; }
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 // LDS layout (byte offsets); (swz) as in chunk.hpp. K and Q are read only by
-// the tiles stage, and Tb, QKD, A16, AT live from the decay stage to the
-// record stores, so the two groups share bytes (a barrier separates the two
-// uses); the decay tables follow the larger of the two.
-template <int K>
+// the tiles stage, and Tb, QKD, A16, AT (and with LO Tb's low part) live from
+// the decay stage to the record stores, so the two groups share bytes (a
+// barrier separates the two uses); the decay tables follow the larger of the
+// two.
+template <int K, bool LO>
 struct PrepLayout {
   static constexpr int KPB = 2 * K + 32;
   static constexpr int SPB = 2 * CH + 32;
@@ -60,7 +62,9 @@ struct PrepLayout {
   static constexpr int A16 = QKD + CH * SPB;            // [64 t][64 s] fp16: off-diagonal A, diagonal D (swz)
   static constexpr int AT = A16 + CH * SPB;             // [4 tiles][16][16] fp32 diagonal tiles of A
   static constexpr int AT_END = AT + 4 * 16 * ATP;
-  static constexpr int SC = AT_END > 2 * KQ_MAT ? AT_END : 2 * KQ_MAT;  // [2 heads][11][64] fp32 decay tables
+  static constexpr int TBL = AT_END;                    // LO: [64 t][64 s] fp16 low part of Tb (swz)
+  static constexpr int TBL_END = LO ? TBL + CH * SPB : AT_END;
+  static constexpr int SC = TBL_END > 2 * KQ_MAT ? TBL_END : 2 * KQ_MAT;  // [2 heads][11][64] fp32 decay tables
   static constexpr int SC_HEAD = 11 * CH * 4;
   static constexpr int CUM = 0, GAM = 256, DEC = 512, BET = 768, CUM4 = 1024, BET4 = 1280, BU4 = 1536,
                        SU4 = 1792, W1 = 2048;
@@ -69,12 +73,17 @@ struct PrepLayout {
 
 template <int K, typename TIn>
 struct PrepBlock {
-  using L = PrepLayout<K>;
+  // float32 inputs also store Tb's low fp16 part, so that the scan forms U = Tb X
+  // from high/low pairs
+  static constexpr bool LO = sizeof(TIn) == 4;
+  static constexpr int RB = rec_bytes<TIn>();
+  using L = PrepLayout<K, LO>;
   using Op = OpOf<TIn>;
   using O8 = typename Op::T8;
   using Inputs = ChunkInputs<K, TIn, PNT, L, false, true>;
   static constexpr int KS = K / 32;  // contraction steps over keys
   static_assert(K == 64 || K == 128, "K must be 64 or 128");
+  static_assert(L::TBL_END <= L::SC, "Tb's low part before the decay tables");
   static_assert(L::BYTES * prep_wg_per_cu<TIn>() <= 160 * 1024, "prep LDS");
 
   unsigned char *lds;
@@ -269,7 +278,14 @@ struct PrepBlock {
     // yt = tile(D^T): lane (g, c) holds D[c][4g + i], row c of D at columns 4g..
     const uint32_t o = 16 * w * L::SPB + 32 * w + sp_tile;
     st(L::A16 + o, to_half4(yt));
-    st(L::TB + o, to_half4(yt * bw));
+    put_tb(o, yt * bw);
+  }
+
+  // A tile of Tb (fp32) -> the fp16 Tb tile, and with LO its low part.
+  __device__ void put_tb(uint32_t o, float4_t tb) const {
+    const half4_t hi = to_half4(tb);
+    st(L::TB + o, hi);
+    if constexpr (LO) st(L::TBL + o, to_half4(tb - to_float4(hi)));
   }
 
   // Off-diagonal blocks of T:
@@ -287,7 +303,7 @@ struct PrepBlock {
     };
     auto put = [&](int r, int s, float4_t mt) {  // mt = tile((D_r Y_rs)^T) = -tile(T_rs^T)
       const float4_t bs = ld<float4_t>(L::SC + jh * L::SC_HEAD + L::BET + (16 * s + 4 * g4) * 4);
-      st(L::TB + 16 * r * L::SPB + 32 * s + sp_tile, to_half4(-mt * bs));
+      put_tb(16 * r * L::SPB + 32 * s + sp_tile, -mt * bs);
     };
     if (chain == 0) {
       const half4_t a10 = aop(1, 0), a20 = aop(2, 0), a21 = aop(2, 1);
@@ -315,19 +331,24 @@ struct PrepBlock {
     }
   }
 
-  // Fragments f = wave, wave + 4, wave + 8 of Tb (f < 6) and QKD (f >= 6) and
-  // one decay vector per wave (wave 3: c itself) -> the workspace record. rec < 0 issues the same stores with a zero-size resource.
+  // Fragments f = wave + 4 j of Tb (f < 6), QKD (6 <= f < 12) and with LO
+  // Tb's low part (12 <= f < 18), and one decay vector per wave (wave 3: c
+  // itself) -> the workspace record. Every wave issues the same stores (past
+  // the last fragment to an offset out of range); rec < 0 issues them with a
+  // zero-size resource.
   __device__ void out(long rec, int h, int jh) const {
-    const __amdgpu_buffer_rsrc_t rr =
-        rsrc(p.ws + (rec * p.Hv + h) * static_cast<long>(REC_BYTES), rec >= 0 ? REC_BYTES : 0);
+    const __amdgpu_buffer_rsrc_t rr = rsrc(p.ws + (rec * p.Hv + h) * static_cast<long>(RB), rec >= 0 ? RB : 0);
+    constexpr int NF = (LO ? 3 : 2) * NFRAG;
 #pragma unroll
-    for (int j = 0; j < 3; ++j) {
+    for (int j = 0; j < (NF + 3) / 4; ++j) {
       const int f = wave + 4 * j;
-      const int fi = f < NFRAG ? f : f - NFRAG;
+      const int m = f < NF ? f / NFRAG : 0;  // 0 Tb, 1 QKD, 2 Tb low
+      const int fi = f < NF ? f - m * NFRAG : 0;
       const int r = fi < 2 ? fi : 2 + ((fi - 2) >> 1);
       const int kk = fi < 2 ? 0 : ((fi - 2) & 1);
-      const uint32_t src = (f < NFRAG ? L::TB : L::QKD) + 16 * r * L::SPB + sp_frag + 64 * kk;
-      const uint32_t dst = (f < NFRAG ? REC_TB : REC_QKD) + fi * FRAG_BYTES + lane * 16;
+      const uint32_t src = (m == 0 ? L::TB : m == 1 ? L::QKD : L::TBL) + 16 * r * L::SPB + sp_frag + 64 * kk;
+      const uint32_t dst = f < NF ? (m == 0 ? REC_TB : m == 1 ? REC_QKD : REC_TBL) + fi * FRAG_BYTES + lane * 16
+                                  : OUT_OF_RANGE;
       const u32x4_t x = __builtin_bit_cast(u32x4_t, ld<half8_t>(src));
       if (nt) {
         __builtin_amdgcn_raw_buffer_store_b128(x, rr, dst, 0, 2);
@@ -348,13 +369,15 @@ struct PrepBlock {
     }
   }
 
-  // Blocks (0, 1) and (2, 3) of Tb and QKD lie above the diagonal inside the
-  // fragments the record holds and must read as zero; the staging of K and Q
-  // overwrote them, so each wave clears one of the four per item.
+  // Blocks (0, 1) and (2, 3) of Tb and QKD (and of Tb's low part) lie above
+  // the diagonal inside the fragments the record holds and must read as
+  // zero; the staging of K and Q overwrote them, so each wave clears one of
+  // the four per item (and one of Tb's low part).
   __device__ void clear_upper() const {
     const int r = (wave & 1) ? 2 : 0;
     const uint32_t base = (wave & 2) ? L::QKD : L::TB;
     st(base + 16 * r * L::SPB + 32 * (r + 1) + sp_tile, half4_t{});
+    if constexpr (LO) st(L::TBL + 16 * r * L::SPB + 32 * (r + 1) + sp_tile, half4_t{});  // waves 0, 2 and 1, 3 alike
   }
 
   // Items of this workgroup (prep_share, schedule.hpp).
@@ -428,7 +451,7 @@ constexpr long REC_STREAM_BYTES = 64L << 20;
 template <int K, typename TIn>
 int launch_prep(const ChunkParams &p, long records, hipStream_t stream) {
   static std::atomic<bool> configured[MAX_DEVICES];  // the attribute is set per device
-  const size_t smem = PrepLayout<K>::BYTES;
+  const size_t smem = PrepLayout<K, sizeof(TIn) == 4>::BYTES;
   auto kernel = prep_kernel<K, TIn>;
   if (!smem_configured(reinterpret_cast<const void *>(kernel), smem, configured)) return PBGDN_ERR_LAUNCH;
   const int hpi = ((p.Hv / p.Hk) % 2 == 0) ? 2 : 1;  // value heads per item (PrepBlock::hpi)
@@ -437,7 +460,7 @@ int launch_prep(const ChunkParams &p, long records, hipStream_t stream) {
   const long grid = prep_grid(items, p.cus, prep_wg_per_cu<TIn>(), p.xcds);
   // Records of a large call are written non-temporally: measured on the
   // 32,768-token call (213 MB of records), the scan then reads them 2% faster.
-  const int nt = records * p.Hv * static_cast<long>(REC_BYTES) > REC_STREAM_BYTES ? 1 : 0;
+  const int nt = records * p.Hv * static_cast<long>(rec_bytes<TIn>()) > REC_STREAM_BYTES ? 1 : 0;
   hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(PNT), smem, stream, p, static_cast<int>(items), nt);
   return hipGetLastError() == hipSuccess ? PBGDN_OK : PBGDN_ERR_LAUNCH;
 }

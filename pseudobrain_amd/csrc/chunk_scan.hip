@@ -52,6 +52,11 @@
 //     (chunk.hpp) before it becomes fp16: each X wave publishes its tile's
 //     scale, the U waves bring the tiles to the chunk's smallest one through
 //     the lanes of their Tb fragments, and U, O are restored in fp32.
+//   * float32 inputs form U = Tb X from fp16 high/low pairs of both (three
+//     products: high x high, high x low, low x high): the prep kernel's records
+//     carry Tb's low part (staged into one buffer, read the tick after), and
+//     X's low part goes through the output tile that is idle that tick. This
+//     is the product whose fp16 rounding bounded the float32 state error.
 //
 // LDS costs that shape the code (MI355X, CU cycles per wave64 instruction):
 // 16-byte fragment reads and transposing reads 4, 8-byte tile writes 6.7 in
@@ -69,7 +74,7 @@ constexpr int NT = NCW * 64 + NLT;      // threads per scan workgroup
 // LDS layout (byte offsets); (swz) as in chunk.hpp. Two chunk buffers, each
 // [K, Q][64 t][K] in the operand type (swz), V [64 t][16] 16-bit in 32-byte
 // rows, and the chunk's workspace record as stored; two O tiles [64 t][16].
-template <int K>
+template <int K, bool LO>
 struct ScanLayout {
   static constexpr int KPB = 2 * K + 32;
   static constexpr int SPB = 2 * CH + 32;
@@ -87,7 +92,10 @@ struct ScanLayout {
   static constexpr int OT = SL + VT * KPB;            // [2][64 t][16] output type
   static constexpr int OT_BUF = CH * VT * 4;
   static constexpr int RS = OT + 2 * OT_BUF;          // fp32 range scales: [4] X tiles, [2] chunk by parity
-  static constexpr int BYTES = RS + 32;
+  // LO (float32 inputs): Tb's low fragments of the next chunk, one buffer
+  // (staged in the third phase, read in the first of the next tick)
+  static constexpr int TBL = RS + 32;
+  static constexpr int BYTES = TBL + (LO ? NFRAG * FRAG_BYTES : 0);
   // Chained streams only: the initial state of the sequence whose first
   // chunk is in chunk buffer b ([K rows][16 columns] as stored), staged by the
   // loader waves with that chunk.
@@ -100,6 +108,11 @@ struct ScanLayout {
   __device__ static constexpr int rec(int b) { return b * BUF + REC_OFF; }
   __device__ static constexpr int ot(int b) { return OT + b * OT_BUF; }
   __device__ static constexpr int ut(int b) { return UT + b * VT * SPB; }
+  // LO: X's low part [16 col][64 t] fp16 (swz, as XT) in the O tile of the
+  // chunk's own parity, which holds nothing from the tick's first phase until
+  // the output waves write the chunk's O a tick later
+  __device__ static constexpr int xtl(int b) { return ot(b); }
+  static_assert(!LO || VT * SPB <= OT_BUF, "X's low part fits an O tile");
 };
 
 // Staging of one chunk by the loader threads: 16-byte units numbered K, Q
@@ -110,13 +123,15 @@ struct ScanLayout {
 // the loads and stores compile without branches.
 template <int K, typename TIn>
 struct ScanStage {
-  using L = ScanLayout<K>;
+  static constexpr bool LO = sizeof(TIn) == 4;
+  using L = ScanLayout<K, LO>;
   static constexpr int EPU = 16 / sizeof(TIn);  // elements per unit
   static constexpr int ROW_UNITS = K / EPU;
   static constexpr int MAT_UNITS = CH * ROW_UNITS;
   static constexpr int KQ_UNITS = 2 * MAT_UNITS;
   static constexpr int V_UNITS = CH * VT / EPU;
-  static constexpr int R_UNITS = REC_BYTES / 16;
+  static constexpr int R_UNITS = rec_bytes<TIn>() / 16;
+  static constexpr int TBL_UNIT = KQ_UNITS + V_UNITS + REC_BYTES / 16;  // LO: units from here on are Tb's low part
   static constexpr int UNITS = KQ_UNITS + V_UNITS + R_UNITS;
   static constexpr int UPT = (UNITS + NLT - 1) / NLT;
   static constexpr int SLOT_K = MAT_UNITS / NLT;   // slots [0, SLOT_K): K; [SLOT_K, SLOT_V): Q
@@ -130,19 +145,22 @@ struct ScanStage {
   static_assert(REC_SC == 0 && SLOT_P2 < SLOT_P3 && SLOT_P3 <= UPT, "record vectors lead the record");
   static_assert(MAT_UNITS % NLT == 0, "K and Q must fill whole slots");
   static_assert(V_UNITS % 64 == 0 && V_UNITS <= NLT, "V must end at a wave boundary of its slot");
+  static_assert(TBL_UNIT % 64 == 0, "Tb's low part starts at a wave boundary of its slot");
 
   struct Regs {
     uint4 u[UPT];
   };
 
   uint32_t src[UPT];  // byte offset of the unit in its source (OUT_OF_RANGE if none)
-  uint32_t dst[UPT];  // LDS byte offset of the unit within a chunk buffer
+  uint32_t dst[UPT];  // LDS byte offset of the unit within a chunk buffer (Tb's low part: within LDS)
+  uint32_t tbl;       // bit i: this wave's unit of slot i is Tb's low part (one buffer, not per chunk)
   bool v_wave;        // this loader wave's slot SLOT_V unit is V (else record); wave-uniform
   float vscale;       // fp32 inputs: V's range scale (a power of two)
 
   __device__ __forceinline__ void init(const ChunkParams &p, int l, float in_down) {
     v_wave = __builtin_amdgcn_readfirstlane(l & ~63) < V_UNITS;
     vscale = in_down;
+    tbl = 0;
 #pragma unroll
     for (int i = 0; i < UPT; ++i) {
       const int u = l + NLT * i;
@@ -163,9 +181,15 @@ struct ScanStage {
       } else if (u < UNITS) {
         const int w = u - KQ_UNITS - V_UNITS;
         src[i] = 16 * w;
-        dst[i] = L::REC_OFF + 16 * w;
+        if (LO && u >= TBL_UNIT) {
+          dst[i] = L::TBL + 16 * (u - TBL_UNIT);
+          tbl |= 1u << i;
+        } else {
+          dst[i] = L::REC_OFF + 16 * w;
+        }
       }
     }
+    tbl = __builtin_amdgcn_readfirstlane(tbl);  // wave-uniform: the boundaries are whole waves
   }
 
   // Issue the loads of the chunk at tokens t0.. (`len` left, may be <= 0) of
@@ -178,7 +202,7 @@ struct ScanStage {
     const long v_bytes = rows > 0 ? ((rows - 1) * p.Hv * p.V + VT) * static_cast<long>(sizeof(TIn)) : 0;
     const __amdgpu_buffer_rsrc_t rk = rsrc(static_cast<const TIn *>(p.k) + qk_base, qk_bytes);
     const __amdgpu_buffer_rsrc_t rq = rsrc(static_cast<const TIn *>(p.q) + qk_base, qk_bytes);
-    const __amdgpu_buffer_rsrc_t rr = rsrc(rec, rec ? REC_BYTES : 0);
+    const __amdgpu_buffer_rsrc_t rr = rsrc(rec, rec ? rec_bytes<TIn>() : 0);
     const __amdgpu_buffer_rsrc_t rvr =
         v_wave ? rsrc(static_cast<const TIn *>(p.v) + (t0 * p.Hv + h) * static_cast<long>(p.V) + v0, v_bytes) : rr;
 #pragma unroll
@@ -199,19 +223,19 @@ struct ScanStage {
     const long v_bytes = rows > 0 ? ((rows - 1) * p.Hv * p.V + VT) * static_cast<long>(sizeof(TIn)) : 0;
     const __amdgpu_buffer_rsrc_t rk = rsrc(static_cast<const TIn *>(p.k) + qk_base, qk_bytes);
     const __amdgpu_buffer_rsrc_t rq = rsrc(static_cast<const TIn *>(p.q) + qk_base, qk_bytes);
-    const __amdgpu_buffer_rsrc_t rr = rsrc(rec, rec ? REC_BYTES : 0);
+    const __amdgpu_buffer_rsrc_t rr = rsrc(rec, rec ? rec_bytes<TIn>() : 0);
     const __amdgpu_buffer_rsrc_t rvr =
         v_wave ? rsrc(static_cast<const TIn *>(p.v) + (t0 * p.Hv + h) * static_cast<long>(p.V) + v0, v_bytes) : rr;
 #pragma unroll
     for (int i = I0; i < I1; ++i) {
-      store_unit(lds + base, r, l, i);
+      store_unit(lds, base, r, l, i);
       r.u[i] = buf_load16(i < SLOT_K ? rk : i < SLOT_V ? rq : i == SLOT_V ? rvr : rr, src[i]);
     }
   }
 
-  __device__ __forceinline__ void store_unit(unsigned char *buf, const Regs &r, int l, int i) const {
+  __device__ __forceinline__ void store_unit(unsigned char *lds, int base, const Regs &r, int l, int i) const {
     if (l + NLT * i >= UNITS) return;
-    unsigned char *d = buf + dst[i];
+    unsigned char *d = lds + (LO && ((tbl >> i) & 1) ? 0 : base) + dst[i];
     if (EPU == 4 && i == SLOT_V && v_wave) {  // fp32 V, range-scaled: bf16 high and low parts
       const uint4 x = r.u[i];
       bf16x4_t hi, lo;
@@ -234,7 +258,7 @@ struct ScanStage {
   // nothing: their slot is skipped by range.
   __device__ __forceinline__ void store(unsigned char *lds, int base, const Regs &r, int l) const {
 #pragma unroll
-    for (int i = 0; i < UPT; ++i) store_unit(lds + base, r, l, i);
+    for (int i = 0; i < UPT; ++i) store_unit(lds, base, r, l, i);
   }
 };
 
@@ -270,7 +294,8 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 // plain counters.
 template <int K, typename TIn, typename TOut, bool CHAIN>
 struct ScanBlock {
-  using L = ScanLayout<K>;
+  static constexpr bool LO = sizeof(TIn) == 4;  // U = Tb X from high/low pairs
+  using L = ScanLayout<K, LO>;
   using Op = OpOf<TIn>;
   using O4 = typename Op::T4;
   using O8 = typename Op::T8;
@@ -402,7 +427,7 @@ struct ScanBlock {
   }
   __device__ __forceinline__ const unsigned char *rec_of(const Cursor &c) const {
     const bool none = CHAIN ? at_end(c) : c.t0 >= c.eos;
-    return none ? nullptr : p.ws + (c.rec * p.Hv + h) * static_cast<long>(REC_BYTES);
+    return none ? nullptr : p.ws + (c.rec * p.Hv + h) * static_cast<long>(rec_bytes<TIn>());
   }
 
   // ------------------------------------------------------------ loader waves
@@ -621,7 +646,7 @@ struct ScanBlock {
     launder();
     const int b = P;
     const int r = wave;
-    half8_t f0, f1;
+    half8_t f0, f1, fl0, fl1;  // Tb fragments (LO: and their low parts)
     float4_t dd;
     O8 kt[2];
     {
@@ -633,6 +658,10 @@ struct ScanBlock {
       }
       f0 = rec_frag(b, REC_TB, r, 0);
       f1 = second_step(rec_frag(b, REC_TB, r, 1), r);
+      if constexpr (LO) {
+        fl0 = ld<half8_t>(L::TBL + frag_index(r, 0) * FRAG_BYTES + lane * 16);
+        fl1 = second_step(ld<half8_t>(L::TBL + frag_index(r, 1) * FRAG_BYTES + lane * 16), r);
+      }
       dd = rec_rows(b, SC_DEC, r);
       float4_t acc = {0.f, 0.f, 0.f, 0.f}, acl = acc;
 #pragma unroll
@@ -649,13 +678,20 @@ struct ScanBlock {
         down = range_scale(wave_max(xm));
         x *= down;
       }
-      st(L::XT + sp_tile + 32 * r, to_half4(x));
+      const half4_t xh = to_half4(x);
+      st(L::XT + sp_tile + 32 * r, xh);
+      if constexpr (LO) st(L::xtl(b) + sp_tile + 32 * r, to_half4(x - to_float4(xh)));
       if (lane == 0) st(L::RS + 4 * r, down);
     }
     block_sync();
     {
       const half8_t x0 = ld<half8_t>(L::XT + sp_frag);
       const half8_t x1 = ld<half8_t>(L::XT + sp_frag + 64);
+      half8_t xl0, xl1;
+      if constexpr (LO) {
+        xl0 = ld<half8_t>(L::xtl(b) + sp_frag);
+        xl1 = ld<half8_t>(L::xtl(b) + sp_frag + 64);
+      }
       const float4_t downs = ld<float4_t>(L::RS);
       fetch_kt(b, kt);
       // the chunk's scale: the smallest of its tiles'; the Tb lanes that
@@ -667,10 +703,22 @@ struct ScanBlock {
         const int t = g4 >> 1;
         f0 *= static_cast<half_t>(d / downs[t]);
         f1 *= static_cast<half_t>(d / downs[2 + t]);
+        if constexpr (LO) {
+          fl0 *= static_cast<half_t>(d / downs[t]);
+          fl1 *= static_cast<half_t>(d / downs[2 + t]);
+        }
       }
       // no branch between the products and their first reads
       float4_t u = mfma32(f0, x0, float4_t{0.f, 0.f, 0.f, 0.f});
+      if constexpr (LO) {
+        u = mfma32(f0, xl0, u);
+        u = mfma32(fl0, x0, u);
+      }
       u = mfma32(f1, x1, u);
+      if constexpr (LO) {
+        u = mfma32(f1, xl1, u);
+        u = mfma32(fl1, x1, u);
+      }
       const uint32_t o = sp_tile + 32 * r;
       st(L::ut(b) + o, to_half4(u));  // U' = U d, for O of this chunk
       if (wave == 0 && lane == 0) st(L::RS + 16 + 4 * b, d);
@@ -900,7 +948,9 @@ __global__ __launch_bounds__(NT) void scan_kernel(ChunkParams p) {
 template <int K, typename TIn, typename TOut, bool CHAIN>
 int launch_scan_kernel(const ChunkParams &p, hipStream_t stream) {
   static std::atomic<bool> configured[MAX_DEVICES];  // the attribute is set per device
-  const size_t smem = CHAIN ? ScanLayout<K>::CHAIN_BYTES : ScanLayout<K>::BYTES;
+  using L = ScanLayout<K, sizeof(TIn) == 4>;
+  static_assert(L::CHAIN_BYTES <= 160 * 1024, "scan LDS");
+  const size_t smem = CHAIN ? L::CHAIN_BYTES : L::BYTES;
   auto kernel = scan_kernel<K, TIn, TOut, CHAIN>;
   if (!smem_configured(reinterpret_cast<const void *>(kernel), smem, configured)) return PBGDN_ERR_LAUNCH;
   const int total = (p.V / VT) * p.Hv * p.seq_groups;

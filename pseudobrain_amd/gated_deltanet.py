@@ -199,7 +199,7 @@ def _chunk_fwd(q, k, v, g, beta, scale: float, h0=None, cu_seqlens=None, *,
         raise ValueError("out must be a contiguous [B,T,Hv,V] tensor of out_dtype")
     final = torch.empty(nseq, hv, dk, dv, dtype=torch.float32, device=dev) if output_final_state else None
     lib = _lib.lib()
-    ws_bytes = lib.pbgdn_chunk_workspace_size(batch, length, hv, nseq)
+    ws_bytes = lib.pbgdn_chunk_workspace_size(batch, length, hv, nseq, _lib.DTYPE_CODES[q.dtype])
     workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     codes = _lib.DTYPE_CODES
     status = lib.pbgdn_chunk_fwd(
@@ -259,7 +259,7 @@ def chunk_fwd_slots(q, k, v, g, beta, scale: float, states, state_idx, cu_seqlen
     elif out.shape != (batch, length, hv, dv) or out.dtype != out_dtype or not out.is_contiguous():
         raise ValueError("out must be a contiguous [B,T,Hv,V] tensor of out_dtype")
     lib = _lib.lib()
-    ws_bytes = lib.pbgdn_chunk_workspace_size(batch, length, hv, nseq)
+    ws_bytes = lib.pbgdn_chunk_workspace_size(batch, length, hv, nseq, _lib.DTYPE_CODES[q.dtype])
     workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     codes = _lib.DTYPE_CODES
     status = lib.pbgdn_chunk_fwd(

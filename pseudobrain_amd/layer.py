@@ -371,7 +371,7 @@ def _chunk_layer(shapes, dev, q, k, v, g, beta, scale, cu_seqlens, nseq, gate, o
     fuses = lib.pbgdn_chunk_layer_fuses(codes[q.dtype], codes[gate.dtype], codes[out_dtype], gate_stride, nseq, hv,
                                         dk, dv)
     o = None if fuses == 1 else torch.empty(batch, length, hv, dv, dtype=q.dtype, device=dev)
-    ws_bytes = lib.pbgdn_chunk_workspace_size(batch, length, hv, nseq)
+    ws_bytes = lib.pbgdn_chunk_workspace_size(batch, length, hv, nseq, _lib.DTYPE_CODES[q.dtype])
     workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     status = lib.pbgdn_chunk_layer_fwd(
         _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), codes[q.dtype], _lib.ptr(g), _lib.ptr(beta), codes[beta.dtype],

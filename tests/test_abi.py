@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version_and_status_strings():
-    assert _lib.lib().pbgdn_abi_version() == _lib.ABI_VERSION == 12
+    assert _lib.lib().pbgdn_abi_version() == _lib.ABI_VERSION == 13
     header = open(HEADER).read()
     assert re.search(r"#define PBGDN_ABI_VERSION (\d+)", header).group(1) == str(_lib.ABI_VERSION)
     assert _lib.status_string(0) == "ok"
@@ -55,7 +55,7 @@ def test_chunk_fwd_noalloc_rejects_calls_beyond_its_scratch():
     header = open(HEADER).read()
     assert re.search(r"#define PBGDN_NOALLOC_SCRATCH_BYTES \(64u << 20\)", header)
     lib = _lib.lib()
-    assert lib.pbgdn_chunk_workspace_size(1, 32768, 32, 1) > _lib.NOALLOC_SCRATCH_BYTES
+    assert lib.pbgdn_chunk_workspace_size(1, 32768, 32, 1, _lib.BF16) > _lib.NOALLOC_SCRATCH_BYTES
     args = dict(q=FAKE, k=FAKE, v=FAKE, in_dtype=1, g=FAKE, beta=FAKE, beta_dtype=0, h0=None, ht=None, sdt=0,
                 sidx=None, has_init=None, nstates=0, cu=None, nseq=1, o=FAKE, out_dtype=1, B=1, T=32768, Hk=16,
                 Hv=32, K=128, V=128, scale=0.1, chunk=64, stream=None)
@@ -149,15 +149,19 @@ def test_stream_probe_empty_is_ok():
 
 def test_chunk_workspace_size():
     lib = _lib.lib()
-    rec = 13 * 1024  # bytes per (64-token chunk, value head) record
+    rec = 13 * 1024  # bytes per (64-token chunk, value head) record, 16-bit inputs
+    rec32 = 19 * 1024  # float32 inputs: Tb's low part as well
     tail = 4096      # float32 inputs' range scale and its partial maxima
     # B*T tokens in N sequences: floor(B*T / 64) + N + 1 chunk records per value head
-    assert lib.pbgdn_chunk_workspace_size(1, 32768, 32, 1) == (512 + 2) * 32 * rec + tail
-    assert lib.pbgdn_chunk_workspace_size(1, 262144, 32, 8) == (4096 + 9) * 32 * rec + tail
-    assert lib.pbgdn_chunk_workspace_size(4, 100, 2, 4) == (6 + 5) * 2 * rec + tail
-    assert lib.pbgdn_chunk_workspace_size(1, 0, 4, 1) == 2 * 4 * rec + tail
-    assert lib.pbgdn_chunk_workspace_size(-1, 10, 4, 1) == 0
-    assert lib.pbgdn_chunk_workspace_size(1, 10, 0, 1) == 0
+    for dt in (_lib.BF16, _lib.F16):
+        assert lib.pbgdn_chunk_workspace_size(1, 32768, 32, 1, dt) == (512 + 2) * 32 * rec + tail
+        assert lib.pbgdn_chunk_workspace_size(1, 262144, 32, 8, dt) == (4096 + 9) * 32 * rec + tail
+        assert lib.pbgdn_chunk_workspace_size(4, 100, 2, 4, dt) == (6 + 5) * 2 * rec + tail
+        assert lib.pbgdn_chunk_workspace_size(1, 0, 4, 1, dt) == 2 * 4 * rec + tail
+    assert lib.pbgdn_chunk_workspace_size(1, 2048, 4, 1, _lib.F32) == (32 + 2) * 4 * rec32 + tail
+    assert lib.pbgdn_chunk_workspace_size(-1, 10, 4, 1, _lib.BF16) == 0
+    assert lib.pbgdn_chunk_workspace_size(1, 10, 0, 1, _lib.BF16) == 0
+    assert lib.pbgdn_chunk_workspace_size(1, 10, 4, 1, 7) == 0  # dtype code
 
 
 CH = 2 * 16 * 128 + 32 * 128  # q, k, v channels of the Qwen3-Next layer

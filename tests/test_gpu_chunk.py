@@ -44,7 +44,9 @@ def test_prefill_small_fp32_inputs():
     o, s = gd.gated_delta_rule(*to_dev(q, k, v, g, beta), 64 ** -0.5, h0.to(DEV), kernel="chunked")
     torch.cuda.synchronize()
     assert o.dtype == torch.float32 and s.dtype == torch.float32
-    assert_parity("prefill_small", o, o_ref, s, s_ref)
+    # U = Tb X from fp16 high/low pairs for float32 inputs: S 2.9e-4 (6.6e-4 with
+    # single fp16 operands), held to half the 1e-3 bound
+    assert_parity("prefill_small", o, o_ref, s, s_ref, s_tol=5e-4)
 
 
 @pytest.mark.parametrize("length", [4096])

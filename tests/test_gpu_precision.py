@@ -54,6 +54,12 @@ def test_large_initial_state():
     assert_parity("h0 x 100", o, o_ref, s, s_ref)
 
 
+# float32 inputs form U = Tb X from fp16 high/low pairs: their state error
+# (1.6-3.3e-4 in these cases, 6.6-8.5e-4 with single fp16 operands) is held to
+# half the 1e-3 bound
+FP32_S_TOL = 5e-4
+
+
 @pytest.mark.parametrize("dk", [64, 128])
 def test_fp32_inputs_beyond_fp16_range(dk):
     """fp32 q, k, v (the reference CPU path's dtype) with |v| up to ~4e5."""
@@ -61,7 +67,7 @@ def test_fp32_inputs_beyond_fp16_range(dk):
     v = v * 1e5
     o, s = run(q, k, v, g, beta, dk ** -0.5, h0)
     o_ref, s_ref = oracle(q, k, v, g, beta, dk ** -0.5, h0)
-    assert_parity(f"fp32 |v|~1e5 K={dk}", o, o_ref, s, s_ref)
+    assert_parity(f"fp32 |v|~1e5 K={dk}", o, o_ref, s, s_ref, s_tol=FP32_S_TOL)
 
 
 def test_fp32_inputs_beyond_fp16_range_state_slots():
@@ -81,7 +87,7 @@ def test_fp32_inputs_beyond_fp16_range_state_slots():
     torch.cuda.synchronize()
     init = torch.stack([pool[4], pool[1], torch.zeros(4, 64, 64)])
     o_ref, s_ref = oracle(q, k, v, g, beta, 0.125, init, cu_seqlens=cu)
-    assert_parity("fp32 |v|~1e5 slots", o, o_ref, dpool.cpu()[[4, 1]], s_ref[:2])
+    assert_parity("fp32 |v|~1e5 slots", o, o_ref, dpool.cpu()[[4, 1]], s_ref[:2], s_tol=FP32_S_TOL)
     assert torch.equal(dpool.cpu()[[0, 2, 3, 5]], pool[[0, 2, 3, 5]])
 
 

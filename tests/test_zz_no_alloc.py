@@ -30,7 +30,7 @@ def call(noalloc, q, k, v, g, beta, h0, cu, hk, hv, dk, dv, scale):
     if noalloc:
         status = lib.pbgdn_chunk_fwd_noalloc(*common, stream)
     else:
-        ws_bytes = lib.pbgdn_chunk_workspace_size(batch, length, hv, nseq)
+        ws_bytes = lib.pbgdn_chunk_workspace_size(batch, length, hv, nseq, _lib.DTYPE_CODES[q.dtype])
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
         status = lib.pbgdn_chunk_fwd(*common, _lib.ptr(ws), ws_bytes, stream)
     _lib.check(status, "noalloc" if noalloc else "chunk_fwd")
@@ -74,7 +74,7 @@ def test_noalloc_refuses_a_call_beyond_its_scratch():
     dev = [x.to(DEV) for x in (q, k, v, g, beta, h0)]
     o = torch.zeros(1, 16384, 32, 128, dtype=torch.bfloat16, device=DEV)
     lib = _lib.lib()
-    assert lib.pbgdn_chunk_workspace_size(1, 16384, 32, 1) > _lib.NOALLOC_SCRATCH_BYTES
+    assert lib.pbgdn_chunk_workspace_size(1, 16384, 32, 1, _lib.BF16) > _lib.NOALLOC_SCRATCH_BYTES
     status = lib.pbgdn_chunk_fwd_noalloc(
         *(_lib.ptr(x) for x in dev[:3]), _lib.BF16, _lib.ptr(dev[3]), _lib.ptr(dev[4]), _lib.F32,
         _lib.ptr(dev[5]), None, _lib.F32, None, None, 0, None, 1, _lib.ptr(o), _lib.BF16, 1, 16384, 16, 32, 128,
