@@ -24,8 +24,9 @@ namespace pbgdn {
 namespace {
 
 constexpr int LNT = 256;       // threads per workgroup
-constexpr int TT = 128;        // prologue tokens per workgroup
-constexpr int TPL = TT / 16;   // tokens per lane row
+constexpr int UPW = 16;        // prologue: 8-channel units per workgroup (lanes of a lane row)
+constexpr int TPL = 8;         // prologue: tokens per lane row
+constexpr int TT = LNT / UPW * TPL;  // prologue tokens per workgroup
 constexpr int MAX_CONV = 4;          // widest filter with a kernel
 
 // Eight consecutive elements starting at element i of a tensor of `dtype`
@@ -185,6 +186,9 @@ struct PrologueParams {
   // tail_cs == conv-1), both 16-byte aligned in 8-element pieces, so a
   // lane's eight channels move in whole vectors; 0: element by element.
   int tail_vec;
+  // The gate rows take eight heads per lane in 16-byte pieces (Hv % 8 == 0,
+  // decay, g and beta 16-byte aligned, decay rows in 8-element steps).
+  bool gate_vec;
 };
 
 // Where a lane's eight channels go: q, k (L2-normalised over the key head,
@@ -196,45 +200,104 @@ struct OutLane {
   void *ptr;
   long step, col;
   __device__ __forceinline__ OutLane(const PrologueParams &p, int u, int c0) {
+    // channel c0 of a part is element c0 of its [heads x width] token row
     const int qk_units = p.Hk * p.K / 8;
-    int head, off;
-    if (u < qk_units) {
-      kind = 0;
-      head = c0 / p.K;
-      off = c0 % p.K;
-    } else if (u < 2 * qk_units) {
-      kind = 1;
-      head = (c0 - 8 * qk_units) / p.K;
-      off = (c0 - 8 * qk_units) % p.K;
-    } else {
-      kind = 2;
-      head = (c0 - 16 * qk_units) / p.V;
-      off = (c0 - 16 * qk_units) % p.V;
-    }
+    kind = u < qk_units ? 0 : u < 2 * qk_units ? 1 : 2;
+    col = c0 - 8L * qk_units * kind;
     head_lanes = p.K / 8;
     const int width = kind < 2 ? p.K : p.V;
     ptr = kind == 0 ? p.q : kind == 1 ? p.k : p.v;
     step = static_cast<long>(kind < 2 ? p.Hk : p.Hv) * width;
-    col = static_cast<long>(head) * width + off;
   }
-  // y = SiLU(conv) of one token: the q/k norm (every lane of the row takes
-  // part in its sum), then the store at element i when `store`.
+  // y = SiLU(conv) of one token: the q/k norm (every lane of a head's group
+  // takes part in its sum; the q/k boundary is a multiple of the group, so
+  // whole groups take the branch), then the store at element i when `store`.
+  template <bool STREAM = false>
   __device__ __forceinline__ bool finish(const PrologueParams &p, float (&y)[8], bool store, long i) const {
-    float ss = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ss += y[e] * y[e];
-    ss = group_sum(ss, head_lanes);  // DPP: a shuffle's LDS trip and wait per step sat on every token's path
-    if (!store) return false;
     if (kind < 2) {
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += y[e] * y[e];
+      ss = group_sum(ss, head_lanes);  // DPP: a shuffle's LDS trip and wait per step sat on every token's path
+      // 1 / max(sqrt(ss), eps) ('max') or 1 / sqrt(ss + eps) ('hf') on
+      // v_rsq_f32 (1 ulp): the IEEE-exact square root and division cost ~30
+      // VALU operations a token
       constexpr float l2_eps = 1e-6f;
-      const float n = p.l2_mode == 0 ? 1.f / fmaxf(sqrtf(ss), l2_eps) : rsqrtf(ss + l2_eps);
+      const float n = p.l2_mode == 0 ? (ss >= l2_eps * l2_eps ? __builtin_amdgcn_rsqf(ss) : 1.f / l2_eps)
+                                     : __builtin_amdgcn_rsqf(ss + l2_eps);
 #pragma unroll
       for (int e = 0; e < 8; ++e) y[e] *= n;
     }
-    store8(ptr, i, p.out_dtype, y);
+    if (!store) return false;
+    store8<STREAM>(ptr, i, p.out_dtype, y);
     return true;
   }
 };
+
+// Gates of a token tile, g = -exp(A_log) softplus(a + dt_bias) and
+// beta = sigmoid(b), eight heads per lane: every lane's a and b pieces of a
+// round are loaded before any is used, and g and beta leave in 16-byte
+// stores. Rows past the tile's end read zeros and store nothing.
+template <typename TIn, bool STREAM>
+__device__ __forceinline__ void tile_gates_vec(const PrologueParams &p, int b, int t_tile, int tid) {
+  constexpr int GU = 4;  // 8-head units per lane per round
+  const int hu = p.Hv / 8;
+  const int rows = min(TT, p.T - t_tile);
+  const int n = rows * hu;
+  const long row0 = static_cast<long>(b) * p.T + t_tile;
+  const auto rd = rsrc(static_cast<const TIn *>(p.decay) + row0 * p.decay_stride,
+                       (static_cast<long>(rows - 1) * p.decay_stride + 2L * p.Hv) * static_cast<long>(sizeof(TIn)));
+  for (int i0 = 0; i0 < n; i0 += GU * LNT) {
+    Raw8 ra[GU], rb[GU];
+#pragma unroll
+    for (int j = 0; j < GU; ++j) {
+      const int i = i0 + tid + j * LNT;
+      const int t = i / hu, hh = i - (i / hu) * hu;
+      const uint32_t off = static_cast<uint32_t>((static_cast<long>(t) * p.decay_stride + 8 * hh) * sizeof(TIn));
+      ra[j] = load_raw8<sizeof(TIn) == 4, STREAM>(rd, i < n ? off : OUT_OF_RANGE);
+      rb[j] = load_raw8<sizeof(TIn) == 4, STREAM>(
+          rd, i < n ? off + static_cast<uint32_t>(p.Hv * sizeof(TIn)) : OUT_OF_RANGE);
+    }
+#pragma unroll
+    for (int j = 0; j < GU; ++j) {
+      const int i = i0 + tid + j * LNT;
+      if (i >= n) continue;
+      const int t = i / hu, hh = i - (i / hu) * hu;
+      float a[8], bb[8];
+      decode8<TIn>(ra[j], a);
+      decode8<TIn>(rb[j], bb);
+      float gv[8], bv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int h = 8 * hh + e;
+        gv[e] = -exp_fast(p.a_log[h]) * softplus_fast(a[e] + p.dt_bias[h]);
+        bv[e] = sigmoid_fast(bb[e]);
+      }
+      const long o = (row0 + t) * p.Hv + 8 * hh;
+      put16<STREAM>(reinterpret_cast<float4_t *>(p.g + o), float4_t{gv[0], gv[1], gv[2], gv[3]});
+      put16<STREAM>(reinterpret_cast<float4_t *>(p.g + o + 4), float4_t{gv[4], gv[5], gv[6], gv[7]});
+      put16<STREAM>(reinterpret_cast<float4_t *>(p.beta + o), float4_t{bv[0], bv[1], bv[2], bv[3]});
+      put16<STREAM>(reinterpret_cast<float4_t *>(p.beta + o + 4), float4_t{bv[4], bv[5], bv[6], bv[7]});
+    }
+  }
+}
+
+// Gates of a token tile, one element per thread and step (the general form
+// of tile_gates_vec).
+template <typename TIn>
+__device__ __forceinline__ void tile_gates(const PrologueParams &p, int b, int t_tile, int tid) {
+  constexpr int IN = dtype_of<TIn>();
+  const int n = min(TT, p.T - t_tile) * p.Hv;
+  for (int i = tid; i < n; i += LNT) {
+    const int t = t_tile + i / p.Hv;
+    const int h = i % p.Hv;
+    const long row = static_cast<long>(b) * p.T + t;
+    const float a = load_elem(p.decay, row * p.decay_stride + h, IN);
+    const float bb = load_elem(p.decay, row * p.decay_stride + p.Hv + h, IN);
+    p.g[row * p.Hv + h] = -exp_fast(p.a_log[h]) * softplus_fast(a + p.dt_bias[h]);
+    p.beta[row * p.Hv + h] = sigmoid_fast(bb);
+  }
+}
 
 // CONV is the filter width (0: SiLU only). Every input row a lane needs (its
 // TPL tokens and the CONV-1 before them) is loaded before any is used, so the
@@ -242,30 +305,24 @@ struct OutLane {
 // sequence's start read zeros: the first CONV-1 tokens of every sequence
 // (batch row or packed sequence) are redone against the sequence's own tail by
 // edge_kernel, which also writes the new tails, so this pass reads and writes
-// no tail and needs no per-token sequence lookup.
-template <int CONV, typename TIn>
+// no tail and needs no per-token sequence lookup. STREAM: non-temporal stores
+// and gate loads (a call moving more bytes than the caches hold).
+template <int CONV, typename TIn, bool STREAM>
 __global__ __launch_bounds__(LNT) void prologue_kernel(PrologueParams p) {
-  constexpr int IN = dtype_of<TIn>();
   constexpr int HALO = CONV > 1 ? CONV - 1 : 0;  // rows before a lane's first token
   const int tid = threadIdx.x;
   const int b = blockIdx.z;
   const int t_tile = blockIdx.y * TT;
   if (static_cast<int>(blockIdx.x) >= p.ch_blocks) {
-    // Gates of the tile: g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b).
-    const int n = min(TT, p.T - t_tile) * p.Hv;
-    for (int i = tid; i < n; i += LNT) {
-      const int t = t_tile + i / p.Hv;
-      const int h = i % p.Hv;
-      const long row = static_cast<long>(b) * p.T + t;
-      const float a = load_elem(p.decay, row * p.decay_stride + h, IN);
-      const float bb = load_elem(p.decay, row * p.decay_stride + p.Hv + h, IN);
-      p.g[row * p.Hv + h] = -expf(p.a_log[h]) * softplusf(a + p.dt_bias[h]);
-      p.beta[row * p.Hv + h] = sigmoidf(bb);
+    if (p.gate_vec) {
+      tile_gates_vec<TIn, STREAM>(p, b, t_tile, tid);
+    } else {
+      tile_gates<TIn>(p, b, t_tile, tid);
     }
     return;
   }
-  const int u = blockIdx.x * 16 + (tid & 15);   // this lane's 8-channel unit
-  const int tl = tid >> 4;                       // lane row: tokens tl*TPL ..
+  const int u = blockIdx.x * UPW + tid % UPW;   // this lane's 8-channel unit
+  const int tl = tid / UPW;                      // lane row: tokens tl*TPL ..
   const int t_first = t_tile + tl * TPL;
   if (t_first >= p.T) return;  // the whole 16-lane row: no tokens (no shuffle partner is lost)
   const bool live = u < p.units;
@@ -284,18 +341,20 @@ __global__ __launch_bounds__(LNT) void prologue_kernel(PrologueParams p) {
                        (static_cast<long>(end_row - 1 - base_row) * p.qkv_stride + chans) *
                            static_cast<long>(sizeof(TIn)));
   Raw8 raw[HALO + TPL];  // rows t_first - HALO ..
+  // row m at off0 + m row strides (a scalar step: one add per row); the
+  // inputs are loaded cacheable, since neighbouring lane rows and tiles read
+  // each other's halo rows
+  const uint32_t row_bytes = static_cast<uint32_t>(p.qkv_stride * sizeof(TIn));
+  const uint32_t off0 = static_cast<uint32_t>(t_first - HALO - base_row) * row_bytes + c0 * sizeof(TIn);
 #pragma unroll
   for (int m = 0; m < HALO + TPL; ++m) {
     const int t = t_first - HALO + m;
-    const uint32_t off = live && t >= 0 && t < p.T
-                             ? (static_cast<uint32_t>(t - base_row) * static_cast<uint32_t>(p.qkv_stride) + c0) *
-                                   sizeof(TIn)
-                             : OUT_OF_RANGE;
+    const uint32_t off = live && t >= 0 && t < p.T ? off0 + m * row_bytes : OUT_OF_RANGE;
     raw[m] = load_raw8<sizeof(TIn) == 4>(rq, off);
   }
-  float xr[HALO + TPL][8];
+  float xr[HALO + TPL][8];  // decoded as the token loop reaches them (fewer live registers)
 #pragma unroll
-  for (int m = 0; m < HALO + TPL; ++m) decode8<TIn>(raw[m], xr[m]);
+  for (int m = 0; m < HALO; ++m) decode8<TIn>(raw[m], xr[m]);
   float w[8][CONV > 0 ? CONV : 1];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -307,6 +366,7 @@ __global__ __launch_bounds__(LNT) void prologue_kernel(PrologueParams p) {
 #pragma unroll
   for (int i = 0; i < TPL; ++i) {
     const int t = t_first + i;
+    decode8<TIn>(raw[HALO + i], xr[HALO + i]);
     float y[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -315,19 +375,32 @@ __global__ __launch_bounds__(LNT) void prologue_kernel(PrologueParams p) {
       for (int j = 0; j < CONV; ++j) acc += w[e][j] * xr[HALO + i - (CONV - 1) + j][e];  // tap j: row t-(CONV-1)+j
       y[e] = siluf(acc);
     }
-    out.finish(p, y, live && t < p.T, out0 + i * out.step);
+    out.template finish<STREAM>(p, y, live && t < p.T, out0 + i * out.step);
   }
 }
 
+// A call moving more bytes than this (inputs in, outputs out) streams them
+// with non-temporal hints; smaller calls keep them cacheable, since their
+// inputs were most likely just written and their outputs are read next.
+constexpr long STREAM_BYTES = 192L << 20;
+
+template <typename TIn, bool STREAM>
+void launch_prologue_s(int conv, dim3 grid, hipStream_t st, const PrologueParams &prm) {
+  switch (conv) {
+    case 0: hipLaunchKernelGGL((prologue_kernel<0, TIn, STREAM>), grid, dim3(LNT), 0, st, prm); break;
+    case 1: hipLaunchKernelGGL((prologue_kernel<1, TIn, STREAM>), grid, dim3(LNT), 0, st, prm); break;
+    case 2: hipLaunchKernelGGL((prologue_kernel<2, TIn, STREAM>), grid, dim3(LNT), 0, st, prm); break;
+    case 3: hipLaunchKernelGGL((prologue_kernel<3, TIn, STREAM>), grid, dim3(LNT), 0, st, prm); break;
+    default: hipLaunchKernelGGL((prologue_kernel<4, TIn, STREAM>), grid, dim3(LNT), 0, st, prm); break;
+  }
+}
 template <typename TIn>
 void launch_prologue(int conv, dim3 grid, hipStream_t st, const PrologueParams &prm) {
-  switch (conv) {
-    case 0: hipLaunchKernelGGL((prologue_kernel<0, TIn>), grid, dim3(LNT), 0, st, prm); break;
-    case 1: hipLaunchKernelGGL((prologue_kernel<1, TIn>), grid, dim3(LNT), 0, st, prm); break;
-    case 2: hipLaunchKernelGGL((prologue_kernel<2, TIn>), grid, dim3(LNT), 0, st, prm); break;
-    case 3: hipLaunchKernelGGL((prologue_kernel<3, TIn>), grid, dim3(LNT), 0, st, prm); break;
-    default: hipLaunchKernelGGL((prologue_kernel<4, TIn>), grid, dim3(LNT), 0, st, prm); break;
-  }
+  const long in_elem = sizeof(TIn), out_elem = prm.out_dtype == PBGDN_F32 ? 4 : 2;
+  const long bytes = static_cast<long>(prm.B) * prm.T *
+                     (8L * prm.units * (in_elem + out_elem) + 2L * prm.Hv * (in_elem + 4));
+  bytes > STREAM_BYTES ? launch_prologue_s<TIn, true>(conv, grid, st, prm)
+                       : launch_prologue_s<TIn, false>(conv, grid, st, prm);
 }
 
 // After the prologue: thread (unit u, sequence s) redoes tokens 0 .. CONV-2
@@ -368,8 +441,16 @@ __global__ __launch_bounds__(LNT) void edge_kernel(PrologueParams p) {
                                       : OUT_OF_RANGE;
   };
   float old[TAIL][8], x[TAIL][8];  // the old tail; the sequence's first TAIL inputs
+  // every input row this thread reads is loaded before any store (the stores
+  // may alias the inputs for all the compiler knows, so a later load would
+  // wait for them): the first TAIL rows, then the last TAIL (row r of the new
+  // tail is row len + r of (old tail ++ inputs): input row len + r - TAIL,
+  // out of range when that is an old tail row)
+  Raw8 last[TAIL];
 #pragma unroll
   for (int j = 0; j < TAIL; ++j) decode8<TIn>(load_raw8<sizeof(TIn) == 4>(r_head, row_off(j)), x[j]);
+#pragma unroll
+  for (int r = 0; r < TAIL; ++r) last[r] = load_raw8<sizeof(TIn) == 4>(r_last, row_off(len + r - TAIL - last0));
   const bool from_pool = live && slot >= 0 && slot < p.num_slots && !(p.has_initial && !p.has_initial[s]);
   if (!from_pool) {
 #pragma unroll
@@ -430,7 +511,7 @@ __global__ __launch_bounds__(LNT) void edge_kernel(PrologueParams p) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) nt[r][k] = old[e < TAIL ? e : 0][k];
     } else {
-      decode8<TIn>(load_raw8<sizeof(TIn) == 4>(r_last, row_off(e - TAIL - last0)), nt[r]);
+      decode8<TIn>(last[r], nt[r]);
     }
   }
   if (p.tail_vec == 1) {
@@ -489,10 +570,6 @@ struct EpilogueParams {
 // g, g + G, ... (G = groups per workgroup); all loads issue before any use.
 constexpr int EPI_ROWS = 1;
 
-// A call moving more bytes than this (o and gate in, the output out) streams
-// them with non-temporal hints; smaller calls keep them cacheable, since their
-// o was most likely just written by the scan and is still in the caches.
-constexpr long EPILOGUE_STREAM_BYTES = 192L << 20;
 
 template <typename TO, typename TG, int V, bool STREAM>
 __global__ __launch_bounds__(LNT) void epilogue_kernel(EpilogueParams p) {
@@ -553,7 +630,7 @@ void launch_epilogue_v(int gate_dtype, dim3 grid, hipStream_t st, const Epilogue
 template <typename TO>
 void launch_epilogue(int gate_dtype, dim3 grid, hipStream_t st, const EpilogueParams &prm) {
   const long elem_out = prm.out_dtype == PBGDN_F32 ? 4 : 2, elem_gate = gate_dtype == PBGDN_F32 ? 4 : 2;
-  const bool stream = prm.rows * prm.V * (static_cast<long>(sizeof(TO)) + elem_gate + elem_out) > EPILOGUE_STREAM_BYTES;
+  const bool stream = prm.rows * prm.V * (static_cast<long>(sizeof(TO)) + elem_gate + elem_out) > STREAM_BYTES;
   if (prm.V == 64) {
     stream ? launch_epilogue_v<TO, 64, true>(gate_dtype, grid, st, prm)
            : launch_epilogue_v<TO, 64, false>(gate_dtype, grid, st, prm);
@@ -565,6 +642,12 @@ void launch_epilogue(int gate_dtype, dim3 grid, hipStream_t st, const EpiloguePa
 
 bool valid_dtype(int d) { return d == PBGDN_F32 || d == PBGDN_BF16 || d == PBGDN_F16; }
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+// The gate rows move in 16-byte pieces of eight heads: tile_gates_vec's
+// conditions, and its 32-bit offsets within a tile's decay rows.
+bool gates_vectorize(const void *decay, long decay_stride, long in_elem, const float *g, const float *beta, int Hv) {
+  return Hv % 8 == 0 && decay_stride % 8 == 0 && aligned16(decay) && aligned16(g) && aligned16(beta) &&
+         static_cast<long>(TT) * decay_stride * in_elem <= 0x7ffffff0L - 64;
+}
 
 }  // namespace
 }  // namespace pbgdn
@@ -602,8 +685,9 @@ extern "C" int pbgdn_prologue_fwd(const void *qkv, long qkv_stride, const void *
   if (channels / 8 > 0x7fffffffL / 16 || static_cast<long>(T) + TT > 0x7fffffffL) return PBGDN_ERR_UNSUPPORTED;
   PrologueParams prm{qkv, decay, tail, tail_out, conv_weight, a_log, dt_bias, q, k, v, g, beta, qkv_stride,
                      decay_stride, in_dtype, tail_dtype, out_dtype, B, T, Hk, Hv, K, V, conv, l2_mode,
-                     static_cast<int>(channels / 8), static_cast<int>((channels / 8 + 15) / 16),
-                     nullptr, nullptr, nullptr, B, B, (conv - 1) * channels, channels, 1, 1};
+                     static_cast<int>(channels / 8), static_cast<int>((channels / 8 + UPW - 1) / UPW),
+                     nullptr, nullptr, nullptr, B, B, (conv - 1) * channels, channels, 1, 1, false};
+  prm.gate_vec = gates_vectorize(decay, decay_stride, in_elem, g, beta, Hv);
   const dim3 grid(prm.ch_blocks + 1, (T + TT - 1) / TT, B);
   if (grid.y > 0x7fffffffu || B > 65535 || grid.y > 65535u) return PBGDN_ERR_UNSUPPORTED;
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -648,9 +732,10 @@ extern "C" int pbgdn_prologue_varlen_fwd(const void *qkv, long qkv_stride, const
   if (channels / 8 > 0x7fffffffL / 16 || static_cast<long>(T) + TT > 0x7fffffffL) return PBGDN_ERR_UNSUPPORTED;
   PrologueParams prm{qkv, decay, tail, tail_out, conv_weight, a_log, dt_bias, q, k, v, g, beta, qkv_stride,
                      decay_stride, in_dtype, tail_dtype, out_dtype, 1, T, Hk, Hv, K, V, conv, l2_mode,
-                     static_cast<int>(channels / 8), static_cast<int>((channels / 8 + 15) / 16), cu_seqlens,
+                     static_cast<int>(channels / 8), static_cast<int>((channels / 8 + UPW - 1) / UPW), cu_seqlens,
                      slot_idx, has_initial_state, num_seqs, num_slots, tail_slot_stride, tail_row_stride,
-                     tail_chan_stride, 0};
+                     tail_chan_stride, 0, false};
+  prm.gate_vec = gates_vectorize(decay, decay_stride, in_elem, g, beta, Hv);
   if (has_tail && tail_slot_stride % 8 == 0 && aligned16(tail) && aligned16(tail_out)) {
     if (tail_chan_stride == 1 && tail_row_stride % 8 == 0) prm.tail_vec = 1;
     if (tail_row_stride == 1 && tail_chan_stride == conv - 1) prm.tail_vec = 2;
