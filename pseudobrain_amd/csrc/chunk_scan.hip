@@ -744,10 +744,22 @@ struct ScanBlock {
     block_sync();
   }
 
+  // Four output elements as one LDS store (8 bytes for 16-bit outputs).
+  __device__ __forceinline__ void put_out4(uint32_t off, float4_t o) const {
+    if constexpr (sizeof(TOut) == 4) {
+      st(off, o);
+    } else {
+      typedef TOut out4_t __attribute__((ext_vector_type(4)));
+      st(off, out4_t{out_elem<TOut>(o[0]), out_elem<TOut>(o[1]), out_elem<TOut>(o[2]), out_elem<TOut>(o[3])});
+    }
+  }
+
   // Output waves: O = scale gamma Q S + QKD U of the chunk of parity ob (its
-  // U^T is in U^T buffer ob) -> O tile ob; lane (g, c) holds
-  // O[16 r + 4 g + i][c].
-  __device__ __forceinline__ void out_tile(int ob, const float4_t &qs, const float4_t &gs, const half8_t &f0,
+  // U^T is in U^T buffer ob) -> O tile ob. The products are formed
+  // transposed (the operands' fragments swap roles, the same registers), so
+  // lane (g, c) holds O[16 r + c][4 g + i], four consecutive columns of one
+  // token: one LDS store of them instead of four, 512 contiguous bytes per wave.
+  __device__ __forceinline__ void out_tile(int ob, const float4_t &qs, float gs, const half8_t &f0,
                                            const half8_t &f1) {
     const int r = wave & 3;
     // U^T of the chunk holds U d (d its range scale, usually 1): O = (scale gamma Q S d + QKD U d) / d
@@ -756,20 +768,19 @@ struct ScanBlock {
     float4_t o = qs * gs;
     if (d < 1.f) o *= d;
     // no branch between the products and their first reads
-    o = mfma32(f0, ld<half8_t>(L::ut(ob) + sp_frag), o);
-    o = mfma32(f1, ld<half8_t>(L::ut(ob) + sp_frag + 64), o);
+    o = mfma32(ld<half8_t>(L::ut(ob) + sp_frag), f0, o);
+    o = mfma32(ld<half8_t>(L::ut(ob) + sp_frag + 64), f1, o);
     o *= rd;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) st(L::ot(ob) + ((16 * r + 4 * g4 + i) * VT + c16) * sizeof(TOut), out_elem<TOut>(o[i]));
+    put_out4(L::ot(ob) + ((16 * r + c16) * VT + 4 * g4) * sizeof(TOut), o);
   }
 
-  // Output waves. Phase 1: Q S (high part) of chunk n. Phase 2: O of chunk
-  // n-1, then this chunk's QKD fragments and scale gamma rows (for its O in
-  // the next tick); K^T for phase 3. Phase 3: the state update (K = 128),
-  // then the Q rows of the next chunk.
+  // Output waves. Phase 1: (Q S)^T (high part) of chunk n. Phase 2: O of
+  // chunk n-1, then this chunk's QKD fragments and its lane's scale gamma
+  // (for its O in the next tick); K^T for phase 3. Phase 3: the state update
+  // (K = 128), then the Q rows of the next chunk.
   template <int P>
   __device__ __forceinline__ void tick_output(long n, O8 (&mf)[KS], float4_t &qs, float4_t &qs_prev,
-                                              float4_t &gs, half8_t &f0, half8_t &f1) {
+                                              float &gs, half8_t &f0, half8_t &f1) {
     launder();
     const int b = P;
     const int r = wave & 3;
@@ -780,7 +791,7 @@ struct ScanBlock {
       for (int kk = 0; kk < KS; ++kk) shi[kk] = ld<O8>(L::SH + kp_frag + 64 * kk);
       float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kk = 0; kk < KS; ++kk) acc = mma(mf[kk], shi[kk], acc);
+      for (int kk = 0; kk < KS; ++kk) acc = mma(shi[kk], mf[kk], acc);  // (Q S)^T: columns 4 g.., token c
       qs_prev = qs;
       qs = acc;
     }
@@ -788,7 +799,7 @@ struct ScanBlock {
     {
       const half8_t n0 = rec_frag(b, REC_QKD, r, 0);
       const half8_t n1 = second_step(rec_frag(b, REC_QKD, r, 1), r);
-      const float4_t ngs = rec_rows(b, SC_GSC, r);
+      const float ngs = ld<float>(L::rec(b) + REC_SC + SC_GSC + (16 * r + c16) * 4);
       if constexpr (NKT > 4) fetch_kt(b, kt);
       if (n > 0) out_tile(b ^ 1, qs_prev, gs, f0, f1);
       f0 = n0;
@@ -922,7 +933,8 @@ struct ScanBlock {
     } else {
       O8 mf[KS];
       fetch_rows(0, 1, mf);
-      float4_t qs = {0.f, 0.f, 0.f, 0.f}, qs_prev = qs, gs = qs;
+      float4_t qs = {0.f, 0.f, 0.f, 0.f}, qs_prev = qs;
+      float gs = 0.f;
       half8_t f0 = {}, f1 = {};
       long n = 0;
       for (; n + 1 < nchunks; n += 2) {
