@@ -6,6 +6,7 @@ A missing or stale library raises; there is no fallback.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -13,6 +14,8 @@ import threading
 import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpbgdn.so")
+# The debug build of the same sources (build.py): LDS and outputs poisoned with NaN.
+DEBUG_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpbgdn_debug.so")
 ABI_VERSION = 13
 
 F32, BF16, F16 = 0, 1, 2
@@ -66,6 +69,22 @@ class PbgdnError(RuntimeError):
         super().__init__(f"{where}: pbgdn status {status}: {status_string(status)}")
 
 
+def _load(path: str) -> ctypes.CDLL:
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"pbgdn HIP library not found at {path}; build it with "
+            "`python -m pseudobrain_amd.build` (there is no CPU fallback)")
+    handle = ctypes.CDLL(path)
+    for name, (args, res) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.argtypes = args
+        fn.restype = res
+    version = handle.pbgdn_abi_version()
+    if version != ABI_VERSION:
+        raise RuntimeError(f"{os.path.basename(path)} ABI version {version}, expected {ABI_VERSION}; rebuild it")
+    return handle
+
+
 def lib() -> ctypes.CDLL:
     """The loaded library; raises RuntimeError when it is not built."""
     global _lib
@@ -73,20 +92,29 @@ def lib() -> ctypes.CDLL:
         return _lib
     with _lock:
         if _lib is None:
-            if not os.path.exists(LIB_PATH):
-                raise RuntimeError(
-                    f"pbgdn HIP library not found at {LIB_PATH}; build it with "
-                    "`python -m pseudobrain_amd.build` (there is no CPU fallback)")
-            handle = ctypes.CDLL(LIB_PATH)
-            for name, (args, res) in SIGNATURES.items():
-                fn = getattr(handle, name)
-                fn.argtypes = args
-                fn.restype = res
-            version = handle.pbgdn_abi_version()
-            if version != ABI_VERSION:
-                raise RuntimeError(f"libpbgdn.so ABI version {version}, expected {ABI_VERSION}; rebuild it")
-            _lib = handle
+            _lib = _load(LIB_PATH)
     return _lib
+
+
+_debug: ctypes.CDLL | None = None
+
+
+@contextlib.contextmanager
+def debug_library():
+    """Within the block every call of this package goes to libpbgdn_debug.so,
+    whose kernels fill their LDS with NaN before use and whose entry points
+    fill their outputs and workspaces with NaN before launching (a test aid:
+    an unwritten output element or a read of unwritten LDS then shows as NaN).
+    Not thread-safe: the other library is restored on exit."""
+    global _lib, _debug
+    prev = lib()
+    if _debug is None:
+        _debug = _load(DEBUG_LIB_PATH)
+    _lib = _debug
+    try:
+        yield _debug
+    finally:
+        _lib = prev
 
 
 def status_string(status: int) -> str:

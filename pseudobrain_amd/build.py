@@ -19,6 +19,11 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(PKG, "libpbgdn.so")
+# The debug build (-DPBGDN_DEBUG): every kernel fills its LDS with NaN before
+# use, and the entry points fill their outputs and workspaces with NaN before
+# launching, so that a read of unwritten LDS or an output element no kernel
+# writes shows as NaN (tests/test_gpu_debug_canaries.py).
+DEBUG_LIB = os.path.join(PKG, "libpbgdn_debug.so")
 SOURCES = ("abi.hip", "recurrent.hip", "chunk.hip", "chunk_prep.hip", "chunk_scan.hip", "chunk_wide.hip",
            "chunk_bwd.hip",
            "layer.hip", "decode_layer.hip", "device.hip")
@@ -48,21 +53,28 @@ def _run(cmd):
 
 
 def build(verbose: bool = False) -> str:
-    """Compile every source and link libpbgdn.so; returns its path."""
-    objdir = os.path.join(PKG, "_build")
-    os.makedirs(objdir, exist_ok=True)
+    """Compile every source and link libpbgdn.so and libpbgdn_debug.so; returns
+    the path of the first."""
     cc = hipcc()
+    libs = []  # (library, objects)
     jobs = []
-    for src in SOURCES:
-        obj = os.path.join(objdir, src.replace(".hip", ".o"))
-        jobs.append((obj, [cc, *HIPCC_FLAGS, f"-I{INCLUDE}", "-c", os.path.join(CSRC, src), "-o", obj]))
-    with ThreadPoolExecutor(max_workers=len(jobs)) as pool:
-        for proc in pool.map(lambda job: _run(job[1]), jobs):
+    for lib, objdir, extra in ((LIB, "_build", []), (DEBUG_LIB, "_build_debug", ["-DPBGDN_DEBUG"])):
+        objdir = os.path.join(PKG, objdir)
+        os.makedirs(objdir, exist_ok=True)
+        objs = []
+        for src in SOURCES:
+            obj = os.path.join(objdir, src.replace(".hip", ".o"))
+            objs.append(obj)
+            jobs.append([cc, *HIPCC_FLAGS, *extra, f"-I{INCLUDE}", "-c", os.path.join(CSRC, src), "-o", obj])
+        libs.append((lib, objs))
+    with ThreadPoolExecutor(max_workers=min(len(jobs), os.cpu_count() or 8)) as pool:
+        for proc in pool.map(_run, jobs):
             if verbose and proc.stderr:
                 sys.stderr.write(proc.stderr)
-    tmp = LIB + ".tmp"
-    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *(obj for obj, _ in jobs)])
-    os.replace(tmp, LIB)
+    for lib, objs in libs:
+        tmp = lib + ".tmp"
+        _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
+        os.replace(tmp, lib)
     return LIB
 
 

@@ -154,6 +154,9 @@ struct RangeParams {
 // Partial maxima of |v| and of |the initial states the call reads| (NaNs
 // are passed over; an infinity makes the scale 1).
 __global__ __launch_bounds__(256) void range_max_kernel(RangeParams p) {
+  __shared__ float wm[4];
+  PBGDN_POISON_LDS(wm, sizeof(wm));
+  PBGDN_POISON_SYNC();
   float m = 0.f;
   const long stride = static_cast<long>(gridDim.x) * 256;
   for (long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x; i < p.nv; i += stride) m = fmaxf(m, fabsf(p.v[i]));
@@ -169,7 +172,6 @@ __global__ __launch_bounds__(256) void range_max_kernel(RangeParams p) {
     }
   }
   m = wave_max(m);
-  __shared__ float wm[4];
   if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
   __syncthreads();
   if (threadIdx.x == 0) p.part[blockIdx.x] = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
@@ -255,6 +257,14 @@ extern "C" int pbgdn_chunk_fwd(const void *q, const void *k, const void *v, int 
                                     Hv, K, V, scale, chunk, workspace, workspace_bytes, p, records, empty);
   if (st != PBGDN_OK || empty) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  {  // debug builds: every element the call writes starts as NaN, so do the records the scan reads
+    const long esz = out_dtype == PBGDN_F32 ? 4 : 2, ssz = state_dtype == PBGDN_F32 ? 4 : 2;
+    pbgdn::debug_poison(o, static_cast<size_t>(static_cast<long>(B) * T * Hv * V * esz), s);
+    if (ht && ht != h0 && !state_idx) {
+      pbgdn::debug_poison(ht, static_cast<size_t>(static_cast<long>(num_seqs) * Hv * K * V * ssz), s);
+    }
+    pbgdn::debug_poison(workspace, workspace_bytes, s);
+  }
   if (in_dtype == PBGDN_F32) {  // the range scale of v and the initial states, into the workspace's tail
     float *part = reinterpret_cast<float *>(static_cast<unsigned char *>(workspace) +
                                             records * Hv * pbgdn::rec_bytes_of(PBGDN_F32));
@@ -313,12 +323,22 @@ extern "C" int pbgdn_chunk_layer_fwd(const void *q, const void *k, const void *v
       p.o_norm = o_norm;
       p.eps = eps;
       hipStream_t s = static_cast<hipStream_t>(stream);
+      {  // debug builds: the outputs start as NaN (as in pbgdn_chunk_fwd)
+        const long hsz = hs_dtype == PBGDN_F32 ? 4 : 2, ssz = state_dtype == PBGDN_F32 ? 4 : 2;
+        pbgdn::debug_poison(hs, static_cast<size_t>(static_cast<long>(B) * T * Hv * V * hsz), s);
+        if (ht && ht != h0 && !state_idx) {
+          pbgdn::debug_poison(ht, static_cast<size_t>(static_cast<long>(num_seqs) * Hv * K * V * ssz), s);
+        }
+        pbgdn::debug_poison(workspace, workspace_bytes, s);
+      }
       return in_dtype == PBGDN_BF16 ? pbgdn::run_chunk_epilogue<pbgdn::u16>(p, records, hs_dtype, s)
                                     : pbgdn::run_chunk_epilogue<pbgdn::half_t>(p, records, hs_dtype, s);
     }
   }
   // Two passes: o in the inputs' dtype, then the epilogue.
   if (!o || !aligned16(o)) return PBGDN_ERR_INVALID_ARGUMENT;
+  pbgdn::debug_poison(hs, static_cast<size_t>(static_cast<long>(B) * T * Hv * V * (hs_dtype == PBGDN_F32 ? 4 : 2)),
+                      static_cast<hipStream_t>(stream));
   const int st = pbgdn_chunk_fwd(q, k, v, in_dtype, g, beta, beta_dtype, h0, ht, state_dtype, state_idx,
                                  has_initial_state, num_states, cu_seqlens, num_seqs, o, in_dtype, B, T, Hk, Hv, K,
                                  V, scale, chunk, workspace, workspace_bytes, stream);

@@ -456,6 +456,8 @@ template <int K, int V, typename TIn>
 __global__ __launch_bounds__(BNT) void bwd_local_kernel(BwdParams p) {
   constexpr int PADE = 16 / sizeof(TIn), LK = K + PADE, LV = V + PADE;
   extern __shared__ __align__(16) float lds[];
+  PBGDN_POISON_LDS(lds, (local_lds<K, V, TIn>()));
+  PBGDN_POISON_SYNC();
   TIn *sq = reinterpret_cast<TIn *>(lds), *sk = sq + BC * LK, *sdo = sk + BC * LK;
   float *sa = reinterpret_cast<float *>(sdo + BC * LV);
   float *sc = sa + BC * LC, *sgam = sc + BC, *sbeta = sgam + BC, *sr = sbeta + BC;
@@ -1051,8 +1053,15 @@ __device__ __forceinline__ void adjoint_pass(const BwdParams &p, float *lds, int
 // fill the XCDs evenly all tiles of a pair are given indices on one XCD
 // (xcd_group) and those reads come from its L2 after the first.
 template <int K, typename TIn>
+constexpr size_t scan_lds();
+template <int K, typename TIn>
+constexpr size_t grad_lds();
+
+template <int K, typename TIn>
 __global__ __launch_bounds__(BNT) void bwd_scans_kernel(BwdParams p) {
   extern __shared__ __align__(16) float lds[];
+  PBGDN_POISON_LDS(lds, (scan_lds<K, TIn>()));
+  PBGDN_POISON_SYNC();
   const int tiles = p.V / 16, pairs = 2 * p.B * p.Hv;
   const int l = blockIdx.x;
   int pair, tile;
@@ -1092,6 +1101,8 @@ __global__ __launch_bounds__(GNT) void bwd_grad_kernel(BwdParams p) {
   // tiles as high + low parts); other input types on the fp32 MFMA
   constexpr bool BF = std::is_same<TIn, u16>::value;
   extern __shared__ __align__(16) float lds[];
+  PBGDN_POISON_LDS(lds, (grad_lds<K, TIn>()));
+  PBGDN_POISON_SYNC();
   constexpr int LB = BC + 8, LO = 16 + 8, PAIR = 2 * 16 * LB;
   // T and M: float rows of LC, or (bf16 inputs) bf16 high/low pairs of rows LB
   constexpr int TSZ = BF ? BC * LB : BC * LC;
@@ -1735,6 +1746,18 @@ extern "C" int pbgdn_chunk_bwd(const void *q, const void *k, const void *v, int 
   }
   float *ws = static_cast<float *>(workspace);
   const long recs = static_cast<long>(B) * Hv * n;
+  {  // debug builds: the gradients and the workspace start as NaN
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const long isz = in_dtype == PBGDN_F32 ? 4 : 2, bsz = beta_dtype == PBGDN_F32 ? 4 : 2;
+    const long bt = static_cast<long>(B) * T;
+    debug_poison(dq, static_cast<size_t>(bt * Hk * K * isz), s);
+    debug_poison(dk, static_cast<size_t>(bt * Hk * K * isz), s);
+    debug_poison(dv, static_cast<size_t>(bt * Hv * V * isz), s);
+    debug_poison(dg, static_cast<size_t>(bt * Hv * 4), s);
+    debug_poison(dbeta, static_cast<size_t>(bt * Hv * bsz), s);
+    debug_poison(dh0, static_cast<size_t>(static_cast<long>(B) * Hv * K * V * 4), s);
+    debug_poison(workspace, workspace_bytes, s);
+  }
   BwdParams p{};
   DeviceShape shape;
   if (!device_shape(shape)) return PBGDN_ERR_LAUNCH;

@@ -434,6 +434,8 @@ struct PrepBlock {
 template <int K, typename TIn>
 __global__ __launch_bounds__(PNT, prep_wg_per_cu<TIn>()) void prep_kernel(ChunkParams p, int items, int nt) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
+  PBGDN_POISON_LDS(smem_raw, (PrepLayout<K, sizeof(TIn) == 4>::BYTES));
+  PBGDN_POISON_SYNC();
   if constexpr (sizeof(TIn) == 4) {  // the range scale the scan reads (prep reads none of v)
     if (p.range_part && blockIdx.x == 0 && threadIdx.x < 64) {
       range_scale_wave(p.range_part, const_cast<float *>(p.in_scale));

@@ -332,6 +332,16 @@ struct ScanBlock {
   // Per-lane LDS byte offsets (see lane_offsets()).
   uint32_t kp_frag, sp_frag, kp_tile, sp_tile, tr_v, tr_k0, tr_k1;
 
+  // Debug builds: the barriers this wave has passed (audited at the end:
+  // every wave of the workgroup must pass the same number, whatever its role).
+  uint32_t nbar = 0;
+  __device__ __forceinline__ void sync() {
+    block_sync();
+#ifdef PBGDN_DEBUG
+    ++nbar;
+#endif
+  }
+
   __device__ __forceinline__ ScanBlock(unsigned char *l, const ChunkParams &prm) : lds(l), p(prm) {
     tid = threadIdx.x;
     lane = tid & 63;
@@ -683,7 +693,7 @@ struct ScanBlock {
       if constexpr (LO) st(L::xtl(b) + sp_tile + 32 * r, to_half4(x - to_float4(xh)));
       if (lane == 0) st(L::RS + 4 * r, down);
     }
-    block_sync();
+    sync();
     {
       const half8_t x0 = ld<half8_t>(L::XT + sp_frag);
       const half8_t x1 = ld<half8_t>(L::XT + sp_frag + 64);
@@ -728,7 +738,7 @@ struct ScanBlock {
       st(L::UH + o, hi);
       st(L::UL + o, Op::from(du - Op::to(hi)));
     }
-    block_sync();
+    sync();
     {
       O8 nmf[KS];
       fetch_rows(b ^ 1, 0, nmf);
@@ -741,7 +751,7 @@ struct ScanBlock {
       vv = nvv;
       gg = ngg;
     }
-    block_sync();
+    sync();
   }
 
   // Four output elements as one LDS store (8 bytes for 16-bit outputs).
@@ -795,7 +805,7 @@ struct ScanBlock {
       qs_prev = qs;
       qs = acc;
     }
-    block_sync();
+    sync();
     {
       const half8_t n0 = rec_frag(b, REC_QKD, r, 0);
       const half8_t n1 = second_step(rec_frag(b, REC_QKD, r, 1), r);
@@ -806,7 +816,7 @@ struct ScanBlock {
       f1 = n1;
       gs = ngs;
     }
-    block_sync();
+    sync();
     {
       O8 nmf[KS];
       fetch_rows(b ^ 1, 1, nmf);
@@ -817,7 +827,7 @@ struct ScanBlock {
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk) mf[kk] = nmf[kk];
     }
-    block_sync();
+    sync();
   }
 
   // Tick n of a loader wave: register set P (= n mod 2) holds chunk n+1 on
@@ -836,15 +846,15 @@ struct ScanBlock {
     const long len = len_of(lc);
     const unsigned char *rec = rec_of(lc);
     stage.template restage<0, Stage::SLOT_P2>(p, lds, L::kq(P ^ 1), regs[P], lt, t0, len, hk, h, v0, rec);
-    block_sync();
+    sync();
     stage.template restage<Stage::SLOT_P2, Stage::SLOT_P3>(p, lds, L::kq(P ^ 1), regs[P], lt, t0, len, hk, h, v0,
                                                             rec);
-    block_sync();
+    sync();
     store_out(n - 1);
     if (n > 0) advance(oc);
     stage.template restage<Stage::SLOT_P3, Stage::UPT>(p, lds, L::kq(P ^ 1), regs[P], lt, t0, len, hk, h, v0, rec);
     advance(lc);
-    block_sync();
+    sync();
   }
 
   // Chunks of the group's sequences, summed over the whole workgroup (one
@@ -865,11 +875,11 @@ struct ScanBlock {
     for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, 64);
     int *part = reinterpret_cast<int *>(lds + L::OT);  // the O tiles are not in use yet
     if (lane == 0) part[wave] = c;
-    block_sync();
+    sync();
     long total = 0;
 #pragma unroll
     for (int w = 0; w < NT / 64; ++w) total += part[w];
-    block_sync();
+    sync();
     return total;
   }
 
@@ -906,18 +916,18 @@ struct ScanBlock {
       load_chunk(regs[1], lc);
       advance(lc);
       store_out(-1);
-      block_sync();
+      sync();
       long n = 0;
       for (; n + 1 < nchunks; n += 2) {
         tick_loader<0>(n);
         tick_loader<1>(n + 1);
       }
       if (n < nchunks) tick_loader<0>(n);
-      block_sync();  // the O tile of the last chunk is complete
+      sync();  // the O tile of the last chunk is complete
       if (nchunks > 0) store_out(nchunks - 1);
       return;
     }
-    block_sync();
+    sync();
     if (wave < 4) {
       O8 mf[KS];
       fetch_rows(0, 0, mf);
@@ -929,7 +939,7 @@ struct ScanBlock {
         tick_chain<1>(mf, vv, gg);
       }
       if (n < nchunks) tick_chain<0>(mf, vv, gg);
-      block_sync();
+      sync();
     } else {
       O8 mf[KS];
       fetch_rows(0, 1, mf);
@@ -943,18 +953,34 @@ struct ScanBlock {
       }
       if (n < nchunks) tick_output<0>(n, mf, qs, qs_prev, gs, f0, f1);
       if (nchunks > 0) out_tile(static_cast<int>((nchunks - 1) & 1), qs, gs, f0, f1);
-      block_sync();
+      sync();
     }
     // With CHAIN, final states went out at each sequence's last chunk (next_chunk).
     if (!CHAIN && kt < NKT && !at_end(cc)) final_state(cc.s, kt, sacc);
   }
 };
 
+#ifdef PBGDN_DEBUG
+// Debug builds: barrier counts of the waves of each workgroup of the last
+// scan launch that used its row (blockIdx modulo AUDIT_ROWS), read by
+// pbgdn_debug_scan_barriers.
+constexpr int AUDIT_ROWS = 4096;
+__device__ uint32_t scan_barrier_audit[AUDIT_ROWS * (NT / 64)];
+#endif
+
 template <int K, typename TIn, typename TOut, bool CHAIN>
 __global__ __launch_bounds__(NT) void scan_kernel(ChunkParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
+  using L = ScanLayout<K, sizeof(TIn) == 4>;
+  PBGDN_POISON_LDS(smem_raw, CHAIN ? L::CHAIN_BYTES : L::BYTES);
+  PBGDN_POISON_SYNC();
   ScanBlock<K, TIn, TOut, CHAIN> blk(smem_raw, p);
   blk.run();
+#ifdef PBGDN_DEBUG
+  if ((threadIdx.x & 63) == 0) {
+    scan_barrier_audit[(blockIdx.x % AUDIT_ROWS) * (NT / 64) + (threadIdx.x >> 6)] = blk.nbar;
+  }
+#endif
 }
 
 template <int K, typename TIn, typename TOut, bool CHAIN>
@@ -990,3 +1016,26 @@ template int launch_scan<128, half_t, float>(const ChunkParams &, hipStream_t);
 template int launch_scan<128, float, float>(const ChunkParams &, hipStream_t);
 
 }  // namespace pbgdn
+
+#ifdef PBGDN_DEBUG
+// Debug builds only (no counterpart in the reference; not in the header): with
+// `reset`, fill the narrow scan's barrier audit with 0xffffffff; then copy it
+// (rows of 12 per-wave counts, `rows` of them at most) to host memory `out`.
+// A workgroup whose waves passed different numbers of barriers shows as a row
+// whose entries differ. Synchronises the device.
+extern "C" int pbgdn_debug_scan_barriers(uint32_t *out, int rows, int reset) {
+  using namespace pbgdn;
+  constexpr size_t BYTES = sizeof(scan_barrier_audit);
+  if (hipDeviceSynchronize() != hipSuccess) return PBGDN_ERR_LAUNCH;
+  if (reset) {
+    static uint32_t fill[AUDIT_ROWS * (NT / 64)];
+    for (auto &x : fill) x = 0xffffffffu;
+    if (hipMemcpyToSymbol(HIP_SYMBOL(scan_barrier_audit), fill, BYTES) != hipSuccess) return PBGDN_ERR_LAUNCH;
+  }
+  if (out && rows > 0) {
+    const size_t n = std::min<size_t>(BYTES, static_cast<size_t>(rows) * (NT / 64) * sizeof(uint32_t));
+    if (hipMemcpyFromSymbol(out, HIP_SYMBOL(scan_barrier_audit), n) != hipSuccess) return PBGDN_ERR_LAUNCH;
+  }
+  return PBGDN_OK;
+}
+#endif

@@ -638,6 +638,8 @@ struct WideBlock {
 template <int K, typename TIn, typename TOut, bool EPI>
 __global__ __launch_bounds__(WNT) __attribute__((amdgpu_waves_per_eu(2, 2))) void wide_kernel(ChunkParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
+  PBGDN_POISON_LDS(smem_raw, WideLayout<K>::BYTES);
+  PBGDN_POISON_SYNC();
   WideBlock<K, TIn, TOut, EPI> blk(smem_raw, p);
   blk.run();
 }

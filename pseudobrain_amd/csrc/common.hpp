@@ -176,4 +176,20 @@ __device__ __forceinline__ float4_t to_float4(half4_t x) {
                   static_cast<float>(x[2]), static_cast<float>(x[3])};
 }
 
+// Debug build (PBGDN_DEBUG): a kernel fills its LDS with a quiet NaN in every
+// 32-bit word before its first use (PBGDN_POISON_LDS on each region, then
+// PBGDN_POISON_SYNC), so that a read of LDS the launch has not written first
+// gives NaN and shows in the outputs. Nothing in a normal build.
+#ifdef PBGDN_DEBUG
+__device__ __forceinline__ void debug_poison_lds(void *base, uint32_t bytes) {
+  uint32_t *w = static_cast<uint32_t *>(base);
+  for (uint32_t i = threadIdx.x; i < bytes / 4; i += blockDim.x) w[i] = 0x7fc00000u;
+}
+#define PBGDN_POISON_LDS(base, bytes) ::pbgdn::debug_poison_lds((base), static_cast<uint32_t>(bytes))
+#define PBGDN_POISON_SYNC() __syncthreads()
+#else
+#define PBGDN_POISON_LDS(base, bytes) ((void)0)
+#define PBGDN_POISON_SYNC() ((void)0)
+#endif
+
 }  // namespace pbgdn

@@ -145,6 +145,16 @@ __global__ __launch_bounds__(DNT, (sizeof(TS) == 2 ? 5 : 4)) void decode_layer_k
   __shared__ float4_t red_k[NW][CG];
   __shared__ float4_t red_q[NW][CG];
   __shared__ float part[2][NW];
+  PBGDN_POISON_LDS(sk, sizeof(sk));
+  PBGDN_POISON_LDS(sq, sizeof(sq));
+  PBGDN_POISON_LDS(sv, sizeof(sv));
+  PBGDN_POISON_LDS(sgate, sizeof(sgate));
+  PBGDN_POISON_LDS(salpha, sizeof(salpha));
+  PBGDN_POISON_LDS(sbeta, sizeof(sbeta));
+  PBGDN_POISON_LDS(red_k, sizeof(red_k));
+  PBGDN_POISON_LDS(red_q, sizeof(red_q));
+  PBGDN_POISON_LDS(part, sizeof(part));
+  PBGDN_POISON_SYNC();
 
   const long slot = p.state_idx ? static_cast<long>(p.state_idx[b]) : static_cast<long>(b);
   if (slot < 0 || slot >= p.num_states) {  // padded entry: nothing is read or written but a zero output
@@ -402,6 +412,8 @@ extern "C" int pbgdn_decode_layer_fwd(const void *z, long z_stride, int in_dtype
                              conv_chan_stride, conv_weight, conv, a_log, dt_bias, l2_mode, state, state_idx,
                              num_states, o_norm, eps, hs, out_dtype, Hk, Hv, scale};
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // debug builds: hs starts as NaN (the pools are updated in place)
+  pbgdn::debug_poison(hs, static_cast<size_t>(static_cast<long>(B) * Hv * V * (out_dtype == PBGDN_F32 ? 4 : 2)), s);
   switch (state_dtype) {
     case PBGDN_F32: return pbgdn::dispatch_decode_layer<float>(p, B, K, V, state_policy, s);
     case PBGDN_BF16: return pbgdn::dispatch_decode_layer<pbgdn::u16>(p, B, K, V, state_policy, s);

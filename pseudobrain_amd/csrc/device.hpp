@@ -30,4 +30,17 @@ bool device_shape(DeviceShape &out);
 // runtime refuses.
 bool smem_configured(const void *kernel, size_t bytes, std::atomic<bool> *flags);
 
+// Debug build (PBGDN_DEBUG, libpbgdn_debug.so): the entry points fill their
+// pure outputs and workspaces with 0xff bytes (a NaN in float32, bfloat16 and
+// float16) on the stream before launching, so that an element no kernel
+// writes stays NaN; in-place buffers (state pools, carried tails) are left
+// alone. Nothing in a normal build.
+#ifdef PBGDN_DEBUG
+inline void debug_poison(void *p, size_t bytes, hipStream_t st) {
+  if (p && bytes) (void)hipMemsetAsync(p, 0xff, bytes, st);
+}
+#else
+inline void debug_poison(void *, size_t, hipStream_t) {}
+#endif
+
 }  // namespace pbgdn

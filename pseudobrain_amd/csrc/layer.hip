@@ -641,6 +641,16 @@ void launch_epilogue(int gate_dtype, dim3 grid, hipStream_t st, const EpiloguePa
 }
 
 bool valid_dtype(int d) { return d == PBGDN_F32 || d == PBGDN_BF16 || d == PBGDN_F16; }
+
+// Debug builds: q, k, v, g and beta of `rows` token rows start as NaN.
+void poison_prologue_outputs(const PrologueParams &prm, long rows, hipStream_t st) {
+  const long osz = prm.out_dtype == PBGDN_F32 ? 4 : 2;
+  debug_poison(prm.q, static_cast<size_t>(rows * prm.Hk * prm.K * osz), st);
+  debug_poison(prm.k, static_cast<size_t>(rows * prm.Hk * prm.K * osz), st);
+  debug_poison(prm.v, static_cast<size_t>(rows * prm.Hv * prm.V * osz), st);
+  debug_poison(prm.g, static_cast<size_t>(rows * prm.Hv * 4), st);
+  debug_poison(prm.beta, static_cast<size_t>(rows * prm.Hv * 4), st);
+}
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 // The gate rows move in 16-byte pieces of eight heads: tile_gates_vec's
 // conditions, and its 32-bit offsets within a tile's decay rows.
@@ -691,6 +701,11 @@ extern "C" int pbgdn_prologue_fwd(const void *qkv, long qkv_stride, const void *
   const dim3 grid(prm.ch_blocks + 1, (T + TT - 1) / TT, B);
   if (grid.y > 0x7fffffffu || B > 65535 || grid.y > 65535u) return PBGDN_ERR_UNSUPPORTED;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  poison_prologue_outputs(prm, static_cast<long>(B) * T, st);
+  if (has_tail && tail_out != tail) {
+    debug_poison(tail_out, static_cast<size_t>(static_cast<long>(B) * (conv - 1) * channels *
+                                               (tail_dtype == PBGDN_F32 ? 4 : 2)), st);
+  }
   switch (in_dtype) {  // tails: row-major [B, conv-1, C], batch row b in slot b
     case PBGDN_F32: launch_prologue_and_edges<float>(prm, grid, B, st); break;
     case PBGDN_BF16: launch_prologue_and_edges<u16>(prm, grid, B, st); break;
@@ -743,6 +758,7 @@ extern "C" int pbgdn_prologue_varlen_fwd(const void *qkv, long qkv_stride, const
   const dim3 grid(prm.ch_blocks + 1, (T + TT - 1) / TT, 1);
   if (grid.y > 65535u || num_seqs > 65535) return PBGDN_ERR_UNSUPPORTED;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  poison_prologue_outputs(prm, T, st);
   switch (in_dtype) {
     case PBGDN_F32: launch_prologue_and_edges<float>(prm, grid, num_seqs, st); break;
     case PBGDN_BF16: launch_prologue_and_edges<u16>(prm, grid, num_seqs, st); break;
@@ -776,6 +792,7 @@ extern "C" int pbgdn_epilogue_fwd(const void *o, int o_dtype, const void *gate, 
   if (blocks > 0x7fffffffL) return PBGDN_ERR_UNSUPPORTED;
   const dim3 grid(static_cast<unsigned>(blocks));
   hipStream_t st = static_cast<hipStream_t>(stream);
+  debug_poison(out, static_cast<size_t>(rows * V * (out_dtype == PBGDN_F32 ? 4 : 2)), st);  // debug builds: NaN first
   switch (o_dtype) {
     case PBGDN_F32: launch_epilogue<float>(gate_dtype, grid, st, prm); break;
     case PBGDN_BF16: launch_epilogue<u16>(gate_dtype, grid, st, prm); break;

@@ -87,6 +87,11 @@ __global__ __launch_bounds__(256, (recurrent_wg_per_cu<K, VW, ONE, ONE && sizeof
   __shared__ float sq[K];
   __shared__ float4_t red_k[NW][CG];
   __shared__ float4_t red_q[NW][CG];
+  PBGDN_POISON_LDS(sk, sizeof(sk));
+  PBGDN_POISON_LDS(sq, sizeof(sq));
+  PBGDN_POISON_LDS(red_k, sizeof(red_k));
+  PBGDN_POISON_LDS(red_q, sizeof(red_q));
+  PBGDN_POISON_SYNC();
 
   const long slot = p.state_idx ? static_cast<long>(p.state_idx[b]) : static_cast<long>(b);
   if (slot < 0 || slot >= p.num_states) {  // padded entry: no state, zero output
@@ -363,6 +368,13 @@ extern "C" int pbgdn_recurrent_fwd(const void *q, const void *k, const void *v, 
   if (B > 65535) return PBGDN_ERR_UNSUPPORTED;
   pbgdn::RecurrentParams p{q, k, v, in_dtype, g, beta, beta_dtype, state_in, state_out,
                            state_idx, nullptr, num_states, o, out_dtype, T, Hk, Hv, scale};
+  {  // debug builds: the outputs start as NaN (in-place states excepted)
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    pbgdn::debug_poison(o, static_cast<size_t>(static_cast<long>(B) * T * Hv * V * (out_dtype == PBGDN_F32 ? 4 : 2)), s);
+    if (state_out != state_in && !state_idx) {
+      pbgdn::debug_poison(state_out, static_cast<size_t>(static_cast<long>(B) * Hv * K * V * (state_dtype == PBGDN_F32 ? 4 : 2)), s);
+    }
+  }
   return pbgdn::recurrent_fwd(p, state_dtype, B, K, V, state_policy, static_cast<hipStream_t>(stream));
 }
 
@@ -390,5 +402,7 @@ extern "C" int pbgdn_recurrent_verify_fwd(const void *q, const void *k, const vo
   if (B > 65535) return PBGDN_ERR_UNSUPPORTED;
   pbgdn::RecurrentParams p{q, k, v, in_dtype, g, beta, beta_dtype, state_in, states,
                            state_idx, token_state_idx, num_states, o, out_dtype, T, Hk, Hv, scale};
+  pbgdn::debug_poison(o, static_cast<size_t>(static_cast<long>(B) * T * Hv * V * (out_dtype == PBGDN_F32 ? 4 : 2)),
+                      static_cast<hipStream_t>(stream));  // debug builds: o starts as NaN
   return pbgdn::recurrent_fwd(p, state_dtype, B, K, V, PBGDN_STATE_STREAM, static_cast<hipStream_t>(stream));
 }
