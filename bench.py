@@ -31,9 +31,10 @@ prefill input. The backward's roofline is against the bf16 dense MFMA peak
 (its products run on bf16 MFMA for bf16 inputs), with its counter traffic.
 
 Before its W warmup steps the headline step runs untimed for DEVICE_WARMUP_S
-(0.3 s, `device_warmup_s` in the line): the GPU has sat idle through the CPU
-baseline, and its first ~25 ms of work run ~10% slower on these boxes, so the
-K timed steps measure the steady state.
+(0.3 s, `device_warmup_s` in the line), and every other line's step for
+0.2 s: the GPU has sat idle through the CPU baseline (and through the host
+work that makes each line's inputs), and its first ~25 ms of work run ~10%
+slower on these boxes, so the timed steps measure the steady state.
 
 `roofline.traffic` (HBM bytes per launch) comes from the rocprofv3 counter
 summary committed under profiles/ (FETCH_SIZE and WRITE_SIZE per dispatch,
@@ -316,12 +317,17 @@ def cpu_baseline(seed: int = 0, decode_steps: int = 50):
 # ---------------------------------------------------------------------------
 # GPU measurements
 # ---------------------------------------------------------------------------
-def timed_steps(fn, steps, warmup):
-    """Run `warmup` untimed steps, then time `steps` back-to-back steps. Returns
-    (host seconds per step between two synchronizations, device seconds per
-    launch from two HIP events recorded around the same launches on the stream
-    they run on, torch's current stream)."""
+def timed_steps(fn, steps, warmup, device_warm_s=0.2):
+    """Run fn untimed for `device_warm_s` seconds (device_warmup: the inputs of
+    many lines are made on the host first, and the idle GPU's first
+    milliseconds of work run slow), then `warmup` untimed steps, then time
+    `steps` back-to-back steps. Returns (host seconds per step between two
+    synchronizations, device seconds per launch from two HIP events recorded
+    around the same launches on the stream they run on, torch's current
+    stream)."""
     import torch
+    if device_warm_s > 0:
+        device_warmup(fn, device_warm_s)
     for _ in range(warmup):
         fn()
     stream = torch.cuda.current_stream()
@@ -371,8 +377,7 @@ def bench_prefill(steps, warmup):
     def step():
         gd.chunk_fwd(q, k, v, g, beta, scale, h0, out=out)
 
-    device_warmup(step)
-    sec, ksec = timed_steps(step, steps, warmup)
+    sec, ksec = timed_steps(step, steps, warmup, device_warm_s=DEVICE_WARMUP_S)
     flops = prefill_flops(s.length, s.hv, s.dk, s.dv)
     nbytes = prefill_bytes(s.length, s.hk, s.hv, s.dk, s.dv)
     return s, sec, ksec, flops, nbytes
