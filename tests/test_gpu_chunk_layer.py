@@ -6,9 +6,10 @@ layer_epilogue on that o.
 
 Shapes that the wide scan takes (16-bit inputs, K = V = 128, at least 128
 (sequence, value head) pairs) run the epilogue inside the scan; the others
-(one long sequence, V = 64, a gate in another dtype) write o and run the
-epilogue kernel after it. Tolerances: hs 2e-2 and final states 1e-3
-(infinity-norm relative error against the oracle), as the operator's outputs."""
+(one or a few long sequences on the narrow scan, chained short sequences,
+V = 64, a gate in another dtype) write o and run the epilogue kernel after
+it. Tolerances: hs 2e-2 and final states 1e-3 (infinity-norm relative error
+against the oracle), as the operator's outputs."""
 import numpy as np
 import pytest
 import torch
@@ -93,14 +94,47 @@ def test_fused_matches_operator_then_epilogue():
     assert err <= 1e-2
 
 
+@pytest.mark.parametrize("batch,length,dtype,out_dtype", [
+    (1, 1000, torch.bfloat16, torch.float32),   # one sequence, a padded last chunk
+    (1, 1000, torch.bfloat16, torch.bfloat16),  # hs in the inputs' dtype
+    (1, 640, torch.float16, torch.float16),     # fp16, whole chunks
+    (1, 640, torch.float16, torch.float32),
+    (1, 1, torch.bfloat16, torch.float32),      # one token
+    (2, 2100, torch.bfloat16, torch.float32),   # two sequences, a workgroup each
+])
+def test_narrow_scan_then_epilogue(batch, length, dtype, out_dtype):
+    check(f"narrow scan + epilogue B={batch} T={length} {dtype}->{out_dtype}",
+          layer_case(batch, length, 16, 32, 128, dtype, seed=length + batch), out_dtype=out_dtype)
+
+
+def test_narrow_scan_then_epilogue_with_range_scaled_chunks():
+    check("narrow scan + epilogue v x 1e3", layer_case(1, 500, 16, 32, 128, torch.bfloat16, seed=6, v_scale=1e3))
+
+
+def test_narrow_scan_layer_call_is_operator_then_epilogue():
+    """One sequence: chunk_layer_fwd runs the same two kernels as chunk_fwd
+    followed by layer_epilogue, so hs and the final states are equal bit for
+    bit."""
+    q, k, v, g, beta, h0, gate, o_norm = [x.to(DEV) for x in layer_case(1, 3000, 16, 32, 128, torch.bfloat16, 19)]
+    with torch.no_grad():
+        hs, s = chunk_layer_fwd(q, k, v, g, beta, 128 ** -0.5, h0, gate, o_norm, EPS)
+        o, s2 = gd.chunk_fwd(q, k, v, g, beta, 128 ** -0.5, h0)
+        hs2 = layer_epilogue(o, gate, o_norm, EPS)
+    torch.cuda.synchronize()
+    assert torch.equal(s, s2)
+    assert torch.equal(hs, hs2)
+
+
 @pytest.mark.parametrize("batch,length,dv,gate_dtype", [
-    (1, 1000, 128, None),               # one sequence: the narrow scan, then the epilogue kernel
     (4, 200, 64, None),                 # V = 64
     (4, 200, 128, torch.float32),       # a float32 gate with bf16 operator inputs
+    (1, 700, 128, None),                # chained sequences (cu_seqlens below): o, then the epilogue kernel
 ])
 def test_two_pass_shapes(batch, length, dv, gate_dtype):
+    cu = cu_seqlens_of([300, 0, 400]) if length == 700 else None  # too few for the wide scan, one group
     check(f"two-pass B={batch} T={length} V={dv} gate={gate_dtype}",
-          layer_case(batch, length, 16, 32, dv, torch.bfloat16, seed=length + dv, gate_dtype=gate_dtype))
+          layer_case(batch, length, 16, 32, dv, torch.bfloat16, seed=length + dv, gate_dtype=gate_dtype,
+                     nstates=None if cu is None else 3), cu=cu)
 
 
 def test_float32_inputs():

@@ -40,7 +40,10 @@ CASES = {
     # prefill with the layer epilogue: fused in the wide scan, and the two-kernel path
     "fused layer epilogue": lambda: test_gpu_chunk_layer.test_fused_in_the_wide_scan(
         4, 300, 16, torch.bfloat16, torch.float32),
-    "two-pass layer epilogue": lambda: test_gpu_chunk_layer.test_two_pass_shapes(1, 1000, 128, None),
+    "narrow scan, then the layer epilogue": lambda: test_gpu_chunk_layer.test_narrow_scan_then_epilogue(
+        1, 1000, torch.bfloat16, torch.float32),
+    "chained narrow scan, then the layer epilogue": lambda: test_gpu_chunk_layer.test_two_pass_shapes(
+        1, 700, 128, None),
     # decode
     "decode step, B=64": test_gpu_recurrent.test_decode_b64_one_step,
     "multi-token recurrent, bf16": lambda: test_gpu_recurrent.test_sequential_kernel_multi_token(
