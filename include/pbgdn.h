@@ -61,7 +61,7 @@
 extern "C" {
 #endif
 
-#define PBGDN_ABI_VERSION 13
+#define PBGDN_ABI_VERSION 14
 
 /* element types */
 #define PBGDN_F32 0
@@ -497,13 +497,45 @@ int pbgdn_decode_layer_fwd(const void *z, long z_stride, int in_dtype,
                            float scale, int state_policy, void *stream);
 
 /*
+ * The residuals that pseudobrain::gated_delta_chunk returns beside o and the
+ * final state (gated_deltanet.py:200-217, `_fla_chunk_op`: fla's gc and A for
+ * 64-token chunks, which its backward op takes back at :230-249), from the
+ * operator's own inputs:
+ *
+ *   gc  [B, T, Hv] float32: the inclusive cumulative sum of g within each
+ *       64-token chunk, in token order
+ *   a   [B, T, Hv, 64] a_dtype: row t of the chunk of token t of
+ *       T = (I + strict_lower(beta_t (k_t . k_s) exp(gc_t - gc_s)))^-1, the
+ *       `solve` of delta_rule_chunked (:141-149), in float32 arithmetic
+ *
+ * k [B, T, Hk, K] in k_dtype (value head h reads key head h / (Hv / Hk)), g
+ * [B, T, Hv] float32, beta [B, T, Hv] in beta_dtype. Either output may be
+ * NULL. Any K >= 1.
+ */
+int pbgdn_chunk_residuals(const void *k, int k_dtype, const float *g,
+                          const void *beta, int beta_dtype, float *gc, void *a,
+                          int a_dtype, int B, int T, int Hk, int Hv, int K,
+                          void *stream);
+
+/*
+ * The inverse of gc: g_t = gc_t - gc_{t-1} within each 64-token chunk (gc_t
+ * at a chunk's first token), [B, T, Hv] float32, gc and g distinct. What
+ * pseudobrain::gated_delta_chunk_backward's callers hold is gc (:230-249);
+ * pbgdn_chunk_bwd takes g. Each g_t comes back to within the rounding of the
+ * cumulative sum it was added to.
+ */
+int pbgdn_chunk_decumulate(const float *gc, float *g, int B, int T, int Hv,
+                           void *stream);
+
+/*
  * Streaming copy of `bytes` from src to dst on `stream`: 16-byte non-temporal
  * buffer loads and stores, four pieces in flight per thread, 16 workgroups of
  * 256 threads per compute unit of the current device. No counterpart in the
  * reference: a measurement aid, the read + write bandwidth this GPU sustains
  * for a plain stream, against which the decode step's state traffic is
  * reported. bytes a multiple of 16, at most 2 GiB - 16; src and dst 16-byte
- * aligned and not overlapping.
+ * aligned and either equal (a pass in place: every piece is read before the
+ * same thread writes it back) or not overlapping.
  */
 int pbgdn_stream_probe(const void *src, void *dst, int64_t bytes, void *stream);
 

@@ -22,7 +22,11 @@ a (I - b k k^T) S + b k v^T, by a scalar (K=1) recurrence solved in closed form,
 by beta=0 pure decay, and by exact retrieval with orthonormal keys; the chunked
 algorithm by equality with the sequential one for chunk sizes 1..128, padding
 and segment invariance, and linearity in (V, S0). GQA, varlen and streaming by
-their definitions (repeat_interleave, per-sequence calls, state carry).
+their definitions (repeat_interleave, per-sequence calls, state carry). The
+residuals gc and A (chunk_residuals) by scipy's unit lower-triangular solve of
+I + a with a built by loops (decays as sums of g), by A (I + a) = I, by the
+identity for orthogonal keys, by the two-token closed form and by gc against
+per-chunk sums, and by mutants those pins catch.
 """
 from __future__ import annotations
 
@@ -111,6 +115,42 @@ def unit_lower_inverse(a: np.ndarray) -> np.ndarray:
         row[..., t] = 1.0
         inv[..., t, :] = row
     return inv
+
+
+def chunk_residuals(k, g, beta, chunk: int = CHUNK):
+    """The residuals gc and A of the reference's fla op (gated_deltanet.py:
+    200-217, 64-token chunks), as delta_rule_chunked forms them
+    (:141-149): gc = the inclusive cumsum of g within each chunk (:141), and
+    A [B,T,H,chunk], row t of its chunk's T = (I + strict_lower(b_t (k_t.k_i)
+    exp(gc_t - gc_i)))^-1 (:145-149). k [B,T,Hk,K] (repeated to the H value
+    heads of g), g and beta [B,T,H]. A chunk shorter than `chunk` (the last)
+    is padded with k = g = b = 0, which leaves its rows unchanged."""
+    k = np.asarray(k)
+    g = np.asarray(g)
+    beta = np.asarray(beta)
+    dtype = _compute_dtype(k, g, beta)
+    batch, length, heads = g.shape
+    k = repeat_heads(k.astype(dtype), heads)
+    gc = np.empty((batch, length, heads), dtype)
+    a_out = np.empty((batch, length, heads, chunk), dtype)
+    strict = np.tril(np.ones((chunk, chunk), dtype=bool), -1)
+    for t0 in range(0, length, chunk):
+        n = min(chunk, length - t0)
+        for b in range(batch):
+            for h in range(heads):
+                c = np.cumsum(g[b, t0:t0 + n, h].astype(dtype), dtype=dtype)
+                kk = np.zeros((chunk, k.shape[-1]), dtype)
+                kk[:n] = k[b, t0:t0 + n, h]
+                cc = np.zeros(chunk, dtype)
+                cc[:n] = c
+                cc[n:] = c[-1] if n else 0
+                bb = np.zeros(chunk, dtype)
+                bb[:n] = beta[b, t0:t0 + n, h]
+                decay = np.exp(np.where(strict, cc[:, None] - cc[None, :], -np.inf))
+                a = np.where(strict, bb[:, None] * (kk @ kk.T) * decay, 0.0).astype(dtype)
+                gc[b, t0:t0 + n, h] = c
+                a_out[b, t0:t0 + n, h] = unit_lower_inverse(a)[:n]
+    return gc, a_out
 
 
 def _chunked_head(q, k, v, c, beta, state, scale, size):

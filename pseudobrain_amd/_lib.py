@@ -16,7 +16,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpbgdn.so")
 # The debug build of the same sources (build.py): LDS and outputs poisoned with NaN.
 DEBUG_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpbgdn_debug.so")
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 F32, BF16, F16 = 0, 1, 2
 OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED, ERR_LAUNCH, ERR_SCRATCH = 0, 1, 2, 3, 4
@@ -54,6 +54,8 @@ SIGNATURES = {
     "pbgdn_chunk_bwd": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                          _vp, ctypes.c_size_t, _i, _i, _i, _i, _i, _i, _f, _vp], _i),
     "pbgdn_chunk_bwd_workspace_size": ([_i, _i, _i, _i, _i, _i], ctypes.c_size_t),
+    "pbgdn_chunk_residuals": ([_vp, _i, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp], _i),
+    "pbgdn_chunk_decumulate": ([_vp, _vp, _i, _i, _i, _vp], _i),
     "pbgdn_stream_probe": ([_vp, _vp, ctypes.c_int64, _vp], _i),
 }
 

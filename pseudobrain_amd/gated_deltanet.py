@@ -457,6 +457,136 @@ def _chunk_grad(ctx, grad_o, grad_final):
 gated_delta_chunk.register_autograd(_chunk_grad, setup_context=_chunk_setup)
 
 
+def chunk_residuals(k, g, beta, *, a_dtype: torch.dtype | None = None):
+    """Launch pbgdn_chunk_residuals: the gc and A that the reference's
+    pseudobrain::gated_delta_chunk returns beside o and the final state
+    (gated_deltanet.py:200-217, fla's residuals for 64-token chunks): gc
+    [B,T,Hv] float32, the inclusive cumulative sum of g within each chunk, and
+    A [B,T,Hv,64] in a_dtype (k's by default), row t of its chunk's
+    T = (I + strict_lower(beta_t k_t.k_s exp(gc_t - gc_s)))^-1 (the `solve` of
+    delta_rule_chunked, :141-149). k [B,T,Hk,K], g and beta [B,T,Hv]."""
+    if k.ndim != 4 or g.ndim != 3 or g.shape[:2] != k.shape[:2] or beta.shape != g.shape:
+        raise ValueError("expected k [B,T,Hk,K] and g, beta [B,T,Hv]")
+    batch, length, hk, dk = k.shape
+    hv = g.shape[2]
+    if hk < 1 or hv % hk:
+        raise ValueError("gated deltanet value heads must be a multiple of the key heads")
+    dev = _require_device(k, g, beta)
+    codes = _lib.DTYPE_CODES
+    a_dtype = k.dtype if a_dtype is None else a_dtype
+    if k.dtype not in codes or a_dtype not in codes:
+        raise ValueError("k and A must be float32, bfloat16 or float16")
+    k = k.contiguous()
+    g = g.to(torch.float32).contiguous()
+    beta = (beta if beta.dtype in codes else beta.to(torch.float32)).contiguous()
+    gc = torch.empty(batch, length, hv, dtype=torch.float32, device=dev)
+    a = torch.empty(batch, length, hv, CHUNK, dtype=a_dtype, device=dev)
+    status = _lib.lib().pbgdn_chunk_residuals(
+        _lib.ptr(k), codes[k.dtype], _lib.ptr(g), _lib.ptr(beta), codes[beta.dtype], _lib.ptr(gc), _lib.ptr(a),
+        codes[a_dtype], batch, length, hk, hv, dk, _lib.stream_handle(dev))
+    _lib.check(status, "pbgdn_chunk_residuals")
+    return gc, a
+
+
+def chunk_decumulate(gc):
+    """Launch pbgdn_chunk_decumulate: g [B,T,Hv] float32 from the chunk-local
+    cumulative sums gc that chunk_residuals returns."""
+    if gc.ndim != 3:
+        raise ValueError("expected gc [B,T,Hv]")
+    dev = _require_device(gc)
+    gc = gc.to(torch.float32).contiguous()
+    g = torch.empty_like(gc)
+    status = _lib.lib().pbgdn_chunk_decumulate(_lib.ptr(gc), _lib.ptr(g), gc.shape[0], gc.shape[1], gc.shape[2],
+                                                _lib.stream_handle(dev))
+    _lib.check(status, "pbgdn_chunk_decumulate")
+    return g
+
+
+# The reference's own op pair, schemas and all (gated_deltanet.py:200-277):
+# the forward returns fla's residuals gc and A beside o and the final state,
+# and the backward takes them back. Here A is informational (the backward
+# recomputes everything from g, which it recovers from gc).
+_FLA_FWD_SCHEMA = ("(Tensor q, Tensor k, Tensor v, Tensor g, Tensor beta, Tensor h0, float scale) "
+                   "-> (Tensor, Tensor, Tensor, Tensor)")
+_FLA_BWD_SCHEMA = ("(Tensor q, Tensor k, Tensor v, Tensor gc, Tensor beta, Tensor a, Tensor h0, Tensor grad_o, "
+                   "Tensor grad_final, float scale) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)")
+
+
+def _fla_forward(q, k, v, g, beta, h0, scale):
+    """(o [B,T,Hv,V] in q's dtype, final state fp32, gc, A) as _fla_chunk_op
+    (gated_deltanet.py:205-216) returns them."""
+    o, final = _chunk_fwd(q, k, v, g, beta, scale, h0, None)
+    gc, a = chunk_residuals(k, g, beta)
+    return o, final, gc, a
+
+
+def _fla_forward_fake(q, k, v, g, beta, h0, scale):
+    batch, length, _, dk = q.shape
+    hv, dv = v.shape[2], v.shape[3]
+    return (q.new_empty(batch, length, hv, dv), h0.new_empty(batch, hv, dk, dv, dtype=torch.float32),
+            g.new_empty(batch, length, hv, dtype=torch.float32), k.new_empty(batch, length, hv, CHUNK))
+
+
+def _fla_backward(q, k, v, gc, beta, a, h0, grad_o, grad_final, scale):
+    """(dq, dk, dv, dg fp32, dbeta, dh0) in the dtypes _fla_chunk_backward_op
+    returns (gated_deltanet.py:235-249); a is not read."""
+    dq, dk, dv, dg, dbeta, dh0 = chunk_bwd(q, k, v, chunk_decumulate(gc), beta, scale, h0, grad_o, grad_final)
+    return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg.float(), dbeta.to(beta.dtype), dh0.to(h0.dtype)
+
+
+def _fla_backward_fake(q, k, v, gc, beta, a, h0, grad_o, grad_final, scale):
+    return (torch.empty_like(q), torch.empty_like(k), torch.empty_like(v),
+            torch.empty_like(gc, dtype=torch.float32), torch.empty_like(beta), torch.empty_like(h0))
+
+
+def _define_fla_ops(name: str):
+    """The forward op `name` and its backward `name`_backward with the
+    reference's schemas and autograd (_fla_setup, _fla_grad:
+    gated_deltanet.py:259-277)."""
+    fwd = torch.library.custom_op(name, _fla_forward, mutates_args=(), schema=_FLA_FWD_SCHEMA)
+    bwd = torch.library.custom_op(f"{name}_backward", _fla_backward, mutates_args=(), schema=_FLA_BWD_SCHEMA)
+    fwd.register_fake(_fla_forward_fake)
+    bwd.register_fake(_fla_backward_fake)
+
+    def setup(ctx, inputs, output):
+        q, k, v, _g, beta, h0, scale = inputs
+        _o, _final, gc, a = output
+        ctx.save_for_backward(q, k, v, gc, beta, a, h0)
+        ctx.scale = scale
+
+    def grad(ctx, grad_o, grad_final, _grad_gc, _grad_a):
+        q, k, v, gc, beta, a, h0 = ctx.saved_tensors
+        if grad_o is None:
+            grad_o = torch.zeros(*q.shape[:2], v.shape[2], v.shape[3], dtype=q.dtype, device=q.device)
+        if grad_final is None:
+            grad_final = torch.zeros(h0.shape, dtype=torch.float32, device=h0.device)
+        dq, dk, dv, dg, dbeta, dh0 = bwd(q, k, v, gc, beta, a, h0, grad_o.to(q.dtype), grad_final.float(), ctx.scale)
+        return dq, dk, dv, dg, dbeta, dh0, None
+
+    fwd.register_autograd(grad, setup_context=setup)
+    return fwd, bwd
+
+
+# pbgdn::gated_delta_chunk_fla and pbgdn::gated_delta_chunk_fla_backward: the
+# reference's schemas under this package's namespace, always defined.
+gated_delta_chunk_fla, gated_delta_chunk_fla_backward = _define_fla_ops("pbgdn::gated_delta_chunk_fla")
+_REFERENCE_OPS = {}
+
+
+def register_reference_ops():
+    """Define pseudobrain::gated_delta_chunk and
+    pseudobrain::gated_delta_chunk_backward, the reference's op names and
+    schemas (gated_deltanet.py:200-277), on these kernels, for code that calls
+    torch.ops.pseudobrain.* in a process without the reference module (which
+    defines them itself, on fla). Returns the two ops; a second call returns
+    the same ones. Raises RuntimeError when the names exist already."""
+    if not _REFERENCE_OPS:
+        if hasattr(torch.ops.pseudobrain, "gated_delta_chunk"):
+            raise RuntimeError("pseudobrain::gated_delta_chunk is already defined (is the reference module imported?)")
+        _REFERENCE_OPS["ops"] = _define_fla_ops("pseudobrain::gated_delta_chunk")
+    return _REFERENCE_OPS["ops"]
+
+
 @torch.library.custom_op("pbgdn::recurrent_step_", mutates_args=("state",),
                          schema="(Tensor q, Tensor k, Tensor v, Tensor g, Tensor beta, Tensor(a!) state, "
                                 "Tensor? state_idx, float scale, bool state_resident=False) -> Tensor")

@@ -76,6 +76,27 @@ def test_custom_ops_are_registered_with_shape_inference():
         assert o3.shape == (1, 300, 4, 64) and o3.dtype == torch.bfloat16
 
 
+def test_reference_schema_ops_infer_the_reference_shapes():
+    """pbgdn::gated_delta_chunk_fla and its backward have the reference's
+    schemas (gated_deltanet.py:200-256) and its fake outputs: o, final fp32,
+    gc fp32 [B,T,H], A [B,T,H,64] in k's dtype; the backward's gradients like
+    its inputs."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    assert "(Tensor q, Tensor k, Tensor v, Tensor g, Tensor beta, Tensor h0, float scale)" in str(
+        torch.ops.pbgdn.gated_delta_chunk_fla.default._schema)
+    assert "Tensor gc, Tensor beta, Tensor a, Tensor h0, Tensor grad_o, Tensor grad_final, float scale" in str(
+        torch.ops.pbgdn.gated_delta_chunk_fla_backward.default._schema)
+    with FakeTensorMode():
+        q, k, v, g, beta, h0 = inputs(batch=2, length=100, hk=4, hv=4, dk=64, dv=64)
+        o, final, gc, a = torch.ops.pbgdn.gated_delta_chunk_fla(q, k, v, g, beta, h0, 0.125)
+        assert o.shape == (2, 100, 4, 64) and final.shape == (2, 4, 64, 64) and final.dtype == torch.float32
+        assert gc.shape == (2, 100, 4) and gc.dtype == torch.float32
+        assert a.shape == (2, 100, 4, 64) and a.dtype == k.dtype
+        grads = torch.ops.pbgdn.gated_delta_chunk_fla_backward(q, k, v, gc, beta, a, h0, o, final, 0.125)
+        assert [x.shape for x in grads] == [q.shape, k.shape, v.shape, gc.shape, beta.shape, h0.shape]
+        assert grads[3].dtype == torch.float32
+
+
 def test_entry_points_without_backward_refuse_grad_before_anything_runs():
     """With grad mode on, a grad-requiring input to an entry point that has no
     backward raises (before any device work) instead of silently detaching."""

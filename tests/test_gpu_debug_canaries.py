@@ -20,8 +20,8 @@ import torch
 from pseudobrain_amd import _lib
 from pseudobrain_amd import gated_deltanet as gd
 from pseudobrain_amd.workloads import generate
-from tests import (test_gpu_backward, test_gpu_chunk, test_gpu_chunk_layer, test_gpu_decode_layer, test_gpu_layer,
-                   test_gpu_prologue_varlen, test_gpu_recurrent, test_gpu_state_pools, test_gpu_wide)
+from tests import (test_gpu_backward, test_gpu_chunk, test_gpu_chunk_layer, test_gpu_decode_layer, test_gpu_fla_schema,
+                   test_gpu_layer, test_gpu_prologue_varlen, test_gpu_recurrent, test_gpu_state_pools, test_gpu_wide)
 
 pytestmark = pytest.mark.gpu
 
@@ -61,6 +61,9 @@ CASES = {
         1, 333, 1, 4, 128, 64, torch.bfloat16),
     "backward, float32, 16 chunks": lambda: test_gpu_backward.test_backward_matches_the_oracle(
         1, 1000, 2, 2, 128, 128, torch.float32),
+    # fla's residuals (gc, A) of the reference's op
+    "chunk residuals, GQA 2 -> 4": lambda: test_gpu_fla_schema.test_residuals_match_the_oracle(
+        1, 130, 2, 4, 64, torch.bfloat16),
 }
 
 

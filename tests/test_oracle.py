@@ -373,3 +373,86 @@ def test_backward_pins_catch_mutants(old, new):
     got = bad(*inputs[:5], 0.8, inputs[5], do, dht)
     want = numeric_gradients(list(inputs), 0.8, do, dht)
     assert not all(close(a, b, 1e-7) for a, b in zip(got, want))
+
+
+# ---------------------------------------------------------------------------
+# fla's residuals of the chunk forward (gated_deltanet.py:200-217, :141-149)
+# ---------------------------------------------------------------------------
+def brute_a(k, g, beta, t0, n):
+    """strict_lower(b_t (k_t.k_s) exp(g_{s+1} + ... + g_t)) of the chunk at t0
+    (n tokens) of one head, by loops: the decay as the sum of the decays
+    between the two tokens, not a difference of cumulative sums."""
+    a = np.zeros((n, n))
+    for t in range(n):
+        for s in range(t):
+            a[t, s] = beta[t0 + t] * (k[t0 + t] @ k[t0 + s]) * np.exp(np.sum(g[t0 + s + 1:t0 + t + 1]))
+    return a
+
+
+def test_residuals_invert_i_plus_a():
+    """Each chunk's rows of A are the inverse of I + a (a built by loops), as
+    scipy's unit lower-triangular solve gives it; GQA 1 -> 2, a short last chunk."""
+    from scipy.linalg import solve_triangular
+    _, k, _, g, beta, _ = rand_inputs(1, 150, 2, 16, 4, hk=1)
+    gc, a = gdn.chunk_residuals(k, g, beta)
+    assert a.shape == (1, 150, 2, 64) and gc.shape == (1, 150, 2)
+    for h in range(2):
+        for t0 in (0, 64, 128):
+            n = min(64, 150 - t0)
+            m = np.eye(n) + brute_a(k[0, :, 0], g[0, :, h], beta[0, :, h], t0, n)
+            inv = solve_triangular(m, np.eye(n), lower=True, unit_diagonal=True)
+            rows = a[0, t0:t0 + n, h]
+            assert close(rows[:, :n], inv, 1e-12)
+            assert np.all(rows[:, n:] == 0)
+            assert close(rows[:, :n] @ m, np.eye(n), 1e-12)
+
+
+def test_residuals_gc_restarts_at_each_chunk():
+    _, k, _, g, beta, _ = rand_inputs(2, 200, 1, 4, 4)
+    gc, _ = gdn.chunk_residuals(k, g, beta)
+    for b in range(2):
+        for t in range(200):
+            assert abs(gc[b, t, 0] - np.sum(g[b, 64 * (t // 64):t + 1, 0])) < 1e-12
+
+
+def test_residuals_orthogonal_keys_give_the_identity():
+    """Keys orthogonal within each chunk: a = 0, so every chunk's T is I."""
+    rng = np.random.default_rng(5)
+    basis = np.linalg.qr(rng.standard_normal((64, 64)))[0]
+    k = np.concatenate([basis, basis[:36]])[None, :, None, :]
+    g = -rng.random((1, 100, 1))
+    beta = rng.random((1, 100, 1))
+    _, a = gdn.chunk_residuals(k, g, beta)
+    for t in range(100):
+        expect = np.zeros(64)
+        expect[t % 64] = 1.0
+        assert np.allclose(a[0, t, 0], expect, atol=1e-12)
+
+
+def test_residuals_two_tokens_closed_form():
+    """T = 2: T = [[1, 0], [-b_1 (k_1.k_0) e^{g_1}, 1]]."""
+    _, k, _, g, beta, _ = rand_inputs(1, 2, 1, 5, 5)
+    gc, a = gdn.chunk_residuals(k, g, beta)
+    assert np.allclose(gc[0, :, 0], [g[0, 0, 0], g[0, 0, 0] + g[0, 1, 0]], atol=1e-15)
+    assert np.allclose(a[0, 0, 0, :2], [1.0, 0.0]) and np.allclose(a[0, 1, 0, 1], 1.0)
+    assert np.isclose(a[0, 1, 0, 0], -beta[0, 1, 0] * (k[0, 1, 0] @ k[0, 0, 0]) * np.exp(g[0, 1, 0]))
+
+
+RESIDUAL_MUTANTS = [
+    ("cc[:, None] - cc[None, :]", "cc[None, :] - cc[:, None]"),           # decay exponent sign
+    ("bb[:, None] * (kk @ kk.T)", "bb[None, :] * (kk @ kk.T)"),           # beta of the column
+    ("unit_lower_inverse(a)[:n]", "unit_lower_inverse(-a)[:n]"),          # (I - a)^-1
+    ("np.cumsum(g[b, t0:t0 + n, h].astype(dtype), dtype=dtype)",
+     "np.cumsum(g[b, t0:t0 + n, h].astype(dtype), dtype=dtype) + g[b, :t0, h].sum()"),  # no restart
+]
+
+
+@pytest.mark.parametrize("old,new", RESIDUAL_MUTANTS)
+def test_residual_pins_catch_mutants(old, new):
+    bad = _mutant(gdn.chunk_residuals, old, new)
+    _, k, _, g, beta, _ = rand_inputs(1, 100, 1, 8, 4)
+    gc, a = bad(k, g, beta)
+    rows_ok = all(close(a[0, t0:t0 + n, 0, :n] @ (np.eye(n) + brute_a(k[0, :, 0], g[0, :, 0], beta[0, :, 0], t0, n)),
+                        np.eye(n), 1e-9) for t0, n in ((0, 64), (64, 36)))
+    gc_ok = all(abs(gc[0, t, 0] - np.sum(g[0, 64 * (t // 64):t + 1, 0])) < 1e-9 for t in range(100))
+    assert not (rows_ok and gc_ok)
