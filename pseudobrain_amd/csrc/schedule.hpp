@@ -24,9 +24,11 @@ __host__ __device__ inline void xcd_group(int L, int ngroups, int gsize, int xcd
 // The prep kernel's items: the grid is resident from the start with tiers =
 // grid / cus workgroups per CU (1 to 3), and the k-th workgroup dispatched to
 // a CU (block / cus) runs slower than the ones before it (the oldest waves
-// win issue arbitration): measured on MI355X at T = 32K, the second and third
-// go at about 0.85 and 0.74 of the first one's pace. The items are split into
-// one contiguous segment per tier in proportion to these paces; within a
+// win issue arbitration). The items are split into one contiguous segment
+// per tier in proportion to paces of 1, 0.80 and 0.66: the best of the splits
+// timed on MI355X at T = 32K (c1 prefill 0.6735-0.6750 ms, against
+// 0.6755-0.6769 with 0.85 and 0.74, 0.6750-0.6765 with 0.74 and 0.58,
+// 0.678 with equal shares, 0.680 with 0.68 and 0.50); within a
 // segment the tier's workgroups take every `stride`-th item from `first`,
 // numbered so that consecutive items (the value heads of one key head) share
 // an XCD. Every item of [0, items) belongs to exactly one workgroup.
@@ -34,7 +36,7 @@ struct PrepShare {
   int first, stride, end;
 };
 __host__ __device__ inline PrepShare prep_share(int items, int grid, int block, int cus, int xcds) {
-  const int pace[3] = {100, 85, 74};
+  const int pace[3] = {100, 80, 66};
   const int tiers = (cus > 0 && grid % cus == 0 && grid / cus >= 1 && grid / cus <= 3) ? grid / cus : 1;
   PrepShare s;
   s.stride = grid / tiers;
