@@ -77,6 +77,22 @@ __host__ __device__ constexpr int rec_bytes() { return sizeof(TIn) == 4 ? REC_BY
 __host__ __device__ constexpr int rec_bytes_of(int in_dtype) { return in_dtype == PBGDN_F32 ? REC_BYTES_F32 : REC_BYTES; }
 
 __host__ __device__ constexpr int frag_index(int r, int kk) { return r < 2 ? r : 2 * r - 2 + kk; }
+// The record's 16-byte units that are zero by structure: lanes g = 2, 3 of
+// fragments 0 (row tile 0) and 3 (row tile 2, second contraction step) of
+// Tb, QKD and Tb's low part hold columns 32 kk + 8 g .. past the tile's last
+// row, where the lower-triangular matrices vanish (2 KiB of a 13 KiB record).
+// The prep kernel does not store them and the scans do not fetch them: their
+// loads go out of range, and the zeros such a load returns are what they
+// stage.
+__host__ __device__ constexpr bool rec_zero_unit(int byte) {
+  return byte >= REC_TB && (((byte - REC_TB) / FRAG_BYTES) % NFRAG == 0 ||
+                            ((byte - REC_TB) / FRAG_BYTES) % NFRAG == 3) &&
+         ((byte - REC_TB) % FRAG_BYTES) / 16 >= 32;
+}
+static_assert(!rec_zero_unit(REC_TB + 31 * 16) && rec_zero_unit(REC_TB + 32 * 16) &&
+                  rec_zero_unit(REC_QKD + 3 * FRAG_BYTES + 63 * 16) && !rec_zero_unit(REC_QKD + FRAG_BYTES + 40 * 16) &&
+                  !rec_zero_unit(REC_SC + 64),
+              "structural zeros of the record");
 
 __host__ __device__ inline long rec_base(long bos, int s) { return bos / CH + s; }
 

@@ -332,7 +332,8 @@ struct PrepBlock {
   }
 
   // Fragments f = wave + 4 j of Tb (f < 6), QKD (6 <= f < 12) and with LO
-  // Tb's low part (12 <= f < 18), and one decay vector per wave (wave 3: c
+  // Tb's low part (12 <= f < 18) but for their units that are zero by
+  // structure (rec_zero_unit), and one decay vector per wave (wave 3: c
   // itself) -> the workspace record. Every wave issues the same stores (past
   // the last fragment to an offset out of range); rec < 0 issues them with a
   // zero-size resource.
@@ -347,8 +348,9 @@ struct PrepBlock {
       const int r = fi < 2 ? fi : 2 + ((fi - 2) >> 1);
       const int kk = fi < 2 ? 0 : ((fi - 2) & 1);
       const uint32_t src = (m == 0 ? L::TB : m == 1 ? L::QKD : L::TBL) + 16 * r * L::SPB + sp_frag + 64 * kk;
-      const uint32_t dst = f < NF ? (m == 0 ? REC_TB : m == 1 ? REC_QKD : REC_TBL) + fi * FRAG_BYTES + lane * 16
-                                  : OUT_OF_RANGE;
+      // the units that are zero by structure are not stored: the scans do not fetch them
+      const uint32_t at = (m == 0 ? REC_TB : m == 1 ? REC_QKD : REC_TBL) + fi * FRAG_BYTES + lane * 16;
+      const uint32_t dst = f < NF && !rec_zero_unit(static_cast<int>(at)) ? at : OUT_OF_RANGE;
       const u32x4_t x = __builtin_bit_cast(u32x4_t, ld<half8_t>(src));
       if (nt) {
         __builtin_amdgcn_raw_buffer_store_b128(x, rr, dst, 0, 2);
