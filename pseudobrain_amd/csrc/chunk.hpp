@@ -49,7 +49,7 @@ constexpr int VT = 16;                  // value columns per scan workgroup
 
 // Workspace record of one (chunk, value head), REC_BYTES bytes:
 //   REC_SC   fp32 [64] gamma_t, [64] scale gamma_t, [64] exp(c_63 - c_t),
-//            [64] c_t
+//            then 256 bytes not written
 //   REC_TB   6 fragments of Tb as 16x16x32 fp16 A operands (64 lanes x 16 B):
 //            row tile r, contraction step kk <= r / 2 (the others are zero),
 //            at fragment frag_index(r, kk); lane (g, c) holds
@@ -77,22 +77,30 @@ __host__ __device__ constexpr int rec_bytes() { return sizeof(TIn) == 4 ? REC_BY
 __host__ __device__ constexpr int rec_bytes_of(int in_dtype) { return in_dtype == PBGDN_F32 ? REC_BYTES_F32 : REC_BYTES; }
 
 __host__ __device__ constexpr int frag_index(int r, int kk) { return r < 2 ? r : 2 * r - 2 + kk; }
-// The record's 16-byte units that are zero by structure: lanes g = 2, 3 of
-// fragments 0 (row tile 0) and 3 (row tile 2, second contraction step) of
-// Tb, QKD and Tb's low part hold columns 32 kk + 8 g .. past the tile's last
-// row, where the lower-triangular matrices vanish (2 KiB of a 13 KiB record).
-// The prep kernel does not store them and the scans do not fetch them: their
-// loads go out of range, and the zeros such a load returns are what they
-// stage.
-__host__ __device__ constexpr bool rec_zero_unit(int byte) {
-  return byte >= REC_TB && (((byte - REC_TB) / FRAG_BYTES) % NFRAG == 0 ||
-                            ((byte - REC_TB) / FRAG_BYTES) % NFRAG == 3) &&
-         ((byte - REC_TB) % FRAG_BYTES) / 16 >= 32;
+// The record's 16-byte units that hold nothing a scan reads: the lanes
+// (g, c) of a fragment (r, kk) whose 8 columns 32 kk + 8 g .. all lie past
+// their row 16 r + c, where the lower-triangular Tb, QKD (and Tb's low part)
+// vanish (32 of the 64 lanes of fragments (0, 0) and (2, 1), 8 of the others
+// but (2, 0) and (3, 0): 3 KiB of a 13 KiB record), and the vector of c after
+// the three decay vectors (no scan uses it). The prep kernel does not store
+// them and the scans do not fetch them: their loads go out of range, and the
+// zeros such a load returns are what they stage.
+__host__ __device__ constexpr bool rec_unused_unit(int byte) {
+  if (byte >= REC_SC + 768 && byte < REC_TB) return true;  // c
+  if (byte < REC_TB) return false;
+  const int f = ((byte - REC_TB) / FRAG_BYTES) % NFRAG;
+  const int lane = ((byte - REC_TB) % FRAG_BYTES) / 16;
+  const int r = f < 2 ? f : 2 + (f - 2) / 2, kk = f < 2 ? 0 : (f - 2) % 2;  // frag_index(r, kk) == f
+  return 32 * kk + 8 * (lane >> 4) > 16 * r + (lane & 15);
 }
-static_assert(!rec_zero_unit(REC_TB + 31 * 16) && rec_zero_unit(REC_TB + 32 * 16) &&
-                  rec_zero_unit(REC_QKD + 3 * FRAG_BYTES + 63 * 16) && !rec_zero_unit(REC_QKD + FRAG_BYTES + 40 * 16) &&
-                  !rec_zero_unit(REC_SC + 64),
-              "structural zeros of the record");
+static_assert(frag_index(2, 1) == 3 && frag_index(3, 0) == 4 && frag_index(3, 1) == 5, "fragment order");
+static_assert(!rec_unused_unit(REC_TB + 7 * 16) && rec_unused_unit(REC_TB + 16 * 16) &&
+                  !rec_unused_unit(REC_TB + 24 * 16) && rec_unused_unit(REC_TB + 32 * 16) &&
+                  rec_unused_unit(REC_QKD + 3 * FRAG_BYTES + 63 * 16) &&
+                  !rec_unused_unit(REC_QKD + 2 * FRAG_BYTES + 63 * 16) &&
+                  rec_unused_unit(REC_QKD + FRAG_BYTES + 48 * 16) && !rec_unused_unit(REC_QKD + FRAG_BYTES + 56 * 16) &&
+                  !rec_unused_unit(REC_SC + 512) && rec_unused_unit(REC_SC + 768),
+              "units of the record no scan reads");
 
 __host__ __device__ inline long rec_base(long bos, int s) { return bos / CH + s; }
 

@@ -332,9 +332,9 @@ struct PrepBlock {
   }
 
   // Fragments f = wave + 4 j of Tb (f < 6), QKD (6 <= f < 12) and with LO
-  // Tb's low part (12 <= f < 18) but for their units that are zero by
-  // structure (rec_zero_unit), and one decay vector per wave (wave 3: c
-  // itself) -> the workspace record. Every wave issues the same stores (past
+  // Tb's low part (12 <= f < 18) but for their units no scan reads
+  // (rec_unused_unit), and the decay vectors of waves 0-2 -> the workspace
+  // record. Every wave issues the same stores (past
   // the last fragment to an offset out of range); rec < 0 issues them with a
   // zero-size resource.
   __device__ void out(long rec, int h, int jh) const {
@@ -348,9 +348,9 @@ struct PrepBlock {
       const int r = fi < 2 ? fi : 2 + ((fi - 2) >> 1);
       const int kk = fi < 2 ? 0 : ((fi - 2) & 1);
       const uint32_t src = (m == 0 ? L::TB : m == 1 ? L::QKD : L::TBL) + 16 * r * L::SPB + sp_frag + 64 * kk;
-      // the units that are zero by structure are not stored: the scans do not fetch them
+      // the units no scan reads are not stored
       const uint32_t at = (m == 0 ? REC_TB : m == 1 ? REC_QKD : REC_TBL) + fi * FRAG_BYTES + lane * 16;
-      const uint32_t dst = f < NF && !rec_zero_unit(static_cast<int>(at)) ? at : OUT_OF_RANGE;
+      const uint32_t dst = f < NF && !rec_unused_unit(static_cast<int>(at)) ? at : OUT_OF_RANGE;
       const u32x4_t x = __builtin_bit_cast(u32x4_t, ld<half8_t>(src));
       if (nt) {
         __builtin_amdgcn_raw_buffer_store_b128(x, rr, dst, 0, 2);
@@ -363,7 +363,7 @@ struct PrepBlock {
     const float val = wave == 0 ? gam
                       : wave == 1 ? p.scale * gam
                       : ld<float>(sc + (wave == 2 ? L::DEC : L::CUM) + lane * 4);
-    const uint32_t dst = REC_SC + 256 * wave + lane * 4;  // SC_GAM, SC_GSC, SC_DEC, c
+    const uint32_t dst = wave < 3 ? REC_SC + 256 * wave + lane * 4 : OUT_OF_RANGE;  // SC_GAM, SC_GSC, SC_DEC
     if (nt) {
       __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, val), rr, dst, 0, 2);
     } else {

@@ -180,7 +180,7 @@ struct ScanStage {
         dst[i] = L::V16_OFF + tv * 32 + c0 * 2;
       } else if (u < UNITS) {
         const int w = u - KQ_UNITS - V_UNITS;
-        src[i] = rec_zero_unit(16 * w) ? OUT_OF_RANGE : 16 * w;  // zeros by structure are not fetched
+        src[i] = rec_unused_unit(16 * w) ? OUT_OF_RANGE : 16 * w;  // units no scan reads are not fetched
         if (LO && u >= TBL_UNIT) {
           dst[i] = L::TBL + 16 * (u - TBL_UNIT);
           tbl |= 1u << i;

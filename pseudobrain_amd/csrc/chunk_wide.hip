@@ -275,8 +275,8 @@ struct WideBlock {
 #pragma unroll
     for (int s_ = 0; s_ < (DMA_REC + WT - 1) / WT; ++s_) {
       const int i = wave + WT * s_;
-      const uint32_t roff = 1024 * i + lane * 16;  // zeros by structure: an out-of-range load stages zeros
-      if (i < DMA_REC) dma(rr, L::rec(b3) + 1024 * i, rec_zero_unit(static_cast<int>(roff)) ? OUT_OF_RANGE : roff);
+      const uint32_t roff = 1024 * i + lane * 16;  // units no scan reads: an out-of-range load stages zeros
+      if (i < DMA_REC) dma(rr, L::rec(b3) + 1024 * i, rec_unused_unit(static_cast<int>(roff)) ? OUT_OF_RANGE : roff);
     }
     kp += CH * kqs;
     qp += CH * kqs;
