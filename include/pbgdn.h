@@ -140,7 +140,9 @@ const char *pbgdn_status_string(int status);
  *               call to the second; its contents need no initialisation and
  *               are dead when the call's work on `stream` completes
  *
- * Supported: K in {64, 128}; V a multiple of 16; Hv a multiple of Hk.
+ * Supported: K in {64, 128} with V a multiple of 16, and K = 256 with in_dtype
+ * BF16 or F16 and V a multiple of 32 (keys 128 < K <= 256 zero-padded to 256
+ * by the caller; the padded keys add nothing); Hv a multiple of Hk.
  * Ranges: the products run on fp16/bf16 MFMA operands with fp32 accumulation;
  * a chunk whose intermediate V - gamma K S leaves the fp16 range is scaled by
  * a power of two internally. With in_dtype F32, q and k enter as fp16

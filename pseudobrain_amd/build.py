@@ -25,7 +25,7 @@ LIB = os.path.join(PKG, "libpbgdn.so")
 # writes shows as NaN (tests/test_gpu_debug_canaries.py).
 DEBUG_LIB = os.path.join(PKG, "libpbgdn_debug.so")
 SOURCES = ("abi.hip", "recurrent.hip", "chunk.hip", "chunk_prep.hip", "chunk_scan.hip", "chunk_wide.hip",
-           "chunk_bwd.hip", "chunk_residuals.hip",
+           "chunk_k256.hip", "chunk_bwd.hip", "chunk_residuals.hip",
            "layer.hip", "decode_layer.hip", "device.hip")
 ARCH = "gfx950"
 

@@ -72,6 +72,29 @@ int dispatch_in(const ChunkParams &p, long records, int in_dtype, int out_dtype,
   }
 }
 
+// 256-wide keys, 16-bit inputs: the prep kernel, then the k256 scan with the
+// waves per workgroup of k256_waves. PBGDN_K256_WAVES=2|4 in the
+// environment forces them (for measurements) where they divide V.
+inline int k256_waves_forced() {
+  static const int forced = [] {
+    const char *e = getenv("PBGDN_K256_WAVES");
+    const int w = e ? atoi(e) : 0;
+    return (w == 2 || w == 4) ? w : 0;
+  }();
+  return forced;
+}
+
+template <typename TIn>
+int run_chunk_k256(const ChunkParams &p, long records, int out_dtype, hipStream_t s) {
+  const int st = launch_prep<256, TIn>(p, records, s);
+  if (st != PBGDN_OK) return st;
+  int wt = k256_waves(p.V, static_cast<long>(p.num_seqs) * p.Hv, p.cus);
+  const int forced = k256_waves_forced();
+  if (forced && p.V % (16 * forced) == 0) wt = forced;
+  if (out_dtype == PBGDN_F32) return launch_k256<TIn, float>(p, wt, s);
+  return launch_k256<TIn, TIn>(p, wt, s);  // out_dtype == in_dtype, checked by the caller
+}
+
 // The prefill with the layer epilogue in the wide scan (p.o is hs).
 template <typename TIn>
 int run_chunk_epilogue(const ChunkParams &p, long records, int hs_dtype, hipStream_t s) {
@@ -207,7 +230,9 @@ int chunk_setup(const void *q, const void *k, const void *v, int in_dtype, const
   if (state_idx && num_states < 0) return PBGDN_ERR_INVALID_ARGUMENT;
   if (cu_seqlens ? B != 1 : num_seqs != B) return PBGDN_ERR_INVALID_ARGUMENT;
   if (chunk != pbgdn::CH) return PBGDN_ERR_UNSUPPORTED;
-  if (!(K == 64 || K == 128) || V % pbgdn::VT != 0) return PBGDN_ERR_UNSUPPORTED;
+  if (!(K == 64 || K == 128 || K == 256) || V % pbgdn::VT != 0) return PBGDN_ERR_UNSUPPORTED;
+  // 256-wide keys (chunk_k256.hip): 16-bit inputs, V a multiple of 32
+  if (K == 256 && (in_dtype == PBGDN_F32 || V % 32 != 0)) return PBGDN_ERR_UNSUPPORTED;
   if (!(out_dtype == PBGDN_F32 || out_dtype == in_dtype)) return PBGDN_ERR_UNSUPPORTED;
   // Per-chunk buffer ranges and per-lane offsets are 32-bit byte counts.
   if (static_cast<long>(pbgdn::CH) * Hv * V * 4 > 0x7fffffffL ||
@@ -278,6 +303,9 @@ extern "C" int pbgdn_chunk_fwd(const void *q, const void *k, const void *v, int 
   switch (K) {
     case 64: return pbgdn::dispatch_in<64>(p, records, in_dtype, out_dtype, s);
     case 128: return pbgdn::dispatch_in<128>(p, records, in_dtype, out_dtype, s);
+    case 256:
+      return in_dtype == PBGDN_BF16 ? pbgdn::run_chunk_k256<pbgdn::u16>(p, records, out_dtype, s)
+                                    : pbgdn::run_chunk_k256<pbgdn::half_t>(p, records, out_dtype, s);
     default: return PBGDN_ERR_UNSUPPORTED;
   }
 }
@@ -351,7 +379,7 @@ extern "C" int pbgdn_chunk_layer_fuses(int in_dtype, int gate_dtype, int hs_dtyp
                                        int Hv, int K, int V) {
   using pbgdn::valid_dtype;
   if (!valid_dtype(in_dtype) || !valid_dtype(gate_dtype) || !valid_dtype(hs_dtype) || num_seqs < 0 || Hv <= 0 ||
-      !(V == 64 || V == 128) || !(K == 64 || K == 128)) {
+      !(V == 64 || V == 128) || !(K == 64 || K == 128 || K == 256)) {
     return -1;
   }
   if (!pbgdn::layer_fusable(in_dtype, gate_dtype, hs_dtype, gate_stride, K, V)) return 0;

@@ -436,12 +436,18 @@ struct ChunkInputs {
   }
 };
 
-// Launchers (explicitly instantiated in chunk_prep.hip / chunk_scan.hip).
+// Launchers (explicitly instantiated in chunk_prep.hip, chunk_scan.hip,
+// chunk_wide.hip and chunk_k256.hip).
 template <int K, typename TIn>
 int launch_prep(const ChunkParams &p, long records, hipStream_t stream);
 template <int K, typename TIn, typename TOut>
 int launch_scan(const ChunkParams &p, hipStream_t stream);
 template <int K, typename TIn, typename TOut, bool EPI>
 int launch_wide(const ChunkParams &p, hipStream_t stream);
+// The scan for 256-wide keys (chunk_k256.hip): `wt` waves (4 or 2) per
+// workgroup, 16 wt columns each; k256_waves picks wt for a call.
+template <typename TIn, typename TOut>
+int launch_k256(const ChunkParams &p, int wt, hipStream_t stream);
+int k256_waves(int V, long pairs_of_seq_and_head, int cus);
 
 }  // namespace pbgdn

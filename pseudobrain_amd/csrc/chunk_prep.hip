@@ -39,9 +39,10 @@ namespace {
 
 constexpr int PNT = 256;          // threads per prep workgroup
 // Resident workgroups per CU: three when the registers allow it (16-bit
-// inputs); fp32 inputs hold more registers and keep two.
-template <typename TIn>
-constexpr int prep_wg_per_cu() { return sizeof(TIn) == 4 ? 2 : 3; }
+// inputs); fp32 inputs hold more registers and keep two, and so do 256-wide
+// keys (their K and Q rows take twice the LDS).
+template <int K, typename TIn>
+constexpr int prep_wg_per_cu() { return sizeof(TIn) == 4 || K == 256 ? 2 : 3; }
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
@@ -82,9 +83,9 @@ struct PrepBlock {
   using O8 = typename Op::T8;
   using Inputs = ChunkInputs<K, TIn, PNT, L, false, true>;
   static constexpr int KS = K / 32;  // contraction steps over keys
-  static_assert(K == 64 || K == 128, "K must be 64 or 128");
+  static_assert(K == 64 || K == 128 || (K == 256 && sizeof(TIn) == 2), "K must be 64 or 128, or 256 (16-bit)");
   static_assert(L::TBL_END <= L::SC, "Tb's low part before the decay tables");
-  static_assert(L::BYTES * prep_wg_per_cu<TIn>() <= 160 * 1024, "prep LDS");
+  static_assert(L::BYTES * prep_wg_per_cu<K, TIn>() <= 160 * 1024, "prep LDS");
 
   unsigned char *lds;
   const ChunkParams &p;
@@ -434,7 +435,7 @@ struct PrepBlock {
 };
 
 template <int K, typename TIn>
-__global__ __launch_bounds__(PNT, prep_wg_per_cu<TIn>()) void prep_kernel(ChunkParams p, int items, int nt) {
+__global__ __launch_bounds__(PNT, (prep_wg_per_cu<K, TIn>())) void prep_kernel(ChunkParams p, int items, int nt) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   PBGDN_POISON_LDS(smem_raw, (PrepLayout<K, sizeof(TIn) == 4>::BYTES));
   PBGDN_POISON_SYNC();
@@ -461,7 +462,7 @@ int launch_prep(const ChunkParams &p, long records, hipStream_t stream) {
   const int hpi = ((p.Hv / p.Hk) % 2 == 0) ? 2 : 1;  // value heads per item (PrepBlock::hpi)
   const long items = records * (p.Hv / hpi);
   if (items > 0x3fffffffL) return PBGDN_ERR_UNSUPPORTED;  // item numbers are 32-bit
-  const long grid = prep_grid(items, p.cus, prep_wg_per_cu<TIn>(), p.xcds);
+  const long grid = prep_grid(items, p.cus, prep_wg_per_cu<K, TIn>(), p.xcds);
   // Records of a large call are written non-temporally: measured on the
   // 32,768-token call (213 MB of records), the scan then reads them 2% faster.
   const int nt = records * p.Hv * static_cast<long>(rec_bytes<TIn>()) > REC_STREAM_BYTES ? 1 : 0;
@@ -475,5 +476,7 @@ template int launch_prep<64, float>(const ChunkParams &, long, hipStream_t);
 template int launch_prep<128, u16>(const ChunkParams &, long, hipStream_t);
 template int launch_prep<128, half_t>(const ChunkParams &, long, hipStream_t);
 template int launch_prep<128, float>(const ChunkParams &, long, hipStream_t);
+template int launch_prep<256, u16>(const ChunkParams &, long, hipStream_t);
+template int launch_prep<256, half_t>(const ChunkParams &, long, hipStream_t);
 
 }  // namespace pbgdn

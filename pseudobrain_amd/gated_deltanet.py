@@ -45,7 +45,8 @@ from . import _lib
 CHUNK = 64            # gated_deltanet.py:49
 SEQUENTIAL_MAX = 4    # gated_deltanet.py:54
 KERNELS = ("sequential", "chunked", "hip")
-CHUNK_HEAD_DIMS = (64, 128)               # key widths the chunk kernel is built for
+CHUNK_HEAD_DIMS = (64, 128, 256)          # key widths the chunk kernels are built for
+CHUNK_WIDE_KEY = 256                      # 16-bit inputs only, V a multiple of 32 (chunk_k256.hip)
 RECURRENT_HEAD_DIMS = (32, 64, 128, 256)  # key and value widths of the recurrent kernel
 BACKWARD_HEAD_DIMS = (64, 128)            # key and value widths of the chunk backward
 MAX_HEAD_DIM = 256                        # widest head a device path takes (fla_usable, :189-197)
@@ -137,11 +138,25 @@ def _pad_state(h: torch.Tensor | None, dk: int, dv: int) -> torch.Tensor | None:
 
 def _chunk_widths(dk: int, dv: int, grad: bool) -> tuple[int, int]:
     """(K, V) a chunk-kernel call of these head widths runs at: K in
-    CHUNK_HEAD_DIMS, V a multiple of 16 (in BACKWARD_HEAD_DIMS when a backward
-    may follow)."""
+    CHUNK_HEAD_DIMS, V a multiple of 16, of 32 at K = 256 (in
+    BACKWARD_HEAD_DIMS when a backward may follow)."""
     if grad:
         return _width_at_least(dk, BACKWARD_HEAD_DIMS), _width_at_least(dv, BACKWARD_HEAD_DIMS)
-    return _width_at_least(dk, CHUNK_HEAD_DIMS), -(-dv // 16) * 16
+    kp = _width_at_least(dk, CHUNK_HEAD_DIMS)
+    step = 32 if kp == CHUNK_WIDE_KEY else 16
+    return kp, -(-dv // step) * step
+
+
+def _chunk_shape_ok(dk: int, dv: int, dtype: torch.dtype) -> bool:
+    """The chunk kernels take these widths and input dtype: K 64 or 128 with V
+    a multiple of 16, or K 256 with 16-bit inputs and V a multiple of 32."""
+    if dk == CHUNK_WIDE_KEY:
+        return dtype in (torch.bfloat16, torch.float16) and dv % 32 == 0
+    return dk in CHUNK_HEAD_DIMS and dv % 16 == 0
+
+
+_CHUNK_SHAPES = ("chunk kernel supports K 64 or 128 with V a multiple of 16, and K 256 with bfloat16 or "
+                 "float16 inputs and V a multiple of 32")
 
 
 # ----------------------------------------------------------------------------
@@ -164,8 +179,8 @@ def _chunk_args(q, k, v, g, beta, h0, cu_seqlens):
     shapes = _shapes(q, k, v, g, beta)
     batch, length, hk, hv, dk, dv = shapes
     dev = _require_device(q, k, v, g, beta, h0, cu_seqlens)
-    if dk not in CHUNK_HEAD_DIMS or dv % 16:
-        raise ValueError(f"chunk kernel supports K in {CHUNK_HEAD_DIMS} and V a multiple of 16")
+    if not _chunk_shape_ok(dk, dv, q.dtype):
+        raise ValueError(_CHUNK_SHAPES)
     q, k, v, g, beta = _operands(q, k, v, g, beta)
     if cu_seqlens is not None:
         if batch != 1:
@@ -233,8 +248,8 @@ def chunk_fwd_slots(q, k, v, g, beta, scale: float, states, state_idx, cu_seqlen
     if out_dtype is not None and out_dtype not in (torch.float32, q.dtype):
         raise ValueError(f"chunk kernel writes o as float32 or q's dtype ({q.dtype}), not {out_dtype}")
     dev = _require_device(q, k, v, g, beta, states, state_idx, cu_seqlens, has_initial_state)
-    if dk not in CHUNK_HEAD_DIMS or dv % 16:
-        raise ValueError(f"chunk kernel supports K in {CHUNK_HEAD_DIMS} and V a multiple of 16")
+    if not _chunk_shape_ok(dk, dv, q.dtype):
+        raise ValueError(_CHUNK_SHAPES)
     _state_pool(states, hv, dk, dv)
     q, k, v, g, beta = _operands(q, k, v, g, beta)
     if cu_seqlens is not None:
@@ -624,9 +639,11 @@ def delta_rule_hip(q, k, v, g, beta, scale, h0, cu_seqlens=None):
     """The device prefill with the fla path's conventions (gated_deltanet.py:280-285):
     q/k/v at their own precision, fp32 state and decay; returns (o.float(), final).
 
-    K <= 128: the chunk kernel through pbgdn::gated_delta_chunk (differentiable
-    for [B,T] batches with K, V <= 128), the head widths zero-padded to the
-    kernel's. 128 < K <= 256: the recurrent kernel over every token (no backward)."""
+    The chunk kernels through pbgdn::gated_delta_chunk, the head widths
+    zero-padded to theirs: K <= 128 for every input dtype (differentiable for
+    [B,T] batches with K, V <= 128), and 128 < K <= 256 for bfloat16 and
+    float16 inputs (K padded to 256, no backward). float32 inputs with
+    128 < K <= 256 run the recurrent kernel over every token (no backward)."""
     batch, length, hk, hv, dk, dv = _shapes(q, k, v, g, beta)
     _require_device(q, k, v, g, beta, h0, cu_seqlens)
     _head_bound(dk, dv)
@@ -638,7 +655,7 @@ def delta_rule_hip(q, k, v, g, beta, scale, h0, cu_seqlens=None):
         if dk > BACKWARD_HEAD_DIMS[-1] or dv > BACKWARD_HEAD_DIMS[-1]:
             raise RuntimeError(f"the chunk backward is built for K, V <= {BACKWARD_HEAD_DIMS[-1]} "
                                f"(got K={dk}, V={dv}); call under torch.no_grad()")
-    if dk > CHUNK_HEAD_DIMS[-1]:
+    if dk > CHUNK_HEAD_DIMS[-2] and q.dtype not in (torch.bfloat16, torch.float16):
         return _recurrent_prefill(q, k, v, g, beta, scale, h0, cu_seqlens)
     kp, vp = _chunk_widths(dk, dv, grad)
     o, final = gated_delta_chunk(_pad_last(q, kp), _pad_last(k, kp), _pad_last(v, vp), g, beta,
@@ -706,14 +723,16 @@ def hip_usable(*tensors: torch.Tensor) -> bool:
     """The chunkwise device prefill applies (the fla_usable gate,
     gated_deltanet.py:189-197, which select_kernel consults only for calls
     longer than SEQUENTIAL_MAX tokens): every tensor on the device, a dtype
-    the kernels read (float32, bfloat16, float16), a key width K <= 128 (the
-    chunk kernel's; wider keys would run token by token on the recurrent
-    kernel, so fla or the reference's chunked path keeps them) and a value
-    width V <= 256; when a gradient will be wanted, V <= 128 as well (the
-    chunk backward's widths), so that a training call the device cannot
-    differentiate stays on the reference's PyTorch path. tensors[0] is the
-    matrix state [..., K, V]. Raises if the tensors are on a GPU but the
-    library is missing: a GPU caller never silently loses the kernel."""
+    the kernels read (float32, bfloat16, float16), head widths K, V <= 256,
+    and a key width K <= 128 unless every other floating-point tensor is
+    bfloat16 or float16 (the chunk kernel for 128 < K <= 256 takes 16-bit
+    inputs; float32 ones would run token by token on the recurrent kernel, so
+    fla or the reference's chunked path keeps them); when a gradient will be
+    wanted, K, V <= 128 (the chunk backward's widths), so that a training call
+    the device cannot differentiate stays on the reference's PyTorch path.
+    tensors[0] is the matrix state [..., K, V]. Raises if the tensors are on a
+    GPU but the library is missing: a GPU caller never silently loses the
+    kernel."""
     if not tensors or not all(t.is_cuda for t in tensors):
         return False
     if not all(t.dtype in _lib.DTYPE_CODES for t in tensors if t.is_floating_point()):
@@ -721,9 +740,12 @@ def hip_usable(*tensors: torch.Tensor) -> bool:
     state = tensors[0]
     dv = state.shape[-1]
     dk = state.shape[-2] if state.ndim >= 2 else 0
-    if dk > CHUNK_HEAD_DIMS[-1]:
+    if dk > CHUNK_HEAD_DIMS[-1] or dv > MAX_HEAD_DIM:
         return False
-    if dv > (BACKWARD_HEAD_DIMS[-1] if grad_needed(*tensors) else MAX_HEAD_DIM):
+    if grad_needed(*tensors) and (dk > BACKWARD_HEAD_DIMS[-1] or dv > BACKWARD_HEAD_DIMS[-1]):
+        return False
+    if dk > CHUNK_HEAD_DIMS[-2] and not all(t.dtype in (torch.bfloat16, torch.float16)
+                                            for t in tensors[1:] if t.is_floating_point()):
         return False
     _lib.lib()
     return True

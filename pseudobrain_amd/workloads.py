@@ -40,6 +40,9 @@ WORKLOADS = {
     "decode_b64": Shape(64, 1, 16, 32, 128, 128, torch.bfloat16, 0.02),
     "varlen_8seq": Shape(1, 262144, 16, 32, 128, 128, torch.bfloat16, 0.02),
     "stream_1m": Shape(1, 1048576, 16, 32, 128, 128, torch.bfloat16, 0.02),
+    # the prefill shape with 256-wide key and value heads (the widest the
+    # reference's device gate admits, gated_deltanet.py:189-197)
+    "prefill_k256": Shape(1, 32768, 16, 32, 256, 256, torch.bfloat16, 0.02),
 }
 STREAM_SEGMENT = 65536
 VARLEN_SEQS = 8

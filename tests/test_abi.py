@@ -82,7 +82,9 @@ def recurrent_call(**over):
     (dict(q=None), _lib.ERR_INVALID_ARGUMENT),
     (dict(chunk=32), _lib.ERR_UNSUPPORTED),
     (dict(K=96), _lib.ERR_UNSUPPORTED),
-    (dict(K=256), _lib.ERR_UNSUPPORTED),
+    (dict(K=512), _lib.ERR_UNSUPPORTED),
+    (dict(K=256, in_dtype=0), _lib.ERR_UNSUPPORTED),  # 256-wide keys take 16-bit inputs
+    (dict(K=256, V=80), _lib.ERR_UNSUPPORTED),        # and V a multiple of 32
     (dict(V=120), _lib.ERR_UNSUPPORTED),
     (dict(ws=None), _lib.ERR_INVALID_ARGUMENT),
     (dict(ws=FAKE + 8), _lib.ERR_INVALID_ARGUMENT),     # workspace must be 16-byte aligned

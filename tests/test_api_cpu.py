@@ -133,10 +133,16 @@ def test_entry_points_without_backward_refuse_grad_before_anything_runs():
 
 
 def test_head_widths_route_to_kernels_that_run():
-    """The widths a call runs at: the chunk kernel's K in {64, 128} and V a
-    multiple of 16 (the backward's {64, 128} when grad is wanted); wider keys
-    (up to 256) go to the recurrent kernel; above 256 there is no device path."""
+    """The widths a call runs at: the chunk kernels' K in {64, 128} with V a
+    multiple of 16, and K 256 (16-bit inputs) with V a multiple of 32 (the
+    backward's {64, 128} when grad is wanted); float32 keys above 128 go to
+    the recurrent kernel; above 256 there is no device path."""
     assert gd._chunk_widths(128, 128, False) == (128, 128)
+    assert gd._chunk_widths(200, 100, False) == (256, 128)
+    assert gd._chunk_widths(256, 80, False) == (256, 96)
+    assert gd._chunk_shape_ok(256, 96, torch.bfloat16) and gd._chunk_shape_ok(256, 64, torch.float16)
+    assert not gd._chunk_shape_ok(256, 64, torch.float32) and not gd._chunk_shape_ok(256, 48, torch.bfloat16)
+    assert gd._chunk_shape_ok(128, 48, torch.float32) and not gd._chunk_shape_ok(96, 64, torch.bfloat16)
     assert gd._chunk_widths(96, 40, False) == (128, 48)
     assert gd._chunk_widths(32, 16, False) == (64, 16)
     assert gd._chunk_widths(96, 40, True) == (128, 64)

@@ -3,7 +3,7 @@
 set_scan_backend's "fused" backend, scan.py:100, :143-161), checked against the
 oracle: every name select_kernel returns for a device tensor runs, every head
 width up to 256 runs (zero-padded to the kernels' widths, or through the
-recurrent kernel for K > 128), and gradients either flow (compared with the
+recurrent kernel for float32 inputs with K > 128), and gradients either flow (compared with the
 oracle's reverse mode) or the call raises.
 
 Tolerances: outputs 2e-2 and final states 1e-3 (infinity-norm relative, against
@@ -48,22 +48,26 @@ def test_fused_backend_selects_and_runs_the_device_kernel(length, expect):
     assert_parity(f"select {name} T={length}", o, o_ref, s, s_ref)
 
 
-@pytest.mark.parametrize("dk,dv,hk,hv,length", [
-    (256, 256, 1, 2, 150),   # K above the chunk kernel's widths: the recurrent kernel over every token
-    (256, 64, 2, 2, 70),
-    (64, 48, 2, 4, 200),     # V a multiple of 16 the kernels do not pad
-    (96, 40, 1, 2, 130),     # both widths padded (K 96 -> 128, V 40 -> 48)
-    (32, 16, 2, 2, 100),     # K 32 -> 64
-    (200, 100, 1, 1, 90),    # K 200 -> 256, V 100 -> 128 on the recurrent path
+@pytest.mark.parametrize("dk,dv,hk,hv,length,dtype", [
+    (256, 256, 1, 2, 150, torch.bfloat16),  # K 256: the chunk kernel for 256-wide keys
+    (256, 64, 2, 2, 70, torch.bfloat16),
+    (200, 100, 1, 1, 90, torch.float16),    # K 200 -> 256, V 100 -> 128 (a multiple of 32)
+    (256, 64, 1, 2, 70, torch.float32),     # float32 above K 128: the recurrent kernel over every token
+    (200, 100, 1, 1, 90, torch.float32),    # K 200 -> 256, V 100 -> 128 on the recurrent path
+    (64, 48, 2, 4, 200, torch.bfloat16),    # V a multiple of 16 the kernels do not pad
+    (96, 40, 1, 2, 130, torch.bfloat16),    # both widths padded (K 96 -> 128, V 40 -> 48)
+    (32, 16, 2, 2, 100, torch.bfloat16),    # K 32 -> 64
 ])
 @pytest.mark.parametrize("kernel", ["hip", "chunked"])
-def test_every_head_width_up_to_256_runs(dk, dv, hk, hv, length, kernel):
-    q, k, v, g, beta, h0 = inputs(1, length, hk, hv, dk, dv, seed=dk + dv)
+def test_every_head_width_up_to_256_runs(dk, dv, hk, hv, length, dtype, kernel):
+    q, k, v, g, beta, h0 = inputs(1, length, hk, hv, dk, dv, dtype=dtype, seed=dk + dv)
     dq, dk_, dv_, dg, db, dh = to_dev(q, k, v, g, beta, h0)
-    # the gate admits the chunk kernel's key widths only: a wider key would run
-    # token by token, so in the reference's wiring fla or chunked keeps it
-    assert gd.hip_usable(dh, dq) == (dk <= 128)
-    assert gd.select_kernel("fused", False, length, dh, dq) == ("hip" if dk <= 128 else "chunked")
+    # the gate admits what runs chunkwise: K <= 128, and K <= 256 for 16-bit
+    # inputs; float32 inputs wider than 128 would run token by token, so in the
+    # reference's wiring fla or chunked keeps them
+    chunkwise = dk <= 128 or dtype != torch.float32
+    assert gd.hip_usable(dh, dq) == chunkwise
+    assert gd.select_kernel("fused", False, length, dh, dq) == ("hip" if chunkwise else "chunked")
     o, s = gd.gated_delta_rule(dq, dk_, dv_, dg, db, dk ** -0.5, dh, kernel=kernel)
     torch.cuda.synchronize()
     assert o.shape == (1, length, hv, dv) and s.shape == (1, hv, dk, dv)
@@ -80,17 +84,19 @@ def test_sequential_at_odd_widths(dk, dv):
     assert_parity(f"sequential K={dk} V={dv}", o, o_ref, s, s_ref)
 
 
-def test_packed_sequences_with_k256():
-    """cu_seqlens at K = 256 (recurrent route, one call per sequence), an empty
-    sequence keeping its initial state."""
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_packed_sequences_with_k256(dtype):
+    """cu_seqlens at K = 256 (bfloat16: the chunk kernel for 256-wide keys;
+    float32: the recurrent route, one call per sequence), an empty sequence
+    keeping its initial state."""
     lengths = [70, 0, 130, 5]
-    q, k, v, g, beta, h0 = inputs(1, sum(lengths), 1, 2, 256, 128, seed=3, nstates=len(lengths))
+    q, k, v, g, beta, h0 = inputs(1, sum(lengths), 1, 2, 256, 128, dtype=dtype, seed=3, nstates=len(lengths))
     cu = cu_seqlens_of(lengths)
     o, s = gd.gated_delta_rule(*to_dev(q, k, v, g, beta), 256 ** -0.5, h0.to(DEV), kernel="hip",
                                cu_seqlens=cu.to(DEV))
     torch.cuda.synchronize()
     o_ref, s_ref = oracle(q, k, v, g, beta, 256 ** -0.5, h0, cu_seqlens=cu)
-    assert_parity("packed K=256", o, o_ref, s, s_ref)
+    assert_parity(f"packed K=256 {dtype}", o, o_ref, s, s_ref)
     assert torch.equal(s[1].cpu(), h0[1])
 
 
@@ -140,12 +146,13 @@ def test_training_call_without_a_device_backward_raises():
     with torch.no_grad():
         o, _ = gd.gated_delta_rule(*leaves[:5], 0.0625, leaves[5], kernel="hip")
     assert not o.requires_grad
-    # the gate sends such calls (K = 256, above the chunk kernel's keys) to the
-    # reference's path, with or without a gradient
+    # the gate sends such calls (K = 256, above the chunk backward's keys) to
+    # the reference's path when a gradient is wanted, and takes them (16-bit
+    # inputs, the chunk kernel for 256-wide keys) for inference
     assert not gd.hip_usable(leaves[5], leaves[0])
     assert gd.select_kernel("fused", False, 100, leaves[5], leaves[0]) == "chunked"
     with torch.no_grad():
-        assert not gd.hip_usable(leaves[5], leaves[0])
+        assert gd.hip_usable(leaves[5], leaves[0])
     # a value width the chunk kernel takes but its backward does not: usable for
     # inference only
     wide_v = torch.zeros(1, 2, 64, 256, device=DEV, requires_grad=True)
