@@ -404,6 +404,41 @@ def bench_prefill_small(steps=50, warmup=5):
                                                    "frac": flops / ksec / 1e12 / MFMA_PEAK_TFLOPS}}
 
 
+def bench_prefill_k256(steps=10, warmup=2, serial_tokens=2048):
+    """The prefill at 256-wide key and value heads (prefill_k256: B=1, T=32768,
+    Hk=16 -> Hv=32, K=V=256, bf16), the widest the reference's device gate
+    admits: the chunk path (prep kernel, then the scan for 256-wide keys),
+    beside the token-serial recurrent kernel that such heads ran on before,
+    timed over the first `serial_tokens` tokens and scaled to the call."""
+    import torch
+    from pseudobrain_amd import gated_deltanet as gd
+    from pseudobrain_amd.workloads import WORKLOADS, workload
+    s = WORKLOADS["prefill_k256"]
+    q, k, v, g, beta, h0 = (x.cuda() for x in workload("prefill_k256", seed=0))
+    scale = s.dk ** -0.5
+    out = torch.empty(1, s.length, s.hv, s.dv, dtype=torch.bfloat16, device="cuda")
+
+    def step():
+        gd.chunk_fwd(q, k, v, g, beta, scale, h0, out=out)
+
+    sec, ksec = timed_steps(step, steps, warmup)
+    flops = prefill_flops(s.length, s.hv, s.dk, s.dv)
+    n = serial_tokens
+    state = h0.clone()
+
+    def serial():
+        gd.recurrent_fwd(q[:, :n], k[:, :n], v[:, :n], g[:, :n], beta[:, :n], scale, state, state)
+
+    ssec, _ = timed_steps(serial, 2, 1, device_warm_s=0.0)
+    return {"workload": "prefill_k256", "B": s.batch, "T": s.length, "Hk": s.hk, "Hv": s.hv, "K": s.dk,
+            "V": s.dv, "value": s.length / sec / 1e6, "unit": "Mtok/s", "ms_per_call": sec * 1e3,
+            "roofline": {"bound": "mfma", "achieved": flops / ksec / 1e12, "peak": MFMA_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": flops / ksec / 1e12 / MFMA_PEAK_TFLOPS,
+                         "kernel_ms": ksec * 1e3, "algorithmic_flops": flops},
+            "token_serial_ms_per_call": ssec * 1e3 * s.length / n,
+            "token_serial_sample_tokens": n}
+
+
 def bench_decode(batch, steps, warmup=10, state_dtype=None, pools=1, resident=False):
     """Decode steps at `batch` sequences. With pools > 1 the steps rotate over
     that many separate state pools (step i updates pool i % pools), so that
@@ -701,6 +736,7 @@ def main(argv=None):
     ap.add_argument("--no-layer", action="store_true", help="skip the layer prologue/epilogue kernels")
     ap.add_argument("--no-long", action="store_true", help="skip the varlen and streamed prefill workloads")
     ap.add_argument("--no-backward", action="store_true", help="skip the chunk backward")
+    ap.add_argument("--no-k256", action="store_true", help="skip the 256-wide-head prefill")
     args = ap.parse_args(argv)
     world = int(os.environ.get("WORLD_SIZE", args.gpus))
     if args.gpus != 1 or world != 1:
@@ -744,6 +780,8 @@ def main(argv=None):
     if cpu is not None:
         result["cpu_baseline_ratio"] = result["value"] / cpu["value"]
     result["prefill_small"] = bench_prefill_small()
+    if not args.no_k256:
+        result["prefill_k256_ungraded"] = bench_prefill_k256()
     if not args.no_decode:
         # the c2 workload: one pool stepped 1000 times in place, declared resident
         dec = bench_decode(64, args.decode_steps, resident=True)
