@@ -73,26 +73,27 @@ int dispatch_in(const ChunkParams &p, long records, int in_dtype, int out_dtype,
 }
 
 // 256-wide keys, 16-bit inputs: the prep kernel, then the k256 scan with the
-// waves per workgroup of k256_waves. PBGDN_K256_WAVES=2|4 in the
-// environment forces them (for measurements) where they divide V.
-inline int k256_waves_forced() {
-  static const int forced = [] {
-    const char *e = getenv("PBGDN_K256_WAVES");
-    const int w = e ? atoi(e) : 0;
-    return (w == 2 || w == 4) ? w : 0;
-  }();
-  return forced;
+// tiles per workgroup of k256_waves (two waves per tile, each a half of the
+// keys, with two tiles). PBGDN_K256_WAVES=2|4 and PBGDN_K256_SPLIT=1|2 in the
+// environment force them (for measurements) where they apply.
+inline int env_choice(const char *name, int a, int b) {
+  const char *e = getenv(name);
+  const int w = e ? atoi(e) : 0;
+  return (w == a || w == b) ? w : 0;
 }
 
 template <typename TIn>
 int run_chunk_k256(const ChunkParams &p, long records, int out_dtype, hipStream_t s) {
+  static const int forced_wt = env_choice("PBGDN_K256_WAVES", 2, 4);
+  static const int forced_kh = env_choice("PBGDN_K256_SPLIT", 1, 2);
   const int st = launch_prep<256, TIn>(p, records, s);
   if (st != PBGDN_OK) return st;
   int wt = k256_waves(p.V, static_cast<long>(p.num_seqs) * p.Hv, p.cus);
-  const int forced = k256_waves_forced();
-  if (forced && p.V % (16 * forced) == 0) wt = forced;
-  if (out_dtype == PBGDN_F32) return launch_k256<TIn, float>(p, wt, s);
-  return launch_k256<TIn, TIn>(p, wt, s);  // out_dtype == in_dtype, checked by the caller
+  if (forced_wt && p.V % (16 * forced_wt) == 0) wt = forced_wt;
+  int kh = wt == 2 ? 2 : 1;
+  if (forced_kh && (forced_kh == 1 || wt == 2)) kh = forced_kh;
+  if (out_dtype == PBGDN_F32) return launch_k256<TIn, float>(p, wt, kh, s);
+  return launch_k256<TIn, TIn>(p, wt, kh, s);  // out_dtype == in_dtype, checked by the caller
 }
 
 // The prefill with the layer epilogue in the wide scan (p.o is hs).

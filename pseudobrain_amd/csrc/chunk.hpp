@@ -444,10 +444,11 @@ template <int K, typename TIn, typename TOut>
 int launch_scan(const ChunkParams &p, hipStream_t stream);
 template <int K, typename TIn, typename TOut, bool EPI>
 int launch_wide(const ChunkParams &p, hipStream_t stream);
-// The scan for 256-wide keys (chunk_k256.hip): `wt` waves (4 or 2) per
-// workgroup, 16 wt columns each; k256_waves picks wt for a call.
+// The scan for 256-wide keys (chunk_k256.hip): `wt` tiles (4 or 2) of 16
+// columns per workgroup, each held by `kh` waves (1, or 2 with wt = 2: each
+// wave a half of the keys); k256_waves picks wt for a call.
 template <typename TIn, typename TOut>
-int launch_k256(const ChunkParams &p, int wt, hipStream_t stream);
+int launch_k256(const ChunkParams &p, int wt, int kh, hipStream_t stream);
 int k256_waves(int V, long pairs_of_seq_and_head, int cus);
 
 }  // namespace pbgdn

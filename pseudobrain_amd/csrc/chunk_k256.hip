@@ -1,7 +1,8 @@
 // Scan kernel of the chunkwise prefill for 256-wide keys (128 < K <= 256, the
 // keys zero-padded to 256 by the caller): the state-dependent part, chunk by
 // chunk (the serial loop of delta_rule_chunked, pseudobrain/gated_deltanet.py:158-165),
-// one wave per 16-column tile of the state and WT tiles per workgroup.
+// KH waves (1 or 2) per 16-column tile of the state and WT tiles per
+// workgroup.
 //
 // The arithmetic and the operand layouts are the wide scan's (chunk_wide.hip)
 // at twice the keys: the fp32 state tile S [256, 16] is 16 MFMA accumulator
@@ -32,12 +33,25 @@
 // (gated_deltanet.py:127), and so do the record units no scan reads
 // (rec_unused_unit).
 //
-// WT = 2 or 4 waves (32 or 64 columns per workgroup), one per SIMD: the
+// WT = 2 or 4 tiles (32 or 64 columns per workgroup), one wave per SIMD: the
 // LDS allows one workgroup per CU, and a wave holds more registers than two
-// waves per SIMD could (eight waves spilled 52 registers). Two waves spread
+// waves per SIMD could (eight waves spilled 52 registers). Two tiles spread
 // a value head over more workgroups, and so over more CUs, at the price of
-// staging the chunk's K and Q rows once per workgroup. Inputs and the state
-// operands are 16-bit (bf16 or fp16), o in the inputs' type or float32.
+// staging the chunk's K and Q rows once per workgroup.
+//
+// Key halves (KH = 2, with WT = 2: four waves). At one sequence the call has
+// only as many tiles as (value head, 16 columns) pairs, 512 at 32 heads of
+// 256 columns, and a lone wave per SIMD keeps its MFMA pipe busy a third of
+// the time. So each tile can be held by two waves, each owning 128 of the
+// keys (8 state tiles): each forms its partial K S and (Q S)^T over its keys,
+// writes them to LDS before the mid barrier and adds the other wave's after
+// it (one addition, the same in both waves), so both hold the whole X and
+// form U; each then updates its own state rows, and each forms and stores
+// two of the four row tiles of O. A wave issues 90 MFMAs a step instead of
+// 172; the exchange takes 32 KiB of LDS (158 KiB in all).
+//
+// Inputs and the state operands are 16-bit (bf16 or fp16), o in the inputs'
+// type or float32.
 #include "chunk.hpp"
 
 namespace pbgdn {
@@ -47,7 +61,7 @@ constexpr int KW = 256;  // key width of this kernel
 
 typedef unsigned int u32x4_k __attribute__((ext_vector_type(4)));
 
-template <int WT>
+template <int WT, int KH>
 struct K256Layout {
   static constexpr int ROW = 2 * KW;                 // bytes of a staged K or Q row (512)
   static constexpr int MAT = CH * ROW;               // one chunk of K or Q (32 KiB)
@@ -57,7 +71,8 @@ struct K256Layout {
   static constexpr int R_OFF = K_OFF + 2 * MAT;      // [2] record
   static constexpr int Q_OFF = R_OFF + 2 * REC_BYTES;
   static constexpr int V_OFF = Q_OFF + MAT;
-  static constexpr int BYTES = V_OFF + VMAT;
+  static constexpr int XCH = V_OFF + VMAT;           // KH = 2: [wave][8 fp32 tiles] partial X and (Q S)^T
+  static constexpr int BYTES = XCH + (KH == 2 ? WT * KH * 8 * 1024 : 0);
   __device__ static constexpr int kmat(int b) { return K_OFF + b * MAT; }
   __device__ static constexpr int rec(int b) { return R_OFF + b * REC_BYTES; }
 };
@@ -75,29 +90,32 @@ __host__ __device__ constexpr int vswz_k(int r) {
   return 2 * ((r >> (WT == 8 ? 0 : WT == 4 ? 1 : 2)) & (WT - 1));
 }
 
-template <typename TIn, typename TOut, int WT>
+template <typename TIn, typename TOut, int WT, int KH>
 struct K256Block {
-  using L = K256Layout<WT>;
+  using L = K256Layout<WT, KH>;
   using Op = OpOf<TIn>;
   using O4 = typename Op::T4;
   using O8 = typename Op::T8;
   static constexpr int WCOLS = 16 * WT;            // value columns per workgroup
-  static constexpr int NKT = KW / 16;              // state tiles
-  static constexpr int KS = KW / 32;               // key contraction steps
-  static constexpr int KQ_WAVE = L::MAT / 1024 / WT;  // K (or Q) DMA instructions per wave
-  static constexpr int NB = 8 / WT;                // swizzle classes of a wave's K/Q instructions
+  static constexpr int WAVES = WT * KH;            // waves per workgroup
+  static constexpr int KPW = KW / KH;              // keys of a wave's state rows
+  static constexpr int NKT = KPW / 16;             // state tiles of a wave
+  static constexpr int KS = KPW / 32;              // key contraction steps of a wave
+  static constexpr int KQ_WAVE = L::MAT / 1024 / WAVES;  // K (or Q) DMA instructions per wave
+  static constexpr int NB = 8 / WAVES;             // swizzle classes of a wave's K/Q instructions
   static constexpr int DMA_REC = REC_BYTES / 1024;
-  static constexpr int V_WAVE = L::VMAT / 1024 / WT;  // V DMA instructions per wave
+  static constexpr int V_WAVE = L::VMAT / 1024 / WAVES;  // V DMA instructions per wave
   static constexpr int VRPI = 1024 / L::VROW;      // V rows per DMA instruction
-  static constexpr int OUT_STORES = 4;             // O stores a wave issues per chunk
-  static_assert(WT == 2 || WT == 4, "2 or 4 waves");
+  static constexpr int OROWS = 4 / KH;             // O row tiles a wave forms and stores
+  static constexpr int OUT_STORES = OROWS;         // O stores a wave issues per chunk
+  static_assert((WT == 2 || WT == 4) && (KH == 1 || (KH == 2 && WT == 2)), "2 or 4 waves, or 2 x 2 key halves");
   static_assert(sizeof(TIn) == 2, "16-bit inputs (staged as they are)");
   static_assert(L::BYTES <= 160 * 1024, "LDS");
-  static_assert(REC_BYTES % 1024 == 0 && L::VMAT % (1024 * WT) == 0 && V_WAVE == 2, "whole DMA instructions");
+  static_assert(REC_BYTES % 1024 == 0 && L::VMAT % (1024 * WAVES) == 0 && V_WAVE * KH == 2, "whole DMA instructions");
 
   unsigned char *lds;
   const ChunkParams &p;
-  int lane, c16, g4, wave, h, hk, col0, v0, seq;
+  int lane, c16, g4, wave, tile, kh, h, hk, col0, v0, seq;
   long bos, eos, nchunks;
   float4_t s[NKT];  // the state tile, accumulator layout, permuted key rows
 
@@ -117,6 +135,8 @@ struct K256Block {
     const int tid = threadIdx.x;
     lane = tid & 63;
     wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    tile = wave % WT;  // the 16-column tile of this wave
+    kh = wave / WT;    // and its half of the keys (KH = 2)
     c16 = lane & 15;
     g4 = lane >> 4;
     // Block -> (sequence, value head, column group); the column groups and the
@@ -131,19 +151,20 @@ struct K256Block {
     hk = kgrp % p.Hk;
     h = hk * (p.Hv / p.Hk) + member / groups;
     col0 = (member % groups) * WCOLS;
-    v0 = col0 + 16 * wave;
+    v0 = col0 + 16 * tile;
     seq_bounds(p, seq, bos, eos);
     nchunks = (eos - bos + CH - 1) / CH;
 
     const int k = c16 >> 2, q = c16 & 3;
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
-      xa[kk] = c16 * L::ROW + ((4 * kk + g4) ^ kswz(c16)) * 16;  // row c, piece 4kk + g
-      // lane 4k + q of group g: token row 4g + k, keys 32kk + 8q + 4p (piece 4kk + q, half p)
-      tr[kk] = (4 * g4 + k) * L::ROW + ((4 * kk + q) ^ kswz(4 * g4 + k)) * 16;
+      const int kp = kk + KS * kh;  // the key step within the whole row
+      xa[kk] = c16 * L::ROW + ((4 * kp + g4) ^ kswz(c16)) * 16;  // row c, piece 4kp + g
+      // lane 4k + q of group g: token row 4g + k, keys 32kp + 8q + 4p (piece 4kp + q, half p)
+      tr[kk] = (4 * g4 + k) * L::ROW + ((4 * kp + q) ^ kswz(4 * g4 + k)) * 16;
     }
-    // lane 4k + q of group g: token row 4g + k, columns 16 wave + 4q.. (piece 2 wave + q/2, half q & 1)
-    vtr = (4 * g4 + k) * L::VROW + (((2 * wave + (q >> 1)) ^ vswz_k<WT>(4 * g4 + k)) * 16) + 8 * (q & 1);
+    // lane 4k + q of group g: token row 4g + k, columns 16 tile + 4q.. (piece 2 tile + q/2, half q & 1)
+    vtr = (4 * g4 + k) * L::VROW + (((2 * tile + (q >> 1)) ^ vswz_k<WT>(4 * g4 + k)) * 16) + 8 * (q & 1);
     // Tb / QKD fragment rows: tokens 32kk + 4g.. (fragment lane (g/2, c), half
     // g&1) and 32kk + 16 + 4g.. (lane (2 + g/2, c))
     tbo0 = (16 * (g4 >> 1) + c16) * 16 + 8 * (g4 & 1);
@@ -151,18 +172,18 @@ struct K256Block {
     o_off = (c16 * p.Hv * p.V + v0 + 4 * g4) * static_cast<uint32_t>(sizeof(TOut));
     // K/Q instruction i covers token rows 2i, 2i+1: lane l fills row 2i + l/32
     // at position l%32 (piece (l%32) ^ kswz(row)). This wave's are i = wave +
-    // WT s, rows 2 wave + 2 WT s + l/32: instructions 8 apart (s NB apart)
-    // are 16 rows apart and share a swizzle, so class j = s % NB holds the
-    // offset of s = j and the others add 16 rows per NB.
+    // WAVES s, rows 2 wave + 2 WAVES s + l/32: instructions 8 apart (s NB
+    // apart) are 16 rows apart and share a swizzle, so class j = s % NB holds
+    // the offset of s = j and the others add 16 rows per NB.
     const uint32_t kqs = static_cast<uint32_t>(p.Hk) * KW * 2;  // bytes per token row of k, q
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
-      const int r = 2 * wave + 2 * WT * j + (lane >> 5);
+      const int r = 2 * wave + 2 * WAVES * j + (lane >> 5);
       dma_kq[j] = static_cast<uint32_t>(r) * kqs + ((lane & 31) ^ kswz(r)) * 16;
     }
     // V instruction i covers VRPI rows of 2 WT pieces: lane l fills row
-    // VRPI i + l / (2 WT) at position l % (2 WT); this wave's i = wave, wave + WT
-    // (32 rows apart: the same swizzle).
+    // VRPI i + l / (2 WT) at position l % (2 WT); this wave's i = wave (and
+    // wave + WT when KH = 1: 32 rows on, the same swizzle).
     const int rv = wave * VRPI + lane / (2 * WT);
     dma_v = static_cast<uint32_t>(rv) * p.Hv * p.V * 2 + ((lane % (2 * WT)) ^ vswz_k<WT>(rv)) * 16;
     const long kq0 = (bos * p.Hk + hk) * static_cast<long>(KW) * 2;
@@ -205,11 +226,11 @@ struct K256Block {
 #pragma unroll
     for (int s_ = 0; s_ < KQ_WAVE; ++s_) {
       const uint32_t off = dma_kq[s_ % NB] + static_cast<uint32_t>(16 * (s_ / NB)) * static_cast<uint32_t>(kqs);
-      dma(rk, L::kmat(b) + 1024 * (wave + WT * s_), off);
+      dma(rk, L::kmat(b) + 1024 * (wave + WAVES * s_), off);
     }
 #pragma unroll
-    for (int s_ = 0; s_ < (DMA_REC + WT - 1) / WT; ++s_) {
-      const int i = wave + WT * s_;
+    for (int s_ = 0; s_ < (DMA_REC + WAVES - 1) / WAVES; ++s_) {
+      const int i = wave + WAVES * s_;
       const uint32_t roff = 1024 * i + lane * 16;  // units no scan reads: an out-of-range load stages zeros
       if (i < DMA_REC) dma(rr, L::rec(b) + 1024 * i, rec_unused_unit(static_cast<int>(roff)) ? OUT_OF_RANGE : roff);
     }
@@ -223,11 +244,11 @@ struct K256Block {
 #pragma unroll
     for (int s_ = 0; s_ < KQ_WAVE; ++s_) {
       const uint32_t off = dma_kq[s_ % NB] + static_cast<uint32_t>(16 * (s_ / NB)) * static_cast<uint32_t>(kqs);
-      dma(rq, L::Q_OFF + 1024 * (wave + WT * s_), off);
+      dma(rq, L::Q_OFF + 1024 * (wave + WAVES * s_), off);
     }
 #pragma unroll
     for (int s_ = 0; s_ < V_WAVE; ++s_) {
-      dma(rv, L::V_OFF + 1024 * (wave + WT * s_), dma_v + static_cast<uint32_t>(32 * s_) * static_cast<uint32_t>(vs));
+      dma(rv, L::V_OFF + 1024 * (wave + WAVES * s_), dma_v + static_cast<uint32_t>(32 * s_) * static_cast<uint32_t>(vs));
     }
   }
   __device__ __forceinline__ void advance() {
@@ -240,8 +261,10 @@ struct K256Block {
   }
 
   // ------------------------------------------------------------------ state I/O
-  // Lane (g, c) holds rows 4g + i of state tile t = 2kk + p: key 32kk + 8g + 4p + i.
-  __device__ __forceinline__ int key_of(int t, int i) const { return 32 * (t >> 1) + 8 * g4 + 4 * (t & 1) + i; }
+  // Lane (g, c) holds rows 4g + i of state tile t = 2kk + p: key KPW kh + 32kk + 8g + 4p + i.
+  __device__ __forceinline__ int key_of(int t, int i) const {
+    return KPW * kh + 32 * (t >> 1) + 8 * g4 + 4 * (t & 1) + i;
+  }
   __device__ __forceinline__ long slot_of() const {
     return p.state_idx ? static_cast<long>(p.state_idx[seq]) : static_cast<long>(seq);
   }
@@ -385,15 +408,33 @@ struct K256Block {
 #pragma unroll
         for (int r = 0; r < 4; ++r) ah[r] = mma(kf[cur][r], slo, ah[r]);
       }
-      float4_t x[4];
+      // KH = 2: this wave's partial K S and (Q S)^T (its half of the keys) to
+      // LDS for the other wave of its tile
+      const uint32_t xw = L::XCH + static_cast<uint32_t>(wave) * 8192 + lane * 16;
+      if constexpr (KH == 2) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) x[r] = Op::bits_to_float(vraw[r]) - gam[r] * ah[r];
-      // mid: the step's reads of Q and V are done in every wave (each used
-      // its values above); chunk n+1's go into the same buffers
+        for (int r = 0; r < 4; ++r) {
+          *reinterpret_cast<float4_t *>(lds + xw + 1024 * r) = ah[r];
+          *reinterpret_cast<float4_t *>(lds + xw + 1024 * (4 + r)) = aq[r];
+        }
+      }
+      // mid: the step's reads of Q and V are done in every wave, and the
+      // partials are in LDS; chunk n+1's Q and V go into the same buffers
       __builtin_amdgcn_sched_barrier(0);
       barrier();
       issue_qv();
       advance();
+      if constexpr (KH == 2) {  // whole sums over the keys (one addition: the same in both waves)
+        const uint32_t xo = L::XCH + static_cast<uint32_t>(tile + WT * (1 - kh)) * 8192 + lane * 16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          ah[r] += ld<float4_t>(xo + 1024 * r);
+          aq[r] += ld<float4_t>(xo + 1024 * (4 + r));
+        }
+      }
+      float4_t x[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[r] = Op::bits_to_float(vraw[r]) - gam[r] * ah[r];
       // X beyond X_LIMIT anywhere in the tile (a wave vote): scale it into
       // range (range_scale); U, its products and O are restored in fp32 below.
       const bool big = __builtin_amdgcn_ballot_w64(tile_max(x) > X_LIMIT) != 0;
@@ -407,10 +448,12 @@ struct K256Block {
 #pragma unroll
       for (int r = 0; r < 4; ++r) dec[r] = ld<float4_t>(rl + SC_DEC + 64 * r);
       const float g63 = ld<float>(rl + SC_GAM + (CH - 1) * 4 - 16 * g4);
-      const uint32_t tb[KS] = {opaque(km + tr[0]), opaque(km + tr[1]), opaque(km + tr[2]), opaque(km + tr[3]),
-                               opaque(km + tr[4]), opaque(km + tr[5]), opaque(km + tr[6]), opaque(km + tr[7])};
-      // K^T fragments in four groups of 8 state tiles: group j = (token step
-      // j / 2, tiles 8 (j % 2) ..), group j+1 read while group j multiplies
+      uint32_t tb[KS];
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) tb[kk] = opaque(km + tr[kk]);
+      // K^T fragments in groups of 8 state tiles: group j = (token step
+      // j / GPS, tiles 8 (j % GPS) ..), group j+1 read while group j multiplies
+      constexpr int GPS = NKT / 8, NG = 2 * GPS;
       O8 tf[2][8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) tf[0][i] = kt_frag(tb[i >> 1], i & 1, 0);
@@ -445,15 +488,15 @@ struct K256Block {
 #pragma unroll
       for (int t = 0; t < NKT; ++t) s[t] *= g63;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < NG; ++j) {
         const int cur = j & 1;
-        if (j + 1 < 4) {
-          const int ks = (j + 1) >> 1, t0 = 8 * ((j + 1) & 1);
+        if (j + 1 < NG) {
+          const int ks = (j + 1) / GPS, t0 = 8 * ((j + 1) % GPS);
 #pragma unroll
           for (int i = 0; i < 8; ++i) tf[cur ^ 1][i] = kt_frag(tb[(t0 + i) >> 1], (t0 + i) & 1, ks);
         }
         __builtin_amdgcn_sched_barrier(0);
-        const int ks = j >> 1, t0 = 8 * (j & 1);
+        const int ks = j / GPS, t0 = 8 * (j % GPS);
 #pragma unroll
         for (int i = 0; i < 8; ++i) s[t0 + i] = mma(tf[cur][i], dhi[ks], s[t0 + i]);
 #pragma unroll
@@ -472,30 +515,38 @@ struct K256Block {
 #pragma unroll
         for (int r = 0; r < 4; ++r) gsc[r] = ld<float>(rg + 64 * r);
       }
-      float4_t o[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        o[r] = aq[r] * (big ? gsc[r] * down : gsc[r]);
-        o[r] = mfma32(ub[0], qkf[frag_index(r, 0)], o[r]);
-      }
-      o[2] = mfma32(ub[1], qkf[frag_index(2, 1)], o[2]);
-      o[3] = mfma32(ub[1], qkf[frag_index(3, 1)], o[3]);
-      if (big) {
-        const float up = 1.f / down;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) o[r] *= up;
-      }
       const long rows = oleft < CH ? oleft : CH;  // >= 1: chunk n holds tokens
       const __amdgpu_buffer_rsrc_t ro = rsrc(op, (rows - 1) * ostride + p.V * static_cast<long>(sizeof(TOut)));
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
+      const float up = 1.f / down;
+      auto o_row = [&](auto rconst) {  // row tile r of O, formed and stored
+        constexpr int r = decltype(rconst)::value;
+        float4_t o = aq[r] * (big ? gsc[r] * down : gsc[r]);
+        o = mfma32(ub[0], qkf[frag_index(r, 0)], o);
+        if constexpr (r >= 2) o = mfma32(ub[1], qkf[frag_index(r, 1)], o);
+        if (big) o *= up;
         const uint32_t off = o_off + 16 * r * static_cast<uint32_t>(ostride);
         if constexpr (sizeof(TOut) == 4) {
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32_t, o[r]), ro, off, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32_t, o), ro, off, 0, 0);
         } else {
-          const O4 x4 = Op::from(o[r]);
+          const O4 x4 = Op::from(o);
           __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32_t, x4), ro, off, 0, 0);
         }
+      };
+      using R0 = std::integral_constant<int, 0>;
+      using R1 = std::integral_constant<int, 1>;
+      using R2 = std::integral_constant<int, 2>;
+      using R3 = std::integral_constant<int, 3>;
+      if constexpr (KH == 1) {
+        o_row(R0{});
+        o_row(R1{});
+        o_row(R2{});
+        o_row(R3{});
+      } else if (kh == 0) {  // the two waves of a tile split its rows
+        o_row(R0{});
+        o_row(R1{});
+      } else {
+        o_row(R2{});
+        o_row(R3{});
       }
       op += CH * ostride;
       oleft -= CH;
@@ -511,24 +562,24 @@ struct K256Block {
 };
 
 // One workgroup per CU (the LDS), one wave per SIMD (512 registers).
-template <typename TIn, typename TOut, int WT>
-__global__ __launch_bounds__(64 * WT) __attribute__((amdgpu_waves_per_eu(1, 1))) void k256_kernel(ChunkParams p) {
+template <typename TIn, typename TOut, int WT, int KH>
+__global__ __launch_bounds__(64 * WT * KH) __attribute__((amdgpu_waves_per_eu(1, 1))) void k256_kernel(ChunkParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  PBGDN_POISON_LDS(smem_raw, K256Layout<WT>::BYTES);
+  PBGDN_POISON_LDS(smem_raw, (K256Layout<WT, KH>::BYTES));
   PBGDN_POISON_SYNC();
-  K256Block<TIn, TOut, WT> blk(smem_raw, p);
+  K256Block<TIn, TOut, WT, KH> blk(smem_raw, p);
   blk.run();
 }
 
-template <typename TIn, typename TOut, int WT>
+template <typename TIn, typename TOut, int WT, int KH>
 int launch_k256_wt(const ChunkParams &p, hipStream_t stream) {
   static std::atomic<bool> configured[MAX_DEVICES];  // the attribute is set per device
-  const size_t smem = K256Layout<WT>::BYTES;
-  auto kernel = k256_kernel<TIn, TOut, WT>;
+  const size_t smem = K256Layout<WT, KH>::BYTES;
+  auto kernel = k256_kernel<TIn, TOut, WT, KH>;
   if (!smem_configured(reinterpret_cast<const void *>(kernel), smem, configured)) return PBGDN_ERR_LAUNCH;
   const long total = static_cast<long>(p.V / (16 * WT)) * p.Hv * p.num_seqs;
   if (total > 0x7fffffffL) return PBGDN_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(total)), dim3(64 * WT), smem, stream, p);
+  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(total)), dim3(64 * WT * KH), smem, stream, p);
   return hipGetLastError() == hipSuccess ? PBGDN_OK : PBGDN_ERR_LAUNCH;
 }
 
@@ -541,18 +592,17 @@ int k256_waves(int V, long pairs_of_seq_and_head, int cus) {
 }
 
 template <typename TIn, typename TOut>
-int launch_k256(const ChunkParams &p, int wt, hipStream_t stream) {
+int launch_k256(const ChunkParams &p, int wt, int kh, hipStream_t stream) {
   if (p.V % (16 * wt) != 0) return PBGDN_ERR_UNSUPPORTED;
-  switch (wt) {
-    case 4: return launch_k256_wt<TIn, TOut, 4>(p, stream);
-    case 2: return launch_k256_wt<TIn, TOut, 2>(p, stream);
-    default: return PBGDN_ERR_UNSUPPORTED;
-  }
+  if (wt == 4 && kh == 1) return launch_k256_wt<TIn, TOut, 4, 1>(p, stream);
+  if (wt == 2 && kh == 1) return launch_k256_wt<TIn, TOut, 2, 1>(p, stream);
+  if (wt == 2 && kh == 2) return launch_k256_wt<TIn, TOut, 2, 2>(p, stream);
+  return PBGDN_ERR_UNSUPPORTED;
 }
 
-template int launch_k256<u16, u16>(const ChunkParams &, int, hipStream_t);
-template int launch_k256<u16, float>(const ChunkParams &, int, hipStream_t);
-template int launch_k256<half_t, half_t>(const ChunkParams &, int, hipStream_t);
-template int launch_k256<half_t, float>(const ChunkParams &, int, hipStream_t);
+template int launch_k256<u16, u16>(const ChunkParams &, int, int, hipStream_t);
+template int launch_k256<u16, float>(const ChunkParams &, int, int, hipStream_t);
+template int launch_k256<half_t, half_t>(const ChunkParams &, int, int, hipStream_t);
+template int launch_k256<half_t, float>(const ChunkParams &, int, int, hipStream_t);
 
 }  // namespace pbgdn

@@ -20,8 +20,9 @@ import torch
 from pseudobrain_amd import _lib
 from pseudobrain_amd import gated_deltanet as gd
 from pseudobrain_amd.workloads import generate
-from tests import (test_gpu_backward, test_gpu_chunk, test_gpu_chunk_layer, test_gpu_decode_layer, test_gpu_fla_schema,
-                   test_gpu_layer, test_gpu_prologue_varlen, test_gpu_recurrent, test_gpu_state_pools, test_gpu_wide)
+from tests import (test_gpu_backward, test_gpu_chunk, test_gpu_chunk_k256, test_gpu_chunk_layer, test_gpu_decode_layer,
+                   test_gpu_fla_schema, test_gpu_layer, test_gpu_prologue_varlen, test_gpu_recurrent,
+                   test_gpu_state_pools, test_gpu_wide)
 
 pytestmark = pytest.mark.gpu
 
@@ -37,6 +38,10 @@ CASES = {
     "wide scan, B=4 T=300": lambda: test_gpu_wide.test_wide_batch(4, 300, 16, 32, torch.bfloat16),
     "wide scan, packed ragged": test_gpu_wide.test_wide_packed_sequences_with_empty_and_ragged_lengths,
     "prefill state slots, bf16 pool": lambda: test_gpu_state_pools.test_prefill_state_slots(torch.bfloat16),
+    # 256-wide keys: key halves (two tiles a workgroup), one wave a tile (four tiles), packed sequences
+    "256-wide keys, T=300 V=256": lambda: test_gpu_chunk_k256.test_lengths_and_value_widths(300, 256),
+    "256-wide keys, 4-tile workgroups": test_gpu_chunk_k256.test_four_wave_workgroups,
+    "256-wide keys, packed sequences": test_gpu_chunk_k256.test_packed_sequences,
     # prefill with the layer epilogue: fused in the wide scan, and the two-kernel path
     "fused layer epilogue": lambda: test_gpu_chunk_layer.test_fused_in_the_wide_scan(
         4, 300, 16, torch.bfloat16, torch.float32),
