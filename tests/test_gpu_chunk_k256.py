@@ -8,7 +8,8 @@ cover both workgroup widths (2 waves, and 4 waves where the workgroups fill
 the CUs), chunk-edge lengths, packed sequences with empty and one-token
 members, state slots with has_initial_state and a bf16 pool, GQA with an odd
 group, float32 outputs, the X range scaling (|v| ~ 1e3), strong decay, and key
-and value widths the caller pads (K 200 -> 256, V 80 -> 96). At the full
+and value widths the caller pads (K 200 -> 256, V 80 -> 96), and the layer
+core (the operator, then the epilogue kernel). At the full
 32,768-token shape with 32 heads: the whole call against the oracle, and the
 two-call identity (a split at a chunk boundary, the state carried in fp32,
 equals one call bit for bit)."""
@@ -155,3 +156,26 @@ def test_full_shape_split_equals_one_call():
     assert torch.isfinite(o.float()).all() and torch.isfinite(s).all()
     assert torch.equal(o[:, :half], o1) and torch.equal(o[:, half:], o2)
     assert torch.equal(s, s2)
+
+
+def test_layer_core_two_pass():
+    """chunk_layer_fwd at K = 256 (the operator for 256-wide keys, then the
+    epilogue kernel) against the oracle operator and the oracle epilogue."""
+    from oracle import layer as ol
+    from pseudobrain_amd.layer import chunk_layer_fwd
+    from pseudobrain_amd.workloads import to_numpy
+    eps = 1e-5
+    q, k, v, g, beta, h0 = generate(2, 200, 2, 4, 256, 128, torch.bfloat16, 0.02, seed=51)
+    gen = torch.Generator().manual_seed(52)
+    z = torch.randn(2, 200, 3 * 4 * 128, generator=gen).to(torch.bfloat16)
+    gate = z[..., 4 * 128:2 * 4 * 128]  # a column slice of the projection, as the layer has it
+    o_norm = torch.rand(128, generator=gen) + 0.5
+    dev = to_dev(q, k, v, g, beta, h0, gate, o_norm)
+    with torch.no_grad():
+        hs, s = chunk_layer_fwd(*dev[:5], SCALE, dev[5], dev[6], dev[7], eps)
+    torch.cuda.synchronize()
+    o_ref, s_ref = oracle(q, k, v, g, beta, SCALE, h0)
+    hs_ref = ol.layer_epilogue(o_ref, to_numpy(gate.float()), to_numpy(o_norm), eps)
+    assert hs.shape == gate.shape
+    assert rel_err(hs, hs_ref.reshape(hs.shape)) <= 2e-2
+    assert rel_err(s, s_ref) <= 1e-3
