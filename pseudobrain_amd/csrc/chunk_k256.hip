@@ -6,7 +6,7 @@
 //
 // The arithmetic and the operand layouts are the wide scan's (chunk_wide.hip)
 // at twice the keys: the fp32 state tile S [256, 16] is 16 MFMA accumulator
-// tiles (64 registers) with permuted key rows (row 4g + i of state tile
+// tiles (64 registers; 8 in each of two waves with key halves) with permuted key rows (row 4g + i of state tile
 // 2kk + p holds key 32kk + 8g + 4p + i, so the slots of lane group g in key
 // step kk are one contiguous 16-byte piece of a K or Q row), and a chunk step
 // runs X -> U -> S and O without leaving the wave:
@@ -18,7 +18,8 @@
 // What the keys change is the LDS budget. A chunk's K and Q rows take 32 KiB
 // each at K = 256, so the wide scan's three K and two Q buffers (231 KiB with
 // the records and V) do not fit a CU's 160 KiB. Here K and the record are
-// double-buffered and Q and V single-buffered (at most 130 KiB), with two
+// double-buffered and Q and V single-buffered (126-130 KiB; 158 KiB with the
+// key-half exchange below), with two
 // barriers per step n:
 //   top:  chunk n is in LDS; every wave issues its share of the K and record
 //         loads of chunk n+1, into the buffers of chunk n-1
