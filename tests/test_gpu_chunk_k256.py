@@ -97,6 +97,19 @@ def test_packed_sequences():
     assert_parity("k256 packed", o, o_ref, s, s_ref)
 
 
+def test_many_short_sequences():
+    """200 packed sequences of 1 to 130 tokens (one workgroup per sequence,
+    value head and column group, most of them a chunk or less)."""
+    gen = torch.Generator().manual_seed(61)
+    lengths = torch.randint(1, 131, (200,), generator=gen).tolist()
+    q, k, v, g, beta, h0 = generate(1, sum(lengths), 1, 2, 256, 64, torch.bfloat16, 0.02, seed=62,
+                                    nstates=len(lengths))
+    cu = cu_seqlens_of(lengths)
+    o, s = run(q, k, v, g, beta, h0, cu)
+    o_ref, s_ref = oracle(q, k, v, g, beta, SCALE, h0, cu_seqlens=cu)
+    assert_parity("k256 200 short sequences", o, o_ref, s, s_ref)
+
+
 @pytest.mark.parametrize("pool_dtype", [torch.float32, torch.bfloat16])
 def test_state_slots(pool_dtype):
     """chunk_fwd_slots: sequences start from pool slots (zeros where

@@ -1,5 +1,5 @@
-"""The serving decode step, the fused decode layer step and the prefill
-captured in HIP graphs (torch.cuda.CUDAGraph), as a serving engine captures
+"""The serving decode step, the fused decode layer step and the prefill (at
+128- and 256-wide keys) captured in HIP graphs (torch.cuda.CUDAGraph), as a serving engine captures
 its decode loop: every call launches on torch's current stream and allocates
 nothing itself (outputs and workspaces come from torch, so from the graph's
 pool while capturing). Each test replays the graph several times with fresh
@@ -134,4 +134,33 @@ def test_prefill_replays_bit_for_bit():
             ref_o, ref_s = gd.chunk_fwd(*fresh[:5], d ** -0.5, fresh[5])
             torch.cuda.synchronize()
             print(f"[graph prefill] replay {r}", flush=True)
+            assert torch.equal(out, ref_o) and torch.equal(final, ref_s), r
+
+
+def test_prefill_256_wide_keys_replays_bit_for_bit():
+    """chunk_fwd at K = 256 (the prep kernel, then the scan for 256-wide keys)
+    in a graph against eager calls, fresh inputs each replay."""
+    b, t, hk, hv, d = 1, 200, 2, 4, 256
+
+    def draw(seed):
+        gen = torch.Generator().manual_seed(seed)
+        q = torch.nn.functional.normalize(torch.randn(b, t, hk, d, generator=gen), dim=-1).to(torch.bfloat16)
+        k = torch.nn.functional.normalize(torch.randn(b, t, hk, d, generator=gen), dim=-1).to(torch.bfloat16)
+        v = torch.randn(b, t, hv, d, generator=gen).to(torch.bfloat16)
+        g = -torch.rand(b, t, hv, generator=gen) * 0.5
+        beta = torch.rand(b, t, hv, generator=gen)
+        h0 = torch.randn(b, hv, d, d, generator=gen) * 0.05
+        return [x.to(DEV) for x in (q, k, v, g, beta, h0)]
+
+    static = draw(0)
+    with torch.no_grad():
+        graph, (out, final) = capture(lambda: gd.chunk_fwd(*static[:5], d ** -0.5, static[5]))
+        for r in range(REPLAYS):
+            fresh = draw(400 + r)
+            for s, x in zip(static, fresh):
+                s.copy_(x)
+            graph.replay()
+            ref_o, ref_s = gd.chunk_fwd(*fresh[:5], d ** -0.5, fresh[5])
+            torch.cuda.synchronize()
+            print(f"[graph prefill K=256] replay {r}", flush=True)
             assert torch.equal(out, ref_o) and torch.equal(final, ref_s), r

@@ -53,6 +53,8 @@ def case(length, hk, hv, dk, dv, seed, lengths=None, dtype=torch.bfloat16, v_sca
     # float32 inputs (the range scale of v and h0 is reduced into the scratch's
     # tail): v x 1e3, then a smaller call with v x 1e5 and other heads
     ((2048, 4, 4, 64, 64, 5, None, torch.float32, 1e3), (900, 2, 4, 128, 64, 6, [500, 400], torch.float32, 1e5)),
+    # 256-wide keys (the prep kernel at K = 256, then the scan for such keys)
+    ((2000, 2, 4, 256, 128, 7, None), (600, 1, 2, 256, 64, 8, [250, 350])),
 ])
 def test_noalloc_equals_the_workspace_entry_point(first, second):
     for length, hk, hv, dk, dv, seed, lengths, *more in (first, second):
