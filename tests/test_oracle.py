@@ -144,6 +144,25 @@ def test_chunked_equals_sequential(chunk, length):
     assert close(o1, o2, 1e-10) and close(s1, s2, 1e-10)
 
 
+def test_wide_heads_chunked_equals_sequential_and_zero_padding_is_exact():
+    """At 256-wide keys the chunked algorithm still equals the recurrence, and
+    zero-padding the head widths (K 200 -> 256 in q, k, h0; V 80 -> 96 in v,
+    h0, as the device path pads them) leaves the original block of o and of
+    the final state unchanged and the padded parts zero."""
+    q, k, v, g, beta, h0 = rand_inputs(1, 130, 2, 256, 64)
+    o1, s1 = gdn.delta_rule_chunked(q, k, v, g, beta, 0.0625, h0)
+    o2, s2 = gdn.delta_rule_sequential(q, k, v, g, beta, 0.0625, h0)
+    assert close(o1, o2, 1e-10) and close(s1, s2, 1e-10)
+    q, k, v, g, beta, h0 = rand_inputs(1, 100, 2, 200, 80)
+    o, s = gdn.delta_rule_chunked(q, k, v, g, beta, 0.07, h0)
+    pk = ((0, 0), (0, 0), (0, 0), (0, 56))
+    hp = np.pad(h0, ((0, 0), (0, 0), (0, 56), (0, 16)))
+    op, sp = gdn.delta_rule_chunked(np.pad(q, pk), np.pad(k, pk), np.pad(v, ((0, 0), (0, 0), (0, 0), (0, 16))),
+                                    g, beta, 0.07, hp)
+    assert close(op[..., :80], o, 1e-12) and close(sp[..., :200, :80], s, 1e-12)
+    assert not op[..., 80:].any() and not sp[..., 200:, :].any() and not sp[..., :, 80:].any()
+
+
 def test_chunked_low_decay_long_range():
     """Slow decay (g scaled by 0.01): the initial state stays visible for hundreds
     of steps; chunked still equals sequential."""
