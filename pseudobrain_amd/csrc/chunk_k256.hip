@@ -88,7 +88,8 @@ __host__ __device__ constexpr int kswz(int r) { return 4 * (r & 3) + ((r >> 2) &
 // 8-byte positions modulo 256 bytes.
 template <int WT>
 __host__ __device__ constexpr int vswz_k(int r) {
-  return 2 * ((r >> (WT == 8 ? 0 : WT == 4 ? 1 : 2)) & (WT - 1));
+  static_assert(WT == 2 || WT == 4, "2 or 4 tiles");
+  return 2 * ((r >> (WT == 4 ? 1 : 2)) & (WT - 1));
 }
 
 template <typename TIn, typename TOut, int WT, int KH>
