@@ -450,21 +450,50 @@ def _(q, k, v, g, beta, h0, grad_o, grad_final, scale):
 
 def _chunk_setup(ctx, inputs, output):
     q, k, v, g, beta, h0, cu_seqlens, scale = inputs
-    ctx.save_for_backward(q, k, v, g, beta, h0)
+    ctx.save_for_backward(q, k, v, g, beta, h0, cu_seqlens)
     ctx.scale = scale
-    ctx.packed = cu_seqlens is not None
+
+
+def _packed_backward(q, k, v, g, beta, h0, cu_seqlens, grad_o, grad_final, scale):
+    """The backward of a packed call ([1, sum T] with cu_seqlens): each
+    sequence's slice through the batched backward (its own h0 and final-state
+    gradient), the gradients written back into the packed layout. An empty
+    sequence's final state is its h0, so its dh0 is its final-state gradient."""
+    bounds = [min(max(int(x), 0), q.shape[1]) for x in cu_seqlens.tolist()]
+    nseq = len(bounds) - 1
+    dq, dk, dv = torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v)
+    dg = torch.zeros(g.shape, dtype=torch.float32, device=g.device)
+    dbeta = torch.zeros(beta.shape, dtype=beta.dtype if beta.dtype in (torch.float32, q.dtype) else torch.float32,
+                        device=beta.device)
+    dh0 = torch.zeros(nseq, v.shape[2], q.shape[3], v.shape[3], dtype=torch.float32, device=q.device)
+    for n in range(nseq):
+        lo, hi = bounds[n], max(bounds[n], bounds[n + 1])
+        if hi == lo:
+            if grad_final is not None:
+                dh0[n] = grad_final[n]
+            continue
+        sl = slice(lo, hi)
+        r = gated_delta_chunk_backward(q[:, sl], k[:, sl], v[:, sl], g[:, sl], beta[:, sl],
+                                       None if h0 is None else h0[n:n + 1], grad_o[:, sl],
+                                       None if grad_final is None else grad_final[n:n + 1], scale)
+        dq[:, sl], dk[:, sl], dv[:, sl], dg[:, sl], dbeta[:, sl] = r[0], r[1], r[2], r[3], r[4]
+        dh0[n] = r[5][0]
+    return dq, dk, dv, dg, dbeta, dh0
 
 
 def _chunk_grad(ctx, grad_o, grad_final):
     """The reference's _fla_grad (gated_deltanet.py:266-275): zeros for a
-    missing output gradient, each gradient in its input's dtype."""
-    if ctx.packed:
-        raise NotImplementedError("the chunk backward takes [B,T] batches; packed sequences (cu_seqlens) "
-                                  "have no backward here")
-    q, k, v, g, beta, h0 = ctx.saved_tensors
+    missing output gradient, each gradient in its input's dtype. A packed call
+    (cu_seqlens) takes the batched backward sequence by sequence."""
+    q, k, v, g, beta, h0, cu_seqlens = ctx.saved_tensors
     if grad_o is None:
         grad_o = torch.zeros(*q.shape[:2], v.shape[2], v.shape[3], dtype=q.dtype, device=q.device)
-    dq, dk, dv, dg, dbeta, dh0 = gated_delta_chunk_backward(q, k, v, g, beta, h0, grad_o, grad_final, ctx.scale)
+    if cu_seqlens is not None:
+        dq, dk, dv, dg, dbeta, dh0 = _packed_backward(q, k, v, g, beta, h0, cu_seqlens, grad_o, grad_final,
+                                                      ctx.scale)
+    else:
+        dq, dk, dv, dg, dbeta, dh0 = gated_delta_chunk_backward(q, k, v, g, beta, h0, grad_o, grad_final,
+                                                                ctx.scale)
     return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg.to(g.dtype), dbeta.to(beta.dtype),
             None if h0 is None else dh0.to(h0.dtype), None, None)
 
@@ -649,9 +678,6 @@ def delta_rule_hip(q, k, v, g, beta, scale, h0, cu_seqlens=None):
     _head_bound(dk, dv)
     grad = grad_needed(q, k, v, g, beta, h0)
     if grad:
-        if cu_seqlens is not None:
-            raise RuntimeError("the chunk backward takes [B,T] batches: packed sequences (cu_seqlens) have no "
-                               "backward; call under torch.no_grad() or pass a batch")
         if dk > BACKWARD_HEAD_DIMS[-1] or dv > BACKWARD_HEAD_DIMS[-1]:
             raise RuntimeError(f"the chunk backward is built for K, V <= {BACKWARD_HEAD_DIMS[-1]} "
                                f"(got K={dk}, V={dv}); call under torch.no_grad()")

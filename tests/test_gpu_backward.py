@@ -107,6 +107,42 @@ def test_autograd_through_the_operator():
                                      dbeta=torch.float32, dh0=torch.float32))
 
 
+@pytest.mark.parametrize("dtype,dk,dv", [(torch.bfloat16, 128, 128), (torch.float32, 96, 64)])
+def test_autograd_through_packed_sequences(dtype, dk, dv):
+    """A packed training call (cu_seqlens, one h0 per sequence, an empty
+    sequence among them) through gated_delta_rule(..., 'hip'): the backward
+    runs sequence by sequence and gives the oracle's gradients of each."""
+    from pseudobrain_amd.workloads import cu_seqlens_of
+    lengths = [70, 0, 130, 5, 64]
+    n, total = len(lengths), sum(lengths)
+    q, k, v, g, beta, h0 = generate(1, total, 2, 4, dk, dv, dtype, 0.05, seed=21, nstates=n)
+    gen = torch.Generator().manual_seed(22)
+    do = (torch.randn(1, total, 4, dv, generator=gen) * 0.1).to(dtype)
+    dht = torch.randn(n, 4, dk, dv, generator=gen) * 0.1
+    cu = cu_seqlens_of(lengths)
+    leaves = [x.to(DEV).requires_grad_() for x in (q, k, v, g, beta, h0)]
+    o, final = gd.gated_delta_rule(*leaves[:5], dk ** -0.5, leaves[5], "hip", cu_seqlens=cu.to(DEV))
+    loss = (o * do.to(DEV).float()).sum() + (final * dht.to(DEV)).sum()
+    loss.backward()
+    torch.cuda.synchronize()
+    got = [x.grad for x in leaves]
+    parts, dh0 = [], []
+    bounds = cu.tolist()
+    for i in range(n):
+        sl = slice(bounds[i], bounds[i + 1])
+        if bounds[i + 1] == bounds[i]:
+            dh0.append(to_numpy(dht[i].double()))
+            continue
+        r = oracle_grads(q[:, sl], k[:, sl], v[:, sl], g[:, sl], beta[:, sl], dk ** -0.5, h0[i:i + 1],
+                         do[:, sl].float(), dht[i:i + 1])
+        parts.append(r[:5])
+        dh0.append(r[5][0])
+    ref = [np.concatenate([p_[j] for p_ in parts], axis=1) for j in range(5)] + [np.stack(dh0)]
+    check(f"packed autograd {dtype} K={dk} V={dv}", got, ref,
+          dict(dq=dtype, dk=dtype, dv=dtype, dg=torch.float32, dbeta=torch.float32, dh0=torch.float32))
+    assert torch.equal(got[5][1].cpu(), dht[1])  # the empty sequence: its final state is its h0
+
+
 def test_zero_length_gives_the_final_gradient_as_dh0():
     q, k, v, g, beta, h0, do, dht = make(1, 0, 1, 1, 64, 64, torch.float32, seed=3)
     got = gd.chunk_bwd(*[x.to(DEV) for x in (q, k, v, g, beta)], 0.125, h0.to(DEV), do.to(DEV), dht.to(DEV))
