@@ -25,12 +25,14 @@ with h0 / final states [N,Hv,K,V].
 Head widths. Every device call with K, V <= 256 (fla_usable's bound, :189-197)
 runs: widths between the kernels' instantiations are zero-padded, which leaves
 the recurrence exact (a zero key or query dimension never enters a product, and
-zero value columns start and stay zero); K above 128, which the chunk kernel is
-not built for, runs the prefill through the recurrent kernel.
+zero value columns start and stay zero); K above 128 runs on the chunk kernel
+for 256-wide keys with 16-bit inputs, and token by token through the
+recurrent kernel with float32 inputs.
 
 Gradients. gated_delta_rule's device paths are differentiable through the chunk
-operator's backward (pbgdn::gated_delta_chunk, for K, V <= 128 and [B,T]
-batches); a training call through "sequential" (T <= SEQUENTIAL_MAX) takes the
+operator's backward (pbgdn::gated_delta_chunk, for K, V <= 128; a packed
+call's backward runs sequence by sequence); a training call through
+"sequential" (T <= SEQUENTIAL_MAX) takes the
 same operator. The lower-level entry points (chunk_fwd, chunk_fwd_slots,
 recurrent_fwd, the decode and slot ops, the layer kernels in
 pseudobrain_amd.layer) have no backward: with grad mode on and an input that
