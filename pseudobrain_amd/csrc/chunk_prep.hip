@@ -464,8 +464,9 @@ int launch_prep(const ChunkParams &p, long records, hipStream_t stream) {
   if (items > 0x3fffffffL) return PBGDN_ERR_UNSUPPORTED;  // item numbers are 32-bit
   const long grid = prep_grid(items, p.cus, prep_wg_per_cu<K, TIn>(), p.xcds);
   // Records of a large call are written non-temporally: measured on the
-  // 32,768-token call (213 MB of records as laid out, when every unit was
-  // still stored), the scan then reads them 2% faster.
+  // 32,768-token call, the whole call is 2% faster than with cached stores
+  // (0.663-0.666 against 0.673-0.676 ms with the 160 MB of records stored
+  // now; the same with the 213 MB stored before).
   const int nt = records * p.Hv * static_cast<long>(rec_bytes<TIn>()) > REC_STREAM_BYTES ? 1 : 0;
   hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(PNT), smem, stream, p, static_cast<int>(items), nt);
   return hipGetLastError() == hipSuccess ? PBGDN_OK : PBGDN_ERR_LAUNCH;
